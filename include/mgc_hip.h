@@ -1,0 +1,302 @@
+/* MI355X (gfx950) kernel library and model runtime of the ml-graph-compiler `hip` backend.
+ *
+ * This header is the C ABI between the code the hip emitter generates for one model and the
+ * prebuilt library libmgc_hip.so. Every kernel entry point takes plain pointers and sizes; device
+ * pointers point into the single HBM allocation that holds the planner's arena, the weights blob
+ * and the input/output staging buffers of a model.
+ *
+ * Reference counterparts (paths relative to the reference repository):
+ *   mgc_hip_gemm            <- mgc_gemm + mgc_gemm_args/mgc_operand/mgc_epilogue
+ *                              (src/ml_graph_compiler/codegen/runtime/mgc_runtime.h:120-161,
+ *                               mgc_kernels.c:328-396)
+ *   mgc_hip_depthwise       <- mgc_depthwise_nhwc / mgc_depthwise_nchw (mgc_runtime.h:175-182)
+ *   mgc_hip_pool            <- mgc_pool_nhwc / mgc_pool_nchw (mgc_runtime.h:185-190)
+ *   mgc_hip_reduce_mid      <- mgc_reduce_mid (mgc_runtime.h:193)
+ *   mgc_hip_softmax         <- mgc_softmax (mgc_runtime.h:196)
+ *   mgc_hip_layer_norm      <- mgc_layer_norm (mgc_runtime.h:199-200)
+ *   mgc_hip_elementwise     <- the loop nests CEmitter.elementwise/loops emit (codegen/c.py:360-529)
+ *   mgc_hip_copy            <- the identity-body loop nests of op_Transpose/Expand/Tile/Slice/
+ *                              Concat/Split/Pad (codegen/c.py:558-660) and output copies (c.py:1283)
+ *   mgc_hip_fill            <- constant loops of _write_constant/op_ConstantOfShape (c.py:690-722)
+ *   mgc_hip_gather          <- op_Gather (codegen/c.py:662-688), error code 1 on a bad index
+ *   mgc_hip_range           <- op_Range (codegen/c.py:724-734)
+ *   mgc_hip_reduce          <- CEmitter._reduce generic loop (codegen/c.py:736-799)
+ *   mgc_hip_argmax          <- op_ArgMax (codegen/c.py:801-821)
+ *   mgc_hip_model_*         <- what mgc_run and CompiledModel do around the generated function
+ *                              (codegen/c.py:1276-1326, codegen/runtime_lib.py:44-156)
+ */
+#ifndef MGC_HIP_H
+#define MGC_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------------------------------- */
+/* shared enums                                                                             */
+/* ---------------------------------------------------------------------------------------- */
+
+/* Activations fused into GEMM / convolution / depthwise epilogues (same set and order as the
+ * reference's MGC_ACT_*, mgc_runtime.h:93-101). */
+enum {
+    MGC_ACT_NONE = 0,
+    MGC_ACT_RELU = 1,
+    MGC_ACT_CLIP = 2,
+    MGC_ACT_GELU = 3,
+    MGC_ACT_GELU_TANH = 4,
+    MGC_ACT_TANH = 5,
+    MGC_ACT_SIGMOID = 6
+};
+
+/* Element types understood by the elementwise, copy, fill, reduce and gather kernels. */
+enum {
+    MGC_F32 = 0,
+    MGC_F64 = 1,
+    MGC_I64 = 2,
+    MGC_I32 = 3,
+    MGC_I8 = 4,
+    MGC_U8 = 5,
+    MGC_BOOL = 6
+};
+
+/* Status codes returned by the model runtime and by mgc_run. */
+enum {
+    MGC_OK = 0,
+    MGC_ERR_GATHER_INDEX = 1, /* a Gather index was out of range (reference: mgc_run returns 1) */
+    MGC_ERR_HIP = 2,          /* a HIP runtime call failed; see mgc_hip_last_error() */
+    MGC_ERR_ARGS = 3          /* the library was called with arguments it does not accept */
+};
+
+/* Opaque execution context: stream, error flag and profiling state of one model. */
+typedef struct mgc_hip_exec mgc_hip_exec;
+
+/* ---------------------------------------------------------------------------------------- */
+/* GEMM and implicit-GEMM convolution on fp32 MFMA                                            */
+/* ---------------------------------------------------------------------------------------- */
+
+/* How an operand matrix is read.
+ *   MGC_OP_STRIDED:   element (r, c) = p[r * rs + c * cs]
+ *   MGC_OP_CONV_NHWC: A only. Implicit im2col of an NHWC image batch: row m is output pixel
+ *                     (n, oh, ow) with m = (n * OH + oh) * OW + ow, column k is
+ *                     (kh * KW + kw) * cg + c; p already includes the group channel offset.
+ *   MGC_OP_CONV_NCHW: B only. Implicit im2col of one NCHW image: row k = (c * KH + kh) * KW + kw,
+ *                     column = output pixel oh * OW + ow.                                      */
+enum { MGC_OP_STRIDED = 0, MGC_OP_CONV_NHWC = 1, MGC_OP_CONV_NCHW = 2 };
+
+typedef struct {
+    int kind;
+    const float *p;
+    long rs, cs;
+    int H, W, C, KH, KW, SH, SW, DH, DW, PT, PL, OH, OW, cg;
+} mgc_hip_operand;
+
+/* C[z] = act(alpha * A[z] B[z] + bias + beta * R[z]) for every batch index z.
+ * bias_mode 1 adds bias[n] per column, 2 adds bias[m] per row. The batch index z runs over
+ * batch_dims[0..batch_rank) (row-major) and moves each pointer by sum_d idx_d * x_bs[d]
+ * elements. split_k > 1 splits K over that many partial products in `workspace`
+ * (split_k * M * N floats per batch element, with batch_count <= 1); 0 lets the library choose
+ * and then requires workspace_floats to say how much workspace is available. */
+typedef struct {
+    int M, N, K;
+    mgc_hip_operand a, b;
+    float *c;
+    long ldc;
+    float alpha, beta;
+    const float *bias;
+    int bias_mode;
+    const float *res;
+    long ldr;
+    int act;
+    float lo, hi;
+    int batch_rank;
+    int batch_dims[4];
+    long a_bs[4], b_bs[4], c_bs[4], r_bs[4];
+    float *workspace;
+    long workspace_floats;
+    int split_k;
+} mgc_hip_gemm_args;
+
+void mgc_hip_gemm(mgc_hip_exec *x, const mgc_hip_gemm_args *g);
+
+/* Workspace floats mgc_hip_gemm wants for a GEMM of this shape (0 = none). The emitter asks
+ * at compile time and reserves it through the memory planner's workspace hook. */
+long mgc_hip_gemm_workspace(int M, int N, int K, int batch);
+
+/* ---------------------------------------------------------------------------------------- */
+/* memory-bound kernels                                                                      */
+/* ---------------------------------------------------------------------------------------- */
+
+/* Depthwise convolution (one input channel per group) with bias, residual and activation.
+ * NHWC with HWC-ordered weights (w[(kh * KW + kw) * C + c]) or NCHW with CHW weights. */
+void mgc_hip_depthwise(mgc_hip_exec *x, int nhwc, int N, int H, int W, int C, int KH, int KW,
+                       int SH, int SW, int DH, int DW, int PT, int PL, int OH, int OW,
+                       const float *in, const float *w, const float *bias, const float *res,
+                       int act, float lo, float hi, float *out);
+
+/* Max or average pooling; pads are (top, left, bottom, right). */
+void mgc_hip_pool(mgc_hip_exec *x, int nhwc, int is_max, int N, int H, int W, int C, int KH,
+                  int KW, int SH, int SW, int DH, int DW, int PT, int PL, int PB, int PR, int OH,
+                  int OW, int count_include_pad, const float *in, float *out);
+
+/* Mean or max over the middle axis of an [outer, n, inner] float tensor. */
+void mgc_hip_reduce_mid(mgc_hip_exec *x, int is_max, long outer, long n, long inner,
+                        const float *in, float *out);
+
+/* Generic reduction over the middle axis of [outer, n, inner]: kind 0 sum, 1 mean, 2 max,
+ * 3 min, 4 prod; float sums/means/products accumulate in double like the reference. */
+void mgc_hip_reduce(mgc_hip_exec *x, int kind, int dtype, long outer, long n, long inner,
+                    const void *in, void *out);
+
+/* Index of the first maximum along the middle axis of [outer, n, inner]; int64 output. */
+void mgc_hip_argmax(mgc_hip_exec *x, int dtype, long outer, long n, long inner, const void *in,
+                    int64_t *out);
+
+/* Softmax or log-softmax along the middle axis of an [outer, n, inner] float tensor. */
+void mgc_hip_softmax(mgc_hip_exec *x, long outer, long n, long inner, const float *in,
+                     float *out, int log_softmax);
+
+/* Layer normalization of each row of [rows, cols]; scale and bias may be NULL. */
+void mgc_hip_layer_norm(mgc_hip_exec *x, long rows, long cols, const float *in,
+                        const float *scale, const float *bias, float eps, float *out);
+
+/* ---------------------------------------------------------------------------------------- */
+/* elementwise programs, copies, fills, gathers                                              */
+/* ---------------------------------------------------------------------------------------- */
+
+#define MGC_EW_MAX_RANK 6
+#define MGC_EW_MAX_LEAVES 16
+#define MGC_EW_MAX_INSTR 32
+
+/* Elementwise opcodes (one per reference elementwise operator, ops.py:122-375). */
+enum {
+    MGC_EW_ADD = 0, MGC_EW_SUB, MGC_EW_MUL, MGC_EW_DIV, MGC_EW_POW, MGC_EW_MAX, MGC_EW_MIN,
+    MGC_EW_EQUAL, MGC_EW_LESS, MGC_EW_GREATER, MGC_EW_LESS_EQUAL, MGC_EW_GREATER_EQUAL,
+    MGC_EW_AND, MGC_EW_OR, MGC_EW_XOR, MGC_EW_WHERE, MGC_EW_RELU, MGC_EW_SIGMOID, MGC_EW_TANH,
+    MGC_EW_ERF, MGC_EW_SQRT, MGC_EW_EXP, MGC_EW_LOG, MGC_EW_NEG, MGC_EW_ABS, MGC_EW_RECIPROCAL,
+    MGC_EW_FLOOR, MGC_EW_CEIL, MGC_EW_SIN, MGC_EW_COS, MGC_EW_SOFTPLUS, MGC_EW_IDENTITY,
+    MGC_EW_NOT, MGC_EW_GELU, MGC_EW_GELU_TANH, MGC_EW_LEAKY_RELU, MGC_EW_HARD_SIGMOID,
+    MGC_EW_CLIP, MGC_EW_CAST, MGC_EW_COUNT
+};
+
+typedef struct {
+    const void *p;
+    int dtype;
+    long strides[MGC_EW_MAX_RANK]; /* element strides over the output dims (0 = broadcast) */
+} mgc_hip_ew_leaf;
+
+/* One instruction: out_dtype = op(args) where args index the register file (leaves first,
+ * then instruction results; -1 = absent). in_dtype is the dtype of the first argument; fa/fb
+ * are float attributes (LeakyRelu alpha, HardSigmoid alpha/beta, Clip bounds when args are
+ * absent). */
+typedef struct {
+    int op, in_dtype, out_dtype;
+    int args[3];
+    float fa, fb;
+} mgc_hip_ew_instr;
+
+typedef struct {
+    int rank;
+    long dims[MGC_EW_MAX_RANK];
+    long out_strides[MGC_EW_MAX_RANK];
+    long out_base;
+    int n_leaves, n_instr;
+    mgc_hip_ew_leaf leaf[MGC_EW_MAX_LEAVES];
+    mgc_hip_ew_instr instr[MGC_EW_MAX_INSTR];
+    void *out;
+    int out_dtype;
+} mgc_hip_ew_args;
+
+void mgc_hip_elementwise(mgc_hip_exec *x, const mgc_hip_ew_args *e);
+
+/* N-d strided copy: out[o_base + sum i_d * o_st_d] = in[i_base + sum (i_d % mod_d) * i_st_d]
+ * over dims (mod_d = 0 means no modulus). Element size in bytes: 1, 2, 4 or 8. */
+typedef struct {
+    int rank;
+    long dims[MGC_EW_MAX_RANK];
+    long in_strides[MGC_EW_MAX_RANK];
+    long out_strides[MGC_EW_MAX_RANK];
+    long in_mod[MGC_EW_MAX_RANK];
+    long in_base, out_base;
+    const void *in;
+    void *out;
+    int elem_bytes;
+} mgc_hip_copy_args;
+
+void mgc_hip_copy(mgc_hip_exec *x, const mgc_hip_copy_args *c);
+
+/* Fill n elements of elem_bytes each with the bit pattern `bits`. */
+void mgc_hip_fill(mgc_hip_exec *x, void *out, long n, int elem_bytes, uint64_t bits);
+
+/* out[o, t, :] = src[o, idx[t], :] with negative indices wrapped; an index out of [0, dim)
+ * sets the model's error flag (mgc_run then returns MGC_ERR_GATHER_INDEX). */
+void mgc_hip_gather(mgc_hip_exec *x, const void *src, const void *idx, int idx_dtype,
+                    long outer, long dim, long n, long inner_bytes, void *out);
+
+/* out[o] = start + o * delta for o < n (dtype MGC_F32/F64/I64/I32). */
+void mgc_hip_range(mgc_hip_exec *x, int dtype, const void *start, const void *delta, long n,
+                   void *out);
+
+/* ---------------------------------------------------------------------------------------- */
+/* model runtime                                                                             */
+/* ---------------------------------------------------------------------------------------- */
+
+/* The forward function the emitter generates: one launcher call per scheduled node. A, W, in
+ * and out are device pointers. */
+typedef void (*mgc_hip_forward_fn)(mgc_hip_exec *x, const void *const *in, void *const *out,
+                                   unsigned char *A, const unsigned char *W);
+
+typedef struct {
+    size_t arena_bytes;
+    size_t weights_bytes;
+    int n_inputs, n_outputs;
+    const size_t *input_bytes;
+    const size_t *output_bytes;
+    int n_nodes;       /* nodes with profiling markers (0 when compiled without profile) */
+    mgc_hip_forward_fn forward;
+    void *state;       /* owned by the runtime */
+} mgc_hip_model;
+
+/* Allocate one HBM block (arena | weights | input staging | output staging | flags), upload
+ * the weights once and return the device arena and weights pointers. Idempotent. */
+int mgc_hip_model_init(mgc_hip_model *m, const unsigned char *weights_host, unsigned char **A,
+                       unsigned char **W);
+/* Host inputs/outputs: H2D copy, replay of the captured hipGraph, D2H copy, synchronize. */
+int mgc_hip_model_run(mgc_hip_model *m, const void *const *inputs, void *const *outputs,
+                      unsigned char *A, const unsigned char *W);
+/* Device inputs/outputs (for example torch tensors); the graph is re-captured when the pointer
+ * set changes. Synchronizes and returns the status. */
+int mgc_hip_model_run_device(mgc_hip_model *m, const void *const *inputs, void *const *outputs,
+                             unsigned char *A, const unsigned char *W);
+/* Resident-input execution for benchmarks: upload once, then enqueue replays without copies. */
+int mgc_hip_model_upload(mgc_hip_model *m, const void *const *inputs);
+int mgc_hip_model_launch(mgc_hip_model *m, int replays);
+int mgc_hip_model_sync(mgc_hip_model *m);
+int mgc_hip_model_download(mgc_hip_model *m, void *const *outputs);
+/* Eager (non-graph) execution on the staged inputs with a hipEvent pair around every profiled
+ * node; seconds accumulate into the per-node profile. */
+int mgc_hip_model_profile_run(mgc_hip_model *m, int replays);
+const double *mgc_hip_model_profile_data(mgc_hip_model *m);
+void mgc_hip_model_profile_reset(mgc_hip_model *m);
+/* Time `replays` graph replays between two hipEvents on the model stream; milliseconds. */
+double mgc_hip_model_time_graph(mgc_hip_model *m, int replays);
+void mgc_hip_model_release(mgc_hip_model *m);
+
+/* Profiling markers emitted around each node when the model is compiled with profile=True. */
+void mgc_hip_node_begin(mgc_hip_exec *x, int node);
+void mgc_hip_node_end(mgc_hip_exec *x, int node);
+
+/* Text of the last HIP error seen by the library (empty when none). */
+const char *mgc_hip_last_error(void);
+/* Version string of the kernel library. */
+const char *mgc_hip_version(void);
+/* Number of visible HIP devices (0 without a GPU; never fails). */
+int mgc_hip_device_count(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MGC_HIP_H */

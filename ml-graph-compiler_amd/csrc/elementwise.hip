@@ -1,0 +1,469 @@
+// Elementwise programs, strided copies, fills, gathers and ranges.
+//
+// The reference's C backend emits one broadcast-strided loop nest per elementwise node or
+// FusedElementwise program (src/ml_graph_compiler/codegen/c.py:360-529) and identity-body loop
+// nests for the copy family (c.py:558-660). Here those bodies are data: the emitter encodes the
+// program (leaf operands with element strides over the collapsed output dims, then a list of
+// typed instructions) into mgc_hip_ew_args, and one grid-stride kernel evaluates it per element.
+// Every branch on the program is uniform across the wavefront (it depends only on kernel
+// arguments), so it runs on the scalar unit; the vector unit only does the arithmetic, loads
+// and stores. Registers hold 64-bit patterns: float32 bits, float64 bits, or sign-extended
+// integers, and every integer result is narrowed to its output dtype the way numpy's _keep does.
+#include "mgc_device.h"
+
+namespace mgc {
+
+__device__ __forceinline__ float rf(uint64_t v) { return __uint_as_float((uint32_t)v); }
+__device__ __forceinline__ uint64_t wf(float f) { return (uint64_t)__float_as_uint(f); }
+__device__ __forceinline__ double rd(uint64_t v) { return __longlong_as_double((long long)v); }
+__device__ __forceinline__ uint64_t wd(double d) { return (uint64_t)__double_as_longlong(d); }
+
+__device__ __forceinline__ bool is_float(int dt) { return dt == MGC_F32 || dt == MGC_F64; }
+
+__device__ __forceinline__ uint64_t load_elem(const void *p, int dt, long i) {
+    switch (dt) {
+    case MGC_F32: return wf(static_cast<const float *>(p)[i]);
+    case MGC_F64: return wd(static_cast<const double *>(p)[i]);
+    case MGC_I64: return (uint64_t) static_cast<const long long *>(p)[i];
+    case MGC_I32: return (uint64_t)(long long) static_cast<const int *>(p)[i];
+    case MGC_I8: return (uint64_t)(long long) static_cast<const signed char *>(p)[i];
+    case MGC_U8: return (uint64_t) static_cast<const unsigned char *>(p)[i];
+    default: return static_cast<const unsigned char *>(p)[i] != 0 ? 1u : 0u;
+    }
+}
+
+__device__ __forceinline__ void store_elem(void *p, int dt, long i, uint64_t v) {
+    switch (dt) {
+    case MGC_F32: static_cast<float *>(p)[i] = rf(v); break;
+    case MGC_F64: static_cast<double *>(p)[i] = rd(v); break;
+    case MGC_I64: static_cast<long long *>(p)[i] = (long long)v; break;
+    case MGC_I32: static_cast<int *>(p)[i] = (int)(long long)v; break;
+    case MGC_I8: static_cast<signed char *>(p)[i] = (signed char)(long long)v; break;
+    case MGC_U8: static_cast<unsigned char *>(p)[i] = (unsigned char)(long long)v; break;
+    default: static_cast<unsigned char *>(p)[i] = v != 0 ? 1 : 0; break;
+    }
+}
+
+// Narrow an int64 result to the width of dtype (wrap-around like a numpy cast).
+__device__ __forceinline__ uint64_t narrow(long long v, int dt) {
+    switch (dt) {
+    case MGC_I32: return (uint64_t)(long long)(int)v;
+    case MGC_I8: return (uint64_t)(long long)(signed char)v;
+    case MGC_U8: return (uint64_t)(unsigned char)v;
+    case MGC_BOOL: return v != 0 ? 1u : 0u;
+    default: return (uint64_t)v;
+    }
+}
+
+// Convert a register of dtype `from` to dtype `to` (ONNX Cast; float -> int truncates).
+__device__ __forceinline__ uint64_t cast_reg(uint64_t v, int from, int to) {
+    if (from == to) return v;
+    if (to == MGC_BOOL) {
+        if (from == MGC_F32) return rf(v) != 0.0f;
+        if (from == MGC_F64) return rd(v) != 0.0;
+        return (long long)v != 0;
+    }
+    if (to == MGC_F32) {
+        if (from == MGC_F64) return wf((float)rd(v));
+        return wf((float)(long long)v);
+    }
+    if (to == MGC_F64) {
+        if (from == MGC_F32) return wd((double)rf(v));
+        return wd((double)(long long)v);
+    }
+    long long iv;
+    if (from == MGC_F32)
+        iv = (long long)rf(v);
+    else if (from == MGC_F64)
+        iv = (long long)rd(v);
+    else
+        iv = (long long)v;
+    return narrow(iv, to);
+}
+
+__device__ __forceinline__ float f32_op(const mgc_hip_ew_instr &in, float a, float b, float c,
+                                        bool has_b, bool has_c) {
+    switch (in.op) {
+    case MGC_EW_ADD: return a + b;
+    case MGC_EW_SUB: return a - b;
+    case MGC_EW_MUL: return a * b;
+    case MGC_EW_DIV: return a / b;
+    case MGC_EW_POW: return powf(a, b);
+    case MGC_EW_MAX: return fmaxf(a, b);
+    case MGC_EW_MIN: return fminf(a, b);
+    case MGC_EW_RELU: return a > 0.0f ? a : 0.0f;
+    case MGC_EW_SIGMOID: return sigmoid_f(a);
+    case MGC_EW_TANH: return tanhf(a);
+    case MGC_EW_ERF: return erf_rational(a);
+    case MGC_EW_SQRT: return sqrtf(a);
+    case MGC_EW_EXP: return expf(a);
+    case MGC_EW_LOG: return logf(a);
+    case MGC_EW_NEG: return -a;
+    case MGC_EW_ABS: return fabsf(a);
+    case MGC_EW_RECIPROCAL: return 1.0f / a;
+    case MGC_EW_FLOOR: return floorf(a);
+    case MGC_EW_CEIL: return ceilf(a);
+    case MGC_EW_SIN: return sinf(a);
+    case MGC_EW_COS: return cosf(a);
+    case MGC_EW_SOFTPLUS: return a > 20.0f ? a : log1pf(expf(a));
+    case MGC_EW_GELU: return gelu_erf_f(a);
+    case MGC_EW_GELU_TANH: return gelu_tanh_f(a);
+    case MGC_EW_LEAKY_RELU: return a >= 0.0f ? a : in.fa * a;
+    case MGC_EW_HARD_SIGMOID: return fminf(fmaxf(in.fa * a + in.fb, 0.0f), 1.0f);
+    case MGC_EW_CLIP: return fminf(fmaxf(a, has_b ? b : in.fa), has_c ? c : in.fb);
+    default: return a;  // Identity
+    }
+}
+
+__device__ __forceinline__ double f64_op(const mgc_hip_ew_instr &in, double a, double b,
+                                         double c, bool has_b, bool has_c) {
+    switch (in.op) {
+    case MGC_EW_ADD: return a + b;
+    case MGC_EW_SUB: return a - b;
+    case MGC_EW_MUL: return a * b;
+    case MGC_EW_DIV: return a / b;
+    case MGC_EW_POW: return pow(a, b);
+    case MGC_EW_MAX: return fmax(a, b);
+    case MGC_EW_MIN: return fmin(a, b);
+    case MGC_EW_RELU: return a > 0.0 ? a : 0.0;
+    case MGC_EW_TANH: return tanh(a);
+    case MGC_EW_SQRT: return sqrt(a);
+    case MGC_EW_EXP: return exp(a);
+    case MGC_EW_LOG: return log(a);
+    case MGC_EW_NEG: return -a;
+    case MGC_EW_ABS: return fabs(a);
+    case MGC_EW_RECIPROCAL: return 1.0 / a;
+    case MGC_EW_FLOOR: return floor(a);
+    case MGC_EW_CEIL: return ceil(a);
+    case MGC_EW_CLIP: return fmin(fmax(a, has_b ? b : (double)in.fa), has_c ? c : (double)in.fb);
+    default: return a;
+    }
+}
+
+__device__ __forceinline__ long long int_op(const mgc_hip_ew_instr &in, long long a, long long b,
+                                            long long c, bool has_b, bool has_c) {
+    switch (in.op) {
+    case MGC_EW_ADD: return a + b;
+    case MGC_EW_SUB: return a - b;
+    case MGC_EW_MUL: return a * b;
+    case MGC_EW_DIV: return b != 0 ? a / b : 0;
+    case MGC_EW_MAX: return a > b ? a : b;
+    case MGC_EW_MIN: return a < b ? a : b;
+    case MGC_EW_NEG: return -a;
+    case MGC_EW_ABS: return a < 0 ? -a : a;
+    case MGC_EW_RELU: return a > 0 ? a : 0;
+    case MGC_EW_CLIP: {
+        long long v = a;
+        if (has_b && v < b) v = b;
+        if (has_c && v > c) v = c;
+        return v;
+    }
+    default: return a;
+    }
+}
+
+// Compare / logical ops produce bool from operands of dtype dt.
+__device__ __forceinline__ bool cmp_op(int op, uint64_t a, uint64_t b, int dt) {
+    if (op == MGC_EW_AND) return a != 0 && b != 0;
+    if (op == MGC_EW_OR) return a != 0 || b != 0;
+    if (op == MGC_EW_XOR) return (a != 0) != (b != 0);
+    if (dt == MGC_F32) {
+        float x = rf(a), y = rf(b);
+        switch (op) {
+        case MGC_EW_EQUAL: return x == y;
+        case MGC_EW_LESS: return x < y;
+        case MGC_EW_GREATER: return x > y;
+        case MGC_EW_LESS_EQUAL: return x <= y;
+        default: return x >= y;
+        }
+    }
+    if (dt == MGC_F64) {
+        double x = rd(a), y = rd(b);
+        switch (op) {
+        case MGC_EW_EQUAL: return x == y;
+        case MGC_EW_LESS: return x < y;
+        case MGC_EW_GREATER: return x > y;
+        case MGC_EW_LESS_EQUAL: return x <= y;
+        default: return x >= y;
+        }
+    }
+    long long x = (long long)a, y = (long long)b;
+    switch (op) {
+    case MGC_EW_EQUAL: return x == y;
+    case MGC_EW_LESS: return x < y;
+    case MGC_EW_GREATER: return x > y;
+    case MGC_EW_LESS_EQUAL: return x <= y;
+    default: return x >= y;
+    }
+}
+
+__device__ __forceinline__ uint64_t eval_instr(const mgc_hip_ew_instr &in, uint64_t a, uint64_t b,
+                                               uint64_t c) {
+    const bool has_b = in.args[1] >= 0, has_c = in.args[2] >= 0;
+    switch (in.op) {
+    case MGC_EW_EQUAL:
+    case MGC_EW_LESS:
+    case MGC_EW_GREATER:
+    case MGC_EW_LESS_EQUAL:
+    case MGC_EW_GREATER_EQUAL:
+    case MGC_EW_AND:
+    case MGC_EW_OR:
+    case MGC_EW_XOR: return cmp_op(in.op, a, b, in.in_dtype) ? 1u : 0u;
+    case MGC_EW_NOT: return a != 0 ? 0u : 1u;
+    case MGC_EW_WHERE: return a != 0 ? b : c;
+    case MGC_EW_CAST: return cast_reg(a, in.in_dtype, in.out_dtype);
+    default: break;
+    }
+    if (in.in_dtype == MGC_F32) return wf(f32_op(in, rf(a), rf(b), rf(c), has_b, has_c));
+    if (in.in_dtype == MGC_F64) return wd(f64_op(in, rd(a), rd(b), rd(c), has_b, has_c));
+    return narrow(int_op(in, (long long)a, (long long)b, (long long)c, has_b, has_c), in.out_dtype);
+}
+
+#define MGC_NREG (MGC_EW_MAX_LEAVES + MGC_EW_MAX_INSTR)
+
+// Register file access with constant indices only, so it stays in VGPRs. `idx` is uniform.
+__device__ __forceinline__ uint64_t reg_get(const uint64_t (&R)[MGC_NREG], int idx) {
+    switch (idx) {
+#define MGC_CASE(i) case i: return R[i];
+        MGC_CASE(0) MGC_CASE(1) MGC_CASE(2) MGC_CASE(3) MGC_CASE(4) MGC_CASE(5) MGC_CASE(6)
+        MGC_CASE(7) MGC_CASE(8) MGC_CASE(9) MGC_CASE(10) MGC_CASE(11) MGC_CASE(12) MGC_CASE(13)
+        MGC_CASE(14) MGC_CASE(15) MGC_CASE(16) MGC_CASE(17) MGC_CASE(18) MGC_CASE(19)
+        MGC_CASE(20) MGC_CASE(21) MGC_CASE(22) MGC_CASE(23) MGC_CASE(24) MGC_CASE(25)
+        MGC_CASE(26) MGC_CASE(27) MGC_CASE(28) MGC_CASE(29) MGC_CASE(30) MGC_CASE(31)
+        MGC_CASE(32) MGC_CASE(33) MGC_CASE(34) MGC_CASE(35) MGC_CASE(36) MGC_CASE(37)
+        MGC_CASE(38) MGC_CASE(39) MGC_CASE(40) MGC_CASE(41) MGC_CASE(42) MGC_CASE(43)
+        MGC_CASE(44) MGC_CASE(45) MGC_CASE(46) MGC_CASE(47)
+#undef MGC_CASE
+    default: return 0;
+    }
+}
+
+__device__ __forceinline__ void reg_set(uint64_t (&R)[MGC_NREG], int idx, uint64_t v) {
+    switch (idx) {
+#define MGC_CASE(i) case i: R[i] = v; break;
+        MGC_CASE(16) MGC_CASE(17) MGC_CASE(18) MGC_CASE(19) MGC_CASE(20) MGC_CASE(21)
+        MGC_CASE(22) MGC_CASE(23) MGC_CASE(24) MGC_CASE(25) MGC_CASE(26) MGC_CASE(27)
+        MGC_CASE(28) MGC_CASE(29) MGC_CASE(30) MGC_CASE(31) MGC_CASE(32) MGC_CASE(33)
+        MGC_CASE(34) MGC_CASE(35) MGC_CASE(36) MGC_CASE(37) MGC_CASE(38) MGC_CASE(39)
+        MGC_CASE(40) MGC_CASE(41) MGC_CASE(42) MGC_CASE(43) MGC_CASE(44) MGC_CASE(45)
+        MGC_CASE(46) MGC_CASE(47)
+#undef MGC_CASE
+    default: break;
+    }
+}
+
+__global__ void __launch_bounds__(256) ew_program_kernel(const mgc_hip_ew_args e) {
+    long total = 1;
+    for (int d = 0; d < e.rank; ++d) total *= e.dims[d];
+    for (long idx = blockIdx.x * (long)blockDim.x + threadIdx.x; idx < total;
+         idx += (long)gridDim.x * blockDim.x) {
+        long coord[MGC_EW_MAX_RANK];
+        long rem = idx;
+#pragma unroll
+        for (int d = MGC_EW_MAX_RANK - 1; d >= 0; --d) {
+            if (d < e.rank) {
+                coord[d] = rem % e.dims[d];
+                rem /= e.dims[d];
+            } else {
+                coord[d] = 0;
+            }
+        }
+        uint64_t R[MGC_NREG];
+#pragma unroll
+        for (int l = 0; l < MGC_EW_MAX_LEAVES; ++l) {
+            if (l < e.n_leaves && e.leaf[l].p) {
+                long off = 0;
+#pragma unroll
+                for (int d = 0; d < MGC_EW_MAX_RANK; ++d)
+                    if (d < e.rank) off += coord[d] * e.leaf[l].strides[d];
+                R[l] = load_elem(e.leaf[l].p, e.leaf[l].dtype, off);
+            } else {
+                R[l] = 0;
+            }
+        }
+#pragma unroll
+        for (int i = MGC_EW_MAX_LEAVES; i < MGC_NREG; ++i) R[i] = 0;
+        uint64_t last = 0;
+        for (int i = 0; i < e.n_instr; ++i) {
+            const mgc_hip_ew_instr &in = e.instr[i];
+            uint64_t a = in.args[0] >= 0 ? reg_get(R, in.args[0]) : 0;
+            uint64_t b = in.args[1] >= 0 ? reg_get(R, in.args[1]) : 0;
+            uint64_t c = in.args[2] >= 0 ? reg_get(R, in.args[2]) : 0;
+            last = eval_instr(in, a, b, c);
+            reg_set(R, MGC_EW_MAX_LEAVES + i, last);
+        }
+        long ooff = e.out_base;
+#pragma unroll
+        for (int d = 0; d < MGC_EW_MAX_RANK; ++d)
+            if (d < e.rank) ooff += coord[d] * e.out_strides[d];
+        store_elem(e.out, e.out_dtype, ooff, last);
+    }
+}
+
+// N-d strided copy with optional per-dim modulus (Tile). T is the moved unit.
+template <typename T>
+__global__ void __launch_bounds__(256) copy_kernel(const mgc_hip_copy_args c) {
+    long total = 1;
+    for (int d = 0; d < c.rank; ++d) total *= c.dims[d];
+    const T *src = static_cast<const T *>(c.in);
+    T *dst = static_cast<T *>(c.out);
+    for (long idx = blockIdx.x * (long)blockDim.x + threadIdx.x; idx < total;
+         idx += (long)gridDim.x * blockDim.x) {
+        long rem = idx, io = c.in_base, oo = c.out_base;
+#pragma unroll
+        for (int d = MGC_EW_MAX_RANK - 1; d >= 0; --d) {
+            if (d < c.rank) {
+                long q = rem / c.dims[d];
+                long i = rem - q * c.dims[d];
+                rem = q;
+                oo += i * c.out_strides[d];
+                io += (c.in_mod[d] ? i % c.in_mod[d] : i) * c.in_strides[d];
+            }
+        }
+        dst[oo] = src[io];
+    }
+}
+
+template <typename T>
+__global__ void fill_kernel(T *out, long n, T v) {
+    for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < n;
+         i += (long)gridDim.x * blockDim.x)
+        out[i] = v;
+}
+
+// One workgroup per (outer, t) row; the row is copied in 4-byte words when aligned.
+__global__ void gather_kernel(const unsigned char *src, const void *idx, int idx_dtype,
+                              long outer, long dim, long n, long inner_bytes, unsigned char *out,
+                              int *flag) {
+    for (long row = blockIdx.x; row < outer * n; row += gridDim.x) {
+        const long o = row / n, t = row - (row / n) * n;
+        long k = idx_dtype == MGC_I64 ? static_cast<const long long *>(idx)[t]
+                                      : (long)static_cast<const int *>(idx)[t];
+        if (k < 0) k += dim;
+        if (k < 0 || k >= dim) {
+            if (threadIdx.x == 0) *flag = 1;
+            continue;
+        }
+        const unsigned char *s = src + (o * dim + k) * inner_bytes;
+        unsigned char *d = out + (o * n + t) * inner_bytes;
+        if ((inner_bytes & 3) == 0 && (((uintptr_t)s | (uintptr_t)d) & 3) == 0) {
+            const long words = inner_bytes >> 2;
+            for (long w = threadIdx.x; w < words; w += blockDim.x)
+                reinterpret_cast<unsigned *>(d)[w] = reinterpret_cast<const unsigned *>(s)[w];
+        } else {
+            for (long b = threadIdx.x; b < inner_bytes; b += blockDim.x) d[b] = s[b];
+        }
+    }
+}
+
+template <typename T>
+__global__ void range_kernel(const T *start, const T *delta, long n, T *out) {
+    for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < n;
+         i += (long)gridDim.x * blockDim.x)
+        out[i] = (T)(start[0] + (T)i * delta[0]);
+}
+
+}  // namespace mgc
+
+using namespace mgc;
+
+extern "C" void mgc_hip_elementwise(mgc_hip_exec *x, const mgc_hip_ew_args *e) {
+    long total = 1;
+    for (int d = 0; d < e->rank; ++d) total *= e->dims[d];
+    if (total <= 0) return;
+    MGC_LAUNCH(x, ew_program_kernel, dim3(blocks_for(total, 256, 8192)), dim3(256), 0, *e);
+}
+
+extern "C" void mgc_hip_copy(mgc_hip_exec *x, const mgc_hip_copy_args *c) {
+    long total = 1;
+    for (int d = 0; d < c->rank; ++d) total *= c->dims[d];
+    if (total <= 0) return;
+    mgc_hip_copy_args a = *c;
+    // Move 16-byte units when the innermost dim is contiguous on both sides, a multiple of the
+    // unit, and every stride and base keeps the unit aligned.
+    int r = a.rank;
+    if (r >= 1 && a.elem_bytes <= 8 && a.in_strides[r - 1] == 1 && a.out_strides[r - 1] == 1 &&
+        a.in_mod[r - 1] == 0) {
+        long per = 16 / a.elem_bytes;
+        bool ok = a.dims[r - 1] % per == 0 && a.in_base % per == 0 && a.out_base % per == 0 &&
+                  ((uintptr_t)a.in & 15) == 0 && ((uintptr_t)a.out & 15) == 0;
+        for (int d = 0; d < r - 1 && ok; ++d)
+            ok = a.in_strides[d] % per == 0 && a.out_strides[d] % per == 0 &&
+                 (a.in_mod[d] == 0);
+        if (ok) {
+            a.dims[r - 1] /= per;
+            for (int d = 0; d < r - 1; ++d) {
+                a.in_strides[d] /= per;
+                a.out_strides[d] /= per;
+            }
+            a.in_base /= per;
+            a.out_base /= per;
+            a.elem_bytes = 16;
+            total /= per;
+        }
+    }
+    dim3 grid(blocks_for(total, 256, 8192));
+    switch (a.elem_bytes) {
+    case 1: MGC_LAUNCH(x, copy_kernel<unsigned char>, grid, dim3(256), 0, a); break;
+    case 2: MGC_LAUNCH(x, copy_kernel<unsigned short>, grid, dim3(256), 0, a); break;
+    case 4: MGC_LAUNCH(x, copy_kernel<unsigned>, grid, dim3(256), 0, a); break;
+    case 8: MGC_LAUNCH(x, copy_kernel<unsigned long long>, grid, dim3(256), 0, a); break;
+    default: MGC_LAUNCH(x, copy_kernel<uint4>, grid, dim3(256), 0, a); break;
+    }
+}
+
+extern "C" void mgc_hip_fill(mgc_hip_exec *x, void *out, long n, int elem_bytes, uint64_t bits) {
+    if (n <= 0) return;
+    dim3 grid(blocks_for(n, 256, 8192));
+    switch (elem_bytes) {
+    case 1:
+        MGC_LAUNCH(x, fill_kernel<unsigned char>, grid, dim3(256), 0, (unsigned char *)out, n,
+                   (unsigned char)bits);
+        break;
+    case 2:
+        MGC_LAUNCH(x, fill_kernel<unsigned short>, grid, dim3(256), 0, (unsigned short *)out, n,
+                   (unsigned short)bits);
+        break;
+    case 4:
+        MGC_LAUNCH(x, fill_kernel<unsigned>, grid, dim3(256), 0, (unsigned *)out, n,
+                   (unsigned)bits);
+        break;
+    default:
+        MGC_LAUNCH(x, fill_kernel<unsigned long long>, grid, dim3(256), 0,
+                   (unsigned long long *)out, n, (unsigned long long)bits);
+        break;
+    }
+}
+
+extern "C" void mgc_hip_gather(mgc_hip_exec *x, const void *src, const void *idx, int idx_dtype,
+                               long outer, long dim, long n, long inner_bytes, void *out) {
+    long rows = outer * n;
+    if (rows <= 0 || inner_bytes <= 0) return;
+    unsigned grid = (unsigned)(rows < 65536 ? rows : 65536);
+    MGC_LAUNCH(x, gather_kernel, dim3(grid), dim3(256), 0, (const unsigned char *)src, idx,
+               idx_dtype, outer, dim, n, inner_bytes, (unsigned char *)out, x->flag);
+}
+
+extern "C" void mgc_hip_range(mgc_hip_exec *x, int dtype, const void *start, const void *delta,
+                              long n, void *out) {
+    if (n <= 0) return;
+    dim3 grid(blocks_for(n, 256, 4096));
+    switch (dtype) {
+    case MGC_F32:
+        MGC_LAUNCH(x, range_kernel<float>, grid, dim3(256), 0, (const float *)start,
+                   (const float *)delta, n, (float *)out);
+        break;
+    case MGC_F64:
+        MGC_LAUNCH(x, range_kernel<double>, grid, dim3(256), 0, (const double *)start,
+                   (const double *)delta, n, (double *)out);
+        break;
+    case MGC_I32:
+        MGC_LAUNCH(x, range_kernel<int>, grid, dim3(256), 0, (const int *)start,
+                   (const int *)delta, n, (int *)out);
+        break;
+    default:
+        MGC_LAUNCH(x, range_kernel<long long>, grid, dim3(256), 0, (const long long *)start,
+                   (const long long *)delta, n, (long long *)out);
+        break;
+    }
+}

@@ -1,0 +1,105 @@
+// Internal header of libmgc_hip.so: execution context, launch helpers and device math.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mgc_hip.h"
+
+// One model's execution context (opaque to generated code).
+struct mgc_hip_exec {
+    hipStream_t stream;
+    int *flag;          // device int: 1 after an out-of-range Gather index
+    int profiling;      // 1 while an eager profiled pass runs
+    int n_nodes;
+    hipEvent_t *ev_begin;
+    hipEvent_t *ev_end;
+    int launch_error;   // first launch failure seen since the last check (hipError_t)
+};
+
+namespace mgc {
+
+// Record the first launch error of a pass; the runtime reports it as MGC_ERR_HIP.
+void note_launch(mgc_hip_exec *x);
+void set_error(const char *where, hipError_t err);
+
+inline unsigned blocks_for(long n, int threads, long cap = 1L << 20) {
+    long b = (n + threads - 1) / threads;
+    if (b < 1) b = 1;
+    if (b > cap) b = cap;
+    return (unsigned)b;
+}
+
+// ------------------------------------------------------------------------------------------
+// device math. exp/log/sqrt/tanh come from the HIP device library; erf uses the rational
+// approximation the reference's interpreter and C runtime share (ops.py:201-229,
+// mgc_runtime.h:59-78), so GELU matches them to float rounding.
+// ------------------------------------------------------------------------------------------
+__device__ __forceinline__ float erf_rational(float x) {
+    x = fminf(fmaxf(x, -4.0f), 4.0f);
+    float x2 = x * x;
+    float p = -2.72614225801306e-10f;
+    p = fmaf(p, x2, 2.77068142495902e-08f);
+    p = fmaf(p, x2, -2.10102402082508e-06f);
+    p = fmaf(p, x2, -5.69250639462346e-05f);
+    p = fmaf(p, x2, -7.34990630326855e-04f);
+    p = fmaf(p, x2, -2.95459980854025e-03f);
+    p = fmaf(p, x2, -1.60960333262415e-02f);
+    float q = -1.45660718464996e-05f;
+    q = fmaf(q, x2, -2.13374055278905e-04f);
+    q = fmaf(q, x2, -1.68282697438203e-03f);
+    q = fmaf(q, x2, -7.37332916720468e-03f);
+    q = fmaf(q, x2, -1.42647390514189e-02f);
+    return x * p / q;
+}
+
+__device__ __forceinline__ float tanh_f(float x) { return tanhf(x); }
+
+__device__ __forceinline__ float sigmoid_f(float x) { return 0.5f + 0.5f * tanhf(0.5f * x); }
+
+__device__ __forceinline__ float gelu_erf_f(float x) {
+    return 0.5f * x * (1.0f + erf_rational(x * 0.70710678118654752f));
+}
+
+__device__ __forceinline__ float gelu_tanh_f(float x) {
+    return 0.5f * x * (1.0f + tanhf(0.79788456080286536f * (x + 0.044715f * x * x * x)));
+}
+
+__device__ __forceinline__ float apply_act(float v, int act, float lo, float hi) {
+    switch (act) {
+    case MGC_ACT_RELU: return v > 0.0f ? v : 0.0f;
+    case MGC_ACT_CLIP: return fminf(fmaxf(v, lo), hi);
+    case MGC_ACT_GELU: return gelu_erf_f(v);
+    case MGC_ACT_GELU_TANH: return gelu_tanh_f(v);
+    case MGC_ACT_TANH: return tanh_f(v);
+    case MGC_ACT_SIGMOID: return sigmoid_f(v);
+    default: return v;
+    }
+}
+
+// Wave (64 lanes) reductions through DPP/permute-free shuffles.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+}  // namespace mgc
+
+#define MGC_LAUNCH(x, kernel, grid, block, shmem, ...)                                         \
+    do {                                                                                       \
+        hipLaunchKernelGGL(kernel, grid, block, shmem, (x)->stream, __VA_ARGS__);              \
+        mgc::note_launch(x);                                                                   \
+    } while (0)

@@ -1,0 +1,561 @@
+// Reductions, softmax, layer normalization, pooling and depthwise convolution.
+//
+// All of these are HBM-bound on MI355X. Rows are mapped to whole wavefronts (64 lanes) when the
+// reduced axis is contiguous, with shuffle reductions; when the reduced axis is strided, one
+// thread owns one output and walks the axis while neighbouring threads read neighbouring
+// addresses, so every access is coalesced. Semantics follow the reference's C runtime
+// (src/ml_graph_compiler/codegen/runtime/mgc_kernels.c:405-679): float accumulation for
+// mean/max pooling and softmax, two-pass float LayerNorm, double accumulation for the generic
+// float sum/mean/prod reduction (codegen/c.py:736-799).
+#include "mgc_device.h"
+
+namespace mgc {
+
+// ---- mean / max over the middle axis ---------------------------------------------------------
+__global__ void reduce_mid_strided(int is_max, long outer, long n, long inner, const float *in,
+                                   float *out) {
+    const long total = outer * inner;
+    for (long idx = blockIdx.x * (long)blockDim.x + threadIdx.x; idx < total;
+         idx += (long)gridDim.x * blockDim.x) {
+        const long o = idx / inner, i = idx - (idx / inner) * inner;
+        const float *src = in + o * n * inner + i;
+        float acc = is_max ? -INFINITY : 0.0f;
+        for (long k = 0; k < n; ++k) {
+            float v = src[k * inner];
+            acc = is_max ? (v > acc ? v : acc) : acc + v;
+        }
+        if (!is_max) acc *= n > 0 ? 1.0f / (float)n : 0.0f;
+        out[idx] = acc;
+    }
+}
+
+// inner == 1: one wavefront per row.
+__global__ void reduce_mid_rows(int is_max, long outer, long n, const float *in, float *out) {
+    const int lane = threadIdx.x & 63;
+    const long wave = (blockIdx.x * (long)blockDim.x + threadIdx.x) >> 6;
+    const long waves = ((long)gridDim.x * blockDim.x) >> 6;
+    for (long o = wave; o < outer; o += waves) {
+        const float *src = in + o * n;
+        float acc = is_max ? -INFINITY : 0.0f;
+        for (long k = lane; k < n; k += 64) {
+            float v = src[k];
+            acc = is_max ? fmaxf(acc, v) : acc + v;
+        }
+        acc = is_max ? wave_max(acc) : wave_sum(acc);
+        if (lane == 0) out[o] = is_max ? acc : acc * (n > 0 ? 1.0f / (float)n : 0.0f);
+    }
+}
+
+// ---- generic reduction (sum, mean, max, min, prod) -----------------------------------------
+template <typename T, typename Acc>
+__global__ void reduce_generic(int kind, long outer, long n, long inner, const T *in, T *out) {
+    const long total = outer * inner;
+    for (long idx = blockIdx.x * (long)blockDim.x + threadIdx.x; idx < total;
+         idx += (long)gridDim.x * blockDim.x) {
+        const long o = idx / inner, i = idx - (idx / inner) * inner;
+        const T *src = in + o * n * inner + i;
+        Acc acc;
+        if (kind == 2)
+            acc = (Acc)src[0];
+        else if (kind == 3)
+            acc = (Acc)src[0];
+        else if (kind == 4)
+            acc = (Acc)1;
+        else
+            acc = (Acc)0;
+        for (long k = 0; k < n; ++k) {
+            Acc v = (Acc)src[k * inner];
+            if (kind == 0 || kind == 1)
+                acc += v;
+            else if (kind == 2)
+                acc = v > acc ? v : acc;
+            else if (kind == 3)
+                acc = v < acc ? v : acc;
+            else
+                acc *= v;
+        }
+        if (kind == 1) acc = acc / (Acc)n;
+        out[idx] = (T)acc;
+    }
+}
+
+template <typename T>
+__global__ void argmax_kernel(long outer, long n, long inner, const T *in, long long *out) {
+    const long total = outer * inner;
+    for (long idx = blockIdx.x * (long)blockDim.x + threadIdx.x; idx < total;
+         idx += (long)gridDim.x * blockDim.x) {
+        const long o = idx / inner, i = idx - (idx / inner) * inner;
+        const T *src = in + o * n * inner + i;
+        long best = 0;
+        T bv = src[0];
+        for (long k = 1; k < n; ++k) {
+            T v = src[k * inner];
+            if (v > bv) {
+                bv = v;
+                best = k;
+            }
+        }
+        out[idx] = best;
+    }
+}
+
+// ---- softmax ----------------------------------------------------------------------------------
+// inner == 1: one wavefront per row, the row cached in registers when it fits (n <= 64 * 16).
+__global__ void __launch_bounds__(256) softmax_rows(long outer, long n, const float *in,
+                                                    float *out, int log_softmax) {
+    constexpr int CACHE = 16;
+    const int lane = threadIdx.x & 63;
+    const long wave = (blockIdx.x * (long)blockDim.x + threadIdx.x) >> 6;
+    const long waves = ((long)gridDim.x * blockDim.x) >> 6;
+    const bool cached = n <= 64 * CACHE;
+    for (long o = wave; o < outer; o += waves) {
+        const float *src = in + o * n;
+        float *dst = out + o * n;
+        float v[CACHE];
+        float m = -INFINITY;
+        if (cached) {
+#pragma unroll
+            for (int j = 0; j < CACHE; ++j) {
+                long k = lane + 64L * j;
+                v[j] = k < n ? src[k] : -INFINITY;
+                m = fmaxf(m, v[j]);
+            }
+        } else {
+            for (long k = lane; k < n; k += 64) m = fmaxf(m, src[k]);
+        }
+        m = wave_max(m);
+        float s = 0.0f;
+        if (cached) {
+#pragma unroll
+            for (int j = 0; j < CACHE; ++j) {
+                long k = lane + 64L * j;
+                float e = k < n ? expf(v[j] - m) : 0.0f;
+                s += e;
+                v[j] = e;
+            }
+        } else {
+            for (long k = lane; k < n; k += 64) s += expf(src[k] - m);
+        }
+        s = wave_sum(s);
+        if (log_softmax) {
+            const float ls = logf(s);
+            for (long k = lane; k < n; k += 64) dst[k] = src[k] - m - ls;
+        } else {
+            const float inv = 1.0f / s;
+            if (cached) {
+#pragma unroll
+                for (int j = 0; j < CACHE; ++j) {
+                    long k = lane + 64L * j;
+                    if (k < n) dst[k] = v[j] * inv;
+                }
+            } else {
+                for (long k = lane; k < n; k += 64) dst[k] = expf(src[k] - m) * inv;
+            }
+        }
+    }
+}
+
+// inner > 1: one thread per (outer, inner) position walks the strided axis.
+__global__ void softmax_strided(long outer, long n, long inner, const float *in, float *out,
+                                int log_softmax) {
+    const long total = outer * inner;
+    for (long idx = blockIdx.x * (long)blockDim.x + threadIdx.x; idx < total;
+         idx += (long)gridDim.x * blockDim.x) {
+        const long o = idx / inner, i = idx - (idx / inner) * inner;
+        const float *src = in + o * n * inner + i;
+        float *dst = out + o * n * inner + i;
+        float m = -INFINITY;
+        for (long k = 0; k < n; ++k) m = fmaxf(m, src[k * inner]);
+        float s = 0.0f;
+        for (long k = 0; k < n; ++k) s += expf(src[k * inner] - m);
+        if (log_softmax) {
+            const float ls = logf(s);
+            for (long k = 0; k < n; ++k) dst[k * inner] = src[k * inner] - m - ls;
+        } else {
+            const float inv = 1.0f / s;
+            for (long k = 0; k < n; ++k) dst[k * inner] = expf(src[k * inner] - m) * inv;
+        }
+    }
+}
+
+// ---- layer normalization: one wavefront per row ------------------------------------------------
+__global__ void __launch_bounds__(256) layer_norm_rows(long rows, long cols, const float *in,
+                                                       const float *scale, const float *bias,
+                                                       float eps, float *out) {
+    constexpr int CACHE = 16;
+    const int lane = threadIdx.x & 63;
+    const long wave = (blockIdx.x * (long)blockDim.x + threadIdx.x) >> 6;
+    const long waves = ((long)gridDim.x * blockDim.x) >> 6;
+    const bool cached = cols <= 64 * CACHE;
+    for (long r = wave; r < rows; r += waves) {
+        const float *src = in + r * cols;
+        float *dst = out + r * cols;
+        float v[CACHE];
+        float sum = 0.0f;
+        if (cached) {
+#pragma unroll
+            for (int j = 0; j < CACHE; ++j) {
+                long k = lane + 64L * j;
+                v[j] = k < cols ? src[k] : 0.0f;
+                sum += v[j];
+            }
+        } else {
+            for (long k = lane; k < cols; k += 64) sum += src[k];
+        }
+        const float mean = wave_sum(sum) / (float)cols;
+        float var = 0.0f;
+        if (cached) {
+#pragma unroll
+            for (int j = 0; j < CACHE; ++j) {
+                long k = lane + 64L * j;
+                float d = k < cols ? v[j] - mean : 0.0f;
+                var += d * d;
+            }
+        } else {
+            for (long k = lane; k < cols; k += 64) {
+                float d = src[k] - mean;
+                var += d * d;
+            }
+        }
+        const float inv = 1.0f / sqrtf(wave_sum(var) / (float)cols + eps);
+        if (cached) {
+#pragma unroll
+            for (int j = 0; j < CACHE; ++j) {
+                long k = lane + 64L * j;
+                if (k < cols) {
+                    float y = (v[j] - mean) * inv;
+                    if (scale) y *= scale[k];
+                    if (bias) y += bias[k];
+                    dst[k] = y;
+                }
+            }
+        } else {
+            for (long k = lane; k < cols; k += 64) {
+                float y = (src[k] - mean) * inv;
+                if (scale) y *= scale[k];
+                if (bias) y += bias[k];
+                dst[k] = y;
+            }
+        }
+    }
+}
+
+// ---- pooling -----------------------------------------------------------------------------------
+struct PoolGeo {
+    int N, H, W, C, KH, KW, SH, SW, DH, DW, PT, PL, PB, PR, OH, OW, include_pad, is_max;
+};
+
+__device__ __forceinline__ int window_count(const PoolGeo &g, int oh, int ow) {
+    int count = 0;
+    for (int kh = 0; kh < g.KH; ++kh) {
+        int ih = oh * g.SH - g.PT + kh * g.DH;
+        bool in_h = g.include_pad ? (ih >= -g.PT && ih < g.H + g.PB) : (ih >= 0 && ih < g.H);
+        if (!in_h) continue;
+        for (int kw = 0; kw < g.KW; ++kw) {
+            int iw = ow * g.SW - g.PL + kw * g.DW;
+            bool in_w = g.include_pad ? (iw >= -g.PL && iw < g.W + g.PR) : (iw >= 0 && iw < g.W);
+            if (in_w) ++count;
+        }
+    }
+    return count;
+}
+
+__global__ void pool_nhwc(const PoolGeo g, const float *in, float *out) {
+    const long total = (long)g.N * g.OH * g.OW * g.C;
+    for (long idx = blockIdx.x * (long)blockDim.x + threadIdx.x; idx < total;
+         idx += (long)gridDim.x * blockDim.x) {
+        long t = idx;
+        const int c = (int)(t % g.C);
+        t /= g.C;
+        const int ow = (int)(t % g.OW);
+        t /= g.OW;
+        const int oh = (int)(t % g.OH);
+        const int n = (int)(t / g.OH);
+        const float *img = in + (long)n * g.H * g.W * g.C + c;
+        float acc = g.is_max ? -INFINITY : 0.0f;
+        for (int kh = 0; kh < g.KH; ++kh) {
+            int ih = oh * g.SH - g.PT + kh * g.DH;
+            if (ih < 0 || ih >= g.H) continue;
+            for (int kw = 0; kw < g.KW; ++kw) {
+                int iw = ow * g.SW - g.PL + kw * g.DW;
+                if (iw < 0 || iw >= g.W) continue;
+                float v = img[((long)ih * g.W + iw) * g.C];
+                acc = g.is_max ? (v > acc ? v : acc) : acc + v;
+            }
+        }
+        if (!g.is_max) {
+            int cnt = window_count(g, oh, ow);
+            acc *= cnt > 0 ? 1.0f / (float)cnt : 0.0f;
+        }
+        out[idx] = acc;
+    }
+}
+
+__global__ void pool_nchw(const PoolGeo g, const float *in, float *out) {
+    const long total = (long)g.N * g.C * g.OH * g.OW;
+    for (long idx = blockIdx.x * (long)blockDim.x + threadIdx.x; idx < total;
+         idx += (long)gridDim.x * blockDim.x) {
+        long t = idx;
+        const int ow = (int)(t % g.OW);
+        t /= g.OW;
+        const int oh = (int)(t % g.OH);
+        const long plane = t / g.OH;
+        const float *img = in + plane * g.H * g.W;
+        float acc = g.is_max ? -INFINITY : 0.0f;
+        for (int kh = 0; kh < g.KH; ++kh) {
+            int ih = oh * g.SH - g.PT + kh * g.DH;
+            if (ih < 0 || ih >= g.H) continue;
+            for (int kw = 0; kw < g.KW; ++kw) {
+                int iw = ow * g.SW - g.PL + kw * g.DW;
+                if (iw < 0 || iw >= g.W) continue;
+                float v = img[(long)ih * g.W + iw];
+                acc = g.is_max ? (v > acc ? v : acc) : acc + v;
+            }
+        }
+        if (!g.is_max) {
+            int cnt = window_count(g, oh, ow);
+            acc = cnt > 0 ? acc / (float)cnt : 0.0f;
+        }
+        out[idx] = acc;
+    }
+}
+
+// ---- depthwise convolution ---------------------------------------------------------------------
+struct DwGeo {
+    int N, H, W, C, KH, KW, SH, SW, DH, DW, PT, PL, OH, OW, act;
+    float lo, hi;
+};
+
+// NHWC, four channels per thread (C % 4 == 0): float4 loads of input, weights and bias.
+__global__ void depthwise_nhwc_vec4(const DwGeo g, const float *in, const float *w,
+                                    const float *bias, const float *res, float *out) {
+    const int C4 = g.C >> 2;
+    const long total = (long)g.N * g.OH * g.OW * C4;
+    for (long idx = blockIdx.x * (long)blockDim.x + threadIdx.x; idx < total;
+         idx += (long)gridDim.x * blockDim.x) {
+        long t = idx;
+        const int c4 = (int)(t % C4);
+        t /= C4;
+        const int ow = (int)(t % g.OW);
+        t /= g.OW;
+        const int oh = (int)(t % g.OH);
+        const int n = (int)(t / g.OH);
+        const int c = c4 * 4;
+        float4 acc = bias ? *reinterpret_cast<const float4 *>(bias + c) : make_float4(0, 0, 0, 0);
+        const float *img = in + (long)n * g.H * g.W * g.C + c;
+        for (int kh = 0; kh < g.KH; ++kh) {
+            int ih = oh * g.SH - g.PT + kh * g.DH;
+            if (ih < 0 || ih >= g.H) continue;
+            for (int kw = 0; kw < g.KW; ++kw) {
+                int iw = ow * g.SW - g.PL + kw * g.DW;
+                if (iw < 0 || iw >= g.W) continue;
+                float4 xv = *reinterpret_cast<const float4 *>(img + ((long)ih * g.W + iw) * g.C);
+                float4 wv = *reinterpret_cast<const float4 *>(w + ((long)kh * g.KW + kw) * g.C + c);
+                acc.x = fmaf(xv.x, wv.x, acc.x);
+                acc.y = fmaf(xv.y, wv.y, acc.y);
+                acc.z = fmaf(xv.z, wv.z, acc.z);
+                acc.w = fmaf(xv.w, wv.w, acc.w);
+            }
+        }
+        const long o = idx * 4;
+        if (res) {
+            float4 rv = *reinterpret_cast<const float4 *>(res + o);
+            acc.x += rv.x;
+            acc.y += rv.y;
+            acc.z += rv.z;
+            acc.w += rv.w;
+        }
+        acc.x = apply_act(acc.x, g.act, g.lo, g.hi);
+        acc.y = apply_act(acc.y, g.act, g.lo, g.hi);
+        acc.z = apply_act(acc.z, g.act, g.lo, g.hi);
+        acc.w = apply_act(acc.w, g.act, g.lo, g.hi);
+        *reinterpret_cast<float4 *>(out + o) = acc;
+    }
+}
+
+__global__ void depthwise_nhwc(const DwGeo g, const float *in, const float *w, const float *bias,
+                               const float *res, float *out) {
+    const long total = (long)g.N * g.OH * g.OW * g.C;
+    for (long idx = blockIdx.x * (long)blockDim.x + threadIdx.x; idx < total;
+         idx += (long)gridDim.x * blockDim.x) {
+        long t = idx;
+        const int c = (int)(t % g.C);
+        t /= g.C;
+        const int ow = (int)(t % g.OW);
+        t /= g.OW;
+        const int oh = (int)(t % g.OH);
+        const int n = (int)(t / g.OH);
+        float acc = bias ? bias[c] : 0.0f;
+        const float *img = in + (long)n * g.H * g.W * g.C + c;
+        for (int kh = 0; kh < g.KH; ++kh) {
+            int ih = oh * g.SH - g.PT + kh * g.DH;
+            if (ih < 0 || ih >= g.H) continue;
+            for (int kw = 0; kw < g.KW; ++kw) {
+                int iw = ow * g.SW - g.PL + kw * g.DW;
+                if (iw < 0 || iw >= g.W) continue;
+                acc = fmaf(img[((long)ih * g.W + iw) * g.C], w[((long)kh * g.KW + kw) * g.C + c],
+                           acc);
+            }
+        }
+        if (res) acc += res[idx];
+        out[idx] = apply_act(acc, g.act, g.lo, g.hi);
+    }
+}
+
+__global__ void depthwise_nchw(const DwGeo g, const float *in, const float *w, const float *bias,
+                               const float *res, float *out) {
+    const long total = (long)g.N * g.C * g.OH * g.OW;
+    for (long idx = blockIdx.x * (long)blockDim.x + threadIdx.x; idx < total;
+         idx += (long)gridDim.x * blockDim.x) {
+        long t = idx;
+        const int ow = (int)(t % g.OW);
+        t /= g.OW;
+        const int oh = (int)(t % g.OH);
+        const long plane = t / g.OH;
+        const int c = (int)(plane % g.C);
+        const float *img = in + plane * g.H * g.W;
+        const float *wk = w + (long)c * g.KH * g.KW;
+        float acc = bias ? bias[c] : 0.0f;
+        for (int kh = 0; kh < g.KH; ++kh) {
+            int ih = oh * g.SH - g.PT + kh * g.DH;
+            if (ih < 0 || ih >= g.H) continue;
+            for (int kw = 0; kw < g.KW; ++kw) {
+                int iw = ow * g.SW - g.PL + kw * g.DW;
+                if (iw < 0 || iw >= g.W) continue;
+                acc = fmaf(img[(long)ih * g.W + iw], wk[kh * g.KW + kw], acc);
+            }
+        }
+        if (res) acc += res[idx];
+        out[idx] = apply_act(acc, g.act, g.lo, g.hi);
+    }
+}
+
+}  // namespace mgc
+
+using namespace mgc;
+
+extern "C" void mgc_hip_reduce_mid(mgc_hip_exec *x, int is_max, long outer, long n, long inner,
+                                   const float *in, float *out) {
+    if (outer <= 0 || inner <= 0) return;
+    if (inner == 1 && n >= 64) {
+        MGC_LAUNCH(x, reduce_mid_rows, dim3(blocks_for(outer * 64, 256, 8192)), dim3(256), 0,
+                   is_max, outer, n, in, out);
+    } else {
+        MGC_LAUNCH(x, reduce_mid_strided, dim3(blocks_for(outer * inner, 256, 8192)), dim3(256),
+                   0, is_max, outer, n, inner, in, out);
+    }
+}
+
+extern "C" void mgc_hip_reduce(mgc_hip_exec *x, int kind, int dtype, long outer, long n,
+                               long inner, const void *in, void *out) {
+    if (outer <= 0 || inner <= 0 || n <= 0) return;
+    dim3 grid(blocks_for(outer * inner, 256, 8192));
+    switch (dtype) {
+    case MGC_F32:
+        if (kind == 2 || kind == 3)
+            MGC_LAUNCH(x, (reduce_generic<float, float>), grid, dim3(256), 0, kind, outer, n,
+                       inner, (const float *)in, (float *)out);
+        else
+            MGC_LAUNCH(x, (reduce_generic<float, double>), grid, dim3(256), 0, kind, outer, n,
+                       inner, (const float *)in, (float *)out);
+        break;
+    case MGC_F64:
+        MGC_LAUNCH(x, (reduce_generic<double, double>), grid, dim3(256), 0, kind, outer, n,
+                   inner, (const double *)in, (double *)out);
+        break;
+    case MGC_I64:
+        MGC_LAUNCH(x, (reduce_generic<long long, long long>), grid, dim3(256), 0, kind, outer, n,
+                   inner, (const long long *)in, (long long *)out);
+        break;
+    case MGC_I32:
+        MGC_LAUNCH(x, (reduce_generic<int, long long>), grid, dim3(256), 0, kind, outer, n,
+                   inner, (const int *)in, (int *)out);
+        break;
+    default:
+        mgc::set_error("mgc_hip_reduce: unsupported dtype", hipErrorInvalidValue);
+        break;
+    }
+}
+
+extern "C" void mgc_hip_argmax(mgc_hip_exec *x, int dtype, long outer, long n, long inner,
+                               const void *in, int64_t *out) {
+    if (outer <= 0 || inner <= 0 || n <= 0) return;
+    dim3 grid(blocks_for(outer * inner, 256, 8192));
+    switch (dtype) {
+    case MGC_F32:
+        MGC_LAUNCH(x, argmax_kernel<float>, grid, dim3(256), 0, outer, n, inner,
+                   (const float *)in, (long long *)out);
+        break;
+    case MGC_F64:
+        MGC_LAUNCH(x, argmax_kernel<double>, grid, dim3(256), 0, outer, n, inner,
+                   (const double *)in, (long long *)out);
+        break;
+    case MGC_I64:
+        MGC_LAUNCH(x, argmax_kernel<long long>, grid, dim3(256), 0, outer, n, inner,
+                   (const long long *)in, (long long *)out);
+        break;
+    case MGC_I32:
+        MGC_LAUNCH(x, argmax_kernel<int>, grid, dim3(256), 0, outer, n, inner, (const int *)in,
+                   (long long *)out);
+        break;
+    default:
+        mgc::set_error("mgc_hip_argmax: unsupported dtype", hipErrorInvalidValue);
+        break;
+    }
+}
+
+extern "C" void mgc_hip_softmax(mgc_hip_exec *x, long outer, long n, long inner, const float *in,
+                                float *out, int log_softmax) {
+    if (outer <= 0 || inner <= 0 || n <= 0) return;
+    if (inner == 1) {
+        MGC_LAUNCH(x, softmax_rows, dim3(blocks_for(outer * 64, 256, 16384)), dim3(256), 0, outer,
+                   n, in, out, log_softmax);
+    } else {
+        MGC_LAUNCH(x, softmax_strided, dim3(blocks_for(outer * inner, 256, 8192)), dim3(256), 0,
+                   outer, n, inner, in, out, log_softmax);
+    }
+}
+
+extern "C" void mgc_hip_layer_norm(mgc_hip_exec *x, long rows, long cols, const float *in,
+                                   const float *scale, const float *bias, float eps, float *out) {
+    if (rows <= 0 || cols <= 0) return;
+    MGC_LAUNCH(x, layer_norm_rows, dim3(blocks_for(rows * 64, 256, 16384)), dim3(256), 0, rows,
+               cols, in, scale, bias, eps, out);
+}
+
+extern "C" void mgc_hip_pool(mgc_hip_exec *x, int nhwc, int is_max, int N, int H, int W, int C,
+                             int KH, int KW, int SH, int SW, int DH, int DW, int PT, int PL,
+                             int PB, int PR, int OH, int OW, int count_include_pad,
+                             const float *in, float *out) {
+    PoolGeo g{N, H, W, C, KH, KW, SH, SW, DH, DW, PT, PL, PB, PR, OH, OW, count_include_pad,
+              is_max};
+    long total = (long)N * OH * OW * C;
+    if (total <= 0) return;
+    dim3 grid(blocks_for(total, 256, 16384));
+    if (nhwc)
+        MGC_LAUNCH(x, pool_nhwc, grid, dim3(256), 0, g, in, out);
+    else
+        MGC_LAUNCH(x, pool_nchw, grid, dim3(256), 0, g, in, out);
+}
+
+extern "C" void mgc_hip_depthwise(mgc_hip_exec *x, int nhwc, int N, int H, int W, int C, int KH,
+                                  int KW, int SH, int SW, int DH, int DW, int PT, int PL, int OH,
+                                  int OW, const float *in, const float *w, const float *bias,
+                                  const float *res, int act, float lo, float hi, float *out) {
+    DwGeo g{N, H, W, C, KH, KW, SH, SW, DH, DW, PT, PL, OH, OW, act, lo, hi};
+    long total = (long)N * OH * OW * C;
+    if (total <= 0) return;
+    if (nhwc) {
+        bool vec = C % 4 == 0 && (((uintptr_t)in | (uintptr_t)w | (uintptr_t)out |
+                                   (uintptr_t)bias | (uintptr_t)res) & 15) == 0;
+        if (vec)
+            MGC_LAUNCH(x, depthwise_nhwc_vec4, dim3(blocks_for(total / 4, 256, 16384)), dim3(256),
+                       0, g, in, w, bias, res, out);
+        else
+            MGC_LAUNCH(x, depthwise_nhwc, dim3(blocks_for(total, 256, 16384)), dim3(256), 0, g, in,
+                       w, bias, res, out);
+    } else {
+        MGC_LAUNCH(x, depthwise_nchw, dim3(blocks_for(total, 256, 16384)), dim3(256), 0, g, in, w,
+                   bias, res, out);
+    }
+}

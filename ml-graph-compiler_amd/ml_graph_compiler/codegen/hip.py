@@ -1,0 +1,1015 @@
+"""hip code generation: the counterpart of the reference's C emitter (codegen/c.py:1-1340).
+
+The emitter walks the scheduled graph once and writes one C++ translation unit of host code:
+a forward function with one libmgc_hip.so launcher call per node, every arena, weights, input
+and output pointer a constant offset, plus the exports of include/mgc_model.h. Device work is
+all in the prebuilt kernel library (hand-written gfx950 kernels), so a model builds with g++ in
+about a second and the runtime captures the forward into a hipGraph on first use.
+
+Lowering per operator family:
+
+* MatMul, Gemm, FusedGemm, Conv, FusedConv -> mgc_hip_gemm (fp32 MFMA). Constant right-hand
+  sides are stored transposed ([N][K], k contiguous) in the weights blob so the kernel reads
+  them in 16-byte k quads; NHWC convolutions are implicit GEMMs over M = N * OH * OW (batch
+  folded into M), pointwise ones plain strided GEMMs; NCHW convolutions (below O3) read the image
+  through im2col on the B side with a per-row bias. A small GEMM that cannot fill the chip splits
+  K into a workspace that the memory planner places (its workspace hook).
+* Depthwise convolution -> mgc_hip_depthwise (NHWC float4 over channels).
+* Elementwise nodes and FusedElementwise programs -> mgc_hip_elementwise: leaves with element
+  strides over the collapsed output dims plus a typed instruction list.
+* Transpose/Expand/Slice/Concat/Split/Pad/Tile and output copies -> mgc_hip_copy / mgc_hip_fill.
+* Gather -> mgc_hip_gather (device flag on a bad index -> mgc_run returns 1).
+* Softmax, LayerNorm, pooling, reductions, ArgMax -> their kernels.
+* Views (Reshape, Flatten, Squeeze, Unsqueeze, Identity, Dropout) emit nothing.
+"""
+
+from __future__ import annotations
+
+import hashlib
+import math
+import os
+from collections.abc import Sequence
+from dataclasses import dataclass, field
+from pathlib import Path
+from typing import Any, Callable
+
+import numpy as np
+
+from .. import ops
+from ..errors import CodegenError
+from ..ir import Graph, Node, TensorType, Value, comment_text, numpy_dtype
+from ..memory import ALIAS_OPS, MemoryPlan, Strategy, plan_memory
+
+ALIGN = 256  # arena offsets, weights chunks and the HBM block are 256-byte aligned
+
+DTYPE_CODES = {
+    "float32": 0,
+    "float64": 1,
+    "int64": 2,
+    "int32": 3,
+    "int8": 4,
+    "uint8": 5,
+    "bool": 6,
+}
+INT_DTYPES = ("int64", "int32", "int8", "uint8", "bool")
+
+ACT_CODES = {
+    "none": "MGC_ACT_NONE",
+    "relu": "MGC_ACT_RELU",
+    "clip": "MGC_ACT_CLIP",
+    "gelu": "MGC_ACT_GELU",
+    "gelu_tanh": "MGC_ACT_GELU_TANH",
+    "tanh": "MGC_ACT_TANH",
+    "sigmoid": "MGC_ACT_SIGMOID",
+}
+
+EW_OPCODES = {
+    "Add": "MGC_EW_ADD", "Sub": "MGC_EW_SUB", "Mul": "MGC_EW_MUL", "Div": "MGC_EW_DIV",
+    "Pow": "MGC_EW_POW", "Max": "MGC_EW_MAX", "Min": "MGC_EW_MIN", "Equal": "MGC_EW_EQUAL",
+    "Less": "MGC_EW_LESS", "Greater": "MGC_EW_GREATER", "LessOrEqual": "MGC_EW_LESS_EQUAL",
+    "GreaterOrEqual": "MGC_EW_GREATER_EQUAL", "And": "MGC_EW_AND", "Or": "MGC_EW_OR",
+    "Xor": "MGC_EW_XOR", "Where": "MGC_EW_WHERE", "Relu": "MGC_EW_RELU",
+    "Sigmoid": "MGC_EW_SIGMOID", "Tanh": "MGC_EW_TANH", "Erf": "MGC_EW_ERF",
+    "Sqrt": "MGC_EW_SQRT", "Exp": "MGC_EW_EXP", "Log": "MGC_EW_LOG", "Neg": "MGC_EW_NEG",
+    "Abs": "MGC_EW_ABS", "Reciprocal": "MGC_EW_RECIPROCAL", "Floor": "MGC_EW_FLOOR",
+    "Ceil": "MGC_EW_CEIL", "Sin": "MGC_EW_SIN", "Cos": "MGC_EW_COS",
+    "Softplus": "MGC_EW_SOFTPLUS", "Identity": "MGC_EW_IDENTITY", "Not": "MGC_EW_NOT",
+    "LeakyRelu": "MGC_EW_LEAKY_RELU", "HardSigmoid": "MGC_EW_HARD_SIGMOID",
+    "Clip": "MGC_EW_CLIP", "Cast": "MGC_EW_CAST",
+}
+_ANY_DTYPE = frozenset({"Equal", "Less", "Greater", "LessOrEqual", "GreaterOrEqual", "And", "Or",
+                        "Xor", "Not", "Where", "Cast"})
+_FLOAT32_OPS = frozenset(EW_OPCODES) | {"Gelu"}
+_FLOAT64_OPS = frozenset({"Add", "Sub", "Mul", "Div", "Neg", "Identity"})
+_INT_OPS = frozenset({"Add", "Sub", "Mul", "Div", "Max", "Min", "Neg", "Abs", "Relu", "Identity", "Clip"})
+
+MAX_RANK = 6
+MAX_LEAVES = 16
+MAX_INSTR = 32
+MAX_BATCH_RANK = 4
+
+
+def _f(v: float) -> str:
+    """A C float literal."""
+    v = float(v)
+    if math.isnan(v):
+        return "NAN"
+    if math.isinf(v):
+        return "INFINITY" if v > 0 else "(-INFINITY)"
+    return f"{float(np.float32(v))!r}f"
+
+
+def _strides(shape: Sequence[int]) -> list[int]:
+    out = [1] * len(shape)
+    for i in range(len(shape) - 2, -1, -1):
+        out[i] = out[i + 1] * int(shape[i + 1])
+    return out
+
+
+def _broadcast_strides(shape: Sequence[int], out_shape: Sequence[int]) -> list[int]:
+    """Element strides of ``shape`` broadcast (right-aligned) to ``out_shape``."""
+    src = _strides(shape)
+    pad = len(out_shape) - len(shape)
+    return [0 if d < pad or shape[d - pad] == 1 else src[d - pad] for d in range(len(out_shape))]
+
+
+def collapse(shape: Sequence[int], stride_sets: list[list[int]]) -> tuple[list[int], list[list[int]]]:
+    """Drop unit dims and merge neighbours that are contiguous for every operand
+    (the dimension collapsing of the reference's loop nests, codegen/c.py:370-378)."""
+    keep = [i for i, d in enumerate(shape) if d != 1]
+    dims = [int(shape[i]) for i in keep]
+    strides = [[s[i] for i in keep] for s in stride_sets]
+    d = len(dims) - 1
+    while d > 0:
+        if all(s[d - 1] == s[d] * dims[d] for s in strides):
+            dims[d - 1] *= dims[d]
+            del dims[d]
+            for s in strides:
+                s[d - 1] = s[d]
+                del s[d]
+        d -= 1
+    return dims, strides
+
+
+@dataclass
+class WeightsBuilder:
+    """Constants in one blob at 256-byte aligned offsets (reference: codegen/c.py:166-219).
+
+    Chunks reference the original arrays until ``write``; equal keys share one chunk."""
+
+    chunks: list[tuple[int, np.ndarray]] = field(default_factory=list)
+    size: int = 0
+    by_key: dict[Any, int] = field(default_factory=dict)
+
+    def add(self, array: np.ndarray, key: Any = None) -> int:
+        if key is not None and key in self.by_key:
+            return self.by_key[key]
+        data = np.ascontiguousarray(array)
+        offset = self.size
+        self.chunks.append((offset, data))
+        self.size = offset + data.nbytes
+        self.size += (-self.size) % ALIGN
+        if key is not None:
+            self.by_key[key] = offset
+        return offset
+
+    @property
+    def nbytes(self) -> int:
+        return max(self.size, ALIGN)
+
+    def digest(self) -> str:
+        h = hashlib.blake2b(digest_size=12)
+        for offset, data in self.chunks:
+            h.update(offset.to_bytes(8, "little"))
+            h.update(memoryview(data.reshape(-1).view(np.uint8)))
+        return h.hexdigest()
+
+    def write(self, path: Path) -> None:
+        tmp = path.with_suffix(path.suffix + f".tmp{os.getpid()}")
+        with open(tmp, "wb") as f:
+            pos = 0
+            for offset, data in self.chunks:
+                if offset > pos:
+                    f.write(b"\0" * (offset - pos))
+                f.write(memoryview(data.reshape(-1).view(np.uint8)))
+                pos = offset + data.nbytes
+            if self.nbytes > pos:
+                f.write(b"\0" * (self.nbytes - pos))
+        tmp.replace(path)
+
+    def blob(self) -> np.ndarray:
+        out = np.zeros(self.nbytes, np.uint8)
+        for offset, data in self.chunks:
+            out[offset : offset + data.nbytes] = data.reshape(-1).view(np.uint8)
+        return out
+
+
+def pack_b_nk(b: np.ndarray) -> np.ndarray:
+    """A constant K x N right-hand side stored as its transpose [N][K] (k contiguous), the
+    layout the MFMA GEMM reads with 16-byte k-quad loads."""
+    return np.ascontiguousarray(np.asarray(b, np.float32).T)
+
+
+@dataclass
+class GeneratedModel:
+    source: str
+    weights: WeightsBuilder
+    arena_bytes: int
+    inputs: list[tuple[str, TensorType]]
+    outputs: list[tuple[str, TensorType]]
+    plan: MemoryPlan
+    lines: int
+    kernels: dict[str, int]
+    node_flops: list[int]
+
+
+class HipEmitter:
+    """Generates the host C++ source and weights blob of one scheduled graph."""
+
+    SUPPORTED = frozenset(
+        {
+            *(op for op in ops.REGISTRY if ops.is_elementwise(op)),
+            "FusedElementwise", "Transpose", "Expand", "Slice", "Concat", "Split", "Pad", "Tile",
+            "Gather", "Shape", "Size", "ConstantOfShape", "Range", "ReduceMean", "ReduceSum",
+            "ReduceMax", "ReduceMin", "ReduceProd", "ArgMax", "Softmax", "LogSoftmax",
+            "LayerNormalization", "BatchNormalization", "MatMul", "Gemm", "FusedGemm", "Conv",
+            "FusedConv", "MaxPool", "AveragePool", "GlobalAveragePool", "GlobalMaxPool",
+            *ALIAS_OPS,
+        }
+    )
+
+    def __init__(
+        self,
+        graph: Graph,
+        strategy: Strategy = "greedy_by_size",
+        inplace: bool = True,
+        profile: bool = False,
+        gemm_workspace: Callable[[int, int, int, int], int] | None = None,
+    ) -> None:
+        unsupported = sorted({n.op for n in graph.nodes} - self.SUPPORTED)
+        if unsupported:
+            raise CodegenError(f"the hip backend does not support: {', '.join(unsupported)}")
+        for v in graph.values():
+            if v.type is not None and v.type.dtype == "float16":
+                raise CodegenError(f"float16 tensors are not supported ({v.name})")
+        self.graph = graph
+        self.profile = profile
+        self._gemm_ws = gemm_workspace
+        self.plan = plan_memory(graph, strategy=strategy, alignment=ALIGN, inplace=inplace,
+                                workspace=self._workspace_bytes)
+        self.weights = WeightsBuilder()
+        self.body: list[str] = []
+        self.kernels: dict[str, int] = {}
+        # Constants the emitter creates itself (unfused BatchNorm scale/shift). Weights chunks are
+        # keyed by id(value), so these must outlive the emission or a later temporary could reuse
+        # an id and alias an earlier chunk.
+        self._owned_constants: list[Value] = []
+
+    # -- workspace hook ------------------------------------------------------------------------
+    def _gemm_shape(self, node: Node) -> tuple[int, int, int, int] | None:
+        if node.op == "FusedGemm":
+            a, b = node.input(0).tensor_type, node.input(1).tensor_type
+            k, n = (b.shape[1], b.shape[0]) if int(node.attrs.get("trans_b", 0)) else b.shape
+            return a.size // max(k, 1), n, k, 1
+        if node.op == "Gemm":
+            out = node.output.tensor_type
+            a = node.input(0).tensor_type
+            k = a.shape[0] if int(node.attrs.get("transA", 0)) else a.shape[1]
+            return out.shape[0], out.shape[1], k, 1
+        return None
+
+    def _workspace_bytes(self, node: Node) -> int:
+        if self._gemm_ws is None:
+            return 0
+        shape = self._gemm_shape(node)
+        if shape is None:
+            return 0
+        return 4 * int(self._gemm_ws(*shape))
+
+    # -- pointers ------------------------------------------------------------------------------
+    def _root(self, value: Value) -> Value:
+        while value.data is None and value.producer is not None and value.producer.op in ALIAS_OPS:
+            value = value.producer.input(0)
+        return value
+
+    def const_offset(self, value: Value) -> int:
+        assert value.data is not None
+        return self.weights.add(value.data, key=("raw", id(value)))
+
+    def ptr(self, value: Value) -> str:
+        """Byte-pointer expression (unsigned char *) of a value's storage."""
+        loc = self.plan.location(value)
+        if loc.kind == "const":
+            root = self._root(value)
+            if root.data is None:
+                raise CodegenError(f"constant {value.name!r} has no data")
+            return f"(W + {self.const_offset(root)})"
+        if loc.kind == "input":
+            return f"((const unsigned char *)in[{loc.index}])"
+        if loc.kind == "output":
+            return f"((unsigned char *)out[{loc.index}])"
+        return f"(A + {loc.index})"
+
+    def fptr(self, value: Value) -> str:
+        return f"((float *){self.ptr(value)})"
+
+    def ws_ptr(self, node: Node) -> str:
+        off = self.plan.workspaces.get(id(node))
+        return "NULL" if off is None else f"((float *)(A + {off}))"
+
+    def emit(self, line: str) -> None:
+        self.body.append(line)
+
+    def count(self, kernel: str) -> None:
+        self.kernels[kernel] = self.kernels.get(kernel, 0) + 1
+
+    # -- nodes ---------------------------------------------------------------------------------
+    def node(self, node: Node, index: int) -> None:
+        types = ", ".join(str(o.type) for o in node.outputs)
+        self.emit(f"/* {node.op} {comment_text(node.name)} -> {types} */")
+        if self.profile:
+            self.emit(f"mgc_hip_node_begin(x, {index});")
+        self._lower(node)
+        if self.profile:
+            self.emit(f"mgc_hip_node_end(x, {index});")
+
+    def _lower(self, node: Node) -> None:
+        if node.op in ALIAS_OPS:
+            if node.op == "Dropout" and len(node.outputs) > 1:
+                mask = node.outputs[1]
+                if mask.users or mask in self.graph.outputs:
+                    self.emit(f"mgc_hip_fill(x, {self.ptr(mask)}, {mask.tensor_type.size}L, 1, 1ULL);")
+            self.count("view")
+            return
+        if node.op == "FusedElementwise":
+            program = [(str(op), dict(a), [int(v) for v in args]) for op, a, args in node.attrs["program"]]
+            self.elementwise(node.output, program, list(node.inputs))
+            return
+        if ops.is_elementwise(node.op):
+            args = [i if node.inputs[i] is not None else -1 for i in range(len(node.inputs))]
+            self.elementwise(node.output, [(node.op, dict(node.attrs), args)], list(node.inputs))
+            return
+        getattr(self, f"op_{node.op}")(node)
+
+    # -- elementwise programs ------------------------------------------------------------------
+    def _instr_fields(self, op: str, attrs: dict[str, Any], in_dtype: str, out_dtype: str, n_args: int) -> tuple[str, float, float]:
+        if op in _ANY_DTYPE:
+            return EW_OPCODES[op], 0.0, 0.0
+        ok = (
+            (in_dtype == "float32" and op in _FLOAT32_OPS)
+            or (in_dtype == "float64" and op in _FLOAT64_OPS)
+            or (in_dtype in INT_DTYPES and op in _INT_OPS)
+        )
+        if not ok:
+            raise CodegenError(f"elementwise {op} on {in_dtype} is not supported by the hip backend")
+        if op == "Gelu":
+            tanh = attrs.get("approximate", "none") == "tanh"
+            return ("MGC_EW_GELU_TANH" if tanh else "MGC_EW_GELU"), 0.0, 0.0
+        if op == "LeakyRelu":
+            return EW_OPCODES[op], float(attrs.get("alpha", 0.01)), 0.0
+        if op == "HardSigmoid":
+            return EW_OPCODES[op], float(attrs.get("alpha", 0.2)), float(attrs.get("beta", 0.5))
+        if op == "Clip":
+            return EW_OPCODES[op], float(attrs.get("min", -np.inf)), float(attrs.get("max", np.inf))
+        return EW_OPCODES[op], 0.0, 0.0
+
+    def elementwise(self, out_value: Value, program: list[tuple[str, dict[str, Any], list[int]]], leaves: list[Value | None]) -> None:
+        shape = out_value.tensor_type.shape
+        n_leaves = len(leaves)
+        if n_leaves > MAX_LEAVES or len(program) > MAX_INSTR:
+            raise CodegenError(f"elementwise program too large ({n_leaves} leaves, {len(program)} ops)")
+        present = [(i, v) for i, v in enumerate(leaves) if v is not None]
+        stride_sets = [_strides(shape)] + [_broadcast_strides(v.tensor_type.shape, shape) for _, v in present]
+        dims, coll = collapse(shape, stride_sets)
+        if len(dims) > MAX_RANK:
+            raise CodegenError(f"elementwise over {len(dims)} non-collapsible dims is not supported")
+        total = int(np.prod(dims)) if dims else 1
+        if total == 0 or out_value.tensor_type.size == 0:
+            self.count("elementwise")
+            return
+        lines = ["mgc_hip_ew_args e; memset(&e, 0, sizeof e);", f"e.rank = {len(dims)};"]
+        for d, n in enumerate(dims):
+            lines.append(f"e.dims[{d}] = {n}L; e.out_strides[{d}] = {coll[0][d]}L;")
+        lines.append(f"e.n_leaves = {n_leaves}; e.n_instr = {len(program)};")
+        for k, (i, v) in enumerate(present):
+            st = coll[k + 1]
+            lines.append(
+                f"e.leaf[{i}].p = {self.ptr(v)}; e.leaf[{i}].dtype = {DTYPE_CODES[v.tensor_type.dtype]};"
+                + "".join(f" e.leaf[{i}].strides[{d}] = {s}L;" for d, s in enumerate(st) if s)
+            )
+        types_all: list[TensorType | None] = [None if v is None else v.type for v in leaves]
+        consts: list[np.ndarray | None] = [None if v is None else v.data for v in leaves]
+        for k, (op, attrs, args) in enumerate(program):
+            sub = Node(op, [], [Value("_")], dict(attrs))
+            out_t = ops.spec(op).infer(sub, [types_all[a] if a >= 0 else None for a in args],
+                                       [consts[a] if a >= 0 else None for a in args])[0]
+            first = next((types_all[a] for a in args if a >= 0), None)
+            in_dtype = first.dtype if first is not None else out_t.dtype
+            opcode, fa, fb = self._instr_fields(op, attrs, in_dtype, out_t.dtype, len(args))
+            regs = [(-1 if a < 0 else (a if a < n_leaves else MAX_LEAVES + a - n_leaves)) for a in args]
+            regs = (regs + [-1, -1, -1])[:3]
+            lines.append(
+                f"e.instr[{k}].op = {opcode}; e.instr[{k}].in_dtype = {DTYPE_CODES[in_dtype]}; "
+                f"e.instr[{k}].out_dtype = {DTYPE_CODES[out_t.dtype]}; "
+                f"e.instr[{k}].args[0] = {regs[0]}; e.instr[{k}].args[1] = {regs[1]}; "
+                f"e.instr[{k}].args[2] = {regs[2]}; e.instr[{k}].fa = {_f(fa)}; e.instr[{k}].fb = {_f(fb)};"
+            )
+            types_all.append(out_t)
+            consts.append(None)
+        lines.append(f"e.out = (void *){self.ptr(out_value)}; e.out_dtype = {DTYPE_CODES[out_value.tensor_type.dtype]};")
+        lines.append("mgc_hip_elementwise(x, &e);")
+        self.emit("{ " + " ".join(lines) + " }")
+        self.count("elementwise")
+
+    # -- copies --------------------------------------------------------------------------------
+    def copy(self, shape: Sequence[int], out_ptr: str, out_strides: list[int], out_base: int,
+             in_ptr: str, in_strides: list[int], in_base: int, elem_bytes: int,
+             in_mod: list[int] | None = None) -> None:
+        total = int(np.prod(shape)) if len(shape) else 1
+        if total == 0:
+            return
+        if in_mod is None:
+            dims, (ost, ist) = collapse(shape, [list(out_strides), list(in_strides)])
+            mods = [0] * len(dims)
+        else:
+            dims, ost, ist, mods = [int(d) for d in shape], list(out_strides), list(in_strides), list(in_mod)
+        if len(dims) > MAX_RANK:
+            raise CodegenError(f"copy over {len(dims)} non-collapsible dims is not supported")
+        parts = ["mgc_hip_copy_args c; memset(&c, 0, sizeof c);", f"c.rank = {len(dims)};"]
+        for d, n in enumerate(dims):
+            parts.append(
+                f"c.dims[{d}] = {n}L; c.out_strides[{d}] = {ost[d]}L; c.in_strides[{d}] = {ist[d]}L; c.in_mod[{d}] = {mods[d]}L;"
+            )
+        parts.append(f"c.in_base = {in_base}L; c.out_base = {out_base}L; c.in = {in_ptr}; c.out = {out_ptr};")
+        parts.append(f"c.elem_bytes = {elem_bytes}; mgc_hip_copy(x, &c);")
+        self.emit("{ " + " ".join(parts) + " }")
+
+    def op_Transpose(self, node: Node) -> None:
+        xv = node.input(0)
+        perm = ops.transpose_perm(node, xv.tensor_type.rank)
+        src = _strides(xv.tensor_type.shape)
+        out_t = node.output.tensor_type
+        self.copy(out_t.shape, self.ptr(node.output), _strides(out_t.shape), 0, self.ptr(xv),
+                  [src[p] for p in perm], 0, out_t.itemsize)
+        self.count("transpose")
+
+    def op_Expand(self, node: Node) -> None:
+        out_t = node.output.tensor_type
+        xv = node.input(0)
+        self.copy(out_t.shape, self.ptr(node.output), _strides(out_t.shape), 0, self.ptr(xv),
+                  _broadcast_strides(xv.tensor_type.shape, out_t.shape), 0, out_t.itemsize)
+        self.count("copy")
+
+    def op_Tile(self, node: Node) -> None:
+        xv = node.input(0)
+        xs, os_ = xv.tensor_type.shape, node.output.tensor_type.shape
+        self.copy(os_, self.ptr(node.output), _strides(os_), 0, self.ptr(xv), _strides(xs), 0,
+                  xv.tensor_type.itemsize, in_mod=[int(d) for d in xs])
+        self.count("copy")
+
+    def op_Slice(self, node: Node) -> None:
+        xv = node.input(0)
+        xs = xv.tensor_type.shape
+        sl = ops.slice_params(node, xs, [None if v is None else v.data for v in node.inputs])
+        src = _strides(xs)
+        base = sum(int(s.start or 0) * st for s, st in zip(sl, src))
+        strides = [int(s.step or 1) * st for s, st in zip(sl, src)]
+        out_t = node.output.tensor_type
+        self.copy(out_t.shape, self.ptr(node.output), _strides(out_t.shape), 0, self.ptr(xv), strides, base, out_t.itemsize)
+        self.count("copy")
+
+    def op_Concat(self, node: Node) -> None:
+        out_t = node.output.tensor_type
+        axis = int(node.attrs.get("axis", 0))
+        axis = axis + out_t.rank if axis < 0 else axis
+        ost = _strides(out_t.shape)
+        offset = 0
+        for v in node.inputs:
+            if v is None:
+                continue
+            t = v.tensor_type
+            if t.size:
+                self.copy(t.shape, self.ptr(node.output), ost, offset * ost[axis], self.ptr(v),
+                          _strides(t.shape), 0, t.itemsize)
+            offset += t.shape[axis]
+        self.count("copy")
+
+    def op_Split(self, node: Node) -> None:
+        xv = node.input(0)
+        xt = xv.tensor_type
+        axis = int(node.attrs.get("axis", 0))
+        axis = axis + xt.rank if axis < 0 else axis
+        src = _strides(xt.shape)
+        offset = 0
+        for out_v in node.outputs:
+            t = out_v.tensor_type
+            if out_v.users or out_v in self.graph.outputs:
+                self.copy(t.shape, self.ptr(out_v), _strides(t.shape), 0, self.ptr(xv), src,
+                          offset * src[axis], t.itemsize)
+            offset += t.shape[axis]
+        self.count("copy")
+
+    def op_Pad(self, node: Node) -> None:
+        mode = node.attrs.get("mode", "constant")
+        if mode != "constant":
+            raise CodegenError(f"Pad mode {mode!r} is not supported by the hip backend")
+        xv = node.input(0)
+        xt, ot = xv.tensor_type, node.output.tensor_type
+        pads = ops.pad_amounts(node, xt.rank, [None if v is None else v.data for v in node.inputs])
+        if any(p < 0 for p in pads):
+            raise CodegenError("negative Pad amounts are not supported by the hip backend")
+        fill_v = node.optional_input(2)
+        fill = 0.0
+        if fill_v is not None:
+            if fill_v.data is None:
+                raise CodegenError("Pad value must be a constant")
+            fill = fill_v.data.reshape(()).item()
+        self._fill(node.output, np.asarray(fill, dtype=numpy_dtype(ot.dtype)))
+        ost = _strides(ot.shape)
+        base = sum(p * s for p, s in zip(pads[: xt.rank], ost))
+        self.copy(xt.shape, self.ptr(node.output), ost, base, self.ptr(xv), _strides(xt.shape), 0, xt.itemsize)
+        self.count("copy")
+
+    def _fill(self, value: Value, scalar: np.ndarray) -> None:
+        t = value.tensor_type
+        if t.size == 0:
+            return
+        raw = np.zeros(8, np.uint8)
+        b = np.asarray(scalar, dtype=numpy_dtype(t.dtype)).reshape(1).view(np.uint8)
+        raw[: b.size] = b
+        bits = int(raw.view(np.uint64)[0])
+        self.emit(f"mgc_hip_fill(x, {self.ptr(value)}, {t.size}L, {t.itemsize}, {bits}ULL);")
+
+    def _write_constant(self, value: Value, array: np.ndarray) -> None:
+        t = value.tensor_type
+        flat = np.asarray(array, dtype=numpy_dtype(t.dtype)).reshape(-1)
+        if flat.size and np.all(flat == flat[0]):
+            self._fill(value, flat[0])
+            return
+        off = self.weights.add(flat)
+        self.copy((flat.size,), self.ptr(value), [1], 0, f"(W + {off})", [1], 0, t.itemsize)
+
+    # -- gather and constants ------------------------------------------------------------------
+    def op_Gather(self, node: Node) -> None:
+        xv, idx = node.input(0), node.input(1)
+        xt, it = xv.tensor_type, idx.tensor_type
+        axis = int(node.attrs.get("axis", 0))
+        axis = axis + xt.rank if axis < 0 else axis
+        outer = int(np.prod(xt.shape[:axis])) if axis else 1
+        inner = int(np.prod(xt.shape[axis + 1 :])) if axis + 1 < xt.rank else 1
+        if it.dtype not in ("int64", "int32"):
+            raise CodegenError(f"Gather indices of type {it.dtype} are not supported by the hip backend")
+        self.emit(
+            f"mgc_hip_gather(x, {self.ptr(xv)}, {self.ptr(idx)}, {DTYPE_CODES[it.dtype]}, {outer}L, "
+            f"{xt.shape[axis]}L, {it.size}L, {inner * xt.itemsize}L, {self.ptr(node.output)});"
+        )
+        self.count("gather")
+
+    def op_Shape(self, node: Node) -> None:
+        self._write_constant(node.output, ops.shape_value(node, node.input(0).tensor_type.shape))
+        self.count("constant")
+
+    def op_Size(self, node: Node) -> None:
+        self._write_constant(node.output, np.asarray([node.input(0).tensor_type.size], np.int64))
+        self.count("constant")
+
+    def op_ConstantOfShape(self, node: Node) -> None:
+        value = node.attrs.get("value")
+        fill = np.asarray(value).reshape(-1)[0].item() if value is not None else 0.0
+        self._fill(node.output, np.asarray(fill, dtype=numpy_dtype(node.output.tensor_type.dtype)))
+        self.count("constant")
+
+    def op_Range(self, node: Node) -> None:
+        t = node.output.tensor_type
+        if t.dtype not in ("float32", "float64", "int64", "int32"):
+            raise CodegenError(f"Range of {t.dtype} is not supported by the hip backend")
+        self.emit(
+            f"mgc_hip_range(x, {DTYPE_CODES[t.dtype]}, {self.ptr(node.input(0))}, {self.ptr(node.input(2))}, "
+            f"{t.size}L, {self.ptr(node.output)});"
+        )
+        self.count("constant")
+
+    # -- reductions and normalization ------------------------------------------------------------
+    def _reduce(self, node: Node, kind: str) -> None:
+        xv = node.input(0)
+        xt = xv.tensor_type
+        axes = ops.reduce_axes(node, xt.rank, [None if v is None else v.data for v in node.inputs])
+        out = node.output
+        if not axes:
+            self.copy((xt.size,), self.ptr(out), [1], 0, self.ptr(xv), [1], 0, xt.itemsize)
+            self.count("reduce")
+            return
+        if list(axes) != list(range(axes[0], axes[-1] + 1)):
+            raise CodegenError(f"{node.op} over non-adjacent axes {axes} is not supported")
+        outer = int(np.prod(xt.shape[: axes[0]])) if axes[0] else 1
+        n = int(np.prod([xt.shape[a] for a in axes]))
+        inner = int(np.prod(xt.shape[axes[-1] + 1 :])) if axes[-1] + 1 < xt.rank else 1
+        if kind in ("mean", "max") and xt.dtype == "float32":
+            self.emit(f"mgc_hip_reduce_mid(x, {int(kind == 'max')}, {outer}L, {n}L, {inner}L, {self.fptr(xv)}, {self.fptr(out)});")
+        else:
+            if xt.dtype not in ("float32", "float64", "int64", "int32"):
+                raise CodegenError(f"{node.op} on {xt.dtype} is not supported by the hip backend")
+            code = {"sum": 0, "mean": 1, "max": 2, "min": 3, "prod": 4}[kind]
+            self.emit(f"mgc_hip_reduce(x, {code}, {DTYPE_CODES[xt.dtype]}, {outer}L, {n}L, {inner}L, {self.ptr(xv)}, {self.ptr(out)});")
+        self.count("reduce")
+
+    def op_ReduceMean(self, node: Node) -> None:
+        self._reduce(node, "mean")
+
+    def op_ReduceSum(self, node: Node) -> None:
+        self._reduce(node, "sum")
+
+    def op_ReduceMax(self, node: Node) -> None:
+        self._reduce(node, "max")
+
+    def op_ReduceMin(self, node: Node) -> None:
+        self._reduce(node, "min")
+
+    def op_ReduceProd(self, node: Node) -> None:
+        self._reduce(node, "prod")
+
+    def op_ArgMax(self, node: Node) -> None:
+        xv = node.input(0)
+        xt = xv.tensor_type
+        if xt.dtype not in ("float32", "float64", "int64", "int32"):
+            raise CodegenError(f"ArgMax on {xt.dtype} is not supported by the hip backend")
+        axis = int(node.attrs.get("axis", 0))
+        axis = axis + xt.rank if axis < 0 else axis
+        outer = int(np.prod(xt.shape[:axis])) if axis else 1
+        inner = int(np.prod(xt.shape[axis + 1 :])) if axis + 1 < xt.rank else 1
+        self.emit(f"mgc_hip_argmax(x, {DTYPE_CODES[xt.dtype]}, {outer}L, {xt.shape[axis]}L, {inner}L, {self.ptr(xv)}, (int64_t *){self.ptr(node.output)});")
+        self.count("reduce")
+
+    def _require_f32(self, node: Node, t: TensorType) -> None:
+        if t.dtype != "float32":
+            raise CodegenError(f"{node.op} on {t.dtype} is not supported by the hip backend")
+
+    def _softmax(self, node: Node, log: int) -> None:
+        xv = node.input(0)
+        xt = xv.tensor_type
+        self._require_f32(node, xt)
+        axis = int(node.attrs.get("axis", -1))
+        axis = axis + xt.rank if axis < 0 else axis
+        outer = int(np.prod(xt.shape[:axis])) if axis else 1
+        inner = int(np.prod(xt.shape[axis + 1 :])) if axis + 1 < xt.rank else 1
+        self.emit(f"mgc_hip_softmax(x, {outer}L, {xt.shape[axis]}L, {inner}L, {self.fptr(xv)}, {self.fptr(node.output)}, {log});")
+        self.count("softmax")
+
+    def op_Softmax(self, node: Node) -> None:
+        self._softmax(node, 0)
+
+    def op_LogSoftmax(self, node: Node) -> None:
+        self._softmax(node, 1)
+
+    def _vector_ptr(self, value: Value | None, n: int, what: str) -> str:
+        if value is None:
+            return "NULL"
+        if value.tensor_type.size != n:
+            raise CodegenError(f"{what} must have {n} elements, got {value.tensor_type.shape}")
+        if value.tensor_type.dtype != "float32":
+            raise CodegenError(f"{what} must be float32")
+        return self.fptr(value)
+
+    def op_LayerNormalization(self, node: Node) -> None:
+        xv = node.input(0)
+        xt = xv.tensor_type
+        self._require_f32(node, xt)
+        axis = int(node.attrs.get("axis", -1))
+        axis = axis + xt.rank if axis < 0 else axis
+        cols = int(np.prod(xt.shape[axis:]))
+        rows = xt.size // max(cols, 1)
+        scale = self._vector_ptr(node.optional_input(1), cols, "LayerNormalization scale")
+        bias = self._vector_ptr(node.optional_input(2), cols, "LayerNormalization bias")
+        eps = _f(float(node.attrs.get("epsilon", 1e-5)))
+        self.emit(f"mgc_hip_layer_norm(x, {rows}L, {cols}L, {self.fptr(xv)}, {scale}, {bias}, {eps}, {self.fptr(node.output)});")
+        self.count("layer_norm")
+
+    def op_BatchNormalization(self, node: Node) -> None:
+        xv = node.input(0)
+        xt = xv.tensor_type
+        self._require_f32(node, xt)
+        params = [None if v is None else v.data for v in node.inputs[1:5]]
+        if any(p is None for p in params):
+            raise CodegenError("BatchNormalization parameters must be constants")
+        scale, bias, mean, var = (np.asarray(p, np.float64) for p in params)
+        inv = scale / np.sqrt(var + float(node.attrs.get("epsilon", 1e-5)))
+        shift = bias - mean * inv
+        c = inv.size
+        nhwc = node.attrs.get("layout") == "NHWC"
+        bshape = (c,) if nhwc else (c,) + (1,) * (xt.rank - 2)
+        g = Graph("bn")
+        mul = g.constant(inv.astype(np.float32).reshape(bshape), "bn_mul")
+        add = g.constant(shift.astype(np.float32).reshape(bshape), "bn_add")
+        self._owned_constants += [mul, add]
+        self.elementwise(node.output, [("Mul", {}, [0, 1]), ("Add", {}, [3, 2])], [xv, mul, add])
+
+    # -- GEMM family ---------------------------------------------------------------------------
+    def _gemm_call(self, m: int, n: int, k: int, a: list[str], b: list[str], c: str, ldc: int, *,
+                   batch: Sequence[tuple[int, int, int, int, int]] = (), alpha: float = 1.0,
+                   bias: str = "NULL", bias_mode: int = 0, res: str = "NULL", ldr: int = 0,
+                   beta: float = 1.0, act: str = "none", lo: float = 0.0, hi: float = 6.0,
+                   workspace: str = "NULL", workspace_floats: int = 0) -> None:
+        if len(batch) > MAX_BATCH_RANK:
+            raise CodegenError(f"GEMM with {len(batch)} batch dimensions is not supported")
+        parts = ["mgc_hip_gemm_args g; memset(&g, 0, sizeof g);", f"g.M = {m}; g.N = {n}; g.K = {k};"]
+        parts += a + b
+        parts.append(f"g.c = (float *){c}; g.ldc = {ldc}L;")
+        parts.append(f"g.alpha = {_f(alpha)}; g.beta = {_f(beta)}; g.bias = {bias}; g.bias_mode = {bias_mode};")
+        parts.append(f"g.res = {res}; g.ldr = {ldr}L; g.act = {ACT_CODES[act]}; g.lo = {_f(lo)}; g.hi = {_f(hi)};")
+        if batch:
+            parts.append(f"g.batch_rank = {len(batch)};")
+            for d, (dim, abs_, bbs, cbs, rbs) in enumerate(batch):
+                parts.append(f"g.batch_dims[{d}] = {dim}; g.a_bs[{d}] = {abs_}L; g.b_bs[{d}] = {bbs}L; g.c_bs[{d}] = {cbs}L; g.r_bs[{d}] = {rbs}L;")
+        parts.append(f"g.workspace = {workspace}; g.workspace_floats = {workspace_floats}L;")
+        parts.append("mgc_hip_gemm(x, &g);")
+        self.emit("{ " + " ".join(parts) + " }")
+        self.count("gemm")
+
+    @staticmethod
+    def _strided(field_: str, p: str, rs: int, cs: int) -> list[str]:
+        return [f"g.{field_}.kind = MGC_OP_STRIDED; g.{field_}.p = (const float *){p}; g.{field_}.rs = {rs}L; g.{field_}.cs = {cs}L;"]
+
+    def _packed_b(self, matrix: np.ndarray, key: Any) -> list[str]:
+        """Constant K x N right-hand side stored [N][K]: element (k, n) at n * K + k."""
+        k = matrix.shape[0]
+        off = self.weights.add(pack_b_nk(matrix), key=key)
+        return self._strided("b", f"(W + {off})", 1, k)
+
+    def _act(self, node: Node) -> tuple[str, float, float]:
+        return (str(node.attrs.get("activation", "none")), float(node.attrs.get("clip_min", 0.0)),
+                float(node.attrs.get("clip_max", 6.0)))
+
+    def _workspace(self, node: Node) -> tuple[str, int]:
+        ptr = self.ws_ptr(node)
+        if ptr == "NULL":
+            return "NULL", 0
+        return ptr, self._workspace_bytes(node) // 4
+
+    def op_FusedGemm(self, node: Node) -> None:
+        a, b = node.input(0), node.input(1)
+        at, bt = a.tensor_type, b.tensor_type
+        self._require_f32(node, at)
+        trans = int(node.attrs.get("trans_b", 0))
+        k, n = (bt.shape[1], bt.shape[0]) if trans else bt.shape
+        m = at.size // max(k, 1)
+        if b.data is not None:
+            bspec = self._packed_b(b.data.T if trans else b.data, ("packed", id(b), trans))
+        else:
+            bspec = self._strided("b", self.ptr(b), 1 if trans else n, k if trans else 1)
+        bias_v, res_v = node.optional_input(2), node.optional_input(3)
+        act, lo, hi = self._act(node)
+        ws, ws_floats = self._workspace(node)
+        self._gemm_call(
+            m, n, k, self._strided("a", self.ptr(a), k, 1), bspec, self.ptr(node.output), n,
+            bias=self._vector_ptr(bias_v, n, "FusedGemm bias") if bias_v is not None else "NULL",
+            bias_mode=1 if bias_v is not None else 0,
+            res=self.fptr(res_v) if res_v is not None else "NULL", ldr=n, act=act, lo=lo, hi=hi,
+            workspace=ws, workspace_floats=ws_floats,
+        )
+
+    def op_Gemm(self, node: Node) -> None:
+        a, b, c = node.input(0), node.input(1), node.optional_input(2)
+        at, bt = a.tensor_type, b.tensor_type
+        self._require_f32(node, at)
+        ta, tb = int(node.attrs.get("transA", 0)), int(node.attrs.get("transB", 0))
+        m, k = (at.shape[1], at.shape[0]) if ta else at.shape
+        n = bt.shape[0] if tb else bt.shape[1]
+        alpha = float(node.attrs.get("alpha", 1.0))
+        beta = float(node.attrs.get("beta", 1.0))
+        aspec = self._strided("a", self.ptr(a), 1 if ta else k, m if ta else 1)
+        if b.data is not None:
+            bspec = self._packed_b(b.data.T if tb else b.data, ("packed", id(b), tb))
+        else:
+            bspec = self._strided("b", self.ptr(b), 1 if tb else n, k if tb else 1)
+        bias, mode, res, ldr = "NULL", 0, "NULL", 0
+        if c is not None:
+            ct = c.tensor_type
+            full = np.broadcast_shapes(ct.shape, (m, n))
+            if c.data is not None and ct.size in (1, n) and (ct.rank < 2 or ct.shape[0] == 1):
+                vec = np.broadcast_to(c.data.reshape(-1) * beta, (n,)).astype(np.float32)
+                bias, mode = f"((const float *)(W + {self.weights.add(vec)}))", 1
+            elif c.data is not None and ct.rank == 2 and ct.shape == (m, 1):
+                vec = (c.data.reshape(-1) * beta).astype(np.float32)
+                bias, mode = f"((const float *)(W + {self.weights.add(vec)}))", 2
+            elif tuple(ct.shape) == (m, n) and full == (m, n):
+                res, ldr = self.fptr(c), n
+            else:
+                raise CodegenError(f"Gemm bias of shape {ct.shape} is not supported")
+        ws, ws_floats = self._workspace(node)
+        self._gemm_call(m, n, k, aspec, bspec, self.ptr(node.output), n, alpha=alpha, bias=bias,
+                        bias_mode=mode, res=res, ldr=ldr, beta=beta, workspace=ws, workspace_floats=ws_floats)
+
+    def op_MatMul(self, node: Node) -> None:
+        a, b = node.input(0), node.input(1)
+        at, bt = a.tensor_type, b.tensor_type
+        self._require_f32(node, at)
+        ashape = (1, *at.shape) if at.rank == 1 else at.shape
+        bshape = (*bt.shape, 1) if bt.rank == 1 else bt.shape
+        m, k = ashape[-2], ashape[-1]
+        n = bshape[-1]
+        batch_shape = tuple(int(d) for d in np.broadcast_shapes(ashape[:-2], bshape[:-2]))
+        a_bs = [s * m * k for s in _broadcast_strides(ashape[:-2], batch_shape)]
+        b_bs = [s * k * n for s in _broadcast_strides(bshape[:-2], batch_shape)]
+        c_bs = [s * m * n for s in _strides(batch_shape)]
+        dims, (a_c, b_c, c_c) = collapse(batch_shape, [a_bs, b_bs, c_bs])
+        batch = [(d, sa, sb, sc, 0) for d, sa, sb, sc in zip(dims, a_c, b_c, c_c)]
+        if b.data is not None and not any(b_c):
+            bmat = b.data.reshape(k, n)
+            bspec = self._packed_b(bmat, ("packed", id(b), 0))
+        else:
+            bspec = self._strided("b", self.ptr(b), n, 1)
+        self._gemm_call(m, n, k, self._strided("a", self.ptr(a), k, 1), bspec, self.ptr(node.output), n, batch=batch)
+
+    # -- convolution and pooling ---------------------------------------------------------------
+    @staticmethod
+    def depthwise(node: Node) -> bool:
+        if node.op not in ("Conv", "FusedConv"):
+            return False
+        group = int(node.attrs.get("group", 1))
+        w = node.input(1).tensor_type
+        nhwc = node.attrs.get("layout") == "NHWC"
+        cg, k = (w.shape[2], w.shape[3]) if nhwc else (w.shape[1], w.shape[0])
+        return group > 1 and cg == 1 and k == group
+
+    def op_Conv(self, node: Node) -> None:
+        self.op_FusedConv(node)
+
+    def op_FusedConv(self, node: Node) -> None:
+        xv, wv = node.input(0), node.input(1)
+        xt, wt = xv.tensor_type, wv.tensor_type
+        self._require_f32(node, xt)
+        nhwc = ops.conv_layout(node) == "NHWC"
+        group = int(node.attrs.get("group", 1))
+        if nhwc:
+            nb, h, wd, c = xt.shape
+            kh, kw, cg, kout = wt.shape
+        else:
+            nb, c, h, wd = xt.shape
+            kout, cg, kh, kw = wt.shape
+        g = ops.window_geometry(node, (h, wd), (kh, kw))
+        oh, ow = g.out_hw
+        pt, pl = g.pads[0], g.pads[1]
+        bias_v, res_v = node.optional_input(2), node.optional_input(3)
+        act, lo, hi = self._act(node) if node.op == "FusedConv" else ("none", 0.0, 6.0)
+        bias = self._vector_ptr(bias_v, kout, "Conv bias") if bias_v is not None else "NULL"
+        res = self.fptr(res_v) if res_v is not None else "NULL"
+        if wv.data is None:
+            raise CodegenError("convolution weights must be constant for the hip backend")
+        out_ptr = self.ptr(node.output)
+        if self.depthwise(node):
+            wflat = wv.data.reshape(kh * kw, c) if nhwc else wv.data.reshape(c, kh * kw)
+            woff = self.weights.add(np.ascontiguousarray(wflat, np.float32), key=("dw", id(wv)))
+            self.emit(
+                f"mgc_hip_depthwise(x, {int(nhwc)}, {nb}, {h}, {wd}, {c}, {kh}, {kw}, {g.strides[0]}, {g.strides[1]}, "
+                f"{g.dilations[0]}, {g.dilations[1]}, {pt}, {pl}, {oh}, {ow}, {self.fptr(xv)}, "
+                f"(const float *)(W + {woff}), {bias}, {res}, {ACT_CODES[act]}, {_f(lo)}, {_f(hi)}, (float *){out_ptr});"
+            )
+            self.count("depthwise")
+            return
+        kg = kout // group
+        geo = (f"g.{{f}}.H = {h}; g.{{f}}.W = {wd}; g.{{f}}.C = {c}; g.{{f}}.KH = {kh}; g.{{f}}.KW = {kw}; "
+               f"g.{{f}}.SH = {g.strides[0]}; g.{{f}}.SW = {g.strides[1]}; g.{{f}}.DH = {g.dilations[0]}; "
+               f"g.{{f}}.DW = {g.dilations[1]}; g.{{f}}.PT = {pt}; g.{{f}}.PL = {pl}; g.{{f}}.OH = {oh}; "
+               f"g.{{f}}.OW = {ow}; g.{{f}}.cg = {cg};")
+        for gi in range(group):
+            gbias = f"({bias} + {gi * kg})" if bias != "NULL" else "NULL"
+            if nhwc:
+                wmat = wv.data[:, :, :, gi * kg : (gi + 1) * kg].reshape(kh * kw * cg, kg)
+                bspec = self._packed_b(wmat, ("conv", id(wv), gi))
+                pointwise = kh == kw == 1 and g.strides == (1, 1) and g.pads == (0, 0, 0, 0)
+                xp = f"({self.fptr(xv)} + {gi * cg})"
+                if pointwise:
+                    aspec = self._strided("a", xp, c, 1)
+                else:
+                    aspec = [f"g.a.kind = MGC_OP_CONV_NHWC; g.a.p = {xp}; " + geo.format(f="a")]
+                self._gemm_call(
+                    nb * oh * ow, kg, kh * kw * cg, aspec, bspec, f"({self.fptr(node.output)} + {gi * kg})", kout,
+                    bias=gbias, bias_mode=1 if bias != "NULL" else 0,
+                    res=f"({res} + {gi * kg})" if res != "NULL" else "NULL", ldr=kout, act=act, lo=lo, hi=hi,
+                )
+            else:
+                wmat = np.ascontiguousarray(wv.data[gi * kg : (gi + 1) * kg].reshape(kg, cg * kh * kw), np.float32)
+                woff = self.weights.add(wmat, key=("convA", id(wv), gi))
+                aspec = self._strided("a", f"(W + {woff})", cg * kh * kw, 1)
+                bspec = [f"g.b.kind = MGC_OP_CONV_NCHW; g.b.p = ({self.fptr(xv)} + {gi * cg * h * wd}); " + geo.format(f="b")]
+                plane = oh * ow
+                batch = [(nb, 0, c * h * wd, kout * plane, kout * plane if res != "NULL" else 0)]
+                self._gemm_call(
+                    kg, plane, cg * kh * kw, aspec, bspec, f"({self.fptr(node.output)} + {gi * kg * plane})", plane,
+                    batch=batch, bias=gbias, bias_mode=2 if bias != "NULL" else 0,
+                    res=f"({res} + {gi * kg * plane})" if res != "NULL" else "NULL", ldr=plane, act=act, lo=lo, hi=hi,
+                )
+
+    def _pool(self, node: Node, is_max: int) -> None:
+        xv = node.input(0)
+        xt = xv.tensor_type
+        self._require_f32(node, xt)
+        nhwc = ops.conv_layout(node) == "NHWC"
+        nb, h, wd, c = xt.shape if nhwc else (xt.shape[0], xt.shape[2], xt.shape[3], xt.shape[1])
+        kernel = [int(k) for k in node.attrs["kernel_shape"]]
+        g = ops.window_geometry(node, (h, wd), (kernel[0], kernel[1]), bool(node.attrs.get("ceil_mode", 0)))
+        pt, pl, pb, pr = g.pads
+        oh, ow = g.out_hw
+        include = int(node.attrs.get("count_include_pad", 0))
+        self.emit(
+            f"mgc_hip_pool(x, {int(nhwc)}, {is_max}, {nb}, {h}, {wd}, {c}, {kernel[0]}, {kernel[1]}, "
+            f"{g.strides[0]}, {g.strides[1]}, {g.dilations[0]}, {g.dilations[1]}, {pt}, {pl}, {pb}, {pr}, "
+            f"{oh}, {ow}, {include}, {self.fptr(xv)}, {self.fptr(node.output)});"
+        )
+        self.count("pool")
+
+    def op_MaxPool(self, node: Node) -> None:
+        self._pool(node, 1)
+
+    def op_AveragePool(self, node: Node) -> None:
+        self._pool(node, 0)
+
+    def _global_pool(self, node: Node, is_max: int) -> None:
+        xv = node.input(0)
+        xt = xv.tensor_type
+        self._require_f32(node, xt)
+        if ops.conv_layout(node) == "NHWC":
+            outer, n, inner = xt.shape[0], int(np.prod(xt.shape[1:-1])), xt.shape[-1]
+        else:
+            outer, n, inner = xt.shape[0] * xt.shape[1], int(np.prod(xt.shape[2:])), 1
+        self.emit(f"mgc_hip_reduce_mid(x, {is_max}, {outer}L, {n}L, {inner}L, {self.fptr(xv)}, {self.fptr(node.output)});")
+        self.count("reduce")
+
+    def op_GlobalAveragePool(self, node: Node) -> None:
+        self._global_pool(node, 0)
+
+    def op_GlobalMaxPool(self, node: Node) -> None:
+        self._global_pool(node, 1)
+
+    # -- whole program -------------------------------------------------------------------------
+    def generate(self) -> GeneratedModel:
+        for k, node in enumerate(self.graph.nodes):
+            self.node(node, k)
+        for value, j in self.plan.copies:
+            t = value.tensor_type
+            self.copy((t.nbytes,), f"((unsigned char *)out[{j}])", [1], 0, self.ptr(value), [1], 0, 1)
+        arena = max(self.plan.arena_bytes, ALIGN)
+        weights = self.weights
+        n_in, n_out = len(self.graph.inputs), len(self.graph.named_outputs())
+        in_bytes = ", ".join(f"{v.tensor_type.nbytes}UL" for v in self.graph.inputs) or "0UL"
+        out_bytes = ", ".join(f"{v.tensor_type.nbytes}UL" for _, v in self.graph.named_outputs()) or "0UL"
+        n_prof = len(self.graph.nodes) if self.profile else 0
+        head = [
+            "/* Generated by ml-graph-compiler (hip backend, gfx950). Host code only: every node is",
+            " * one launcher call into libmgc_hip.so with constant offsets. */",
+            "#include <string.h>",
+            "#include <math.h>",
+            '#include "mgc_hip.h"',
+            "",
+            f"/* graph {comment_text(self.graph.name)}: {len(self.graph.nodes)} nodes, arena {arena} bytes, "
+            f"weights {weights.nbytes} bytes */",
+            "",
+            "static void mgc_forward(mgc_hip_exec *x, const void *const *in, void *const *out, unsigned char *A,",
+            "                        const unsigned char *W) {",
+            "    (void)in; (void)out; (void)A; (void)W; (void)x;",
+        ]
+        tail = [
+            "}",
+            "",
+            f"static const size_t mgc_in_bytes[] = {{{in_bytes}}};",
+            f"static const size_t mgc_out_bytes[] = {{{out_bytes}}};",
+            f"static mgc_hip_model MODEL = {{{arena}UL, {weights.nbytes}UL, {n_in}, {n_out}, mgc_in_bytes, "
+            f"mgc_out_bytes, {n_prof}, mgc_forward, NULL}};",
+            "",
+            'extern "C" {',
+            f"size_t mgc_arena_bytes(void) {{ return {arena}UL; }}",
+            f"size_t mgc_weights_bytes(void) {{ return {weights.nbytes}UL; }}",
+            "int mgc_hip_init(const unsigned char *w, unsigned char **A, unsigned char **W) {",
+            "    return mgc_hip_model_init(&MODEL, w, A, W);",
+            "}",
+            "int mgc_run(const void *const *inputs, void *const *outputs, unsigned char *A, const unsigned char *W) {",
+            "    return mgc_hip_model_run(&MODEL, inputs, outputs, A, W);",
+            "}",
+            "int mgc_run_device(const void *const *inputs, void *const *outputs, unsigned char *A,",
+            "                   const unsigned char *W) {",
+            "    return mgc_hip_model_run_device(&MODEL, inputs, outputs, A, W);",
+            "}",
+            "int mgc_hip_upload(const void *const *inputs) { return mgc_hip_model_upload(&MODEL, inputs); }",
+            "int mgc_hip_launch(int replays) { return mgc_hip_model_launch(&MODEL, replays); }",
+            "int mgc_hip_sync(void) { return mgc_hip_model_sync(&MODEL); }",
+            "int mgc_hip_download(void *const *outputs) { return mgc_hip_model_download(&MODEL, outputs); }",
+            "double mgc_hip_time_graph(int replays) { return mgc_hip_model_time_graph(&MODEL, replays); }",
+            "void mgc_hip_release(void) { mgc_hip_model_release(&MODEL); }",
+            "void mgc_set_num_threads(int n) { (void)n; }",
+            "int mgc_get_max_threads(void) { return 1; }",
+            "int mgc_has_openmp(void) { return 0; }",
+            "int mgc_has_neon(void) { return 0; }",
+            "void mgc_set_blocking(int mc, int kc, int npb) { (void)mc; (void)kc; (void)npb; }",
+        ]
+        if self.profile:
+            tail += [
+                f"int mgc_profile_size(void) {{ return {n_prof}; }}",
+                "const double *mgc_profile_data(void) { return mgc_hip_model_profile_data(&MODEL); }",
+                "int mgc_hip_profile_run(int replays) { return mgc_hip_model_profile_run(&MODEL, replays); }",
+                "void mgc_hip_profile_reset(void) { mgc_hip_model_profile_reset(&MODEL); }",
+            ]
+        tail += ["}", ""]
+        body = ["    " + line for line in self.body]
+        source = "\n".join(head + body + tail)
+        return GeneratedModel(
+            source=source,
+            weights=weights,
+            arena_bytes=arena,
+            inputs=[(v.name, v.tensor_type) for v in self.graph.inputs],
+            outputs=[(name, v.tensor_type) for name, v in self.graph.named_outputs()],
+            plan=self.plan,
+            lines=source.count("\n"),
+            kernels=dict(sorted(self.kernels.items())),
+            node_flops=[ops.flops(n) for n in self.graph.nodes],
+        )
+
+
+def generate_hip(
+    graph: Graph,
+    strategy: Strategy = "greedy_by_size",
+    inplace: bool = True,
+    profile: bool = False,
+    gemm_workspace: Callable[[int, int, int, int], int] | None = None,
+) -> GeneratedModel:
+    """Generate the host source and weights blob of a scheduled graph for the hip backend."""
+    return HipEmitter(graph, strategy, inplace, profile, gemm_workspace).generate()

@@ -1,0 +1,90 @@
+"""Test helpers: one-operator IR graphs and comparison of the hip backend with the oracle.
+
+``op_graph`` is the IR counterpart of the reference's ``op_model`` (tests/helpers.py:23-59):
+inputs listed in ``const`` become constants, the others graph inputs fed from the arrays.
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+from typing import Any
+
+import numpy as np
+
+from ml_graph_compiler.ir import Graph, TensorType, dtype_name
+from ml_graph_compiler.passes import optimize
+from ml_graph_compiler.schedule import schedule
+from ml_graph_compiler.shape_inference import infer_shapes
+from oracle import interpreter as oracle
+
+rng = np.random.default_rng(1)
+
+
+def f32(*shape: int) -> np.ndarray:
+    return np.asarray(rng.standard_normal(shape), dtype=np.float32)
+
+
+def pos(*shape: int) -> np.ndarray:
+    return np.asarray(rng.random(shape) + 0.5, dtype=np.float32)
+
+
+def op_graph(
+    op: str,
+    inputs: list[np.ndarray | None],
+    const: set[int] | None = None,
+    attrs: dict[str, Any] | None = None,
+    n_outputs: int = 1,
+) -> tuple[Graph, dict[str, np.ndarray]]:
+    const = const or set()
+    g = Graph("single")
+    values, feeds = [], {}
+    for i, array in enumerate(inputs):
+        if array is None:
+            values.append(None)
+            continue
+        a = np.asarray(array)
+        if i in const:
+            values.append(g.constant(a, f"in{i}"))
+        else:
+            values.append(g.add_input(f"in{i}", TensorType(dtype_name(a.dtype), tuple(a.shape))))
+            feeds[f"in{i}"] = a
+    node = g.add_node(op, values, n_outputs, attrs or {}, name="node", output_names=[f"out{i}" for i in range(n_outputs)])
+    for i, out in enumerate(node.outputs):
+        g.add_output(out, f"out{i}")
+    infer_shapes(g)
+    return g, feeds
+
+
+def compile_hip(graph: Graph, cache: Path, opt: str = "O3", **kwargs: Any):
+    from ml_graph_compiler.codegen import compile_graph
+
+    optimize(graph, opt)
+    schedule(graph)
+    return compile_graph(graph, cache_dir=cache, **kwargs)
+
+
+def check_hip(
+    graph: Graph,
+    feeds: dict[str, np.ndarray],
+    cache: Path,
+    opt: str = "O0",
+    rtol: float = 1e-4,
+    atol: float = 1e-5,
+) -> dict[str, np.ndarray]:
+    """Compile ``graph`` with the hip backend at ``opt``, run it and compare every output with
+    the oracle run on the unoptimized graph; returns the hip outputs."""
+    expected = oracle.run_graph(graph, feeds)
+    model = compile_hip(graph, cache, opt)
+    try:
+        got = model.run(feeds)
+    finally:
+        model.release()
+    assert set(got) == set(expected)
+    for name, value in expected.items():
+        assert got[name].shape == value.shape, (name, got[name].shape, value.shape)
+        assert got[name].dtype == value.dtype, (name, got[name].dtype, value.dtype)
+        if np.issubdtype(value.dtype, np.floating):
+            np.testing.assert_allclose(got[name], value, rtol=rtol, atol=atol, err_msg=name)
+        else:
+            np.testing.assert_array_equal(got[name], value, err_msg=name)
+    return got

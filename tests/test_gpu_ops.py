@@ -1,0 +1,231 @@
+"""Every hip lowering, one operator at a time, against the oracle.
+
+The operator list and shapes follow the reference's backend tests
+(tests/test_codegen.py:94-396): unary and binary elementwise with broadcasting, comparisons,
+integer math, parameterized activations, data movement, reductions, normalization, MatMul and
+Gemm variants, convolution (strides, pads, dilations, groups, depthwise, auto_pad) at O0 and O3,
+pooling (pads, ceil mode, count_include_pad, dilations) and global pooling. The oracle is the
+numpy restatement of the reference interpreter; integer and index results must match exactly.
+"""
+
+from __future__ import annotations
+
+from typing import Any
+
+import numpy as np
+import pytest
+
+from helpers import check_hip, f32, op_graph, pos, rng
+
+pytestmark = pytest.mark.gpu
+
+UNARY = ["Relu", "Sigmoid", "Tanh", "Erf", "Exp", "Neg", "Abs", "Floor", "Ceil", "Sin", "Cos", "Softplus", "Identity"]
+
+
+@pytest.mark.parametrize("op", UNARY)
+def test_unary(op, hip_cache):
+    g, feeds = op_graph(op, [f32(3, 70) * 3])
+    check_hip(g, feeds, hip_cache, rtol=2e-5, atol=2e-6)
+
+
+@pytest.mark.parametrize("op", ["Sqrt", "Log", "Reciprocal"])
+def test_unary_positive(op, hip_cache):
+    g, feeds = op_graph(op, [pos(4, 33)])
+    check_hip(g, feeds, hip_cache)
+
+
+@pytest.mark.parametrize("op", ["Add", "Sub", "Mul", "Div", "Max", "Min", "Pow"])
+@pytest.mark.parametrize("shapes", [((2, 3, 4), (4,)), ((2, 1, 4), (3, 1)), ((5,), (5,)), ((), (2, 2))])
+def test_binary_broadcast(op, shapes, hip_cache):
+    a = pos(*shapes[0]) if op == "Pow" else f32(*shapes[0])
+    g, feeds = op_graph(op, [a, pos(*shapes[1])])
+    check_hip(g, feeds, hip_cache)
+
+
+@pytest.mark.parametrize("op", ["Equal", "Less", "Greater", "LessOrEqual", "GreaterOrEqual"])
+def test_compare(op, hip_cache):
+    a = rng.integers(0, 3, (3, 4)).astype(np.float32)
+    g, feeds = op_graph(op, [a, rng.integers(0, 3, (4,)).astype(np.float32)])
+    check_hip(g, feeds, hip_cache)
+
+
+@pytest.mark.parametrize("op", ["And", "Or", "Xor"])
+def test_logical(op, hip_cache):
+    g, feeds = op_graph(op, [rng.random((3, 4)) > 0.5, rng.random((4,)) > 0.5])
+    check_hip(g, feeds, hip_cache)
+
+
+def test_not_where_cast_and_integer_math(hip_cache):
+    check_hip(*op_graph("Not", [rng.random((5,)) > 0.5]), hip_cache)
+    check_hip(*op_graph("Where", [rng.random((3, 1)) > 0.5, f32(3, 4), f32(4)]), hip_cache)
+    for to, src in [(7, f32(6) * 5), (1, np.arange(6, dtype=np.int64)), (9, np.asarray([0, 1, 2, 0], np.float32))]:
+        check_hip(*op_graph("Cast", [src], attrs={"to": to}), hip_cache)
+    ints = np.asarray([7, -7, 9, 4], np.int64)
+    for op in ("Add", "Sub", "Mul", "Div", "Max", "Min"):
+        check_hip(*op_graph(op, [ints, np.asarray([2, 2, -4, 3], np.int64)]), hip_cache)
+
+
+@pytest.mark.parametrize(
+    "op, attrs, inputs, const",
+    [
+        ("Clip", {}, [f32(3, 5), np.asarray(-0.5, np.float32), np.asarray(0.5, np.float32)], {1, 2}),
+        ("Clip", {}, [f32(3, 5), None, np.asarray(0.2, np.float32)], {2}),
+        ("LeakyRelu", {"alpha": 0.2}, [f32(3, 5)], set()),
+        ("HardSigmoid", {}, [f32(3, 5)], set()),
+        ("Gelu", {}, [f32(3, 5)], set()),
+        ("Gelu", {"approximate": "tanh"}, [f32(3, 5)], set()),
+    ],
+)
+def test_parameterized_elementwise(op, attrs, inputs, const, hip_cache):
+    g, feeds = op_graph(op, inputs, const=const, attrs=attrs)
+    check_hip(g, feeds, hip_cache, rtol=1e-5, atol=1e-6)
+
+
+def test_integer_clip(hip_cache):
+    g, feeds = op_graph("Clip", [np.arange(-5, 5, dtype=np.int64), np.asarray(-2, np.int64), np.asarray(3, np.int64)], const={1, 2})
+    check_hip(g, feeds, hip_cache)
+
+
+@pytest.mark.parametrize(
+    "op, inputs, const, attrs",
+    [
+        ("Transpose", [f32(2, 3, 4, 5)], set(), {"perm": [0, 2, 3, 1]}),
+        ("Transpose", [f32(3, 4)], set(), {}),
+        ("Expand", [f32(3, 1), np.asarray([2, 3, 4], np.int64)], {1}, {}),
+        ("Tile", [f32(2, 3), np.asarray([2, 2], np.int64)], {1}, {}),
+        ("Slice", [f32(6, 8), np.asarray([1, -6], np.int64), np.asarray([5, 100], np.int64),
+                   np.asarray([0, 1], np.int64), np.asarray([2, 3], np.int64)], {1, 2, 3, 4}, {}),
+        ("Slice", [f32(6, 8), np.asarray([4], np.int64), np.asarray([0], np.int64),
+                   np.asarray([1], np.int64), np.asarray([-2], np.int64)], {1, 2, 3, 4}, {}),
+        ("Concat", [f32(2, 3), f32(2, 5), f32(2, 1)], set(), {"axis": 1}),
+        ("Concat", [f32(1, 3), f32(2, 3)], {0}, {"axis": 0}),
+        ("Pad", [f32(2, 3), np.asarray([1, 0, 2, 3], np.int64), np.asarray(1.5, np.float32)], {1, 2}, {}),
+        ("Gather", [f32(10, 4), np.asarray([[1, -1], [3, 0]], np.int64)], set(), {"axis": 0}),
+        ("Gather", [f32(3, 10, 2), np.asarray([4, 2], np.int64)], {1}, {"axis": 1}),
+        ("Shape", [f32(2, 3, 4)], set(), {}),
+        ("Size", [f32(2, 3, 4)], set(), {}),
+        ("ConstantOfShape", [np.asarray([2, 3], np.int64)], {0}, {"value": np.asarray([7], np.int64)}),
+        ("Range", [np.asarray(1.0, np.float32), np.asarray(9.0, np.float32), np.asarray(1.5, np.float32)], {0, 1, 2}, {}),
+        ("ReduceMean", [f32(2, 3, 4)], set(), {"axes": [1, 2], "keepdims": 1}),
+        ("ReduceMean", [f32(2, 3, 4)], set(), {"axes": [-1], "keepdims": 0}),
+        ("ReduceSum", [f32(2, 3, 4), np.asarray([0, 1], np.int64)], {1}, {"keepdims": 0}),
+        ("ReduceMax", [f32(2, 3, 4)], set(), {"axes": [1]}),
+        ("ReduceMin", [f32(2, 3, 4)], set(), {"axes": [2]}),
+        ("ReduceProd", [pos(2, 3)], set(), {"axes": [1]}),
+        ("ArgMax", [f32(3, 7)], set(), {"axis": 1, "keepdims": 0}),
+        ("Softmax", [f32(2, 3, 9)], set(), {"axis": -1}),
+        ("Softmax", [f32(2, 7, 3)], set(), {"axis": 1}),
+        ("LogSoftmax", [f32(4, 9)], set(), {"axis": -1}),
+        ("Flatten", [f32(2, 3, 4)], set(), {"axis": 2}),
+        ("Unsqueeze", [f32(2, 3), np.asarray([0, 3], np.int64)], {1}, {}),
+        ("Squeeze", [f32(2, 1, 3), np.asarray([1], np.int64)], {1}, {}),
+        ("Identity", [f32(4)], set(), {}),
+    ],
+)
+def test_data_movement_and_reductions(op, inputs, const, attrs, hip_cache):
+    g, feeds = op_graph(op, inputs, const=const, attrs=attrs)
+    check_hip(g, feeds, hip_cache)
+
+
+def test_split_and_dropout(hip_cache):
+    g, feeds = op_graph("Split", [f32(4, 9), np.asarray([2, 3, 4], np.int64)], const={1}, attrs={"axis": 1}, n_outputs=3)
+    check_hip(g, feeds, hip_cache)
+    g, feeds = op_graph("Dropout", [f32(3, 4)], n_outputs=2)
+    check_hip(g, feeds, hip_cache)
+
+
+def test_layer_and_batch_norm(hip_cache):
+    check_hip(*op_graph("LayerNormalization", [f32(2, 5, 16), pos(16), f32(16)], const={1, 2},
+                        attrs={"axis": -1, "epsilon": 1e-5}), hip_cache)
+    check_hip(*op_graph("LayerNormalization", [f32(2, 3, 4), pos(3, 4)], attrs={"axis": 1}), hip_cache)
+    check_hip(*op_graph("BatchNormalization", [f32(2, 3, 4, 5), pos(3), f32(3), f32(3), pos(3)], const={1, 2, 3, 4}),
+              hip_cache)
+
+
+@pytest.mark.parametrize(
+    "a_shape, b_shape, const_b",
+    [
+        ((5, 7), (7, 3), False),
+        ((5, 7), (7, 30), True),
+        ((2, 3, 5, 7), (7, 9), True),
+        ((2, 3, 5, 7), (2, 3, 7, 4), False),
+        ((2, 1, 5, 7), (3, 7, 4), False),
+        ((7,), (7, 5), False),
+        ((4, 7), (7,), False),
+        ((1, 1), (1, 1), False),
+        ((33, 65), (65, 29), True),
+        ((200, 136), (136, 264), True),
+        ((3, 130, 68), (3, 68, 132), False),
+    ],
+)
+def test_matmul(a_shape, b_shape, const_b, hip_cache):
+    g, feeds = op_graph("MatMul", [f32(*a_shape), f32(*b_shape)], const={1} if const_b else set())
+    check_hip(g, feeds, hip_cache)
+
+
+@pytest.mark.parametrize(
+    "attrs, c_shape",
+    [
+        ({}, None),
+        ({"transA": 1}, (3,)),
+        ({"transB": 1, "alpha": 0.5, "beta": 2.0}, (1, 3)),
+        ({"beta": 0.5}, (4, 3)),
+        ({}, (4, 1)),
+        ({}, ()),
+    ],
+)
+def test_gemm(attrs, c_shape, hip_cache):
+    a = f32(5, 4) if attrs.get("transA") else f32(4, 5)
+    b = f32(3, 5) if attrs.get("transB") else f32(5, 3)
+    inputs = [a, b] + ([f32(*c_shape)] if c_shape is not None else [])
+    check_hip(*op_graph("Gemm", inputs, const={1, 2}, attrs=attrs), hip_cache)
+    if c_shape in ((4, 3), None):
+        check_hip(*op_graph("Gemm", inputs, attrs=attrs), hip_cache)
+
+
+CONV_CASES = [
+    ({"kernel_shape": [3, 3], "pads": [1, 1, 1, 1]}, (1, 4, 9, 8), (6, 4, 3, 3)),
+    ({"kernel_shape": [3, 3], "strides": [2, 2], "pads": [1, 0, 1, 2]}, (2, 3, 11, 9), (5, 3, 3, 3)),
+    ({"kernel_shape": [2, 3], "dilations": [2, 1]}, (1, 2, 9, 9), (4, 2, 2, 3)),
+    ({"kernel_shape": [3, 3], "pads": [1, 1, 1, 1], "group": 2}, (1, 4, 6, 6), (6, 2, 3, 3)),
+    ({"kernel_shape": [3, 3], "pads": [1, 1, 1, 1], "group": 4}, (1, 4, 7, 7), (4, 1, 3, 3)),
+    ({"kernel_shape": [3, 3], "group": 4, "strides": [2, 2]}, (2, 4, 9, 9), (8, 1, 3, 3)),
+    ({"kernel_shape": [1, 1]}, (1, 16, 5, 5), (24, 16, 1, 1)),
+    ({"kernel_shape": [3, 3], "auto_pad": "SAME_UPPER", "strides": [2, 2]}, (1, 3, 8, 8), (4, 3, 3, 3)),
+    ({"kernel_shape": [3, 3], "pads": [1, 1, 1, 1]}, (2, 64, 10, 12), (96, 64, 3, 3)),
+    ({"kernel_shape": [3, 3], "pads": [1, 1, 1, 1], "group": 32}, (2, 32, 9, 9), (32, 1, 3, 3)),
+]
+
+
+@pytest.mark.parametrize("attrs, x_shape, w_shape", CONV_CASES)
+@pytest.mark.parametrize("opt", ["O0", "O3"])
+def test_conv(attrs, x_shape, w_shape, opt, hip_cache):
+    g, feeds = op_graph("Conv", [f32(*x_shape), f32(*w_shape) * 0.3, f32(w_shape[0])], const={1, 2}, attrs=attrs)
+    check_hip(g, feeds, hip_cache, opt=opt)
+
+
+POOL_CASES = [
+    {"kernel_shape": [3, 3], "strides": [2, 2], "pads": [1, 1, 1, 1]},
+    {"kernel_shape": [2, 2], "strides": [2, 2]},
+    {"kernel_shape": [3, 3], "strides": [2, 2], "ceil_mode": 1},
+    {"kernel_shape": [3, 3], "pads": [1, 1, 1, 1], "count_include_pad": 1},
+    {"kernel_shape": [3, 3], "strides": [2, 2], "pads": [1, 1, 1, 1], "ceil_mode": 1},
+    {"kernel_shape": [2, 2], "dilations": [2, 2]},
+]
+
+
+@pytest.mark.parametrize("attrs", POOL_CASES)
+@pytest.mark.parametrize("op", ["MaxPool", "AveragePool"])
+@pytest.mark.parametrize("opt", ["O0", "O3"])
+def test_pooling(op, attrs, opt, hip_cache):
+    if op == "MaxPool":
+        attrs = {k: v for k, v in attrs.items() if k != "count_include_pad"}
+    g, feeds = op_graph(op, [f32(2, 3, 9, 10)], attrs=attrs)
+    check_hip(g, feeds, hip_cache, opt=opt)
+
+
+@pytest.mark.parametrize("op", ["GlobalAveragePool", "GlobalMaxPool"])
+@pytest.mark.parametrize("opt", ["O0", "O3"])
+def test_global_pooling(op, opt, hip_cache):
+    g, feeds = op_graph(op, [f32(2, 5, 4, 3)])
+    check_hip(g, feeds, hip_cache, opt=opt)
