@@ -1,0 +1,208 @@
+#!/usr/bin/env python3
+"""Benchmark of the hip backend: ResNet-50 fp32 img/s on one MI355X.
+
+A "step" is one forward pass of the compiled model over one batch of synthetic input (seeded
+N(0,1) images, He-normal weights, BatchNorm folded at -O3), replayed as the captured hipGraph
+with inputs already resident in HBM. The timed region is exactly ``--steps`` replays between two
+stream synchronizations (wall clock, cross-checked with hipEvents on the model stream).
+
+Printed: ONE JSON line with the driver's fields plus
+* ``roofline``: the fp32 MFMA GEMM / implicit-GEMM convolution kernels (all conv and FC nodes):
+  algorithmic FLOPs per launch (ops.flops of the node, 2 per MAC) over the kernel's average
+  duration, measured with a hipEvent pair around every node in eager replays on the model
+  stream; ``traffic`` comes from rocprofv3 counter runs (see DESIGN) and is null here;
+* ``cpu_baseline``: the reference's generated-C + OpenMP backend (its own C kernels, built from
+  the reference sources into oracle/_ref) timed on this host's cores on a bounded sample;
+* ``b1``: the same model at batch 1 (latency and img/s).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path[:0] = [str(ROOT), str(ROOT / "ml-graph-compiler_amd")]
+
+import numpy as np  # noqa: E402
+
+MFMA_FP32_PEAK_TFLOPS = 157.3
+HBM_PEAK_GBS = 8000.0
+WORKLOADS = ("resnet50", "bottleneck", "mobilenet_v2", "bert_base", "single_gemm")
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def build_graph(workload: str, batch: int):
+    from ml_graph_compiler import builders
+
+    if workload == "single_gemm":
+        return builders.single_gemm()
+    return builders.CONFIGS[workload](batch=batch)
+
+
+def compile_workload(workload: str, batch: int, cache: Path):
+    from ml_graph_compiler.codegen import compile_graph
+    from ml_graph_compiler.passes import optimize
+    from ml_graph_compiler.schedule import schedule
+
+    g = build_graph(workload, batch)
+    optimize(g, "O3")
+    schedule(g)
+    model = compile_graph(g, cache_dir=cache, name=f"{workload}_b{batch}", profile=True)
+    return g, model
+
+
+def feeds_for(graph, seed: int = 0):
+    from ml_graph_compiler.builders import random_feeds
+
+    return random_feeds(graph, seed, int_high=30522 if any(v.type.dtype == "int64" for v in graph.inputs) else 100)
+
+
+def time_replays(model, steps: int) -> tuple[float, float]:
+    """(wall seconds, event milliseconds) of ``steps`` graph replays on resident inputs."""
+    model.sync()
+    t0 = time.perf_counter()
+    model.launch(steps)
+    model.sync()
+    wall = time.perf_counter() - t0
+    ev_ms = float(model.lib.mgc_hip_time_graph(int(steps)))
+    model.sync()
+    return wall, ev_ms
+
+
+def gemm_roofline(graph, model, replays: int) -> dict:
+    """Achieved TFLOP/s of the MFMA GEMM kernels from per-node hipEvent durations."""
+    model.profile_reset()
+    model.profile_run(replays)
+    prof = model.profile()
+    flops = 0
+    secs = 0.0
+    launches = 0
+    for (op, _name, sec), node, f in zip(prof, graph.nodes, model.node_flops):
+        if op in ("FusedConv", "Conv", "FusedGemm", "Gemm", "MatMul") and not _is_depthwise(node):
+            flops += f * replays
+            secs += sec
+            launches += replays
+    total = sum(sec for _, _, sec in prof)
+    achieved = flops / secs / 1e12 if secs > 0 else 0.0
+    return {
+        "bound": "mfma",
+        "kernel": "gemm_mfma_kernel (fp32 MFMA implicit-GEMM conv / GEMM)",
+        "achieved": round(achieved, 2),
+        "peak": MFMA_FP32_PEAK_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(achieved / MFMA_FP32_PEAK_TFLOPS, 4),
+        "traffic": None,
+        "flops_per_launch": int(flops / max(launches, 1)),
+        "avg_launch_us": round(1e6 * secs / max(launches, 1), 2),
+        "share_of_forward": round(secs / total, 3) if total > 0 else None,
+    }
+
+
+def _is_depthwise(node) -> bool:
+    from ml_graph_compiler.codegen.hip import HipEmitter
+
+    return HipEmitter.depthwise(node)
+
+
+def cpu_baseline(workload: str, seconds_budget: float = 20.0) -> dict | None:
+    """The reference's generated-C backend on this host's cores (bounded sample)."""
+    try:
+        from oracle import cbackend
+    except Exception as exc:  # pragma: no cover - reported, not fatal
+        log(f"cpu baseline unavailable: {exc}")
+        return None
+    try:
+        return cbackend.time_baseline(workload, seconds_budget=seconds_budget)
+    except Exception as exc:
+        log(f"cpu baseline failed: {exc}")
+        return None
+
+
+def main() -> int:
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--workload", choices=WORKLOADS, default="resnet50")
+    p.add_argument("--batch", type=int, default=32)
+    p.add_argument("--profile-replays", type=int, default=5)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-b1", action="store_true")
+    p.add_argument("--cache", default=os.environ.get("MGC_BENCH_CACHE", "/tmp/mgc-bench-cache"))
+    args = p.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU: every GPU box here has one MI355X; "
+                                   "use --gpus 1 (batch sharding across GPUs is described in DESIGN.md)"}))
+        return 2
+    cache = Path(args.cache)
+    batch = 128 if args.workload == "single_gemm" else args.batch
+
+    log(f"compiling {args.workload} b{batch} (O3, hip)")
+    graph, model = compile_workload(args.workload, batch, cache)
+    feeds = feeds_for(graph)
+    model.upload(feeds)
+    log(f"warmup {args.warmup}")
+    model.launch(args.warmup)
+    model.sync()
+    log(f"timing {args.steps} replays")
+    wall, ev_ms = time_replays(model, args.steps)
+    ms_per_step = 1e3 * wall / args.steps
+    units = 1 if args.workload == "single_gemm" else batch
+    value = units * args.steps / wall
+    log(f"{ms_per_step:.3f} ms/step (events {ev_ms / args.steps:.3f} ms), {value:.1f} units/s")
+    roof = gemm_roofline(graph, model, args.profile_replays)
+    log(f"roofline {roof}")
+    total_flops = sum(model.node_flops)
+    model.release()
+
+    b1 = None
+    if args.workload in ("resnet50", "bottleneck", "mobilenet_v2", "bert_base") and not args.no_b1 and batch != 1:
+        g1, m1 = compile_workload(args.workload, 1, cache)
+        m1.upload(feeds_for(g1))
+        m1.launch(args.warmup)
+        m1.sync()
+        w1, e1 = time_replays(m1, max(args.steps, 50))
+        n1 = max(args.steps, 50)
+        b1 = {"ms_per_step": round(1e3 * w1 / n1, 4), "event_ms_per_step": round(e1 / n1, 4),
+              "value": round(n1 / w1, 2)}
+        m1.release()
+        log(f"b1 {b1}")
+
+    cpu = None if args.no_cpu_baseline else cpu_baseline(args.workload)
+    unit = {"resnet50": "img/s", "bottleneck": "img/s", "mobilenet_v2": "img/s", "bert_base": "seq/s",
+            "single_gemm": "calls/s"}[args.workload]
+    line = {
+        "metric": "ResNet-50 fp32 img/s at b1/b32; achieved TFLOP/s vs fp32 MFMA peak"
+        if args.workload == "resnet50" else f"{args.workload} fp32 {unit}",
+        "value": round(value, 2),
+        "unit": unit,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "event_ms_per_step": round(ev_ms / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,1) inputs, random He-normal weights, BN folded at -O3)",
+        "config": {"workload": args.workload, "batch": units if args.workload != "single_gemm" else 1,
+                   "opt": "O3", "backend": "hip", "achieved_tflops_forward": round(total_flops * value / units / 1e12, 2)},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "b1": b1,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -14,8 +14,13 @@
 //    summation order, applied identically to A and B), so each lane's 16 k values are
 //    contiguous in LDS.
 //  * Global loads are float4 (16 B) when the operand is k-contiguous (packed weights, NHWC
-//    activations with channel counts divisible by 4); implicit im2col computes the (kh, kw, c)
-//    split of a k quad once per stage and reuses it for all of a thread's rows.
+//    activations with channel counts divisible by 4) and branch-free (out-of-range lanes read
+//    a valid address and select zero). Implicit im2col computes the (kh, kw, c) split of a
+//    thread's k once per stage and reuses it for all of the thread's rows.
+//  * The epilogue stages the accumulator tile through LDS, then every thread walks the tile in
+//    16-byte chunks: coalesced float4 residual loads and stores, bias per float4, and one
+//    activation dispatch per chunk. This keeps the kernel's code small (an unrolled per-register
+//    epilogue would not fit the instruction cache) and its HBM traffic in full lines.
 //  * The workgroup id is remapped so each of the 8 XCDs (each with its own L2) works on a
 //    contiguous range of tiles, N fastest: tiles that share A rows share an L2.
 //  * Small-M problems (the 128-row GEMM of the single-GEMM config) split K over extra
@@ -45,10 +50,11 @@ struct GemmDev {
     int batch_rank;
     int bdims[4];
     long a_bs[4], b_bs[4], c_bs[4], r_bs[4];
-    int split;   // K splits (1 = none)
-    int kchunk;  // K per split, a multiple of 32
-    float *ws;   // split partials [split][M][N]
+    int split;    // K splits (1 = none)
+    int kchunk;   // K per split, a multiple of 32
+    float *ws;    // split partials [split][M][N]
     int tiles_m, tiles_n;
+    int vec_out;  // 16-byte epilogue accesses are aligned (ldc, ldr, pointers)
 };
 
 __device__ __forceinline__ void batch_offsets(const GemmDev &p, int bz, long &ao, long &bo,
@@ -68,33 +74,36 @@ __device__ __forceinline__ void batch_offsets(const GemmDev &p, int bz, long &ao
     }
 }
 
-// Scalar operand reads for the generic paths (any strides, any channel count).
-__device__ __forceinline__ float load_a_generic(const GemmDev &p, const float *a, int m, int k,
-                                                int kend) {
-    if (m >= p.M || k >= kend) return 0.0f;
-    const mgc_hip_operand &o = p.a;
-    if (o.kind == MGC_OP_STRIDED) return a[(long)m * o.rs + (long)k * o.cs];
-    int ohw = o.OH * o.OW;
-    int n = m / ohw, r = m - n * ohw;
-    int oh = r / o.OW, ow = r - oh * o.OW;
-    int t = k / o.cg, c = k - t * o.cg;
-    int kh = t / o.KW, kw = t - kh * o.KW;
-    int ih = oh * o.SH - o.PT + kh * o.DH, iw = ow * o.SW - o.PL + kw * o.DW;
-    if ((unsigned)ih >= (unsigned)o.H || (unsigned)iw >= (unsigned)o.W) return 0.0f;
-    return a[(long)n * o.H * o.W * o.C + ((long)ih * o.W + iw) * o.C + c];
-}
-
-__device__ __forceinline__ float load_b_generic(const GemmDev &p, const float *b, int k, int n,
-                                                int kend) {
-    if (n >= p.N || k >= kend) return 0.0f;
-    const mgc_hip_operand &o = p.b;
-    if (o.kind == MGC_OP_STRIDED) return b[(long)k * o.rs + (long)n * o.cs];
-    int t = k / o.KW, kw = k - t * o.KW;
-    int c = t / o.KH, kh = t - c * o.KH;
-    int oh = n / o.OW, ow = n - oh * o.OW;
-    int ih = oh * o.SH - o.PT + kh * o.DH, iw = ow * o.SW - o.PL + kw * o.DW;
-    if ((unsigned)ih >= (unsigned)o.H || (unsigned)iw >= (unsigned)o.W) return 0.0f;
-    return b[(long)c * o.H * o.W + (long)ih * o.W + iw];
+__device__ __forceinline__ f4 act4(f4 v, int act, float lo, float hi) {
+    switch (act) {
+    case MGC_ACT_RELU:
+        v[0] = v[0] > 0.0f ? v[0] : 0.0f;
+        v[1] = v[1] > 0.0f ? v[1] : 0.0f;
+        v[2] = v[2] > 0.0f ? v[2] : 0.0f;
+        v[3] = v[3] > 0.0f ? v[3] : 0.0f;
+        return v;
+    case MGC_ACT_CLIP:
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = fminf(fmaxf(v[e], lo), hi);
+        return v;
+    case MGC_ACT_GELU:
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = gelu_erf_f(v[e]);
+        return v;
+    case MGC_ACT_GELU_TANH:
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = gelu_tanh_f(v[e]);
+        return v;
+    case MGC_ACT_TANH:
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = tanh_f(v[e]);
+        return v;
+    case MGC_ACT_SIGMOID:
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = sigmoid_f(v[e]);
+        return v;
+    default: return v;
+    }
 }
 
 template <int BM, int BN, int WGM, int AMODE, int BMODE>
@@ -111,9 +120,14 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(const GemmDev p) {
     constexpr int AG = BM / 8;   // scalar loads per thread per stage (generic A)
     constexpr int BV = BN / 32;
     constexpr int BG = BN / 8;
+    constexpr int LDC = BN + 4;
+    constexpr int SMEM_LOOP = 2 * (BM + BN) * LDK;
+    constexpr int SMEM_EPI = BM * LDC;
+    constexpr int SMEM = SMEM_LOOP > SMEM_EPI ? SMEM_LOOP : SMEM_EPI;
 
-    __shared__ __attribute__((aligned(16))) float As[2][BM * LDK];
-    __shared__ __attribute__((aligned(16))) float Bs[2][BN * LDK];
+    __shared__ __attribute__((aligned(16))) float smem[SMEM];
+    float *const As = smem;                 // [2][BM * LDK]
+    float *const Bs = smem + 2 * BM * LDK;  // [2][BN * LDK]
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -144,30 +158,30 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(const GemmDev p) {
     const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
 
     // ---- per-thread loader state ----------------------------------------------------------
-    const int kq = (tid & 7) * 4;  // k quad inside a stage (vector paths)
-    const float *arow[AV];
-    int aih[AV], aiw[AV];
-    if constexpr (AMODE == AM_VEC) {
-#pragma unroll
-        for (int r = 0; r < AV; ++r) {
-            int m = m0 + (tid >> 3) + 32 * r;
-            arow[r] = m < p.M ? abase + (long)m * p.a.rs : nullptr;
-            aih[r] = aiw[r] = 0;
-        }
-    } else if constexpr (AMODE == AM_CONV_VEC) {
+    // Vector paths: thread t loads rows (t >> 3) + 32 r, k quad (t & 7) * 4 of each stage.
+    // Generic paths: thread t loads rows (t >> 5) + 8 r, k = t & 31 of each stage.
+    const int kq = (tid & 7) * 4;
+    const int kg = tid & 31;
+    constexpr int AROWS = AMODE == AM_GEN ? AG : AV;
+    const float *arow[AROWS];
+    int aih[AROWS], aiw[AROWS];
+    {
         const int ohw = p.a.OH * p.a.OW;
 #pragma unroll
-        for (int r = 0; r < AV; ++r) {
-            int m = m0 + (tid >> 3) + 32 * r;
+        for (int r = 0; r < AROWS; ++r) {
+            const int m = m0 + (AMODE == AM_GEN ? (tid >> 5) + 8 * r : (tid >> 3) + 32 * r);
+            arow[r] = nullptr;
+            aih[r] = aiw[r] = 0;
             if (m < p.M) {
-                int n = m / ohw, rr = m - n * ohw;
-                int oh = rr / p.a.OW, ow = rr - oh * p.a.OW;
-                arow[r] = abase + (long)n * p.a.H * p.a.W * p.a.C;
-                aih[r] = oh * p.a.SH - p.a.PT;
-                aiw[r] = ow * p.a.SW - p.a.PL;
-            } else {
-                arow[r] = nullptr;
-                aih[r] = aiw[r] = 0;
+                if (p.a.kind == MGC_OP_CONV_NHWC) {
+                    int n = m / ohw, rr = m - n * ohw;
+                    int oh = rr / p.a.OW, ow = rr - oh * p.a.OW;
+                    arow[r] = abase + (long)n * p.a.H * p.a.W * p.a.C;
+                    aih[r] = oh * p.a.SH - p.a.PT;
+                    aiw[r] = ow * p.a.SW - p.a.PL;
+                } else {
+                    arow[r] = abase + (long)m * p.a.rs;
+                }
             }
         }
     }
@@ -185,6 +199,8 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(const GemmDev p) {
     f4 breg[BMODE == BD_GEN ? 1 : BV];
     float bgen[BMODE == BD_GEN ? BG : 1];
     const f4 zero4 = {0.f, 0.f, 0.f, 0.f};
+    const float *const asafe = p.a.p;
+    const float *const bsafe = p.b.p;
 
     auto load_stage = [&](int kt) __attribute__((always_inline)) {
         const int k0 = kbeg + kt * BK;
@@ -192,66 +208,108 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(const GemmDev p) {
             const int k = k0 + kq;
             const bool kok = k < kend;
 #pragma unroll
-            for (int r = 0; r < AV; ++r)
-                areg[r] = (kok && arow[r]) ? *reinterpret_cast<const f4 *>(arow[r] + k) : zero4;
+            for (int r = 0; r < AV; ++r) {
+                const bool ok = kok && arow[r] != nullptr;
+                f4 v = *reinterpret_cast<const f4 *>(ok ? arow[r] + k : asafe);
+                areg[r] = ok ? v : zero4;
+            }
         } else if constexpr (AMODE == AM_CONV_VEC) {
             const int k = k0 + kq;
             const bool kok = k < kend;
-            int t = k / p.a.cg;
-            int c = k - t * p.a.cg;
-            int kh = t / p.a.KW, kw = t - (t / p.a.KW) * p.a.KW;
+            const int t = k / p.a.cg;
+            const int c = k - t * p.a.cg;
+            const int kh = t / p.a.KW, kw = t - (t / p.a.KW) * p.a.KW;
             const int dh = kh * p.a.DH, dw = kw * p.a.DW;
 #pragma unroll
             for (int r = 0; r < AV; ++r) {
-                int ih = aih[r] + dh, iw = aiw[r] + dw;
-                bool ok = kok && arow[r] && (unsigned)ih < (unsigned)p.a.H &&
-                          (unsigned)iw < (unsigned)p.a.W;
-                areg[r] = ok ? *reinterpret_cast<const f4 *>(
-                                   arow[r] + ((long)ih * p.a.W + iw) * p.a.C + c)
-                             : zero4;
+                const int ih = aih[r] + dh, iw = aiw[r] + dw;
+                const bool ok = kok && arow[r] != nullptr && (unsigned)ih < (unsigned)p.a.H &&
+                                (unsigned)iw < (unsigned)p.a.W;
+                f4 v = *reinterpret_cast<const f4 *>(
+                    ok ? arow[r] + ((long)ih * p.a.W + iw) * p.a.C + c : asafe);
+                areg[r] = ok ? v : zero4;
             }
         } else {
+            const int k = k0 + kg;
+            const bool kok = k < kend;
+            if (p.a.kind == MGC_OP_CONV_NHWC) {
+                const int t = k / p.a.cg;
+                const int c = k - t * p.a.cg;
+                const int kh = t / p.a.KW, kw = t - (t / p.a.KW) * p.a.KW;
+                const int dh = kh * p.a.DH, dw = kw * p.a.DW;
 #pragma unroll
-            for (int r = 0; r < AG; ++r) {
-                int e = tid + 256 * r;
-                agen[r] = load_a_generic(p, abase, m0 + (e >> 5), k0 + (e & 31), kend);
+                for (int r = 0; r < AG; ++r) {
+                    const int ih = aih[r] + dh, iw = aiw[r] + dw;
+                    const bool ok = kok && arow[r] != nullptr && (unsigned)ih < (unsigned)p.a.H &&
+                                    (unsigned)iw < (unsigned)p.a.W;
+                    float v = *(ok ? arow[r] + ((long)ih * p.a.W + iw) * p.a.C + c : asafe);
+                    agen[r] = ok ? v : 0.0f;
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < AG; ++r) {
+                    const bool ok = kok && arow[r] != nullptr;
+                    float v = *(ok ? arow[r] + (long)k * p.a.cs : asafe);
+                    agen[r] = ok ? v : 0.0f;
+                }
             }
         }
         if constexpr (BMODE == BD_NK_VEC) {
             const int k = k0 + kq;
             const bool kok = k < kend;
 #pragma unroll
-            for (int r = 0; r < BV; ++r)
-                breg[r] = (kok && brow[r]) ? *reinterpret_cast<const f4 *>(brow[r] + k) : zero4;
+            for (int r = 0; r < BV; ++r) {
+                const bool ok = kok && brow[r] != nullptr;
+                f4 v = *reinterpret_cast<const f4 *>(ok ? brow[r] + k : bsafe);
+                breg[r] = ok ? v : zero4;
+            }
         } else if constexpr (BMODE == BD_KN_VEC) {
 #pragma unroll
             for (int r = 0; r < BV; ++r) {
-                int e = tid + 256 * r;
-                int krow = e / (BN / 4);
-                int nq = (e - krow * (BN / 4)) * 4;
-                int k = k0 + krow, n = n0 + nq;
-                breg[r] = (k < kend && n < p.N)
-                              ? *reinterpret_cast<const f4 *>(bbase + (long)k * p.b.rs + n)
-                              : zero4;
+                const int e = tid + 256 * r;
+                const int krow = e / (BN / 4);
+                const int nq = (e - krow * (BN / 4)) * 4;
+                const int k = k0 + krow, n = n0 + nq;
+                const bool ok = k < kend && n < p.N;
+                f4 v = *reinterpret_cast<const f4 *>(ok ? bbase + (long)k * p.b.rs + n : bsafe);
+                breg[r] = ok ? v : zero4;
             }
         } else {
+            const int k = k0 + kg;
+            const bool kok = k < kend;
+            if (p.b.kind == MGC_OP_CONV_NCHW) {
+                const mgc_hip_operand &o = p.b;
+                const int t = k / o.KW, kw = k - (k / o.KW) * o.KW;
+                const int c = t / o.KH, kh = t - (t / o.KH) * o.KH;
+                const float *plane = bbase + (long)c * o.H * o.W;
 #pragma unroll
-            for (int r = 0; r < BG; ++r) {
-                int e = tid + 256 * r;
-                bgen[r] = load_b_generic(p, bbase, k0 + (e & 31), n0 + (e >> 5), kend);
+                for (int r = 0; r < BG; ++r) {
+                    const int n = n0 + (tid >> 5) + 8 * r;
+                    const int oh = n / o.OW, ow = n - (n / o.OW) * o.OW;
+                    const int ih = oh * o.SH - o.PT + kh * o.DH, iw = ow * o.SW - o.PL + kw * o.DW;
+                    const bool ok = kok && n < p.N && (unsigned)ih < (unsigned)o.H &&
+                                    (unsigned)iw < (unsigned)o.W;
+                    float v = *(ok ? plane + (long)ih * o.W + iw : bsafe);
+                    bgen[r] = ok ? v : 0.0f;
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < BG; ++r) {
+                    const int n = n0 + (tid >> 5) + 8 * r;
+                    const bool ok = kok && n < p.N;
+                    float v = *(ok ? bbase + (long)k * p.b.rs + (long)n * p.b.cs : bsafe);
+                    bgen[r] = ok ? v : 0.0f;
+                }
             }
         }
     };
 
     auto store_stage = [&](int buf) __attribute__((always_inline)) {
-        float *as = As[buf];
-        float *bs = Bs[buf];
+        float *as = As + buf * BM * LDK;
+        float *bs = Bs + buf * BN * LDK;
         if constexpr (AMODE == AM_GEN) {
 #pragma unroll
-            for (int r = 0; r < AG; ++r) {
-                int e = tid + 256 * r;
-                as[(e >> 5) * LDK + (e & 31)] = agen[r];
-            }
+            for (int r = 0; r < AG; ++r) as[((tid >> 5) + 8 * r) * LDK + kg] = agen[r];
         } else {
 #pragma unroll
             for (int r = 0; r < AV; ++r)
@@ -259,16 +317,13 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(const GemmDev p) {
         }
         if constexpr (BMODE == BD_GEN) {
 #pragma unroll
-            for (int r = 0; r < BG; ++r) {
-                int e = tid + 256 * r;
-                bs[(e >> 5) * LDK + (e & 31)] = bgen[r];
-            }
+            for (int r = 0; r < BG; ++r) bs[((tid >> 5) + 8 * r) * LDK + kg] = bgen[r];
         } else if constexpr (BMODE == BD_KN_VEC) {
 #pragma unroll
             for (int r = 0; r < BV; ++r) {
-                int e = tid + 256 * r;
-                int krow = e / (BN / 4);
-                int nq = (e - krow * (BN / 4)) * 4;
+                const int e = tid + 256 * r;
+                const int krow = e / (BN / 4);
+                const int nq = (e - krow * (BN / 4)) * 4;
                 bs[(nq + 0) * LDK + krow] = breg[r][0];
                 bs[(nq + 1) * LDK + krow] = breg[r][1];
                 bs[(nq + 2) * LDK + krow] = breg[r][2];
@@ -300,8 +355,8 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(const GemmDev p) {
     for (int kt = 0; kt < nk; ++kt) {
         const int buf = kt & 1;
         if (kt + 1 < nk) load_stage(kt + 1);
-        const float *as = As[buf];
-        const float *bs = Bs[buf];
+        const float *as = As + buf * BM * LDK;
+        const float *bs = Bs + buf * BN * LDK;
         f4 af[RM][4], bf[RN][4];
 #pragma unroll
         for (int i = 0; i < RM; ++i)
@@ -316,61 +371,81 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(const GemmDev p) {
                 bf[j][s] = *reinterpret_cast<const f4 *>(
                     &bs[(wn * WN + j * 32 + li) * LDK + lh * 16 + 4 * s]);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
+        for (int s = 0; s < 4; ++s)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
+            for (int e = 0; e < 4; ++e)
 #pragma unroll
-                for (int i = 0; i < RM; ++i) {
+                for (int i = 0; i < RM; ++i)
 #pragma unroll
-                    for (int j = 0; j < RN; ++j) {
-                        const float av = af[i][s][e];
-                        const float bv = bf[j][s][e];
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc[i][j], 0, 0, 0);
-                    }
-                }
-            }
-        }
+                    for (int j = 0; j < RN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s][e], bf[j][s][e],
+                                                                          acc[i][j], 0, 0, 0);
         if (kt + 1 < nk) store_stage(buf ^ 1);
         __syncthreads();
     }
 
-    // ---- epilogue: block (i, j) register r holds row 8*(r/4) + 4*lh + r%4, column li -------
-    if (p.split > 1) {
-        float *ws = p.ws + (long)ks * p.M * p.N;
-#pragma unroll
-        for (int i = 0; i < RM; ++i)
-#pragma unroll
-            for (int j = 0; j < RN; ++j) {
-                const int col = n0 + wn * WN + j * 32 + li;
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int row = m0 + wm * WM + i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
-                    if (row < p.M && col < p.N) ws[(long)row * p.N + col] = acc[i][j][r];
-                }
-            }
-        return;
-    }
-    float *cbase = p.c + co;
-    const float *rbase = p.res ? p.res + ro : nullptr;
+    // ---- epilogue, pass 1: registers -> LDS tile. Block (i, j) register r holds tile row
+    // 8 * (r / 4) + 4 * lh + r % 4 and column li of that 32x32 block.
+    float *const Cs = smem;
 #pragma unroll
     for (int i = 0; i < RM; ++i)
 #pragma unroll
-        for (int j = 0; j < RN; ++j) {
-            const int col = n0 + wn * WN + j * 32 + li;
-            const bool col_ok = col < p.N;
-            const float cb = (p.bias && p.bias_mode == 1 && col_ok) ? p.bias[col] : 0.0f;
+        for (int j = 0; j < RN; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = m0 + wm * WM + i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
-                if (row < p.M && col_ok) {
-                    float v = p.alpha * acc[i][j][r];
-                    if (p.bias && p.bias_mode == 2) v += p.bias[row];
-                    v += cb;
-                    if (rbase) v += p.beta * rbase[(long)row * p.ldr + col];
-                    cbase[(long)row * p.ldc + col] = apply_act(v, p.act, p.lo, p.hi);
-                }
+            for (int r = 0; r < 16; ++r)
+                Cs[(wm * WM + i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3)) * LDC + wn * WN + j * 32 +
+                   li] = acc[i][j][r];
+    __syncthreads();
+
+    // ---- epilogue, pass 2: 16-byte chunks of the tile, compact loop ------------------------
+    constexpr int C4 = BN / 4;
+    const bool split_out = p.split > 1;
+    float *const cbase = split_out ? p.ws + (long)ks * p.M * p.N : p.c + co;
+    const long ldc = split_out ? (long)p.N : p.ldc;
+    const float *const rbase = (!split_out && p.res) ? p.res + ro : nullptr;
+    const bool vec = split_out ? (p.N % 4 == 0) : (p.vec_out != 0);
+#pragma unroll 1
+    for (int idx = tid; idx < BM * C4; idx += 256) {
+        const int rl = idx / C4;
+        const int cl = (idx - rl * C4) * 4;
+        const int row = m0 + rl, col = n0 + cl;
+        if (row >= p.M || col >= p.N) continue;
+        f4 v = *reinterpret_cast<const f4 *>(&Cs[rl * LDC + cl]);
+        const int ncol = min(4, p.N - col);
+        float *dst = cbase + (long)row * ldc + col;
+        if (split_out) {
+            if (vec && ncol == 4) {
+                *reinterpret_cast<f4 *>(dst) = v;
+            } else {
+                for (int e = 0; e < ncol; ++e) dst[e] = v[e];
+            }
+            continue;
+        }
+        v *= p.alpha;
+        if (p.bias) {
+            if (p.bias_mode == 2) {
+                v += p.bias[row];
+            } else if (vec && ncol == 4) {
+                v += *reinterpret_cast<const f4 *>(p.bias + col);
+            } else {
+                for (int e = 0; e < ncol; ++e) v[e] += p.bias[col + e];
             }
         }
+        if (rbase) {
+            const float *src = rbase + (long)row * p.ldr + col;
+            if (vec && ncol == 4) {
+                v += p.beta * *reinterpret_cast<const f4 *>(src);
+            } else {
+                for (int e = 0; e < ncol; ++e) v[e] += p.beta * src[e];
+            }
+        }
+        v = act4(v, p.act, p.lo, p.hi);
+        if (vec && ncol == 4) {
+            *reinterpret_cast<f4 *>(dst) = v;
+        } else {
+            for (int e = 0; e < ncol; ++e) dst[e] = v[e];
+        }
+    }
 }
 
 // Sum the split-K partials and apply the epilogue (one batch element).
@@ -494,6 +569,10 @@ extern "C" void mgc_hip_gemm(mgc_hip_exec *x, const mgc_hip_gemm_args *g) {
     else if (p.b.kind == MGC_OP_STRIDED && p.b.cs == 1 && p.b.rs % 4 == 0 && p.N % 4 == 0 &&
              aligned16(p.b.p) && bs_div4(p.b_bs, p.batch_rank))
         bm = BD_KN_VEC;
+
+    p.vec_out = p.ldc % 4 == 0 && aligned16(p.c) && bs_div4(p.c_bs, p.batch_rank) &&
+                (!p.res || (p.ldr % 4 == 0 && aligned16(p.res) && bs_div4(p.r_bs, p.batch_rank))) &&
+                (!p.bias || p.bias_mode != 1 || aligned16(p.bias));
 
     TileChoice t = choose_tiles(p.M, p.N, p.K, batch);
     if (t.split > 1 && (g->workspace == nullptr ||
