@@ -88,3 +88,44 @@ def check_hip(
         else:
             np.testing.assert_array_equal(got[name], value, err_msg=name)
     return got
+
+
+def named_graph(
+    nodes: list[tuple[str, list[str], list[str], dict[str, Any]]],
+    inputs: list[tuple[str, tuple[int, ...], str]],
+    outputs: list[str],
+    inits: list[tuple[str, np.ndarray]] = (),
+) -> Graph:
+    """A graph from name-wired nodes, like the reference tests' onnx.helper models: inputs are
+    (name, shape, dtype), inits become constants, an empty input name is an omitted input."""
+    g = Graph("t")
+    env: dict[str, Any] = {}
+    for name, array in inits:
+        env[name] = g.constant(np.asarray(array), name)
+    for name, shape, dtype in inputs:
+        env[name] = g.add_input(name, TensorType(dtype, tuple(shape)))
+    for op, ins, outs, attrs in nodes:
+        node = g.add_node(op, [env[n] if n else None for n in ins], len(outs), attrs, output_names=outs)
+        for n, v in zip(outs, node.outputs):
+            env[n] = v
+    for name in outputs:
+        g.add_output(env[name], name)
+    infer_shapes(g)
+    return g
+
+
+def same_numerics(make, passes: str, rtol: float = 1e-5, atol: float = 1e-5) -> Graph:
+    """Optimize a fresh graph from ``make()`` with ``passes`` and check the oracle agrees with
+    the unoptimized graph on seeded inputs; returns the optimized graph."""
+    from ml_graph_compiler.passes import optimize
+
+    reference = make()
+    feeds = oracle.random_feeds(reference, 3, int_high=20)
+    expected = oracle.run_graph(reference, feeds)
+    graph = make()
+    optimize(graph, passes)
+    got = oracle.run_graph(graph, feeds)
+    for name, value in expected.items():
+        assert got[name].shape == value.shape
+        np.testing.assert_allclose(got[name], value, rtol=rtol, atol=atol, err_msg=name)
+    return graph

@@ -1,0 +1,171 @@
+"""hip backend checks that need no GPU: code generation, the native builds, the exported C ABI,
+error behaviour, and the kernel mixes the reference reports for its configs."""
+
+from __future__ import annotations
+
+import re
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from ml_graph_compiler import builders
+from ml_graph_compiler.codegen import build as native
+from ml_graph_compiler.codegen.hip import HipEmitter, generate_hip, pack_b_nk
+from ml_graph_compiler.errors import CodegenError, ModelImportError
+from ml_graph_compiler.ir import Graph, TensorType
+from ml_graph_compiler.passes import optimize
+from ml_graph_compiler.schedule import schedule
+from helpers import f32, op_graph
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_functions(header: Path) -> set[str]:
+    text = header.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = set()
+    for m in re.finditer(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(mgc_\w+)\s*\(", text, flags=re.M):
+        names.add(m.group(1))
+    return names
+
+
+def exported(lib: Path) -> set[str]:
+    out = subprocess.run(["nm", "-D", "--defined-only", str(lib)], capture_output=True, text=True, check=True).stdout
+    return {line.split()[-1] for line in out.splitlines() if line.strip()}
+
+
+def o3(graph):
+    optimize(graph, "O3")
+    schedule(graph)
+    return graph
+
+
+def test_kernel_library_exports_every_declared_symbol():
+    lib = native.kernel_library_path()
+    declared = declared_functions(ROOT / "include" / "mgc_hip.h")
+    assert {"mgc_hip_gemm", "mgc_hip_model_run", "mgc_hip_elementwise"} <= declared
+    missing = declared - exported(lib)
+    assert not missing, missing
+    handle = native.load_kernel_library()
+    assert handle.mgc_hip_version().startswith(b"mgc_hip")
+    assert handle.mgc_hip_device_count() >= 0
+
+
+def test_model_library_exports_the_model_abi(hip_cache):
+    gen = generate_hip(o3(builders.mlp()), profile=True)
+    built = native.build_model_library(gen.source, cache_dir=hip_cache, name="abi")
+    declared = declared_functions(ROOT / "include" / "mgc_model.h")
+    assert {"mgc_run", "mgc_arena_bytes", "mgc_weights_bytes", "mgc_hip_init", "mgc_profile_data"} <= declared
+    missing = declared - exported(built.library)
+    assert not missing, missing
+    plain = native.build_model_library(generate_hip(o3(builders.mlp())).source, cache_dir=hip_cache, name="abi2")
+    assert "mgc_profile_data" not in exported(plain.library)
+    again = native.build_model_library(gen.source, cache_dir=hip_cache, name="abi")
+    assert again.cached
+
+
+@pytest.mark.parametrize(
+    "name, kernels, arena",
+    [
+        ("resnet50", {"gemm": 54, "pool": 1, "reduce": 1, "transpose": 1, "view": 1}, 7225344),
+        ("mobilenet_v2", {"depthwise": 17, "gemm": 36, "reduce": 1, "transpose": 1, "view": 1}, 6021120),
+        ("tiny-cnn", {"depthwise": 1, "gemm": 9, "pool": 1, "reduce": 1, "transpose": 1, "view": 1}, None),
+    ],
+)
+def test_kernel_mix_matches_reference(name, kernels, arena):
+    """Reference kernel mixes at O3: ResNet-50 gemm 54, pool 1, reduce 1, transpose 1, view 1;
+    MobileNetV2 gemm 36, depthwise 17 (benchmarks/results/ablation_cnn.json:759-830,1468-1540);
+    tiny-cnn gemm 9, depthwise 1 (tests/test_codegen.py:638-647)."""
+    make = builders.SAMPLES.get(name) or builders.CONFIGS[name]
+    gen = generate_hip(o3(make()))
+    assert gen.kernels == kernels
+    if arena is not None:
+        assert gen.arena_bytes == arena
+    assert gen.weights.nbytes % 256 == 0 and len(gen.weights.digest()) == 24
+    assert "mgc_forward" in gen.source and "int mgc_run(" in gen.source
+
+
+def test_every_sample_and_config_generates_and_builds(hip_cache):
+    for name, make in list(builders.SAMPLES.items()) + [("single_gemm", builders.single_gemm), ("bottleneck", builders.bottleneck)]:
+        for level in ("O0", "O3"):
+            g = make()
+            optimize(g, level)
+            schedule(g)
+            gen = generate_hip(g, gemm_workspace=native.gemm_workspace_floats)
+            native.build_model_library(gen.source, cache_dir=hip_cache, name="m")
+
+
+def test_split_k_workspace_is_planned():
+    g = o3(builders.single_gemm())
+    gen = generate_hip(g, gemm_workspace=native.gemm_workspace_floats)
+    assert native.gemm_workspace_floats(128, 3072, 768, 1) > 0
+    assert gen.plan.workspaces and "g.workspace = ((float *)(A + " in gen.source
+    assert gen.arena_bytes >= 4 * native.gemm_workspace_floats(128, 3072, 768, 1)
+
+
+def test_packed_weights_layout():
+    b = np.arange(5 * 14, dtype=np.float32).reshape(5, 14)
+    packed = pack_b_nk(b)
+    assert packed.shape == (14, 5) and packed.flags.c_contiguous
+    np.testing.assert_array_equal(packed, b.T)
+
+
+def test_unsupported_programs_raise():
+    g, _ = op_graph("Trilu", [f32(3, 3)])
+    with pytest.raises(CodegenError, match="Trilu"):
+        generate_hip(g)
+    g, _ = op_graph("Pad", [f32(2, 3), np.asarray([1, 1, 1, 1], np.int64)], const={1}, attrs={"mode": "reflect"})
+    with pytest.raises(CodegenError, match="reflect"):
+        generate_hip(g)
+    g, _ = op_graph("Sqrt", [np.ones((2,), np.int64)])
+    with pytest.raises(CodegenError, match="Sqrt on int64"):
+        generate_hip(g)
+    h = Graph()
+    x = h.add_input("h", TensorType("float16", (2,)))
+    node = h.add_node("Relu", [x])
+    node.output.type = TensorType("float16", (2,))
+    h.add_output(node.output)
+    with pytest.raises(CodegenError, match="float16"):
+        generate_hip(h)
+
+
+def test_hostile_names_cannot_escape_comments(hip_cache):
+    g = Graph("g */ int g_injected; /*")
+    x = g.add_input("x", TensorType("float32", (2, 3)))
+    node = g.add_node("Relu", [x], name="relu */ int injected = 1; /* \n#include <stdlib.h>\n")
+    node.output.type = TensorType("float32", (2, 3))
+    g.add_output(node.output, "y")
+    source = generate_hip(g).source
+    assert "*/ int injected" not in source and "*/ int g_injected" not in source
+    assert "\n#include <stdlib.h>" not in source
+    native.build_model_library(source, cache_dir=hip_cache, name="hostile")
+
+
+def test_build_errors_are_reported(hip_cache):
+    with pytest.raises(CodegenError, match="build failed"):
+        native.build_model_library("this is not C++", cache_dir=hip_cache, name="bad")
+
+
+def test_loading_without_a_gpu_fails_loudly(hip_cache):
+    if native.load_kernel_library().mgc_hip_device_count() > 0:
+        pytest.skip("a GPU is visible")
+    from ml_graph_compiler.codegen import compile_graph
+
+    with pytest.raises(CodegenError, match="no HIP device"):
+        compile_graph(o3(builders.mlp()), cache_dir=hip_cache)
+
+
+def test_other_backends_and_onnx_paths_are_rejected(hip_cache):
+    from ml_graph_compiler.codegen import compile_graph, compile_model
+
+    with pytest.raises(CodegenError, match="not part of this build"):
+        compile_graph(o3(builders.mlp()), cache_dir=hip_cache, backend="c")
+    with pytest.raises(ModelImportError):
+        compile_model("model.onnx")
+
+
+def test_depthwise_detection():
+    g = o3(builders.tiny_cnn())
+    assert sum(HipEmitter.depthwise(n) for n in g.nodes) == 1
