@@ -4,36 +4,73 @@
 // mgc_gemm (src/ml_graph_compiler/codegen/runtime/mgc_kernels.c:282-396), with operands read as
 // strided matrices or through implicit im2col of an NHWC (A) or NCHW (B) image.
 //
-// Design (MI355X-first, not a translation of the reference's Goto/BLIS CPU blocking):
-//  * A workgroup of 256 threads (4 waves of 64) owns a BM x BN output tile; each wave owns a
-//    WM x WN sub-tile made of 32x32 MFMA blocks, accumulated in 16 registers per block.
-//  * K advances 32 at a time through double-buffered LDS. Both operands are stored k-contiguous
-//    in LDS ([row][32 + 4 pad]) so every lane fetches its fragment with ds_read_b128.
-//  * The 32x32x2 MFMA consumes two k per instruction, one per half-wave. The kernel assigns the
-//    first 16 k of a stage to lanes 0-31 and the last 16 to lanes 32-63 (a permutation of the
-//    summation order, applied identically to A and B), so each lane's 16 k values are
-//    contiguous in LDS.
-//  * Global loads are float4 (16 B) when the operand is k-contiguous (packed weights, NHWC
-//    activations with channel counts divisible by 4) and branch-free (out-of-range lanes read
-//    a valid address and select zero). Implicit im2col computes the (kh, kw, c) split of a
-//    thread's k once per stage and reuses it for all of the thread's rows.
-//  * The epilogue stages the accumulator tile through LDS, then every thread walks the tile in
-//    16-byte chunks: coalesced float4 residual loads and stores, bias per float4, and one
-//    activation dispatch per chunk. This keeps the kernel's code small (an unrolled per-register
-//    epilogue would not fit the instruction cache) and its HBM traffic in full lines.
+// Three kernels share the MFMA core (MI355X-first, not a translation of the reference's
+// Goto/BLIS CPU blocking). A workgroup of 256 threads (4 waves of 64) owns a BM x BN output
+// tile; each wave owns a WM x WN sub-tile of 32x32 MFMA blocks (16 accumulators per block).
+// K advances 32 per stage; the 32x32x2 MFMA consumes two k per instruction, one per half-wave,
+// and the kernels give the first 16 k of a stage to lanes 0-31 and the last 16 to lanes 32-63
+// (a permutation of the summation order applied identically to A and B), so a lane's
+// operands are contiguous 16-byte LDS reads.
+//
+//  * gemm_dma_kernel / gemm_stream_kernel (k-contiguous operands: packed weights, NHWC
+//    activations, row-major matrices — every convolution and linear layer). Tiles travel
+//    from HBM to LDS with buffer_load_dwordx4 ... lds (no register staging) through a ring of
+//    stages; masked elements use an offset past the end of the buffer resource, which the
+//    hardware reads as zero. The LDS row layout is fixed by the DMA (a wave's 64 lanes write
+//    1 KB of consecutive LDS), so bank spreading comes from which k-chunk each lane fetches
+//    (an XOR swizzle). Barriers wait only for LDS traffic, so the loads of later stages stay
+//    in flight. Implicit-im2col offsets are advanced incrementally and divisions by shape
+//    constants use host-computed magic numbers.
+//    gemm_stream_kernel is persistent: each workgroup walks a list of tiles and its operand
+//    pipeline runs across tile boundaries, so small-K GEMMs (1x1 convolutions over large
+//    images) overlap the next tile's loads with the current tile's epilogue, which writes
+//    16-byte chunks straight from the accumulators.
+//  * gemm_mfma_kernel: every other operand form (transposed or strided A, NCHW im2col B,
+//    dynamic k-major B), staged through registers into double-buffered LDS.
 //  * The workgroup id is remapped so each of the 8 XCDs (each with its own L2) works on a
 //    contiguous range of tiles, N fastest: tiles that share A rows share an L2.
-//  * Small-M problems (the 128-row GEMM of the single-GEMM config) split K over extra
-//    workgroups into a planner-provided workspace, then a reduction applies the epilogue.
+//  * Few-tile problems split K over extra workgroups into a planner-provided workspace, then
+//    a reduction applies the epilogue.
 #include "mgc_device.h"
 
 namespace mgc {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef unsigned uint4_t __attribute__((ext_vector_type(4)));
 
 enum { AM_VEC = 0, AM_CONV_VEC = 1, AM_GEN = 2 };
+
+// 16 zero bytes: the load address of every out-of-range operand element.
+__device__ __attribute__((aligned(16))) float g_zero_page[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+
+// Loads through the global address space. Every operand lives in device memory; saying so
+// keeps the compiler from falling back to flat loads, which share a wait counter with LDS.
+typedef const __attribute__((address_space(1))) float gfloat;
+typedef const __attribute__((address_space(1))) f4 gf4;
+__device__ __forceinline__ float ldg(const float *ptr) { return *(gfloat *)ptr; }
+__device__ __forceinline__ f4 ldg4(const float *ptr) { return *(gf4 *)ptr; }
 enum { BD_NK_VEC = 0, BD_KN_VEC = 1, BD_GEN = 2 };
+
+// Division by a launch-constant divisor d (1 <= d < 2^31) for numerators 0 <= n < 2^31:
+// q = (umulhi(n, m) + n) >> s with s = ceil(log2 d), m = floor(2^32 (2^s - d) / d) + 1
+// (Granlund and Montgomery, "Division by invariant integers using multiplication", 1994).
+struct FastDiv {
+    unsigned d, m, s;
+};
+
+static FastDiv make_fastdiv(unsigned d) {
+    FastDiv f;
+    f.d = d ? d : 1;
+    f.s = 0;
+    while ((1u << f.s) < f.d) ++f.s;
+    f.m = (unsigned)((((unsigned long long)1 << 32) * (((unsigned long long)1 << f.s) - f.d)) / f.d + 1);
+    return f;
+}
+
+__device__ __forceinline__ int fdiv(int n, const FastDiv &f) {
+    return (int)((__umulhi((unsigned)n, f.m) + (unsigned)n) >> f.s);
+}
 
 struct GemmDev {
     int M, N, K;
@@ -54,7 +91,11 @@ struct GemmDev {
     int kchunk;   // K per split, a multiple of 32
     float *ws;    // split partials [split][M][N]
     int tiles_m, tiles_n;
-    int vec_out;  // 16-byte epilogue accesses are aligned (ldc, ldr, pointers)
+    int vec_out;
+    FastDiv div_ow, div_ohw, div_cg, div_kw;  // A as NHWC image: OW, OH * OW, cg, KW
+    long a_bytes, b_bytes;  // bytes of A and B reachable from a.p / b.p (all batch elements)
+    long c_bytes, r_bytes, ws_bytes;  // and of C, the residual and the split-K workspace
+    int nbatch;                       // batch elements  // 16-byte epilogue accesses are aligned (ldc, ldr, pointers)
 };
 
 __device__ __forceinline__ void batch_offsets(const GemmDev &p, int bz, long &ao, long &bo,
@@ -106,6 +147,116 @@ __device__ __forceinline__ f4 act4(f4 v, int act, float lo, float hi) {
     }
 }
 
+// Epilogue shared by the GEMM kernels: the accumulator tile goes through LDS (smem, at least
+// BM * (BN + 8) floats, free when this is called) and leaves as 16-byte chunks with alpha, bias,
+// residual and activation applied, or raw into the split-K workspace.
+// Pass 2 gives each thread one fixed 16-byte column chunk of the tile and the rows
+// r0, r0 + RSTEP, ..., so the column bias is read once per thread.
+template <int BM, int BN, int WGM, int RM, int RN>
+__device__ __forceinline__ void gemm_store_tile(const GemmDev &p, float *smem,
+                                                     const floatx16 (&acc)[RM][RN], int m0, int n0,
+                                                     int ks, long co, long ro) {
+    constexpr int WGN = 4 / WGM;
+    constexpr int WM = BM / WGM;
+    constexpr int WN = BN / WGN;
+    constexpr int LDC = BN + 8;
+    const f4 zero4 = {0.f, 0.f, 0.f, 0.f};
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave / WGN, wn = wave - (wave / WGN) * WGN;
+    const int li = lane & 31;
+    const int lh = lane >> 5;
+    constexpr int C4 = BN / 4;
+    static_assert(256 % C4 == 0, "column chunks must divide the workgroup");
+    constexpr int RSTEP = 256 / C4;
+    constexpr int ITERS = BM / RSTEP;
+    constexpr int G = ITERS < 4 ? ITERS : 4;
+    // Scalars read once: keeps the compiler from copying the argument block to scratch.
+    const float alpha = p.alpha, beta = p.beta, lo = p.lo, hi = p.hi;
+    const float *const bias = p.bias;
+    const int act = p.act, M = p.M, N = p.N;
+    const bool split_out = p.split > 1;
+    float *const cbase = split_out ? p.ws + (long)ks * M * N : p.c + co;
+    const long ldc = split_out ? (long)N : p.ldc;
+    const float *const rbase = (!split_out && p.res) ? p.res + ro : nullptr;
+    const bool vec = split_out ? (N % 4 == 0) : (p.vec_out != 0);
+    const int cl = (tid % C4) * 4;
+    const int col = n0 + cl;
+    const int r0 = tid / C4;
+    const bool col_ok = col < N;
+    const int ncol = col_ok ? min(4, N - col) : 0;
+    const bool full4 = vec && ncol == 4;
+    const int bmode = split_out ? 0 : p.bias_mode;
+    f4 cbias = zero4;
+    if (bmode == 1 && col_ok) {
+        if (full4) {
+            cbias = ldg4(bias + col);
+        } else {
+            for (int e = 0; e < ncol; ++e) cbias[e] = ldg(bias + col + e);
+        }
+    }
+    // pass 1: registers -> LDS tile. Block (i, j) register r holds tile row
+    // 8 * (r / 4) + 4 * lh + r % 4 and column li of that 32x32 block.
+    float *const Cs = smem;
+#pragma unroll
+    for (int i = 0; i < RM; ++i)
+#pragma unroll
+        for (int j = 0; j < RN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                Cs[(wm * WM + i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3)) * LDC + wn * WN + j * 32 +
+                   li] = acc[i][j][r];
+    __syncthreads();
+
+    // pass 2: LDS tile -> epilogue -> memory, 16 bytes per access, G rows per step with their
+    // residual chunks (and row biases) requested together.
+    if (!col_ok) return;
+    const bool pre_res = rbase != nullptr && full4;
+#pragma unroll 1
+    for (int g = 0; g < ITERS; g += G) {
+        f4 rv[G];
+        float rb[G];
+#pragma unroll
+        for (int u = 0; u < G; ++u) {
+            const int row = m0 + r0 + RSTEP * (g + u);
+            const bool ok = row < M;
+            rv[u] = zero4;
+            rb[u] = 0.0f;
+            if (pre_res)
+                rv[u] = ldg4(ok ? rbase + (long)row * p.ldr + col
+                                                         : g_zero_page);
+            if (bmode == 2) rb[u] = ldg(ok ? bias + row : g_zero_page);
+        }
+#pragma unroll
+        for (int u = 0; u < G; ++u) {
+            const int rl = r0 + RSTEP * (g + u);
+            const int row = m0 + rl;
+            if (row >= M) break;
+            f4 v = *reinterpret_cast<const f4 *>(&Cs[rl * LDC + cl]);
+            float *dst = cbase + (long)row * ldc + col;
+            if (!split_out) {
+                v = v * alpha + cbias;
+                if (bmode == 2) v += rb[u];
+                if (pre_res) {
+                    v += beta * rv[u];
+                } else if (rbase) {
+                    const float *src = rbase + (long)row * p.ldr + col;
+                    for (int e = 0; e < ncol; ++e) v[e] += beta * ldg(src + e);
+                }
+                v = act4(v, act, lo, hi);
+            }
+            if (full4) {
+                *reinterpret_cast<f4 *>(dst) = v;
+            } else {
+                for (int e = 0; e < ncol; ++e) dst[e] = v[e];
+            }
+        }
+    }
+}
+
+
+
 template <int BM, int BN, int WGM, int AMODE, int BMODE>
 __global__ void __launch_bounds__(256) gemm_mfma_kernel(const GemmDev p) {
     constexpr int BK = 32;
@@ -120,7 +271,7 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(const GemmDev p) {
     constexpr int AG = BM / 8;   // scalar loads per thread per stage (generic A)
     constexpr int BV = BN / 32;
     constexpr int BG = BN / 8;
-    constexpr int LDC = BN + 4;
+    constexpr int LDC = BN + 8;
     constexpr int SMEM_LOOP = 2 * (BM + BN) * LDK;
     constexpr int SMEM_EPI = BM * LDC;
     constexpr int SMEM = SMEM_LOOP > SMEM_EPI ? SMEM_LOOP : SMEM_EPI;
@@ -199,8 +350,11 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(const GemmDev p) {
     f4 breg[BMODE == BD_GEN ? 1 : BV];
     float bgen[BMODE == BD_GEN ? BG : 1];
     const f4 zero4 = {0.f, 0.f, 0.f, 0.f};
-    const float *const asafe = p.a.p;
-    const float *const bsafe = p.b.p;
+    // Out-of-range elements load from a zero page instead of being masked after the load: a
+    // select on the loaded value would make the wave wait for the load right where it is
+    // issued instead of where the value is consumed, one pipeline stage later.
+    const float *const asafe = g_zero_page;
+    const float *const bsafe = g_zero_page;
 
     auto load_stage = [&](int kt) __attribute__((always_inline)) {
         const int k0 = kbeg + kt * BK;
@@ -210,8 +364,7 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(const GemmDev p) {
 #pragma unroll
             for (int r = 0; r < AV; ++r) {
                 const bool ok = kok && arow[r] != nullptr;
-                f4 v = *reinterpret_cast<const f4 *>(ok ? arow[r] + k : asafe);
-                areg[r] = ok ? v : zero4;
+                areg[r] = ldg4(ok ? arow[r] + k : asafe);
             }
         } else if constexpr (AMODE == AM_CONV_VEC) {
             const int k = k0 + kq;
@@ -225,9 +378,7 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(const GemmDev p) {
                 const int ih = aih[r] + dh, iw = aiw[r] + dw;
                 const bool ok = kok && arow[r] != nullptr && (unsigned)ih < (unsigned)p.a.H &&
                                 (unsigned)iw < (unsigned)p.a.W;
-                f4 v = *reinterpret_cast<const f4 *>(
-                    ok ? arow[r] + ((long)ih * p.a.W + iw) * p.a.C + c : asafe);
-                areg[r] = ok ? v : zero4;
+                areg[r] = ldg4(ok ? arow[r] + ((long)ih * p.a.W + iw) * p.a.C + c : asafe);
             }
         } else {
             const int k = k0 + kg;
@@ -242,15 +393,13 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(const GemmDev p) {
                     const int ih = aih[r] + dh, iw = aiw[r] + dw;
                     const bool ok = kok && arow[r] != nullptr && (unsigned)ih < (unsigned)p.a.H &&
                                     (unsigned)iw < (unsigned)p.a.W;
-                    float v = *(ok ? arow[r] + ((long)ih * p.a.W + iw) * p.a.C + c : asafe);
-                    agen[r] = ok ? v : 0.0f;
+                    agen[r] = ldg(ok ? arow[r] + ((long)ih * p.a.W + iw) * p.a.C + c : asafe);
                 }
             } else {
 #pragma unroll
                 for (int r = 0; r < AG; ++r) {
                     const bool ok = kok && arow[r] != nullptr;
-                    float v = *(ok ? arow[r] + (long)k * p.a.cs : asafe);
-                    agen[r] = ok ? v : 0.0f;
+                    agen[r] = ldg(ok ? arow[r] + (long)k * p.a.cs : asafe);
                 }
             }
         }
@@ -260,8 +409,7 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(const GemmDev p) {
 #pragma unroll
             for (int r = 0; r < BV; ++r) {
                 const bool ok = kok && brow[r] != nullptr;
-                f4 v = *reinterpret_cast<const f4 *>(ok ? brow[r] + k : bsafe);
-                breg[r] = ok ? v : zero4;
+                breg[r] = ldg4(ok ? brow[r] + k : bsafe);
             }
         } else if constexpr (BMODE == BD_KN_VEC) {
 #pragma unroll
@@ -271,8 +419,7 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(const GemmDev p) {
                 const int nq = (e - krow * (BN / 4)) * 4;
                 const int k = k0 + krow, n = n0 + nq;
                 const bool ok = k < kend && n < p.N;
-                f4 v = *reinterpret_cast<const f4 *>(ok ? bbase + (long)k * p.b.rs + n : bsafe);
-                breg[r] = ok ? v : zero4;
+                breg[r] = ldg4(ok ? bbase + (long)k * p.b.rs + n : bsafe);
             }
         } else {
             const int k = k0 + kg;
@@ -289,16 +436,14 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(const GemmDev p) {
                     const int ih = oh * o.SH - o.PT + kh * o.DH, iw = ow * o.SW - o.PL + kw * o.DW;
                     const bool ok = kok && n < p.N && (unsigned)ih < (unsigned)o.H &&
                                     (unsigned)iw < (unsigned)o.W;
-                    float v = *(ok ? plane + (long)ih * o.W + iw : bsafe);
-                    bgen[r] = ok ? v : 0.0f;
+                    bgen[r] = ldg(ok ? plane + (long)ih * o.W + iw : bsafe);
                 }
             } else {
 #pragma unroll
                 for (int r = 0; r < BG; ++r) {
                     const int n = n0 + (tid >> 5) + 8 * r;
                     const bool ok = kok && n < p.N;
-                    float v = *(ok ? bbase + (long)k * p.b.rs + (long)n * p.b.cs : bsafe);
-                    bgen[r] = ok ? v : 0.0f;
+                    bgen[r] = ldg(ok ? bbase + (long)k * p.b.rs + (long)n * p.b.cs : bsafe);
                 }
             }
         }
@@ -384,66 +529,553 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(const GemmDev p) {
         __syncthreads();
     }
 
-    // ---- epilogue, pass 1: registers -> LDS tile. Block (i, j) register r holds tile row
-    // 8 * (r / 4) + 4 * lh + r % 4 and column li of that 32x32 block.
-    float *const Cs = smem;
+    gemm_store_tile<BM, BN, WGM>(p, smem, acc, m0, n0, ks, co, ro);
+}
+
+// s_waitcnt with only the vector-memory counter constrained (expcnt and lgkmcnt at maximum).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
+}
+
+// Workgroup barrier for the LDS ring: waits for this wave's own LDS accesses only. The
+// __syncthreads() fence would also wait for every outstanding global load, including the
+// DMA loads of later pipeline stages, and drain the ring at every step.
+__device__ __forceinline__ void barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// 16 bytes at byte offset voff of a buffer resource straight into LDS (lane l of the wave
+// writes lds_base + 16 * l); offsets at or past the resource's size read as zeros.
+__device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t r, unsigned voff, float *lds_base) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds_base, 16, (int)voff, 0, 0, 0);
+}
+
+
+// GEMM / implicit-GEMM convolution for k-contiguous operands (A: strided with unit column
+// stride, or an NHWC image with channel groups divisible by 4; B: packed [N][K]).
+//  * Operand tiles travel global -> LDS with global_load_lds_dwordx4 (no register staging)
+//    through a STAGES-deep ring, so loads for stage kt + STAGES - 1 are in flight while stage kt
+//    is multiplied; one barrier per stage.
+//  * Each stage stores a BM x 32 (and BN x 32) float block as rows of eight 16-byte chunks.
+//    The DMA writes a wave's 64 lanes to 1 KB of consecutive LDS, so the row layout is fixed
+//    by the lane order; the bank spread comes from which chunk a lane fetches: lane l loads
+//    k-chunk (l & 7) ^ (l >> 3) of row l >> 3 of its 8-row group, i.e. LDS position p of row r
+//    holds k-chunk p ^ (r & 7). The fragment reads undo that XOR, and eight lanes reading the
+//    same k-chunk of eight consecutive rows hit eight different positions.
+template <int BM, int BN, int WGM, int STAGES, int AMODE>
+__global__ void __launch_bounds__(256) gemm_dma_kernel(const GemmDev p) {
+    constexpr int BK = 32;
+    constexpr int WGN = 4 / WGM;
+    constexpr int WM = BM / WGM;
+    constexpr int WN = BN / WGN;
+    constexpr int RM = WM / 32;
+    constexpr int RN = WN / 32;
+    static_assert(RM >= 1 && RN >= 1 && WGM * WGN == 4, "bad tile");
+    static_assert(STAGES >= 2 && STAGES <= 4, "stages");
+    constexpr int AI = BM / 32;  // DMA instructions per wave per stage, A block
+    constexpr int BI = BN / 32;  // and B block
+    constexpr int STAGE = (BM + BN) * BK;
+    constexpr int SMEM_LOOP = STAGES * STAGE;
+    constexpr int SMEM_EPI = BM * (BN + 8);
+    constexpr int SMEM = SMEM_LOOP > SMEM_EPI ? SMEM_LOOP : SMEM_EPI;
+    static_assert(AMODE == AM_VEC || AMODE == AM_CONV_VEC, "vector A only");
+
+    __shared__ __attribute__((aligned(16))) float smem[SMEM];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WGN, wn = wave - (wave / WGN) * WGN;
+
+    const int nb = gridDim.x;
+    const int full = nb & ~7;
+    int lin = blockIdx.x;
+    if (lin < full) {
+        const int per = full >> 3;
+        lin = (lin & 7) * per + (lin >> 3);
+    }
+    const int tm = lin / p.tiles_n;
+    const int tn = lin - tm * p.tiles_n;
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    const int bz = blockIdx.z / p.split;
+    const int ks = blockIdx.z - bz * p.split;
+    long ao, bo, co, ro;
+    batch_offsets(p, bz, ao, bo, co, ro);
+    const float *abase = p.a.p + ao;
+    const float *bbase = p.b.p + bo;
+    const int kbeg = ks * p.kchunk;
+    const int kend = min(p.K, kbeg + p.kchunk);
+    const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+
+    // ---- DMA source state: row (i * 4 + wave) * 8 + (lane >> 3) of each block --------------
+    // Row r keeps k-chunk q at position q ^ f(r) with f(r) = (r & 7) ^ ((r >> 3) & 1): distinct
+    // over any 8 consecutive rows and over the 8 even (or odd) rows of any aligned 16, so
+    // 16-byte reads of one chunk from 8 or 16 consecutive rows spread over all banks.
+    const int q4 = ((lane & 7) ^ (lane >> 3) ^ (wave & 1)) * 4;  // this lane's k offset
+    const int rsub = lane >> 3;
+    // Operands are read through buffer resources: a masked lane gets an offset past the end of
+    // the resource and the hardware returns zeros for it, so no zero page, no select after
+    // the load and 32-bit offsets instead of 64-bit addresses.
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)abase, (short)0, (int)(p.a_bytes - ao * 4), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)bbase, (short)0, (int)(p.b_bytes - bo * 4), 0x00020000);
+    constexpr unsigned OOB = 0x80000000u;  // past every resource's end (extents are < 2^31 bytes)
+    unsigned aoff[AI];  // byte offset of the row (AM_VEC) or of its window origin (AM_CONV_VEC)
+    int aih[AI], aiw[AI];
+    const int ohw = p.a.OH * p.a.OW;
+#pragma unroll
+    for (int i = 0; i < AI; ++i) {
+        const int m = m0 + (i * 4 + wave) * 8 + rsub;
+        aoff[i] = OOB;
+        aih[i] = aiw[i] = -0x40000000;  // fails the window bounds test
+        if (m < p.M) {
+            if (AMODE == AM_CONV_VEC) {
+                const int n = fdiv(m, p.div_ohw), rr = m - n * ohw;
+                const int oh = fdiv(rr, p.div_ow), ow = rr - oh * p.a.OW;
+                aih[i] = oh * p.a.SH - p.a.PT;
+                aiw[i] = ow * p.a.SW - p.a.PL;
+                aoff[i] = (unsigned)(((n * p.a.H + aih[i]) * p.a.W + aiw[i]) * p.a.C) * 4u;
+            } else {
+                aoff[i] = (unsigned)m * (unsigned)p.a.rs * 4u;
+            }
+        }
+    }
+    unsigned boff[BI];
+#pragma unroll
+    for (int i = 0; i < BI; ++i) {
+        const int n = n0 + (i * 4 + wave) * 8 + rsub;
+        boff[i] = n < p.N ? (unsigned)n * (unsigned)p.b.cs * 4u : OOB;
+    }
+    // The lane's next k and, for an image, its (kh, kw, c) split, advanced one stage per issue.
+    int knext = kbeg + q4;
+    int cc = 0, ckw = 0, ckh = 0;
+    if (AMODE == AM_CONV_VEC) {
+        const int t = fdiv(knext, p.div_cg);
+        cc = knext - t * p.a.cg;
+        ckh = fdiv(t, p.div_kw);
+        ckw = t - ckh * p.a.KW;
+    }
+
+    auto issue = [&](int buf) __attribute__((always_inline)) {
+        const int k = knext;
+        const bool kok = k < kend;
+        float *sa = smem + buf * STAGE;
+        float *sb = sa + BM * BK;
+        if constexpr (AMODE == AM_VEC) {
+#pragma unroll
+            for (int i = 0; i < AI; ++i)
+                dma16_buf(ra, kok ? aoff[i] + (unsigned)k * 4u : OOB, sa + (i * 4 + wave) * 8 * BK);
+        } else {
+            const int dh = ckh * p.a.DH, dw = ckw * p.a.DW;
+            const unsigned koff = (unsigned)((dh * p.a.W + dw) * p.a.C + cc) * 4u;
+#pragma unroll
+            for (int i = 0; i < AI; ++i) {
+                const bool ok = kok && (unsigned)(aih[i] + dh) < (unsigned)p.a.H &&
+                                (unsigned)(aiw[i] + dw) < (unsigned)p.a.W;
+                dma16_buf(ra, ok ? aoff[i] + koff : OOB, sa + (i * 4 + wave) * 8 * BK);
+            }
+            cc += BK;
+            while (cc >= p.a.cg) {
+                cc -= p.a.cg;
+                if (++ckw == p.a.KW) {
+                    ckw = 0;
+                    ++ckh;
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < BI; ++i)
+            dma16_buf(rb, kok ? boff[i] + (unsigned)k * 4u : OOB, sb + (i * 4 + wave) * 8 * BK);
+        knext = k + BK;
+    };
+
+    floatx16 acc[RM][RN];
 #pragma unroll
     for (int i = 0; i < RM; ++i)
 #pragma unroll
         for (int j = 0; j < RN; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                Cs[(wm * WM + i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3)) * LDC + wn * WN + j * 32 +
-                   li] = acc[i][j][r];
-    __syncthreads();
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    // ---- epilogue, pass 2: 16-byte chunks of the tile, compact loop ------------------------
-    constexpr int C4 = BN / 4;
-    const bool split_out = p.split > 1;
-    float *const cbase = split_out ? p.ws + (long)ks * p.M * p.N : p.c + co;
-    const long ldc = split_out ? (long)p.N : p.ldc;
-    const float *const rbase = (!split_out && p.res) ? p.res + ro : nullptr;
-    const bool vec = split_out ? (p.N % 4 == 0) : (p.vec_out != 0);
-#pragma unroll 1
-    for (int idx = tid; idx < BM * C4; idx += 256) {
-        const int rl = idx / C4;
-        const int cl = (idx - rl * C4) * 4;
-        const int row = m0 + rl, col = n0 + cl;
-        if (row >= p.M || col >= p.N) continue;
-        f4 v = *reinterpret_cast<const f4 *>(&Cs[rl * LDC + cl]);
-        const int ncol = min(4, p.N - col);
-        float *dst = cbase + (long)row * ldc + col;
-        if (split_out) {
-            if (vec && ncol == 4) {
-                *reinterpret_cast<f4 *>(dst) = v;
-            } else {
-                for (int e = 0; e < ncol; ++e) dst[e] = v[e];
-            }
-            continue;
-        }
-        v *= p.alpha;
-        if (p.bias) {
-            if (p.bias_mode == 2) {
-                v += p.bias[row];
-            } else if (vec && ncol == 4) {
-                v += *reinterpret_cast<const f4 *>(p.bias + col);
-            } else {
-                for (int e = 0; e < ncol; ++e) v[e] += p.bias[col + e];
-            }
-        }
-        if (rbase) {
-            const float *src = rbase + (long)row * p.ldr + col;
-            if (vec && ncol == 4) {
-                v += p.beta * *reinterpret_cast<const f4 *>(src);
-            } else {
-                for (int e = 0; e < ncol; ++e) v[e] += p.beta * src[e];
-            }
-        }
-        v = act4(v, p.act, p.lo, p.hi);
-        if (vec && ncol == 4) {
-            *reinterpret_cast<f4 *>(dst) = v;
+    const int li = lane & 31;
+    const int lh = lane >> 5;
+    const int sw = (li & 7) ^ ((li >> 3) & 1);  // f(row): fragment rows start at multiples of 32
+
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s)
+        if (s < nk) issue(s);
+
+    constexpr int PER_STAGE = AI + BI;
+    for (int kt = 0; kt < nk; ++kt) {
+        // Stage kt has landed once at most the later stages' loads are outstanding.
+        const int ahead = min(nk - 1 - kt, STAGES - 2);
+        if (STAGES >= 4 && ahead >= 2) {
+            wait_vmcnt<(STAGES >= 4 ? 2 : 0) * PER_STAGE>();
+        } else if (STAGES >= 3 && ahead >= 1) {
+            wait_vmcnt<PER_STAGE>();
         } else {
-            for (int e = 0; e < ncol; ++e) dst[e] = v[e];
+            wait_vmcnt<0>();
+        }
+        barrier_lds();
+        if (kt + STAGES - 1 < nk) issue((kt + STAGES - 1) % STAGES);
+        const float *as = smem + (kt % STAGES) * STAGE;
+        const float *bs = as + BM * BK;
+        f4 af[RM][4], bf[RN][4];
+#pragma unroll
+        for (int i = 0; i < RM; ++i)
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                af[i][s] = *reinterpret_cast<const f4 *>(
+                    &as[(wm * WM + i * 32 + li) * BK + (((lh * 4 + s) ^ sw) << 2)]);
+#pragma unroll
+        for (int j = 0; j < RN; ++j)
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                bf[j][s] = *reinterpret_cast<const f4 *>(
+                    &bs[(wn * WN + j * 32 + li) * BK + (((lh * 4 + s) ^ sw) << 2)]);
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int i = 0; i < RM; ++i)
+#pragma unroll
+                    for (int j = 0; j < RN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s][e], bf[j][s][e],
+                                                                          acc[i][j], 0, 0, 0);
+    }
+    __syncthreads();
+    gemm_store_tile<BM, BN, WGM>(p, smem, acc, m0, n0, ks, co, ro);
+}
+
+// ------------------------------------------------------------------------------------------
+// Persistent streaming GEMM for k-contiguous operands (the hot path: convolutions, linear
+// layers). Each workgroup walks a list of output tiles; the operand pipeline (buffer -> LDS
+// DMA through a STAGES-deep ring, swizzled as in gemm_dma_kernel) runs continuously across
+// tile boundaries, so the next tile's first stages load while the current tile's epilogue
+// runs. The epilogue works straight from the accumulators (no LDS round trip) with buffer
+// stores whose out-of-range offsets are dropped by the hardware.
+// ------------------------------------------------------------------------------------------
+struct TileWork {
+    int m0, n0, kbeg, kend, nk;
+    long ao, bo, co, ro;
+    int ks;
+};
+
+__device__ __forceinline__ void decode_work(const GemmDev &p, int w, int BM_, int BN_, int BK_,
+                                            TileWork &o) {
+    const int tiles = p.tiles_m * p.tiles_n;
+    const int slice = w / tiles;
+    const int t = w - slice * tiles;
+    const int tm = t / p.tiles_n;
+    const int tn = t - tm * p.tiles_n;
+    const int bz = slice / p.split;
+    o.ks = slice - bz * p.split;
+    o.m0 = tm * BM_;
+    o.n0 = tn * BN_;
+    o.kbeg = o.ks * p.kchunk;
+    o.kend = min(p.K, o.kbeg + p.kchunk);
+    o.nk = o.kend > o.kbeg ? (o.kend - o.kbeg + BK_ - 1) / BK_ : 0;
+    batch_offsets(p, bz, o.ao, o.bo, o.co, o.ro);
+}
+
+template <int BM, int BN, int WGM, int STAGES, int AMODE, bool GEN_ACT>
+__global__ void __launch_bounds__(256) gemm_stream_kernel(const GemmDev p) {
+    constexpr int BK = 32;
+    constexpr int WGN = 4 / WGM;
+    constexpr int WM = BM / WGM;
+    constexpr int WN = BN / WGN;
+    constexpr int RM = WM / 32;
+    constexpr int RN = WN / 32;
+    static_assert(RM >= 1 && RN >= 1 && WGM * WGN == 4, "bad tile");
+    static_assert(STAGES >= 2 && STAGES <= 4, "stages");
+    static_assert(AMODE == AM_VEC || AMODE == AM_CONV_VEC, "vector A only");
+    constexpr int AI = BM / 32;
+    constexpr int BI = BN / 32;
+    constexpr int STAGE = (BM + BN) * BK;
+    constexpr int PER_STAGE = AI + BI;
+    constexpr unsigned OOB = 0x80000000u;
+
+    __shared__ __attribute__((aligned(16))) float smem[STAGES * STAGE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WGN, wn = wave - (wave / WGN) * WGN;
+    const int li = lane & 31;
+    const int lh = lane >> 5;
+
+    const int total = p.tiles_m * p.tiles_n * p.nbatch * p.split;
+    const int G = gridDim.x;
+    // Work item j of this workgroup is first + j * G. Workgroup ids are dealt round-robin to the
+    // 8 XCDs; XCD x takes the contiguous range [x * G / 8, (x + 1) * G / 8) of every round, so
+    // tiles that share rows of A share an L2.
+    int first = blockIdx.x;
+    if ((G & 7) == 0) first = (first & 7) * (G >> 3) + (first >> 3);
+    if (first >= total) return;
+
+    // ---- loader state (the work item whose stages are being fetched) ----------------------
+    const int q4 = ((lane & 7) ^ (lane >> 3) ^ (wave & 1)) * 4;
+    const int rsub = lane >> 3;
+    const int ohw = p.a.OH * p.a.OW;
+    int lw = first;
+    TileWork L;
+    decode_work(p, lw, BM, BN, BK, L);
+    int lkt = 0;
+    bool loading = true;
+    __amdgpu_buffer_rsrc_t ra, rb;
+    unsigned aoff[AI], boff[BI];
+    int aih[AI], aiw[AI];
+    int knext = 0, cc = 0, ckw = 0, ckh = 0;
+
+    auto setup_load = [&]() __attribute__((always_inline)) {
+        ra = __builtin_amdgcn_make_buffer_rsrc((void *)(p.a.p + L.ao), (short)0,
+                                               (int)(p.a_bytes - L.ao * 4), 0x00020000);
+        rb = __builtin_amdgcn_make_buffer_rsrc((void *)(p.b.p + L.bo), (short)0,
+                                               (int)(p.b_bytes - L.bo * 4), 0x00020000);
+#pragma unroll
+        for (int i = 0; i < AI; ++i) {
+            const int m = L.m0 + (i * 4 + wave) * 8 + rsub;
+            aoff[i] = OOB;
+            aih[i] = aiw[i] = -0x40000000;
+            if (m < p.M) {
+                if (AMODE == AM_CONV_VEC) {
+                    const int n = fdiv(m, p.div_ohw), rr = m - n * ohw;
+                    const int oh = fdiv(rr, p.div_ow), ow = rr - oh * p.a.OW;
+                    aih[i] = oh * p.a.SH - p.a.PT;
+                    aiw[i] = ow * p.a.SW - p.a.PL;
+                    aoff[i] = (unsigned)(((n * p.a.H + aih[i]) * p.a.W + aiw[i]) * p.a.C) * 4u;
+                } else {
+                    aoff[i] = (unsigned)m * (unsigned)p.a.rs * 4u;
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < BI; ++i) {
+            const int n = L.n0 + (i * 4 + wave) * 8 + rsub;
+            boff[i] = n < p.N ? (unsigned)n * (unsigned)p.b.cs * 4u : OOB;
+        }
+        knext = L.kbeg + q4;
+        if (AMODE == AM_CONV_VEC) {
+            const int t = fdiv(knext, p.div_cg);
+            cc = knext - t * p.a.cg;
+            ckh = fdiv(t, p.div_kw);
+            ckw = t - ckh * p.a.KW;
+        }
+    };
+    // Move the loader to the next work item that has stages (or stop).
+    auto next_load_item = [&]() __attribute__((always_inline)) {
+        do {
+            lw += G;
+            if (lw >= total) {
+                loading = false;
+                return;
+            }
+            decode_work(p, lw, BM, BN, BK, L);
+        } while (L.nk == 0);
+        lkt = 0;
+        setup_load();
+    };
+    if (L.nk == 0) {
+        next_load_item();
+    } else {
+        setup_load();
+    }
+
+    auto issue = [&](int buf) __attribute__((always_inline)) {
+        const int k = knext;
+        const bool kok = k < L.kend;
+        float *sa = smem + buf * STAGE;
+        float *sb = sa + BM * BK;
+        if constexpr (AMODE == AM_VEC) {
+#pragma unroll
+            for (int i = 0; i < AI; ++i)
+                dma16_buf(ra, kok ? aoff[i] + (unsigned)k * 4u : OOB, sa + (i * 4 + wave) * 8 * BK);
+        } else {
+            const int dh = ckh * p.a.DH, dw = ckw * p.a.DW;
+            const unsigned koff = (unsigned)((dh * p.a.W + dw) * p.a.C + cc) * 4u;
+#pragma unroll
+            for (int i = 0; i < AI; ++i) {
+                const bool ok = kok && (unsigned)(aih[i] + dh) < (unsigned)p.a.H &&
+                                (unsigned)(aiw[i] + dw) < (unsigned)p.a.W;
+                dma16_buf(ra, ok ? aoff[i] + koff : OOB, sa + (i * 4 + wave) * 8 * BK);
+            }
+            cc += BK;
+            while (cc >= p.a.cg) {
+                cc -= p.a.cg;
+                if (++ckw == p.a.KW) {
+                    ckw = 0;
+                    ++ckh;
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < BI; ++i)
+            dma16_buf(rb, kok ? boff[i] + (unsigned)k * 4u : OOB, sb + (i * 4 + wave) * 8 * BK);
+        knext = k + BK;
+        if (++lkt == L.nk) next_load_item();
+    };
+
+    // ---- consumer state (the work item being multiplied) ----------------------------------
+    int cw = first;
+    TileWork C;
+    decode_work(p, cw, BM, BN, BK, C);
+    int ckt = 0;
+
+    floatx16 acc[RM][RN];
+#pragma unroll
+    for (int i = 0; i < RM; ++i)
+#pragma unroll
+        for (int j = 0; j < RN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    const bool split_out = p.split > 1;
+    const int bmode = split_out ? 0 : p.bias_mode;
+    // Scalars read once: keeps the compiler from copying the argument block to scratch.
+    const float alpha = p.alpha, beta = p.beta, lo = p.lo, hi = p.hi;
+    const float *const bias = p.bias;
+    const int act = p.act;
+    const bool has_res = !split_out && p.res != nullptr;
+    const bool clampit = p.act != MGC_ACT_NONE;
+
+    // Epilogue of work item C from the accumulators. The MFMA takes B as its first operand, so
+    // block (i, j) holds C^T: lane (li, lh) owns row m0 + wm * WM + i * 32 + li and, in
+    // registers 4g .. 4g + 3, the four consecutive columns n0 + wn * WN + j * 32 + 8g + 4lh + 0..3.
+    // Residual loads and output stores are therefore 16 bytes wide.
+    const f4 zero4 = {0.f, 0.f, 0.f, 0.f};
+    auto epilogue = [&]() __attribute__((always_inline)) {
+        const long cofs = split_out ? (long)C.ks * p.M * p.N : C.co;
+        float *cptr = (split_out ? p.ws : p.c) + cofs;
+        const unsigned ldc = split_out ? (unsigned)p.N : (unsigned)p.ldc;
+        const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)cptr, (short)0, (int)((split_out ? p.ws_bytes : p.c_bytes) - cofs * 4),
+            0x00020000);
+        __amdgpu_buffer_rsrc_t rr = rc;
+        if (has_res)
+            rr = __builtin_amdgcn_make_buffer_rsrc((void *)(p.res + C.ro), (short)0,
+                                                   (int)(p.r_bytes - C.ro * 4), 0x00020000);
+        const int cbase = C.n0 + wn * WN + 4 * lh;
+        {
+#pragma unroll
+            for (int i = 0; i < RM; ++i) {
+                const int row = C.m0 + wm * WM + i * 32 + li;
+                const bool rok = row < p.M;
+                const float rbias = (bmode == 2 && rok) ? ldg(bias + row) : 0.0f;
+#pragma unroll
+                for (int j = 0; j < RN; ++j) {
+                    f4 rv[4], cb[4];
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int col = cbase + j * 32 + 8 * g;
+                        cb[g] = (bmode == 1 && col < p.N) ? ldg4(bias + col) : zero4;
+                        rv[g] = zero4;
+                        if (has_res) {
+                            const unsigned off =
+                                rok && col < p.N
+                                    ? ((unsigned)row * (unsigned)p.ldr + (unsigned)col) * 4u
+                                    : OOB;
+                            rv[g] = __builtin_bit_cast(
+                                f4, __builtin_amdgcn_raw_buffer_load_b128(rr, (int)off, 0, 0));
+                        }
+                    }
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int col = cbase + j * 32 + 8 * g;
+                        f4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                                acc[i][j][4 * g + 3]};
+                        if (!split_out) {
+                            v = v * alpha + cb[g] + rbias;
+                            if (has_res) v += beta * rv[g];
+                            if constexpr (GEN_ACT) {
+#pragma unroll
+                                for (int e = 0; e < 4; ++e) v[e] = apply_act(v[e], act, lo, hi);
+                            } else if (clampit) {
+#pragma unroll
+                                for (int e = 0; e < 4; ++e) v[e] = fminf(fmaxf(v[e], lo), hi);
+                            }
+                        }
+                        const unsigned off =
+                            rok && col < p.N ? ((unsigned)row * ldc + (unsigned)col) * 4u : OOB;
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uint4_t, v), rc,
+                                                               (int)off, 0, 0);
+                    }
+                }
+            }
+        }
+    };
+
+    // ---- pipeline -----------------------------------------------------------------------
+    int issued = 0, consumed = 0;
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s) {
+        if (loading) {
+            issue(s);
+            ++issued;
+        }
+    }
+    while (true) {
+        if (C.nk > 0) {
+            // Step `consumed` has landed once only the later steps' loads are outstanding.
+            const int ahead = issued - consumed - 1;
+            if (STAGES >= 4 && ahead >= 2) {
+                wait_vmcnt<(STAGES >= 4 ? 2 : 0) * PER_STAGE>();
+            } else if (STAGES >= 3 && ahead >= 1) {
+                wait_vmcnt<PER_STAGE>();
+            } else {
+                wait_vmcnt<0>();
+            }
+            barrier_lds();
+            if (loading) {
+                issue(issued % STAGES);
+                ++issued;
+            }
+            const float *as = smem + (consumed % STAGES) * STAGE;
+            const float *bs = as + BM * BK;
+            const int sw = (li & 7) ^ ((li >> 3) & 1);
+            f4 af[RM][4], bf[RN][4];
+#pragma unroll
+            for (int i = 0; i < RM; ++i)
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+                    af[i][s] = *reinterpret_cast<const f4 *>(
+                        &as[(wm * WM + i * 32 + li) * BK + (((lh * 4 + s) ^ sw) << 2)]);
+#pragma unroll
+            for (int j = 0; j < RN; ++j)
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+                    bf[j][s] = *reinterpret_cast<const f4 *>(
+                        &bs[(wn * WN + j * 32 + li) * BK + (((lh * 4 + s) ^ sw) << 2)]);
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+#pragma unroll
+                    for (int i = 0; i < RM; ++i)
+#pragma unroll
+                        for (int j = 0; j < RN; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                                bf[j][s][e], af[i][s][e], acc[i][j], 0, 0, 0);
+            ++consumed;
+            ++ckt;
+        }
+        if (ckt >= C.nk) {
+            // Work item done (or one without stages: an empty K split writes zeros).
+            epilogue();
+#pragma unroll
+            for (int i = 0; i < RM; ++i)
+#pragma unroll
+                for (int j = 0; j < RN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+            cw += G;
+            if (cw >= total) return;
+            decode_work(p, cw, BM, BN, BK, C);
+            ckt = 0;
         }
     }
 }
@@ -486,6 +1118,20 @@ static GemmKernel pick_kernel(int am, int bm) {
     return table[am][bm];
 }
 
+template <int BM, int BN, int WGM>
+static GemmKernel pick_dma(int am) {
+    return am == AM_VEC ? &gemm_dma_kernel<BM, BN, WGM, 2, AM_VEC>
+                        : &gemm_dma_kernel<BM, BN, WGM, 2, AM_CONV_VEC>;
+}
+
+static GemmKernel pick_stream(int am, bool gen_act) {
+    if (gen_act)
+        return am == AM_VEC ? &gemm_stream_kernel<128, 64, 2, 2, AM_VEC, true>
+                            : &gemm_stream_kernel<128, 64, 2, 2, AM_CONV_VEC, true>;
+    return am == AM_VEC ? &gemm_stream_kernel<128, 64, 2, 2, AM_VEC, false>
+                        : &gemm_stream_kernel<128, 64, 2, 2, AM_CONV_VEC, false>;
+}
+
 struct TileChoice {
     int bm, bn, split;
 };
@@ -513,6 +1159,15 @@ static TileChoice choose_tiles(int M, int N, int K, int batch) {
         if (t.split < 1) t.split = 1;
     }
     return t;
+}
+
+// The streaming kernel pays off where each tile has little K to multiply (1x1 convolutions
+// over large images): with K <= 256 a tile is at most 8 stages, and the overlap of one tile's
+// epilogue with the next tile's loads matters. It needs enough 128 x 64 tiles to keep every
+// workgroup slot busy for several tiles.
+static bool prefer_stream(int M, int N, int K, int batch) {
+    const long tiles = (long)((M + 127) / 128) * ((N + 63) / 64) * batch;
+    return K <= 256 && tiles >= 4L * kCUs;
 }
 
 }  // namespace mgc
@@ -590,18 +1245,83 @@ extern "C" void mgc_hip_gemm(mgc_hip_exec *x, const mgc_hip_gemm_args *g) {
     p.kchunk = (kchunk + 31) / 32 * 32;
     if (p.kchunk == 0) p.kchunk = 32;
     p.ws = g->workspace;
+    p.div_ow = make_fastdiv((unsigned)(p.a.OW > 0 ? p.a.OW : 1));
+    p.div_ohw = make_fastdiv((unsigned)(p.a.OH * p.a.OW > 0 ? p.a.OH * p.a.OW : 1));
+    p.div_cg = make_fastdiv((unsigned)(p.a.cg > 0 ? p.a.cg : 1));
+    p.div_kw = make_fastdiv((unsigned)(p.a.KW > 0 ? p.a.KW : 1));
     p.tiles_m = (p.M + t.bm - 1) / t.bm;
     p.tiles_n = (p.N + t.bn - 1) / t.bn;
 
-    GemmKernel kern;
-    if (t.bm == 128 && t.bn == 128)
-        kern = pick_kernel<128, 128, 2>(am, bm);
-    else if (t.bm == 128 && t.bn == 64)
-        kern = pick_kernel<128, 64, 2>(am, bm);
-    else
-        kern = pick_kernel<64, 64, 2>(am, bm);
+    // Reachable extents of the operands from their base pointers: the DMA kernels address them
+    // through buffer resources with 32-bit offsets.
+    long a_ext, b_ext;
+    if (p.a.kind == MGC_OP_CONV_NHWC) {
+        const long ohw = (long)p.a.OH * p.a.OW;
+        const long n_img = ohw > 0 ? (p.M + ohw - 1) / ohw : 0;
+        a_ext = n_img * p.a.H * p.a.W * p.a.C - (p.a.C - p.a.cg);
+    } else {
+        a_ext = (long)(p.M - 1) * p.a.rs + (long)(p.K - 1) * p.a.cs + 1;
+    }
+    b_ext = (long)(p.K - 1) * p.b.rs + (long)(p.N - 1) * p.b.cs + 1;
+    long c_ext = (long)(p.M - 1) * p.ldc + p.N, r_ext = p.res ? (long)(p.M - 1) * p.ldr + p.N : 0;
+    for (int d = 0; d < p.batch_rank; ++d) {
+        a_ext += (long)(p.bdims[d] - 1) * p.a_bs[d];
+        b_ext += (long)(p.bdims[d] - 1) * p.b_bs[d];
+        c_ext += (long)(p.bdims[d] - 1) * p.c_bs[d];
+        if (p.res) r_ext += (long)(p.bdims[d] - 1) * p.r_bs[d];
+    }
+    p.a_bytes = a_ext * 4;
+    p.b_bytes = b_ext * 4;
+    p.c_bytes = c_ext * 4;
+    p.r_bytes = r_ext * 4;
+    p.ws_bytes = p.split > 1 ? (long)p.split * p.M * p.N * 4 : 0;
+    p.nbatch = batch;
+    const long kMaxRes = 0x7fffffffL;  // buffer offsets past this mean "masked"
+    bool nonneg = p.a.rs >= 0 && p.a.cs >= 0 && p.b.rs >= 0 && p.b.cs >= 0 && p.ldc >= 0 &&
+                  p.ldr >= 0;
+    for (int d = 0; d < p.batch_rank; ++d)
+        nonneg = nonneg && p.a_bs[d] >= 0 && p.b_bs[d] >= 0 && p.c_bs[d] >= 0 && p.r_bs[d] >= 0;
+    const bool dma_ok = nonneg && (am == AM_VEC || am == AM_CONV_VEC) && bm == BD_NK_VEC && p.K > 0 &&
+                        p.a_bytes > 0 && p.a_bytes < kMaxRes && p.b_bytes > 0 &&
+                        p.b_bytes < kMaxRes;
+    const bool stream_ok = dma_ok && p.N % 4 == 0 && (p.split > 1 || p.vec_out) &&
+                           p.c_bytes < kMaxRes && p.r_bytes < kMaxRes && p.ws_bytes < kMaxRes;
 
-    dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)(batch * p.split));
+    GemmKernel kern;
+    dim3 grid;
+    if (stream_ok && t.split == 1 && prefer_stream(p.M, p.N, p.K, batch)) {
+        if (p.act == MGC_ACT_RELU) {  // ReLU as a clamp to [0, inf)
+            p.lo = 0.0f;
+            p.hi = __builtin_huge_valf();
+        }
+        const bool gen_act =
+            !(p.act == MGC_ACT_NONE || p.act == MGC_ACT_RELU || p.act == MGC_ACT_CLIP);
+        p.tiles_m = (p.M + 127) / 128;
+        p.tiles_n = (p.N + 63) / 64;
+        // Two 128 x 64 workgroups fit a CU (2 x 48 KB of LDS ring, 2 waves per SIMD).
+        const long items = (long)p.tiles_m * p.tiles_n * batch;
+        const long slots = 2L * kCUs;
+        kern = pick_stream(am, gen_act);
+        grid = dim3((unsigned)(items < slots ? items : slots));
+    } else {
+        p.tiles_m = (p.M + t.bm - 1) / t.bm;
+        p.tiles_n = (p.N + t.bn - 1) / t.bn;
+        if (dma_ok) {
+            if (t.bm == 128 && t.bn == 128)
+                kern = pick_dma<128, 128, 2>(am);
+            else if (t.bm == 128 && t.bn == 64)
+                kern = pick_dma<128, 64, 2>(am);
+            else
+                kern = pick_dma<64, 64, 2>(am);
+        } else if (t.bm == 128 && t.bn == 128) {
+            kern = pick_kernel<128, 128, 2>(am, bm);
+        } else if (t.bm == 128 && t.bn == 64) {
+            kern = pick_kernel<128, 64, 2>(am, bm);
+        } else {
+            kern = pick_kernel<64, 64, 2>(am, bm);
+        }
+        grid = dim3((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)(batch * p.split));
+    }
     MGC_LAUNCH(x, kern, grid, dim3(256), 0, p);
     if (p.split > 1) {
         MGC_LAUNCH(x, gemm_splitk_reduce, dim3(blocks_for((long)p.M * p.N, 256, 4096)), dim3(256),
