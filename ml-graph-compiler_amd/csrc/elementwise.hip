@@ -252,6 +252,216 @@ __device__ __forceinline__ void reg_set(uint64_t (&R)[MGC_NREG], int idx, uint64
     }
 }
 
+// ------------------------------------------------------------------------------------------
+// float32 fast path: programs whose leaves, registers and output are all float32 (the common
+// case: scaling, broadcast adds, activation chains). 32-bit indices with host-computed magic
+// divisors, a float register file that the compiler keeps in VGPRs (uniform indices become
+// v_movrels), and, when the innermost dim allows, four consecutive elements per thread with
+// 16-byte loads and stores.
+// ------------------------------------------------------------------------------------------
+constexpr int EWF_RANK = 4, EWF_LEAVES = 8, EWF_INSTR = 8, EWF_REGS = EWF_LEAVES + EWF_INSTR;
+
+struct EwF32Instr {
+    int op, a, b, c;  // register indices (b, c: -1 when absent)
+    float fa, fb;
+};
+
+struct EwF32Args {
+    int rank;                  // collapsed output rank, innermost last
+    int units;                 // threads' work items (elements, or groups of 4)
+    int dims[EWF_RANK];        // innermost dim counted in work items
+    FastDiv div[EWF_RANK];
+    int n_leaves, n_instr;
+    const float *leaf[EWF_LEAVES];
+    int lst[EWF_LEAVES][EWF_RANK];  // element strides
+    EwF32Instr ins[EWF_INSTR];
+    float *out;
+    int ost[EWF_RANK];
+};
+
+__device__ __forceinline__ float ewf_op(const EwF32Instr &in, float a, float b, float c) {
+    switch (in.op) {
+    case MGC_EW_ADD: return a + b;
+    case MGC_EW_SUB: return a - b;
+    case MGC_EW_MUL: return a * b;
+    case MGC_EW_DIV: return a / b;
+    case MGC_EW_POW: return powf(a, b);
+    case MGC_EW_MAX: return fmaxf(a, b);
+    case MGC_EW_MIN: return fminf(a, b);
+    case MGC_EW_RELU: return a > 0.0f ? a : 0.0f;
+    case MGC_EW_SIGMOID: return sigmoid_f(a);
+    case MGC_EW_TANH: return tanhf(a);
+    case MGC_EW_ERF: return erf_rational(a);
+    case MGC_EW_SQRT: return sqrtf(a);
+    case MGC_EW_EXP: return expf(a);
+    case MGC_EW_LOG: return logf(a);
+    case MGC_EW_NEG: return -a;
+    case MGC_EW_ABS: return fabsf(a);
+    case MGC_EW_RECIPROCAL: return 1.0f / a;
+    case MGC_EW_FLOOR: return floorf(a);
+    case MGC_EW_CEIL: return ceilf(a);
+    case MGC_EW_SIN: return sinf(a);
+    case MGC_EW_COS: return cosf(a);
+    case MGC_EW_SOFTPLUS: return a > 20.0f ? a : log1pf(expf(a));
+    case MGC_EW_GELU: return gelu_erf_f(a);
+    case MGC_EW_GELU_TANH: return gelu_tanh_f(a);
+    case MGC_EW_LEAKY_RELU: return a >= 0.0f ? a : in.fa * a;
+    case MGC_EW_HARD_SIGMOID: return fminf(fmaxf(in.fa * a + in.fb, 0.0f), 1.0f);
+    case MGC_EW_CLIP: return fminf(fmaxf(a, in.b >= 0 ? b : in.fa), in.c >= 0 ? c : in.fb);
+    default: return a;  // Identity
+    }
+}
+
+template <bool VEC>
+__global__ void __launch_bounds__(256) ew_f32_kernel(const EwF32Args e) {
+    constexpr int W = VEC ? 4 : 1;
+    for (int u = blockIdx.x * 256 + threadIdx.x; u < e.units; u += gridDim.x * 256) {
+        int off[EWF_LEAVES];
+#pragma unroll
+        for (int l = 0; l < EWF_LEAVES; ++l) off[l] = 0;
+        int ooff = 0;
+        int rem = u;
+#pragma unroll
+        for (int d = EWF_RANK - 1; d >= 0; --d) {
+            if (d < e.rank) {
+                const int q = fdiv(rem, e.div[d]);
+                int c = rem - q * e.dims[d];
+                rem = q;
+                if (d == e.rank - 1) c *= W;
+                ooff += c * e.ost[d];
+#pragma unroll
+                for (int l = 0; l < EWF_LEAVES; ++l) off[l] += c * e.lst[l][d];
+            }
+        }
+        float R0[EWF_REGS], R1[EWF_REGS], R2[EWF_REGS], R3[EWF_REGS];
+#pragma unroll
+        for (int l = 0; l < EWF_LEAVES; ++l) {
+            float v0 = 0.f, v1 = 0.f, v2 = 0.f, v3 = 0.f;
+            if (l < e.n_leaves) {
+                const float *src = e.leaf[l] + off[l];
+                if (VEC && e.lst[l][e.rank - 1] == 1) {
+                    const float4 v = *reinterpret_cast<const float4 *>(src);
+                    v0 = v.x; v1 = v.y; v2 = v.z; v3 = v.w;
+                } else {
+                    v0 = v1 = v2 = v3 = *src;
+                }
+            }
+            R0[l] = v0; R1[l] = v1; R2[l] = v2; R3[l] = v3;
+        }
+#pragma unroll
+        for (int r = EWF_LEAVES; r < EWF_REGS; ++r) R0[r] = R1[r] = R2[r] = R3[r] = 0.f;
+        float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+        for (int i = 0; i < e.n_instr; ++i) {
+            const EwF32Instr &in = e.ins[i];
+            const int ia = in.a, ib = in.b >= 0 ? in.b : 0, ic = in.c >= 0 ? in.c : 0;
+            o0 = ewf_op(in, R0[ia], R0[ib], R0[ic]);
+            if (VEC) {
+                o1 = ewf_op(in, R1[ia], R1[ib], R1[ic]);
+                o2 = ewf_op(in, R2[ia], R2[ib], R2[ic]);
+                o3 = ewf_op(in, R3[ia], R3[ib], R3[ic]);
+            }
+            R0[EWF_LEAVES + i] = o0;
+            R1[EWF_LEAVES + i] = o1;
+            R2[EWF_LEAVES + i] = o2;
+            R3[EWF_LEAVES + i] = o3;
+        }
+        if (VEC) {
+            *reinterpret_cast<float4 *>(e.out + ooff) = make_float4(o0, o1, o2, o3);
+        } else {
+            e.out[ooff] = o0;
+        }
+    }
+}
+
+// Builds the float32 fast-path arguments, or returns false when the program does not qualify.
+static bool ew_f32_plan(const mgc_hip_ew_args *e, EwF32Args &f, bool &vec) {
+    if (e->out_dtype != MGC_F32 || e->rank < 1 || e->rank > EWF_RANK || e->n_leaves < 1 ||
+        e->n_leaves > EWF_LEAVES || e->n_instr < 1 || e->n_instr > EWF_INSTR)
+        return false;
+    long total = 1;
+    for (int d = 0; d < e->rank; ++d) total *= e->dims[d];
+    if (total <= 0 || total >= (1L << 31)) return false;
+    for (int l = 0; l < e->n_leaves; ++l) {
+        if (e->leaf[l].dtype != MGC_F32 || e->leaf[l].p == nullptr) return false;
+        long ext = 1;
+        for (int d = 0; d < e->rank; ++d) {
+            if (e->leaf[l].strides[d] < 0) return false;
+            ext += (e->dims[d] - 1) * e->leaf[l].strides[d];
+        }
+        if (ext >= (1L << 31)) return false;
+    }
+    long oext = e->out_base + 1;
+    for (int d = 0; d < e->rank; ++d) {
+        if (e->out_strides[d] < 0) return false;
+        oext += (e->dims[d] - 1) * e->out_strides[d];
+    }
+    if (e->out_base < 0 || oext >= (1L << 31)) return false;
+    for (int i = 0; i < e->n_instr; ++i) {
+        const mgc_hip_ew_instr &in = e->instr[i];
+        if (in.in_dtype != MGC_F32 || in.out_dtype != MGC_F32) return false;
+        switch (in.op) {
+        case MGC_EW_EQUAL: case MGC_EW_LESS: case MGC_EW_GREATER: case MGC_EW_LESS_EQUAL:
+        case MGC_EW_GREATER_EQUAL: case MGC_EW_AND: case MGC_EW_OR: case MGC_EW_XOR:
+        case MGC_EW_WHERE: case MGC_EW_NOT: case MGC_EW_CAST:
+            return false;
+        default: break;
+        }
+        for (int k = 0; k < 3; ++k)
+            if (in.args[k] >= e->n_leaves + i) return false;  // only earlier results
+        if (in.args[0] < 0) return false;
+    }
+    const int r = e->rank - 1;
+    vec = e->dims[r] % 4 == 0 && e->out_strides[r] == 1 && e->out_base % 4 == 0 &&
+          (((uintptr_t)e->out) & 15) == 0;
+    for (int d = 0; d < r && vec; ++d) vec = e->out_strides[d] % 4 == 0;
+    for (int l = 0; l < e->n_leaves && vec; ++l) {
+        const long st = e->leaf[l].strides[r];
+        if (st == 1) {
+            vec = (((uintptr_t)e->leaf[l].p) & 15) == 0;
+            for (int d = 0; d < r && vec; ++d) vec = e->leaf[l].strides[d] % 4 == 0;
+        } else {
+            vec = st == 0;
+        }
+    }
+    f.rank = e->rank;
+    f.units = (int)(vec ? total / 4 : total);
+    for (int d = 0; d < EWF_RANK; ++d) {
+        const int dim = d < e->rank ? (int)e->dims[d] : 1;
+        f.dims[d] = (vec && d == r) ? dim / 4 : dim;
+        f.div[d] = make_fastdiv((unsigned)(f.dims[d] > 0 ? f.dims[d] : 1));
+        f.ost[d] = d < e->rank ? (int)e->out_strides[d] : 0;
+    }
+    f.n_leaves = e->n_leaves;
+    f.n_instr = e->n_instr;
+    for (int l = 0; l < EWF_LEAVES; ++l) {
+        f.leaf[l] = l < e->n_leaves ? static_cast<const float *>(e->leaf[l].p) : nullptr;
+        for (int d = 0; d < EWF_RANK; ++d)
+            f.lst[l][d] = (l < e->n_leaves && d < e->rank) ? (int)e->leaf[l].strides[d] : 0;
+    }
+    // Registers: leaves 0 .. n_leaves - 1 keep their numbers; instruction i's result, register
+    // MGC_EW_MAX_LEAVES + i in the generic encoding, becomes EWF_LEAVES + i.
+    auto remap = [&](int a) { return a < 0 ? -1 : (a < MGC_EW_MAX_LEAVES ? a : a - MGC_EW_MAX_LEAVES + EWF_LEAVES); };
+    for (int i = 0; i < EWF_INSTR; ++i) {
+        EwF32Instr &o = f.ins[i];
+        if (i < e->n_instr) {
+            const mgc_hip_ew_instr &in = e->instr[i];
+            o.op = in.op;
+            o.a = remap(in.args[0]);
+            o.b = remap(in.args[1]);
+            o.c = remap(in.args[2]);
+            o.fa = in.fa;
+            o.fb = in.fb;
+        } else {
+            o.op = MGC_EW_IDENTITY;
+            o.a = 0;
+            o.b = o.c = -1;
+            o.fa = o.fb = 0.f;
+        }
+    }
+    f.out = static_cast<float *>(e->out) + e->out_base;
+    return true;
+}
+
 __global__ void __launch_bounds__(256) ew_program_kernel(const mgc_hip_ew_args e) {
     long total = 1;
     for (int d = 0; d < e.rank; ++d) total *= e.dims[d];
@@ -371,6 +581,15 @@ extern "C" void mgc_hip_elementwise(mgc_hip_exec *x, const mgc_hip_ew_args *e) {
     long total = 1;
     for (int d = 0; d < e->rank; ++d) total *= e->dims[d];
     if (total <= 0) return;
+    EwF32Args f;
+    bool vec = false;
+    if (ew_f32_plan(e, f, vec)) {
+        if (vec)
+            MGC_LAUNCH(x, ew_f32_kernel<true>, dim3(blocks_for(f.units, 256, 8192)), dim3(256), 0, f);
+        else
+            MGC_LAUNCH(x, ew_f32_kernel<false>, dim3(blocks_for(f.units, 256, 8192)), dim3(256), 0, f);
+        return;
+    }
     MGC_LAUNCH(x, ew_program_kernel, dim3(blocks_for(total, 256, 8192)), dim3(256), 0, *e);
 }
 

@@ -52,26 +52,6 @@ __device__ __forceinline__ float ldg(const float *ptr) { return *(gfloat *)ptr; 
 __device__ __forceinline__ f4 ldg4(const float *ptr) { return *(gf4 *)ptr; }
 enum { BD_NK_VEC = 0, BD_KN_VEC = 1, BD_GEN = 2 };
 
-// Division by a launch-constant divisor d (1 <= d < 2^31) for numerators 0 <= n < 2^31:
-// q = (umulhi(n, m) + n) >> s with s = ceil(log2 d), m = floor(2^32 (2^s - d) / d) + 1
-// (Granlund and Montgomery, "Division by invariant integers using multiplication", 1994).
-struct FastDiv {
-    unsigned d, m, s;
-};
-
-static FastDiv make_fastdiv(unsigned d) {
-    FastDiv f;
-    f.d = d ? d : 1;
-    f.s = 0;
-    while ((1u << f.s) < f.d) ++f.s;
-    f.m = (unsigned)((((unsigned long long)1 << 32) * (((unsigned long long)1 << f.s) - f.d)) / f.d + 1);
-    return f;
-}
-
-__device__ __forceinline__ int fdiv(int n, const FastDiv &f) {
-    return (int)((__umulhi((unsigned)n, f.m) + (unsigned)n) >> f.s);
-}
-
 struct GemmDev {
     int M, N, K;
     mgc_hip_operand a, b;

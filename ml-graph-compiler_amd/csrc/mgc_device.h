@@ -30,6 +30,26 @@ inline unsigned blocks_for(long n, int threads, long cap = 1L << 20) {
     return (unsigned)b;
 }
 
+// Division by a launch-constant divisor d (1 <= d < 2^31) for numerators 0 <= n < 2^31:
+// q = (umulhi(n, m) + n) >> s with s = ceil(log2 d), m = floor(2^32 (2^s - d) / d) + 1
+// (Granlund and Montgomery, "Division by invariant integers using multiplication", 1994).
+struct FastDiv {
+    unsigned d, m, s;
+};
+
+inline FastDiv make_fastdiv(unsigned d) {
+    FastDiv f;
+    f.d = d ? d : 1;
+    f.s = 0;
+    while ((1u << f.s) < f.d) ++f.s;
+    f.m = (unsigned)((((unsigned long long)1 << 32) * (((unsigned long long)1 << f.s) - f.d)) / f.d + 1);
+    return f;
+}
+
+__device__ __forceinline__ int fdiv(int n, const FastDiv &f) {
+    return (int)((__umulhi((unsigned)n, f.m) + (unsigned)n) >> f.s);
+}
+
 // ------------------------------------------------------------------------------------------
 // device math. exp/log/sqrt/tanh come from the HIP device library; erf uses the rational
 // approximation the reference's interpreter and C runtime share (ops.py:201-229,
