@@ -10,7 +10,9 @@ Printed: ONE JSON line with the driver's fields plus
 * ``roofline``: the fp32 MFMA GEMM / implicit-GEMM convolution kernels (all conv and FC nodes):
   algorithmic FLOPs per launch (ops.flops of the node, 2 per MAC) over the kernel's average
   duration, measured with a hipEvent pair around every node in eager replays on the model
-  stream; ``traffic`` comes from rocprofv3 counter runs (see DESIGN) and is null here;
+  stream; ``traffic`` is the HBM bytes per GEMM launch from the two rocprofv3 counter runs
+  summarized in profiles/<workload>_b<batch>_gemm_traffic.md (``--pmc-probe`` is the program
+  those runs profile and ``--pmc-summary`` turns their CSVs into that file), or null;
 * ``cpu_baseline``: the reference's generated-C + OpenMP backend (its own C kernels, built from
   the reference sources into oracle/_ref) timed on this host's cores on a bounded sample;
 * ``b1``: the same model at batch 1 (latency and img/s).
@@ -126,6 +128,117 @@ def cpu_baseline(workload: str, seconds_budget: float = 20.0) -> dict | None:
         return None
 
 
+TRAFFIC_KEY = "traffic_bytes_per_launch:"
+CALIBRATION_FLOATS = 1 << 26  # 256 MiB copied by the calibration kernel
+
+
+def traffic_file(workload: str, batch: int) -> Path:
+    return ROOT / "profiles" / f"{workload}_b{batch}_gemm_traffic.md"
+
+
+def recorded_traffic(workload: str, batch: int) -> int | None:
+    """HBM bytes per GEMM launch from the committed counter summary, if there is one."""
+    path = traffic_file(workload, batch)
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.strip().startswith(TRAFFIC_KEY):
+            return int(line.split(":", 1)[1].strip())
+    return None
+
+
+def pmc_probe(workload: str, batch: int, cache: Path) -> None:
+    """The program the counter runs profile: one plain copy of CALIBRATION_FLOATS floats (a
+    single-node O0 graph whose Transpose lowers to the 16-byte copy kernel), then one eager
+    forward of the workload with every node launched on its own."""
+    from ml_graph_compiler.codegen import compile_graph
+    from ml_graph_compiler.ir import Graph, TensorType
+    from ml_graph_compiler.shape_inference import infer_shapes
+
+    g = Graph("calibration")
+    x = g.add_input("x", TensorType("float32", (CALIBRATION_FLOATS,)))
+    node = g.add_node("Transpose", [x], attrs={"perm": [0]})
+    g.add_output(node.output, "y")
+    infer_shapes(g)
+    cal = compile_graph(g, cache_dir=cache, name="calibration_copy", profile=True)
+    cal.upload({"x": np.zeros(CALIBRATION_FLOATS, np.float32)})
+    cal.profile_run(1)
+    cal.sync()
+    cal.release()
+    graph, model = compile_workload(workload, batch, cache)
+    model.upload(feeds_for(graph))
+    model.profile_run(1)
+    model.sync()
+    model.release()
+    log("pmc probe done: calibration copy, then one eager forward")
+
+
+def pmc_summary(fetch_dir: Path, write_dir: Path, workload: str, batch: int) -> str:
+    """Markdown summary of the FETCH_SIZE and WRITE_SIZE runs over --pmc-probe."""
+    import csv
+
+    def per_dispatch(d: Path, counter: str) -> list[tuple[str, float]]:
+        rows = []
+        for f in sorted(d.rglob("*counter_collection.csv")):
+            for r in csv.DictReader(open(f)):
+                if r["Counter_Name"] == counter:
+                    rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
+        rows.sort()
+        return [(name, v) for _, name, v in rows]
+
+    fetch = per_dispatch(fetch_dir, "FETCH_SIZE")
+    write = per_dispatch(write_dir, "WRITE_SIZE")
+    nbytes = 4 * CALIBRATION_FLOATS
+    cal_f = next(v for name, v in fetch if "copy_kernel" in name)
+    cal_w = next(v for name, v in write if "copy_kernel" in name)
+    kf, kw = nbytes / (cal_f * 1024.0), nbytes / (cal_w * 1024.0)
+
+    def is_gemm(name: str) -> bool:
+        return "gemm_" in name and "reduce" not in name
+
+    gf = [v for name, v in fetch if is_gemm(name)]
+    gw = [v for name, v in write if is_gemm(name)]
+    n = len(gf)
+    fetch_b = kf * 1024.0 * sum(gf) / n
+    write_b = kw * 1024.0 * sum(gw) / n
+    per_launch = int(round(fetch_b + write_b))
+    # algorithmic bytes: every operand (activations, weights, bias, residual) and the output once
+    from ml_graph_compiler.ir import numpy_dtype
+    from ml_graph_compiler.passes import optimize
+
+    g = build_graph(workload, batch)
+    optimize(g, "O3")
+    algo = []
+    for node in g.nodes:
+        if node.op in ("FusedConv", "Conv", "FusedGemm", "Gemm", "MatMul") and not _is_depthwise(node):
+            vals = [v for v in node.inputs if v is not None] + list(node.outputs)
+            algo.append(sum(int(np.prod(v.type.shape)) * np.dtype(numpy_dtype(v.type.dtype)).itemsize for v in vals))
+    algo_b = sum(algo) / max(len(algo), 1)
+    return "\n".join([
+        f"# HBM traffic of the GEMM kernels: {workload} b{batch} forward (hip backend, -O3)",
+        "",
+        "Commands (repo root, on the MI355X box; one counter per run):",
+        "",
+        "```",
+        "cd /tmp && export TMPDIR=/tmp",
+        f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d $GRAFT_REPO_ROOT/gpurun_out/pmc_fetch -o p -- python3 $GRAFT_REPO_ROOT/bench.py --pmc-probe --workload {workload} --batch {batch}",
+        f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d $GRAFT_REPO_ROOT/gpurun_out/pmc_write -o p -- python3 $GRAFT_REPO_ROOT/bench.py --pmc-probe --workload {workload} --batch {batch}",
+        f"python3 bench.py --pmc-summary gpurun_out/pmc_fetch gpurun_out/pmc_write --workload {workload} --batch {batch}",
+        "```",
+        "",
+        f"Calibration: a plain 16-byte copy of {nbytes} bytes read {cal_f:.0f} KiB (FETCH_SIZE) and wrote "
+        f"{cal_w:.0f} KiB (WRITE_SIZE); scale factors {kf:.4f} (fetch) and {kw:.4f} (write) turn each "
+        "counter into bytes.",
+        "",
+        f"GEMM dispatches in one eager forward: {n}. Average per launch: fetched {fetch_b / 1e6:.2f} MB, "
+        f"written {write_b / 1e6:.2f} MB; the algorithmic minimum (each operand and the output moved "
+        f"once) is {algo_b / 1e6:.2f} MB per launch, so HBM traffic is {(fetch_b + write_b) / algo_b:.2f}x it.",
+        "",
+        f"{TRAFFIC_KEY} {per_launch}",
+        "",
+    ])
+
+
 def main() -> int:
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
@@ -137,13 +250,24 @@ def main() -> int:
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-b1", action="store_true")
     p.add_argument("--cache", default=os.environ.get("MGC_BENCH_CACHE", "/tmp/mgc-bench-cache"))
+    p.add_argument("--pmc-probe", action="store_true", help="run the counter-run program and exit")
+    p.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                   help="summarize the FETCH_SIZE / WRITE_SIZE runs into profiles/ and exit")
     args = p.parse_args()
+    if args.pmc_summary:
+        text = pmc_summary(Path(args.pmc_summary[0]), Path(args.pmc_summary[1]), args.workload, args.batch)
+        traffic_file(args.workload, args.batch).write_text(text)
+        print(text)
+        return 0
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: every GPU box here has one MI355X; "
                                    "use --gpus 1 (batch sharding across GPUs is described in DESIGN.md)"}))
         return 2
     cache = Path(args.cache)
     batch = 128 if args.workload == "single_gemm" else args.batch
+    if args.pmc_probe:
+        pmc_probe(args.workload, batch, cache)
+        return 0
 
     log(f"compiling {args.workload} b{batch} (O3, hip)")
     graph, model = compile_workload(args.workload, batch, cache)
@@ -159,6 +283,7 @@ def main() -> int:
     value = units * args.steps / wall
     log(f"{ms_per_step:.3f} ms/step (events {ev_ms / args.steps:.3f} ms), {value:.1f} units/s")
     roof = gemm_roofline(graph, model, args.profile_replays)
+    roof["traffic"] = recorded_traffic(args.workload, batch)
     log(f"roofline {roof}")
     total_flops = sum(model.node_flops)
     model.release()
