@@ -20,6 +20,9 @@
  *   mgc_hip_fill            <- constant loops of _write_constant/op_ConstantOfShape (c.py:690-722)
  *   mgc_hip_gather          <- op_Gather (codegen/c.py:662-688), error code 1 on a bad index
  *   mgc_hip_range           <- op_Range (codegen/c.py:724-734)
+ *   mgc_hip_attention       <- no single counterpart: replaces the MatMul -> Mul -> Softmax ->
+ *                              MatMul chain and its head Transposes (samples.py:178-245) when
+ *                              the hip emitter recognizes it
  *   mgc_hip_reduce          <- CEmitter._reduce generic loop (codegen/c.py:736-799)
  *   mgc_hip_argmax          <- op_ArgMax (codegen/c.py:801-821)
  *   mgc_hip_model_*         <- what mgc_run and CompiledModel do around the generated function
@@ -161,6 +164,23 @@ void mgc_hip_softmax(mgc_hip_exec *x, long outer, long n, long inner, const floa
 /* Layer normalization of each row of [rows, cols]; scale and bias may be NULL. */
 void mgc_hip_layer_norm(mgc_hip_exec *x, long rows, long cols, const float *in,
                         const float *scale, const float *bias, float eps, float *out);
+
+/* Scaled dot-product attention for every (batch b, head h):
+ *   O[b, s, h, :] = softmax_j(scale * Q[b, s, h, :] . K[b, j, h, :]) V[b, j, h, :]
+ * Element (b, s, h, d) of X in {Q, K, V, O} is at x + b * x_b + s * x_s + h * x_h + d (d is
+ * contiguous). Limits: Skv <= 256 and D <= 64 with D % 4 == 0 (mgc_hip_attention_supported);
+ * pointers and strides must keep 16-byte alignment for Q, K and V. */
+typedef struct {
+    int B, H, S, Skv, D;
+    const float *q, *k, *v;
+    long q_b, q_s, q_h, k_b, k_s, k_h, v_b, v_s, v_h;
+    float *o;
+    long o_b, o_s, o_h;
+    float scale;
+} mgc_hip_attention_args;
+
+int mgc_hip_attention_supported(int S, int Skv, int D);
+void mgc_hip_attention(mgc_hip_exec *x, const mgc_hip_attention_args *a);
 
 /* ---------------------------------------------------------------------------------------- */
 /* elementwise programs, copies, fills, gathers                                              */

@@ -19,6 +19,9 @@ Lowering per operator family:
   strides over the collapsed output dims plus a typed instruction list.
 * Transpose/Expand/Slice/Concat/Split/Pad/Tile and output copies -> mgc_hip_copy / mgc_hip_fill.
 * Gather -> mgc_hip_gather (device flag on a bad index -> mgc_run returns 1).
+* Scaled dot-product attention chains (head-split Reshape/Transpose, MatMul, scale, Softmax,
+  MatMul, head-merge Transpose; see codegen/attention.py) -> one mgc_hip_attention call that
+  reads Q, K and V as strided views of the QKV projection; the chain's other nodes emit nothing.
 * Softmax, LayerNorm, pooling, reductions, ArgMax -> their kernels.
 * Views (Reshape, Flatten, Squeeze, Unsqueeze, Identity, Dropout) emit nothing.
 """
@@ -39,6 +42,7 @@ from .. import ops
 from ..errors import CodegenError
 from ..ir import Graph, Node, TensorType, Value, comment_text, numpy_dtype
 from ..memory import ALIAS_OPS, MemoryPlan, Strategy, plan_memory
+from .attention import AttentionMatch, find_attention
 
 ALIGN = 256  # arena offsets, weights chunks and the HBM block are 256-byte aligned
 
@@ -82,6 +86,9 @@ _ANY_DTYPE = frozenset({"Equal", "Less", "Greater", "LessOrEqual", "GreaterOrEqu
 _FLOAT32_OPS = frozenset(EW_OPCODES) | {"Gelu"}
 _FLOAT64_OPS = frozenset({"Add", "Sub", "Mul", "Div", "Neg", "Identity"})
 _INT_OPS = frozenset({"Add", "Sub", "Mul", "Div", "Max", "Min", "Neg", "Abs", "Relu", "Identity", "Clip"})
+
+# Fuse recognized attention chains into mgc_hip_attention (tests turn it off to compare).
+FUSE_ATTENTION = True
 
 MAX_RANK = 6
 MAX_LEAVES = 16
@@ -244,6 +251,20 @@ class HipEmitter:
         # keyed by id(value), so these must outlive the emission or a later temporary could reuse
         # an id and alias an earlier chunk.
         self._owned_constants: list[Value] = []
+        self._attn_emit: dict[int, AttentionMatch] = {}
+        self._attn_skip: dict[int, AttentionMatch] = {}
+        # Scratch past the planned arena (the plan's offsets stay as they are) for fused
+        # attention outputs that must not be written over their operands.
+        self._scratch_off = (max(self.plan.arena_bytes, ALIGN) + ALIGN - 1) // ALIGN * ALIGN
+        self._scratch_bytes = 0
+        if FUSE_ATTENTION:
+            for m in find_attention(graph, self.plan):
+                self._attn_emit[id(m.emit_at)] = m
+                for n in m.absorbed:
+                    if n is not m.emit_at:
+                        self._attn_skip[id(n)] = m
+                if m.staged:
+                    self._scratch_bytes = max(self._scratch_bytes, m.out.tensor_type.nbytes)
 
     # -- workspace hook ------------------------------------------------------------------------
     def _gemm_shape(self, node: Node) -> tuple[int, int, int, int] | None:
@@ -314,6 +335,13 @@ class HipEmitter:
             self.emit(f"mgc_hip_node_end(x, {index});")
 
     def _lower(self, node: Node) -> None:
+        if id(node) in self._attn_skip:
+            m = self._attn_skip[id(node)]
+            self.emit(f"/* part of the fused attention at {comment_text(m.emit_at.name)} */")
+            return
+        if id(node) in self._attn_emit:
+            self._attention(self._attn_emit[id(node)])
+            return
         if node.op in ALIAS_OPS:
             if node.op == "Dropout" and len(node.outputs) > 1:
                 mask = node.outputs[1]
@@ -800,6 +828,29 @@ class HipEmitter:
             bspec = self._strided("b", self.ptr(b), n, 1)
         self._gemm_call(m, n, k, self._strided("a", self.ptr(a), k, 1), bspec, self.ptr(node.output), n, batch=batch)
 
+    def _attention(self, m: AttentionMatch) -> None:
+        def view(op: Any) -> str:
+            return f"((const float *){self.ptr(op.value)} + {op.col})"
+
+        out = f"((float *)(A + {self._scratch_off}))" if m.staged else self.fptr(m.out)
+
+        fields = [
+            f"t.B = {m.B}; t.H = {m.H}; t.S = {m.S}; t.Skv = {m.Skv}; t.D = {m.D};",
+            f"t.q = {view(m.q)}; t.q_b = {m.q.batch_stride}L; t.q_s = {m.q.row_stride}L; t.q_h = {m.D}L;",
+            f"t.k = {view(m.k)}; t.k_b = {m.k.batch_stride}L; t.k_s = {m.k.row_stride}L; t.k_h = {m.D}L;",
+            f"t.v = {view(m.v)}; t.v_b = {m.v.batch_stride}L; t.v_s = {m.v.row_stride}L; t.v_h = {m.D}L;",
+            f"t.o = {out}; t.o_b = {m.S * m.H * m.D}L; t.o_s = {m.H * m.D}L; t.o_h = {m.D}L;",
+            f"t.scale = {_f(m.scale)};",
+        ]
+        self.emit("{ mgc_hip_attention_args t; memset(&t, 0, sizeof t);")
+        for f_ in fields:
+            self.emit("  " + f_)
+        self.emit("  mgc_hip_attention(x, &t); }")
+        self.count("attention")
+        if m.staged:
+            nbytes = m.out.tensor_type.nbytes
+            self.copy((nbytes,), self.ptr(m.out), [1], 0, f"(A + {self._scratch_off})", [1], 0, 1)
+
     # -- convolution and pooling ---------------------------------------------------------------
     @staticmethod
     def depthwise(node: Node) -> bool:
@@ -929,6 +980,8 @@ class HipEmitter:
             t = value.tensor_type
             self.copy((t.nbytes,), f"((unsigned char *)out[{j}])", [1], 0, self.ptr(value), [1], 0, 1)
         arena = max(self.plan.arena_bytes, ALIGN)
+        if self._scratch_bytes:
+            arena = self._scratch_off + (self._scratch_bytes + ALIGN - 1) // ALIGN * ALIGN
         weights = self.weights
         n_in, n_out = len(self.graph.inputs), len(self.graph.named_outputs())
         in_bytes = ", ".join(f"{v.tensor_type.nbytes}UL" for v in self.graph.inputs) or "0UL"
