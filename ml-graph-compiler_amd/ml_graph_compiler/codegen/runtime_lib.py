@@ -368,9 +368,14 @@ def compile_model(
     reschedule: bool = True,
     **kwargs: Any,
 ) -> HipCompiledModel:
-    """A model (an IR Graph, or the name of a bundled sample/config) to a loaded hip model:
-    optimize, schedule, compile. ONNX files need the onnx package, which this build lacks."""
+    """A model to a loaded hip model: import, optimize, schedule, compile.
+
+    ``model`` is an IR Graph, an ONNX file path, serialized ONNX bytes, a decoded
+    ``onnx_proto.ModelProto``, or the name of a bundled sample/config; ``input_shapes`` and
+    ``dims`` bind the symbolic dimensions of an ONNX model's inputs."""
     from ..builders import CONFIGS, SAMPLES
+    from ..onnx_import import from_onnx
+    from ..onnx_proto import ModelProto
     from ..passes import optimize
     from ..schedule import schedule
 
@@ -380,10 +385,14 @@ def compile_model(
         graph = SAMPLES[model]()
     elif isinstance(model, str) and model in CONFIGS:
         graph = CONFIGS[model]()
+    elif isinstance(model, (ModelProto, bytes, bytearray, memoryview)) or (
+        isinstance(model, (str, Path)) and Path(model).is_file()
+    ):
+        graph = from_onnx(model, input_shapes, dims)
     else:
         raise ModelImportError(
-            f"{model!r}: ONNX import is not available in this build; pass an IR Graph or one of "
-            f"{sorted(SAMPLES) + sorted(CONFIGS)}"
+            f"{model!r} is neither an ONNX file nor a bundled sample or config "
+            f"({', '.join(sorted(SAMPLES) + sorted(CONFIGS))})"
         )
     optimize(graph, opt)
     if reschedule:
