@@ -34,7 +34,7 @@ import numpy as np  # noqa: E402
 
 MFMA_FP32_PEAK_TFLOPS = 157.3
 HBM_PEAK_GBS = 8000.0
-WORKLOADS = ("resnet50", "bottleneck", "mobilenet_v2", "bert_base", "single_gemm")
+WORKLOADS = ("resnet50", "bottleneck", "mobilenet_v2", "bert_base", "gpt2", "single_gemm")
 
 
 def log(msg: str) -> None:

@@ -165,11 +165,18 @@ void mgc_hip_softmax(mgc_hip_exec *x, long outer, long n, long inner, const floa
 void mgc_hip_layer_norm(mgc_hip_exec *x, long rows, long cols, const float *in,
                         const float *scale, const float *bias, float eps, float *out);
 
-/* Scaled dot-product attention for every (batch b, head h):
- *   O[b, s, h, :] = softmax_j(scale * Q[b, s, h, :] . K[b, j, h, :]) V[b, j, h, :]
+/* Scaled dot-product attention for every (batch b, head h), query s and key j:
+ *   t = Q[b, s, h, :] . K[b, j, h, :]
+ *   t = scale_div ? t / scale : t * scale;  if (bias) t += bias[b, h, s, j];
+ *   if (causal || mask) t = keep(s, j) ? t : fill;
+ *   O[b, s, h, :] = sum_j softmax_j(t) V[b, j, h, :]
+ * with keep(s, j) = (j <= s) when causal, else ((mask[b, h, s, j] != 0) == mask_keep).
  * Element (b, s, h, d) of X in {Q, K, V, O} is at x + b * x_b + s * x_s + h * x_h + d (d is
- * contiguous). Limits: Skv <= 256 and D <= 64 with D % 4 == 0 (mgc_hip_attention_supported);
- * pointers and strides must keep 16-byte alignment for Q, K and V. */
+ * contiguous); bias and mask elements are at p + b * p_b + h * p_h + s * p_s + j * p_j (strides
+ * in elements, 0 for a broadcast dimension; bias float, mask one byte per element).
+ * Limits: D <= 64 with D % 4 == 0 (mgc_hip_attention_supported); Q, K and V pointers and row
+ * strides must keep 16-byte alignment. S and Skv are unbounded (keys are streamed in blocks
+ * with a running softmax). */
 typedef struct {
     int B, H, S, Skv, D;
     const float *q, *k, *v;
@@ -177,6 +184,14 @@ typedef struct {
     float *o;
     long o_b, o_s, o_h;
     float scale;
+    int scale_div;
+    const float *bias;
+    long bias_b, bias_h, bias_s, bias_j;
+    const unsigned char *mask;
+    long mask_b, mask_h, mask_s, mask_j;
+    int mask_keep;
+    int causal;
+    float fill;
 } mgc_hip_attention_args;
 
 int mgc_hip_attention_supported(int S, int Skv, int D);

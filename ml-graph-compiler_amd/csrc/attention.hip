@@ -7,14 +7,19 @@
 // projection output and writes O in the [batch, seq, head * dim] layout of the head merge,
 // so the score matrix and the transposed copies never reach HBM.
 //
-// One workgroup of 256 threads (4 waves) owns 64 query rows of one (batch, head):
-//  1. the Q rows go to LDS ([row][d], d contiguous);
-//  2. keys are taken 64 at a time; each wave multiplies a 32x32 block of the scores with
-//     v_mfma_f32_32x32x2f32 and writes it, scaled, into an LDS score tile [64][keys];
-//  3. four threads per row compute the row max, the exponentials and the sum, and leave the
-//     normalized probabilities in the tile;
-//  4. V is taken 64 keys at a time, transposed into LDS as [d][key], and each wave
-//     accumulates a 32x32 block of O = P V; O leaves as 128-byte row segments.
+// One workgroup of 256 threads (4 waves) owns 64 query rows of one (batch, head) and streams
+// the keys in blocks of 64 with a running ("online") softmax, so neither S nor Skv is bounded:
+//  1. the Q rows go to LDS ([row][d], d contiguous) once;
+//  2. per key block, K goes to LDS as [key][d] and V transposed as [d][key]; each wave
+//     multiplies a 32x32 block of the scores with v_mfma_f32_32x32x2f32 and writes it, scaled,
+//     biased and masked as the graph says, into an LDS tile;
+//  3. four threads per row take the block's row maximum, raise the running maximum m, turn the
+//     scores into exp(t - m), add them to the running sum l and publish exp(m_old - m);
+//  4. each wave rescales its 32x32 block of O by that factor and accumulates P V on MFMA;
+//  5. O is divided by l and leaves as 128-byte row segments.
+// With a causal mask, key blocks that lie wholly past the diagonal hold only the fill value; they
+// are skipped when their terms are exactly zero in fp32 (fill = -inf, or fill at least 110
+// below every row's running maximum, where expf underflows to 0).
 // Operand fragments follow the GEMM kernels' convention: within a 32-wide k chunk, lanes
 // 0-31 take k 0..15 and lanes 32-63 take k 16..31 (the same permutation on both operands).
 #include "mgc_device.h"
@@ -27,9 +32,8 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 constexpr int ATT_BQ = 64;      // query rows per workgroup
 constexpr int ATT_BK = 64;      // keys per block
 constexpr int ATT_DMAX = 64;    // head dim limit
-constexpr int ATT_SMAX = 256;   // key count limit
-constexpr int ATT_DP = ATT_DMAX + 4;         // row pitch of Q, K and V^T tiles
-constexpr int ATT_SP = ATT_SMAX + 4;         // row pitch of the score tile
+constexpr int ATT_P = ATT_DMAX + 4;    // row pitch (floats) of every LDS tile
+constexpr float ATT_SKIP_MARGIN = 110.f;
 
 struct AttnDev {
     int B, H, S, Skv, D;
@@ -38,12 +42,22 @@ struct AttnDev {
     float *o;
     long o_b, o_s, o_h;
     float scale;
+    int scale_div;
+    const float *bias;
+    long bias_b, bias_h, bias_s, bias_j;
+    const unsigned char *mask;
+    long mask_b, mask_h, mask_s, mask_j;
+    int mask_keep;
+    int causal;
+    float fill;
 };
 
 __global__ void __launch_bounds__(256) attention_kernel(const AttnDev p) {
-    __shared__ __attribute__((aligned(16))) float Qs[ATT_BQ * ATT_DP];
-    __shared__ __attribute__((aligned(16))) float KVs[ATT_BK * ATT_DP];  // K block, then V^T block
-    __shared__ __attribute__((aligned(16))) float Ss[ATT_BQ * ATT_SP];
+    __shared__ __attribute__((aligned(16))) float Qs[ATT_BQ * ATT_P];
+    __shared__ __attribute__((aligned(16))) float Ks[ATT_BK * ATT_P];
+    __shared__ __attribute__((aligned(16))) float Vt[ATT_DMAX * ATT_P];  // [d][key]
+    __shared__ __attribute__((aligned(16))) float Ps[ATT_BQ * ATT_P];    // scores, then exp terms
+    __shared__ float rowscale[ATT_BQ];  // exp(m_old - m_new) of the block; 1 / l at the end
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -57,28 +71,52 @@ __global__ void __launch_bounds__(256) attention_kernel(const AttnDev p) {
     const float *qbase = p.q + b * p.q_b + h * p.q_h;
     const float *kbase = p.k + b * p.k_b + h * p.k_h;
     const float *vbase = p.v + b * p.v_b + h * p.v_h;
+    const float *bias = p.bias ? p.bias + b * p.bias_b + h * p.bias_h : nullptr;
+    const unsigned char *mask = p.mask ? p.mask + b * p.mask_b + h * p.mask_h : nullptr;
     const int D = p.D, D4 = p.D >> 2;
     const int kblocks = (p.Skv + ATT_BK - 1) / ATT_BK;
     const int dchunks = (D + 31) >> 5;
+    const int q_last = min(q0 + ATT_BQ, p.S) - 1;
+    const float scale = p.scale, fill = p.fill;
+    const bool scale_div = p.scale_div != 0, causal = p.causal != 0, keep_set = p.mask_keep != 0;
+    const float NEG_INF = -__builtin_huge_valf();
     const f4 zero4 = {0.f, 0.f, 0.f, 0.f};
+    // softmax role: four neighbouring threads share a row
+    const int srow = tid >> 2, part = tid & 3;
+    float m_run = NEG_INF, l_run = 0.f;
 
     // 1. Q rows (rows past S and columns past D are zero)
     for (int e = tid; e < ATT_BQ * (ATT_DMAX / 4); e += 256) {
         const int r = e / (ATT_DMAX / 4), c4 = e - r * (ATT_DMAX / 4);
         f4 v = zero4;
         if (q0 + r < p.S && c4 < D4) v = *reinterpret_cast<const f4 *>(qbase + (long)(q0 + r) * p.q_s + c4 * 4);
-        *reinterpret_cast<f4 *>(&Qs[r * ATT_DP + c4 * 4]) = v;
+        *reinterpret_cast<f4 *>(&Qs[r * ATT_P + c4 * 4]) = v;
     }
 
-    // 2. scores, one 64-key block at a time
+    floatx16 oacc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[r] = 0.f;
+
     for (int kb = 0; kb < kblocks; ++kb) {
-        __syncthreads();  // KVs free (previous block consumed), Qs visible
+        const int k0 = kb * ATT_BK;
+        if (causal && k0 > q_last) {
+            // every key from here on is masked in every row of the block
+            const bool zero_terms = q0 + srow > q_last || fill == NEG_INF || fill <= m_run - ATT_SKIP_MARGIN;
+            if (__syncthreads_and(zero_terms)) break;
+        }
+        __syncthreads();  // Ks, Vt, Ps and rowscale free; Qs visible
+        // 2. K block [key][d], V block transposed [d][key] (zero past Skv and past D)
         for (int e = tid; e < ATT_BK * (ATT_DMAX / 4); e += 256) {
             const int r = e / (ATT_DMAX / 4), c4 = e - r * (ATT_DMAX / 4);
-            const int key = kb * ATT_BK + r;
-            f4 v = zero4;
-            if (key < p.Skv && c4 < D4) v = *reinterpret_cast<const f4 *>(kbase + (long)key * p.k_s + c4 * 4);
-            *reinterpret_cast<f4 *>(&KVs[r * ATT_DP + c4 * 4]) = v;
+            const int key = k0 + r;
+            f4 kv = zero4, vv = zero4;
+            if (key < p.Skv && c4 < D4) {
+                kv = *reinterpret_cast<const f4 *>(kbase + (long)key * p.k_s + c4 * 4);
+                vv = *reinterpret_cast<const f4 *>(vbase + (long)key * p.v_s + c4 * 4);
+            }
+            *reinterpret_cast<f4 *>(&Ks[r * ATT_P + c4 * 4]) = kv;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) Vt[(c4 * 4 + j) * ATT_P + r] = vv[j];
         }
         __syncthreads();
         floatx16 acc;
@@ -88,8 +126,8 @@ __global__ void __launch_bounds__(256) attention_kernel(const AttnDev p) {
             f4 af[4], bf[4];
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                af[s] = *reinterpret_cast<const f4 *>(&Qs[(wm * 32 + li) * ATT_DP + c * 32 + lh * 16 + 4 * s]);
-                bf[s] = *reinterpret_cast<const f4 *>(&KVs[(wn * 32 + li) * ATT_DP + c * 32 + lh * 16 + 4 * s]);
+                af[s] = *reinterpret_cast<const f4 *>(&Qs[(wm * 32 + li) * ATT_P + c * 32 + lh * 16 + 4 * s]);
+                bf[s] = *reinterpret_cast<const f4 *>(&Ks[(wn * 32 + li) * ATT_P + c * 32 + lh * 16 + 4 * s]);
             }
 #pragma unroll
             for (int s = 0; s < 4; ++s)
@@ -98,59 +136,73 @@ __global__ void __launch_bounds__(256) attention_kernel(const AttnDev p) {
                     acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[s][e], bf[s][e], acc, 0, 0, 0);
         }
         // register r of lane (li, lh): query row 8 (r / 4) + 4 lh + r % 4, key column li
-        const int key = kb * ATT_BK + wn * 32 + li;
+        const int key = k0 + wn * 32 + li;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int row = wm * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
-            Ss[row * ATT_SP + key] = key < p.Skv ? acc[r] * p.scale : -__builtin_huge_valf();
-        }
-    }
-    __syncthreads();
-
-    // 3. softmax over each row's Skv scores: four neighbouring lanes share a row
-    {
-        const int row = tid >> 2, part = tid & 3;
-        float *srow = &Ss[row * ATT_SP];
-        const int ncol = kblocks * ATT_BK;
-        float m = -__builtin_huge_valf();
-        for (int j = part; j < ncol; j += 4) m = fmaxf(m, srow[j]);
-        m = fmaxf(m, __shfl_xor(m, 1, 64));
-        m = fmaxf(m, __shfl_xor(m, 2, 64));
-        float sum = 0.f;
-        for (int j = part; j < ncol; j += 4) {
-            const float e = srow[j] == -__builtin_huge_valf() ? 0.f : expf(srow[j] - m);
-            srow[j] = e;
-            sum += e;
-        }
-        sum += __shfl_xor(sum, 1, 64);
-        sum += __shfl_xor(sum, 2, 64);
-        const float inv = 1.0f / sum;
-        for (int j = part; j < ncol; j += 4) srow[j] *= inv;
-    }
-
-    // 4. O = P V, one 64-key block of V at a time (V^T in LDS: [d][key])
-    floatx16 oacc;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) oacc[r] = 0.f;
-    for (int kb = 0; kb < kblocks; ++kb) {
-        __syncthreads();  // probabilities written, KVs free
-        for (int e = tid; e < ATT_BK * (ATT_DMAX / 4); e += 256) {
-            const int r = e / (ATT_DMAX / 4), c4 = e - r * (ATT_DMAX / 4);
-            const int key = kb * ATT_BK + r;
-            f4 v = zero4;
-            if (key < p.Skv && c4 < D4) v = *reinterpret_cast<const f4 *>(vbase + (long)key * p.v_s + c4 * 4);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) KVs[(c4 * 4 + j) * ATT_DP + r] = v[j];
+            const int q = q0 + row;
+            float t;
+            if (key >= p.Skv) {
+                t = NEG_INF;
+            } else if (q >= p.S) {
+                t = 0.f;
+            } else {
+                t = scale_div ? acc[r] / scale : acc[r] * scale;
+                if (bias) t += bias[(long)q * p.bias_s + (long)key * p.bias_j];
+                bool keep = true;
+                if (causal) keep = key <= q;
+                else if (mask) keep = (mask[(long)q * p.mask_s + (long)key * p.mask_j] != 0) == keep_set;
+                if (!keep) t = fill;
+            }
+            Ps[row * ATT_P + wn * 32 + li] = t;
         }
         __syncthreads();
+
+        // 3. running softmax over the block's 64 scores of each row (16 per thread)
+        {
+            float *prow = &Ps[srow * ATT_P + part * 16];
+            f4 x[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) x[c] = *reinterpret_cast<const f4 *>(prow + 4 * c);
+            float bm = NEG_INF;
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) bm = fmaxf(bm, x[c][e]);
+            bm = fmaxf(bm, __shfl_xor(bm, 1, 64));
+            bm = fmaxf(bm, __shfl_xor(bm, 2, 64));
+            const float m_new = fmaxf(m_run, bm);
+            const float alpha = m_new == NEG_INF ? 1.f : expf(m_run - m_new);
+            float sum = 0.f;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float pe = x[c][e] == NEG_INF ? 0.f : expf(x[c][e] - m_new);
+                    x[c][e] = pe;
+                    sum += pe;
+                }
+                *reinterpret_cast<f4 *>(prow + 4 * c) = x[c];
+            }
+            sum += __shfl_xor(sum, 1, 64);
+            sum += __shfl_xor(sum, 2, 64);
+            l_run = l_run * alpha + sum;
+            m_run = m_new;
+            if (part == 0) rowscale[srow] = alpha;
+        }
+        __syncthreads();
+
+        // 4. O = alpha O + P V for this block (V^T in LDS: [d][key])
         if (wn * 32 < D) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[r] *= rowscale[wm * 32 + (r >> 2) * 8 + lh * 4 + (r & 3)];
 #pragma unroll
             for (int c = 0; c < ATT_BK / 32; ++c) {
                 f4 af[4], bf[4];
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
-                    af[s] = *reinterpret_cast<const f4 *>(&Ss[(wm * 32 + li) * ATT_SP + kb * ATT_BK + c * 32 + lh * 16 + 4 * s]);
-                    bf[s] = *reinterpret_cast<const f4 *>(&KVs[(wn * 32 + li) * ATT_DP + c * 32 + lh * 16 + 4 * s]);
+                    af[s] = *reinterpret_cast<const f4 *>(&Ps[(wm * 32 + li) * ATT_P + c * 32 + lh * 16 + 4 * s]);
+                    bf[s] = *reinterpret_cast<const f4 *>(&Vt[(wn * 32 + li) * ATT_P + c * 32 + lh * 16 + 4 * s]);
                 }
 #pragma unroll
                 for (int s = 0; s < 4; ++s)
@@ -160,6 +212,9 @@ __global__ void __launch_bounds__(256) attention_kernel(const AttnDev p) {
             }
         }
     }
+    __syncthreads();  // every wave is past its last read of rowscale
+    if (part == 0) rowscale[srow] = 1.0f / l_run;
+    __syncthreads();
 
     // 5. O rows: register r of lane (li, lh) is query 8 (r / 4) + 4 lh + r % 4, column d = li
     const int d = wn * 32 + li;
@@ -167,8 +222,9 @@ __global__ void __launch_bounds__(256) attention_kernel(const AttnDev p) {
         float *obase = p.o + b * p.o_b + h * p.o_h + d;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int q = q0 + wm * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
-            if (q < p.S) obase[(long)q * p.o_s] = oacc[r];
+            const int row = wm * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
+            const int q = q0 + row;
+            if (q < p.S) obase[(long)q * p.o_s] = oacc[r] * rowscale[row];
         }
     }
 }
@@ -178,7 +234,7 @@ __global__ void __launch_bounds__(256) attention_kernel(const AttnDev p) {
 using namespace mgc;
 
 extern "C" int mgc_hip_attention_supported(int S, int Skv, int D) {
-    return S >= 1 && Skv >= 1 && Skv <= ATT_SMAX && D >= 4 && D <= ATT_DMAX && D % 4 == 0;
+    return S >= 1 && Skv >= 1 && D >= 4 && D <= ATT_DMAX && D % 4 == 0;
 }
 
 extern "C" void mgc_hip_attention(mgc_hip_exec *x, const mgc_hip_attention_args *a) {
@@ -186,6 +242,12 @@ extern "C" void mgc_hip_attention(mgc_hip_exec *x, const mgc_hip_attention_args 
     if (!mgc_hip_attention_supported(a->S, a->Skv, a->D)) {
         x->launch_error = (int)hipErrorInvalidValue;
         set_error("mgc_hip_attention: shape outside the kernel's limits", hipErrorInvalidValue);
+        return;
+    }
+    const long blocks = (long)a->B * a->H * ((a->S + ATT_BQ - 1) / ATT_BQ);
+    if (blocks > 0x7fffffffL) {
+        x->launch_error = (int)hipErrorInvalidValue;
+        set_error("mgc_hip_attention: grid too large", hipErrorInvalidValue);
         return;
     }
     AttnDev p;
@@ -211,6 +273,19 @@ extern "C" void mgc_hip_attention(mgc_hip_exec *x, const mgc_hip_attention_args 
     p.o_s = a->o_s;
     p.o_h = a->o_h;
     p.scale = a->scale;
-    const long blocks = (long)a->B * a->H * ((a->S + ATT_BQ - 1) / ATT_BQ);
+    p.scale_div = a->scale_div;
+    p.bias = a->bias;
+    p.bias_b = a->bias_b;
+    p.bias_h = a->bias_h;
+    p.bias_s = a->bias_s;
+    p.bias_j = a->bias_j;
+    p.mask = a->mask;
+    p.mask_b = a->mask_b;
+    p.mask_h = a->mask_h;
+    p.mask_s = a->mask_s;
+    p.mask_j = a->mask_j;
+    p.mask_keep = a->mask_keep;
+    p.causal = a->causal;
+    p.fill = a->fill;
     MGC_LAUNCH(x, attention_kernel, dim3((unsigned)blocks), dim3(256), 0, p);
 }

@@ -393,12 +393,34 @@ def bert_base(batch: int = 1, seq: int = 128, layers: int = 12, seed: int = 0) -
     )
 
 
+def gpt2(batch: int = 1, seq: int = 128, layers: int = 12, seed: int = 0) -> Graph:
+    """GPT-2 small (124M parameters): pre-LN decoder stack with the causal Where mask, tanh
+    GELU, weights ~ N(0, 0.02), and the tied vocabulary head x @ wte^T ([.., 768] x [768, 50257],
+    a FusedGemm with trans_b after O3), the pattern of the reference's causal sample
+    (samples.py:178-245) at GPT-2 size."""
+    return transformer(
+        batch=batch,
+        seq=seq,
+        d_model=768,
+        heads=12,
+        layers=layers,
+        vocab=50257,
+        gelu="tanh",
+        causal=True,
+        seed=seed,
+        weight_scale=0.02,
+        lm_head=True,
+        name="gpt2",
+    )
+
+
 CONFIGS: dict[str, Callable[..., Graph]] = {
     "single_gemm": single_gemm,
     "bottleneck": bottleneck,
     "resnet50": resnet50,
     "mobilenet_v2": mobilenet_v2,
     "bert_base": bert_base,
+    "gpt2": gpt2,
 }
 
 

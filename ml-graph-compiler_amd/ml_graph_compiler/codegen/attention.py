@@ -8,28 +8,39 @@ attention as a chain of separate nodes. After O3 (passes/fusion.py) one layer re
     tq = Transpose(Reshape(q, [B, S, H, D]), perm=[0, 2, 1, 3])
     tk = Transpose(Reshape(k, [B, S, H, D]), perm=[0, 2, 3, 1])
     tv = Transpose(Reshape(v, [B, S, H, D]), perm=[0, 2, 1, 3])
-    p = Softmax(Mul(MatMul(tq, tk), scale), axis=-1)
-    o = Transpose(MatMul(p, tv), perm=[0, 2, 1, 3])  [B, S, H, D]  (then Reshape to [B, S, H*D])
+    t = score ops (MatMul(tq, tk))                 [B, H, S, Skv]
+    o = Transpose(MatMul(Softmax(t, axis=-1), tv), perm=[0, 2, 1, 3])  (then Reshape to [B, S, H*D])
+
+The score ops between QK^T and the softmax are, in this order and each optional: a scale
+(Mul or Div by a scalar constant), an additive bias (Add of a float tensor that broadcasts
+over [B, H, S, Skv], e.g. BERT's padding mask) and a mask (Where(mask, t, fill) or
+Where(mask, fill, t) with a scalar constant fill, e.g. GPT's causal mask). They may be separate
+nodes or one FusedElementwise program (passes/loopfuse.py). A constant mask that keeps exactly
+the keys j <= s is recognized as causal, so the kernel needs no mask tensor and can skip key
+blocks past the diagonal.
 
 ``find_attention`` returns, for each such chain, the nodes a single mgc_hip_attention call
 replaces and the strided views it reads. The memory plan is not touched: the fused call writes
 the final Transpose's planned output, and the intermediate values simply never get written.
 A chain is taken only where that is safe: every intermediate has no other reader and is not a
-graph output, and the chain's nodes are contiguous in the schedule, so nothing else writes the
-arena between the QKV projection and the fused call. Where the planner reused the (by then
-dead) operand memory for the output, the match is marked ``staged``: the call writes a
+graph output, and no other node scheduled between the chain's first and last node writes over
+memory the fused call reads. Where the planner reused the (by then
+dead) memory of an operand for the output, the match is marked ``staged``: the call writes a
 scratch area past the planned arena and a copy moves the result into place.
 """
 
 from __future__ import annotations
 
 from dataclasses import dataclass, field
+from typing import Any
+
+import numpy as np
 
 from ..ir import Graph, Node, Value
 from ..memory import MemoryPlan
 
-ATT_SMAX = 256  # key count limit of the kernel (csrc/attention.hip)
-ATT_DMAX = 64   # head dim limit
+ATT_DMAX = 64   # head dim limit of the kernel (csrc/attention.hip)
+SCORE_OPS = ("Mul", "Div", "Add", "Where")
 
 
 @dataclass
@@ -38,6 +49,23 @@ class Operand:
     col: int          # element offset of the head-0 columns within a row
     row_stride: int   # elements between consecutive sequence positions
     batch_stride: int
+
+
+@dataclass
+class ScoreOps:
+    """What happens to t = Q K^T before the softmax: t = t * scale (t / scale when
+    ``divide``), t += bias, t = keep ? t : fill."""
+
+    scale: float = 1.0
+    divide: bool = False
+    bias: Value | None = None
+    mask: Value | None = None
+    mask_keep: bool = True       # keep the score where the mask element is true (else false)
+    fill: float = 0.0
+    causal: bool = False         # the mask is the constant "key <= query" pattern
+
+    def leaves(self) -> list[Value]:
+        return [v for v in (self.bias, self.mask) if v is not None]
 
 
 @dataclass
@@ -55,6 +83,7 @@ class AttentionMatch:
     emit_at: Node                    # where the fused call goes (that Transpose)
     absorbed: list[Node] = field(default_factory=list)
     staged: bool = False             # output overlaps an operand: write scratch, then copy
+    ops: ScoreOps = field(default_factory=ScoreOps)
 
 
 def _only_user(value: Value, node: Node, graph: Graph) -> bool:
@@ -99,16 +128,33 @@ def find_attention(graph: Graph, plan: MemoryPlan) -> list[AttentionMatch]:
             continue
         lo = min(order[id(n)] for n in m.absorbed)
         hi = max(order[id(n)] for n in m.absorbed)
-        ids = {id(n) for n in m.absorbed}
-        if any(id(n) not in ids for n in graph.nodes[lo : hi + 1]):
-            continue
         if m.emit_at is not graph.nodes[hi]:
             continue
-        # The planner may have put the output where the (by then dead) QKV projection was; the
-        # fused call then writes a scratch area past the planned arena and copies from there.
-        m.staged = any(_overlap(plan, op.value, m.out) for op in (m.q, m.k, m.v))
+        reads = [m.q.value, m.k.value, m.v.value, *m.ops.leaves()]
+        ids = {id(n) for n in m.absorbed}
+        if not all(_harmless(graph.nodes[i], i, reads, order, plan)
+                   for i in range(lo, hi + 1) if id(graph.nodes[i]) not in ids):
+            continue
+        # The planner may have put the output where a dead operand was (the QKV projection, a
+        # bias); the fused call then writes a scratch area past the planned arena and copies.
+        m.staged = any(_overlap(plan, v, m.out) for v in reads)
         found.append(m)
     return found
+
+
+def _harmless(node: Node, at: int, reads: list[Value], order: dict[int, int], plan: MemoryPlan) -> bool:
+    """A node the schedule put between the chain's first and last node (say, the computation of
+    a bias) still runs before the fused call, so once a value the call reads exists, the node
+    must not write over it: the planner may have reused the memory of an operand whose last
+    reader was an absorbed node. (Absorbed intermediates have no other readers, so such a node
+    cannot read one.)"""
+    if id(node) in plan.workspaces:
+        return False
+    for r in reads:
+        born = order.get(id(r.producer), -1) if r.producer is not None else -1
+        if at > born and any(_overlap(plan, out, r) for out in node.outputs):
+            return False
+    return True
 
 
 def _overlap(plan: MemoryPlan, a: Value, b: Value) -> bool:
@@ -121,6 +167,118 @@ def _overlap(plan: MemoryPlan, a: Value, b: Value) -> bool:
     return a0 < b0 + b.tensor_type.nbytes and b0 < a0 + a.tensor_type.nbytes
 
 
+# -- the score ops between QK^T and the softmax -------------------------------------------------
+
+_Expr = tuple[Any, ...]  # ("S", matmul) | ("leaf", value) | (op, [children])
+
+
+def _leads_to_matmul(v: Value | None, depth: int = 0) -> bool:
+    if v is None or depth > 8:
+        return False
+    p = v.producer
+    if p is None:
+        return False
+    if p.op == "MatMul":
+        return True
+    if p.op in SCORE_OPS or p.op == "FusedElementwise":
+        return any(_leads_to_matmul(u, depth + 1) for u in p.inputs)
+    return False
+
+
+def _score_expr(v: Value, consumer: Node, graph: Graph, absorbed: list[Node]) -> _Expr | None:
+    """Expression tree of a value on the score path (the path from QK^T to the softmax)."""
+    p = v.producer
+    if p is None or not _only_user(v, consumer, graph):
+        return None
+    if p.op == "MatMul":
+        return ("S", p)
+    on_path = [i for i, u in enumerate(p.inputs) if _leads_to_matmul(u)]
+    if len(on_path) != 1 or len(p.outputs) != 1:
+        return None
+    if p.op in SCORE_OPS:
+        absorbed.append(p)
+        inner = _score_expr(p.inputs[on_path[0]], p, graph, absorbed)
+        if inner is None:
+            return None
+        return (p.op, [inner if i == on_path[0] else ("leaf", u) for i, u in enumerate(p.inputs)])
+    if p.op == "FusedElementwise":
+        absorbed.append(p)
+        inner = _score_expr(p.inputs[on_path[0]], p, graph, absorbed)
+        if inner is None:
+            return None
+        n = len(p.inputs)
+        results: list[_Expr] = []
+        for op, attrs, args in p.attrs.get("program", []):
+            if op not in SCORE_OPS or attrs or any(a < 0 or a >= n + len(results) for a in args):
+                return None
+            kids = [results[a - n] if a >= n else inner if a == on_path[0] else ("leaf", p.inputs[a]) for a in args]
+            results.append((op, kids))
+        return results[-1] if results else None
+    return None
+
+
+def _on_path(e: _Expr) -> bool:
+    return e[0] != "leaf"
+
+
+def _broadcasts(v: Value, shape: tuple[int, ...]) -> bool:
+    t = v.type
+    if t is None or t.rank > len(shape):
+        return False
+    return all(d in (1, full) for d, full in zip(t.shape, shape[len(shape) - t.rank :]))
+
+
+def _score_ops(e: _Expr, score_shape: tuple[int, ...]) -> tuple[ScoreOps, Node] | None:
+    """Peel Where, then Add, then Mul/Div off the tree (the order the kernel applies them in
+    reverse); what remains must be QK^T itself."""
+    ops = ScoreOps()
+    if e[0] == "Where":
+        c, a, b = e[1]
+        if c[0] != "leaf" or c[1].type is None or c[1].type.dtype != "bool" or not _broadcasts(c[1], score_shape):
+            return None
+        if _on_path(a) and not _on_path(b):
+            keep, fill, e = True, b[1], a
+        elif _on_path(b) and not _on_path(a):
+            keep, fill, e = False, a[1], b
+        else:
+            return None
+        f = _scalar(fill)
+        if f is None or fill.type is None or fill.type.dtype != "float32":
+            return None
+        ops.mask, ops.mask_keep, ops.fill = c[1], keep, f
+    if e[0] == "Add":
+        x, y = e[1]
+        path, other = (x, y) if _on_path(x) else (y, x)
+        if _on_path(other) or other[1].type is None or other[1].type.dtype != "float32":
+            return None
+        if not _broadcasts(other[1], score_shape):
+            return None
+        ops.bias, e = other[1], path
+    if e[0] in ("Mul", "Div"):
+        x, y = e[1]
+        if e[0] == "Div" and not _on_path(x):
+            return None
+        path, other = (x, y) if _on_path(x) else (y, x)
+        if _on_path(other):
+            return None
+        c = _scalar(other[1])
+        if c is None or c == 0.0 or other[1].type is None or other[1].type.dtype != "float32":
+            return None
+        ops.scale, ops.divide, e = c, e[0] == "Div", path
+    if e[0] != "S":
+        return None
+    if ops.mask is not None and ops.mask.data is not None:
+        ops.causal = _is_causal(ops.mask.data, ops.mask_keep, score_shape)
+    return ops, e[1]
+
+
+def _is_causal(mask: np.ndarray, keep_set: bool, score_shape: tuple[int, ...]) -> bool:
+    """True when the constant mask keeps exactly the keys j <= s in every (batch, head)."""
+    S, Skv = score_shape[-2:]
+    keep = np.broadcast_to(np.asarray(mask, bool), score_shape) == keep_set
+    return bool(np.array_equal(keep, np.broadcast_to(np.tril(np.ones((S, Skv), bool)), score_shape)))
+
+
 def _match(sm: Node, graph: Graph) -> AttentionMatch | None:
     if sm.op != "Softmax":
         return None
@@ -131,26 +289,13 @@ def _match(sm: Node, graph: Graph) -> AttentionMatch | None:
     if axis not in (-1, 3):
         return None
     absorbed = [sm]
-    scale = 1.0
-    prod = x.producer
-    if prod is not None and prod.op in ("Mul", "Div"):
-        if not _only_user(x, sm, graph):
-            return None
-        a, b = prod.input(0), prod.input(1)
-        c = _scalar(b)
-        s_in = a
-        if c is None and prod.op == "Mul":
-            c, s_in = _scalar(a), b
-        if c is None or c == 0.0:
-            return None
-        scale = c if prod.op == "Mul" else 1.0 / c
-        absorbed.append(prod)
-        x_user, x = prod, s_in
-    else:
-        x_user = sm
-    qk = x.producer
-    if qk is None or qk.op != "MatMul" or not _only_user(x, x_user, graph):
+    expr = _score_expr(x, sm, graph, absorbed)
+    if expr is None:
         return None
+    found = _score_ops(expr, x.type.shape)
+    if found is None:
+        return None
+    ops, qk = found
     absorbed.append(qk)
     p = sm.output
     if len(p.users) != 1 or p in graph.outputs:
@@ -175,14 +320,14 @@ def _match(sm: Node, graph: Graph) -> AttentionMatch | None:
         views.append(hv[0])
         absorbed += hv[1]
     qs, ks, vs = views
-    for v in (qs, ks, vs, tq, tk, tv, o, x, p):
+    for v in (qs, ks, vs, tq, tk, tv, o, p, qk.output):
         if v.type is None or v.type.dtype != "float32":
             return None
     B, H, S, D = tq.type.shape
     Skv = tk.type.shape[3]
     if tk.type.shape != (B, H, D, Skv) or tv.type.shape != (B, H, Skv, D) or o.type.shape != (B, H, S, D):
         return None
-    if not (1 <= Skv <= ATT_SMAX and 4 <= D <= ATT_DMAX and D % 4 == 0):
+    if x.type.shape != (B, H, S, Skv) or not (Skv >= 1 and 4 <= D <= ATT_DMAX and D % 4 == 0):
         return None
     HD = H * D
     operands = None
@@ -201,5 +346,5 @@ def _match(sm: Node, graph: Graph) -> AttentionMatch | None:
         operands = [Operand(qs, 0, HD, S * HD), Operand(ks, 0, HD, Skv * HD), Operand(vs, 0, HD, Skv * HD)]
     if HD % 4:
         return None
-    return AttentionMatch(B=B, H=H, S=S, Skv=Skv, D=D, scale=scale, q=operands[0], k=operands[1],
-                          v=operands[2], out=tr.output, emit_at=tr, absorbed=absorbed)
+    return AttentionMatch(B=B, H=H, S=S, Skv=Skv, D=D, scale=ops.scale, q=operands[0], k=operands[1],
+                          v=operands[2], out=tr.output, emit_at=tr, absorbed=absorbed, ops=ops)

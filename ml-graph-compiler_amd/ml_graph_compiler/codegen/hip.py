@@ -840,8 +840,19 @@ class HipEmitter:
             f"t.k = {view(m.k)}; t.k_b = {m.k.batch_stride}L; t.k_s = {m.k.row_stride}L; t.k_h = {m.D}L;",
             f"t.v = {view(m.v)}; t.v_b = {m.v.batch_stride}L; t.v_s = {m.v.row_stride}L; t.v_h = {m.D}L;",
             f"t.o = {out}; t.o_b = {m.S * m.H * m.D}L; t.o_s = {m.H * m.D}L; t.o_h = {m.D}L;",
-            f"t.scale = {_f(m.scale)};",
+            f"t.scale = {_f(m.ops.scale)}; t.scale_div = {int(m.ops.divide)};",
         ]
+        if m.ops.bias is not None:
+            sb, sh, sq, sk = self._score_strides(m.ops.bias)
+            fields.append(f"t.bias = {self.fptr(m.ops.bias)}; t.bias_b = {sb}L; t.bias_h = {sh}L; "
+                          f"t.bias_s = {sq}L; t.bias_j = {sk}L;")
+        if m.ops.causal:
+            fields.append(f"t.causal = 1; t.fill = {_f(m.ops.fill)};")
+        elif m.ops.mask is not None:
+            sb, sh, sq, sk = self._score_strides(m.ops.mask)
+            fields.append(f"t.mask = (const unsigned char *){self.ptr(m.ops.mask)}; t.mask_b = {sb}L; "
+                          f"t.mask_h = {sh}L; t.mask_s = {sq}L; t.mask_j = {sk}L; "
+                          f"t.mask_keep = {int(m.ops.mask_keep)}; t.fill = {_f(m.ops.fill)};")
         self.emit("{ mgc_hip_attention_args t; memset(&t, 0, sizeof t);")
         for f_ in fields:
             self.emit("  " + f_)
@@ -850,6 +861,14 @@ class HipEmitter:
         if m.staged:
             nbytes = m.out.tensor_type.nbytes
             self.copy((nbytes,), self.ptr(m.out), [1], 0, f"(A + {self._scratch_off})", [1], 0, 1)
+
+    @staticmethod
+    def _score_strides(value: Value) -> list[int]:
+        """Element strides over (batch, head, query, key) of a tensor that broadcasts over the
+        attention scores [B, H, S, Skv]: 0 for a broadcast dimension."""
+        shape = (1,) * (4 - value.tensor_type.rank) + tuple(value.tensor_type.shape)
+        strides = _strides(shape)
+        return [0 if d == 1 else st for d, st in zip(shape, strides)]
 
     # -- convolution and pooling ---------------------------------------------------------------
     @staticmethod

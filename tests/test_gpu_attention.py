@@ -1,9 +1,13 @@
 """Fused attention (mgc_hip_attention) against the oracle running the unfused chain.
 
 The graphs are the chain the transformer sample builds (head-split Reshape/Transpose, QK^T,
-scale, Softmax, PV, head-merge Transpose), at sizes that exercise the kernel's edges: a query
-count that is not a multiple of the 64-row block, key counts that span several 64-key blocks
-and end mid-block, a head dim below 64, separate Q/K/V tensors and a fused QKV projection.
+score ops, Softmax, PV, head-merge Transpose), at sizes that exercise the kernel's edges: a
+query count that is not a multiple of the 64-row block, key counts that span several 64-key
+blocks and end mid-block, long sequences (the keys stream through a running softmax), a head
+dim below 64, separate Q/K/V tensors and a fused QKV projection. The score ops cover what the
+matcher accepts: Mul or Div by a scalar, an additive bias (constant or computed at run time,
+broadcast over heads or queries), and a Where mask in both polarities (constant causal with a
+finite or -inf fill, an arbitrary constant mask, a mask fed as an input).
 """
 
 from __future__ import annotations
@@ -22,8 +26,15 @@ from ml_graph_compiler.schedule import schedule
 from ml_graph_compiler.shape_inference import infer_shapes
 from oracle import interpreter as oracle
 
+rng = np.random.default_rng(7)
 
-def attention_graph(B: int, H: int, S: int, Skv: int, D: int, fused_qkv: bool, scale: float = 0.125):
+
+def attention_graph(B: int, H: int, S: int, Skv: int, D: int, fused_qkv: bool, scale: float = 0.125,
+                    divide: bool = False, bias: str | None = None, mask: str | None = None,
+                    keep_true: bool = False, fill: float = -1e4):
+    """``bias``: None, "const" ([1, H, S, Skv]) or "input" ([B, 1, 1, Skv], BERT's padding form);
+    ``mask``: None, "causal", "random" (constant [S, Skv]) or "input" ([B, 1, S, Skv] bool);
+    ``keep_true``: Where(mask, t, fill) instead of Where(mask, fill, t)."""
     g = Graph("attention")
     HD = H * D
     feeds = {}
@@ -48,9 +59,41 @@ def attention_graph(B: int, H: int, S: int, Skv: int, D: int, fused_qkv: bool, s
     tk = heads(k, Skv, [0, 2, 3, 1], "k")
     tv = heads(v, Skv, [0, 2, 1, 3], "v")
     s = g.add_node("MatMul", [tq, tk], 1, {}, name="qk", output_names=["scores"]).output
-    c = g.constant(np.array(scale, np.float32), "scale")
-    sc = g.add_node("Mul", [s, c], 1, {}, name="scale_mul", output_names=["scaled"]).output
-    p = g.add_node("Softmax", [sc], 1, {"axis": -1}, name="softmax", output_names=["probs"]).output
+    if divide:
+        c = g.constant(np.array(1.0 / scale, np.float32), "denom")
+        s = g.add_node("Div", [s, c], 1, {}, name="scale_div", output_names=["scaled"]).output
+    else:
+        c = g.constant(np.array(scale, np.float32), "scale")
+        s = g.add_node("Mul", [c, s], 1, {}, name="scale_mul", output_names=["scaled"]).output
+    if bias == "const":
+        bv = g.constant((rng.standard_normal((1, H, S, Skv)) * 0.5).astype(np.float32), "bias")
+        s = g.add_node("Add", [s, bv], 1, {}, name="bias_add", output_names=["biased"]).output
+    elif bias == "input":
+        keep = g.add_input("attention_mask", TensorType("float32", (B, Skv)))
+        feeds["attention_mask"] = (rng.random((B, Skv)) < 0.8).astype(np.float32)
+        r = g.add_node("Reshape", [keep], 1, {"shape": [B, 1, 1, Skv]}, name="mask_r", output_names=["mask_4d"]).output
+        one = g.constant(np.array(1.0, np.float32), "one")
+        big = g.constant(np.array(-1e4, np.float32), "big")
+        inv = g.add_node("Sub", [one, r], 1, {}, name="mask_inv", output_names=["mask_inv"]).output
+        add = g.add_node("Mul", [inv, big], 1, {}, name="mask_scale", output_names=["mask_add"]).output
+        s = g.add_node("Add", [add, s], 1, {}, name="bias_add", output_names=["biased"]).output
+    if mask is not None:
+        if mask == "causal":
+            drop = np.triu(np.ones((S, Skv), bool), 1)[None, None]
+            m = g.constant(~drop if keep_true else drop, "mask")
+        elif mask == "random":
+            drop = rng.random((S, Skv)) < 0.3
+            drop[:, 0] = False  # every row keeps a key
+            m = g.constant(~drop if keep_true else drop, "mask")
+        else:
+            m = g.add_input("mask", TensorType("bool", (B, 1, S, Skv)))
+            drop = rng.random((B, 1, S, Skv)) < 0.3
+            drop[..., 0] = False
+            feeds["mask"] = ~drop if keep_true else drop
+        f = g.constant(np.array(fill, np.float32), "fill")
+        args = [m, s, f] if keep_true else [m, f, s]
+        s = g.add_node("Where", args, 1, {}, name="mask_where", output_names=["masked"]).output
+    p = g.add_node("Softmax", [s], 1, {"axis": -1}, name="softmax", output_names=["probs"]).output
     o = g.add_node("MatMul", [p, tv], 1, {}, name="pv", output_names=["ctx"]).output
     to = g.add_node("Transpose", [o], 1, {"perm": [0, 2, 1, 3]}, name="merge", output_names=["merged"]).output
     y = g.add_node("Reshape", [to], 1, {"shape": [B, S, HD]}, name="flat", output_names=["y"]).output
@@ -67,6 +110,14 @@ def _run(graph, feeds, cache, opt="O3"):
         model.release()
 
 
+def _check(g, feeds, hip_cache, opt="O3", fused=True):
+    expected = oracle.run_graph(g, feeds)["y"]
+    got, kernels = _run(g, feeds, hip_cache, opt)
+    assert (kernels.get("attention") == 1) if fused else ("attention" not in kernels), kernels
+    err = float(np.max(np.abs(got["y"].astype(np.float64) - expected)))
+    assert err <= 2e-5 * max(1.0, float(np.max(np.abs(expected)))), err
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize(
     "B, H, S, Skv, D, fused_qkv",
@@ -75,55 +126,110 @@ def _run(graph, feeds, cache, opt="O3"):
         (1, 2, 50, 200, 64, False),  # separate Q/K/V, 4 key blocks (last partial), S != Skv
         (3, 4, 128, 128, 64, True),  # BERT's shape per head, two query blocks
         (1, 2, 3, 5, 4, False),      # tiny: one query block, one partial key block, D = 4
-        (2, 2, 256, 256, 32, True),  # key limit, D of one MFMA column block
+        (2, 2, 256, 256, 32, True),  # D of one MFMA column block
+        (1, 2, 16, 300, 16, False),  # keys past the old 256 limit
+        (1, 3, 700, 700, 64, True),  # long sequence: 11 query blocks x 11 key blocks
     ],
 )
 def test_fused_attention_matches_oracle(B, H, S, Skv, D, fused_qkv, hip_cache):
     g, feeds = attention_graph(B, H, S, Skv, D, fused_qkv)
-    expected = oracle.run_graph(g, feeds)["y"]
-    got, kernels = _run(g, feeds, hip_cache)
-    assert kernels.get("attention") == 1, kernels
-    err = float(np.max(np.abs(got["y"].astype(np.float64) - expected)))
-    assert err <= 2e-5 * max(1.0, float(np.max(np.abs(expected)))), err
+    _check(g, feeds, hip_cache)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize(
+    "case",
+    [
+        dict(mask="causal"),                                 # GPT sample form: Where(mask, -1e4, t)
+        dict(mask="causal", fill=-np.inf, keep_true=True),   # -inf fill: blocks past the diagonal skipped
+        dict(mask="causal", fill=-3.4028235e38),             # finfo.min fill
+        dict(mask="random", keep_true=True),
+        dict(mask="input"),
+        dict(bias="const", divide=True),
+        dict(bias="input"),
+        dict(bias="input", mask="causal", fill=-np.inf),
+    ],
+    ids=lambda c: "-".join(f"{k}={v}" for k, v in c.items()),
+)
+@pytest.mark.parametrize("opt", ["O2", "O3"])  # separate nodes, then one FusedElementwise program
+def test_masked_and_biased_attention(case, opt, hip_cache):
+    g, feeds = attention_graph(2, 3, 150, 150, 64, True, scale=0.125, **case)
+    _check(g, feeds, hip_cache, opt)
+
+
+@pytest.mark.gpu
+def test_causal_long_sequence(hip_cache):
+    g, feeds = attention_graph(1, 2, 1030, 1030, 64, True, mask="causal", fill=-np.inf)
+    _check(g, feeds, hip_cache)
 
 
 @pytest.mark.gpu
 def test_attention_outside_limits_stays_unfused(hip_cache):
-    g, feeds = attention_graph(1, 2, 16, 300, 16, False)  # Skv > 256
-    expected = oracle.run_graph(g, feeds)["y"]
-    got, kernels = _run(g, feeds, hip_cache)
-    assert "attention" not in kernels
-    assert float(np.max(np.abs(got["y"].astype(np.float64) - expected))) <= 2e-5
+    g, feeds = attention_graph(1, 2, 16, 40, 80, False)  # D > 64
+    _check(g, feeds, hip_cache, fused=False)
 
 
 @pytest.mark.gpu
-def test_fused_and_unfused_tiny_bert_agree(hip_cache, monkeypatch):
-    feeds = oracle.random_feeds(builders.tiny_bert(), 0, int_high=50)
-    expected = oracle.run_graph(builders.tiny_bert(), feeds)
+@pytest.mark.parametrize("sample", ["tiny-bert", "tiny-gpt"])
+def test_fused_and_unfused_samples_agree(sample, hip_cache, monkeypatch):
+    build = builders.SAMPLES[sample]
+    feeds = oracle.random_feeds(build(), 0, int_high=50)
+    expected = oracle.run_graph(build(), feeds)
     outs = {}
     for fuse in (True, False):
         monkeypatch.setattr(hip_codegen, "FUSE_ATTENTION", fuse)
-        got, kernels = _run(builders.tiny_bert(), feeds, hip_cache)
-        assert ("attention" in kernels) == fuse
+        got, kernels = _run(build(), feeds, hip_cache)
+        assert kernels.get("attention", 0) == (2 if fuse else 0)
         outs[fuse] = got
     for name, want in expected.items():
         for fuse in (True, False):
             assert float(np.max(np.abs(outs[fuse][name].astype(np.float64) - want))) <= 5e-5
 
 
-def test_matcher_finds_every_bert_layer():
+def test_matcher_finds_every_bert_and_gpt_layer():
     """CPU: all 12 BERT-base layers match (staged: the planner put the context where the dead
-    QKV projection was); the causal GPT sample, whose mask sits between scale and softmax, does
-    not."""
+    QKV projection was); the causal GPT sample's Where mask is recognized as causal."""
     g = builders.bert_base(1)
     optimize(g, "O3")
     schedule(g)
     found = attn.find_attention(g, plan_memory(g, alignment=256))
     assert len(found) == 12
     assert all(m.S == 128 and m.Skv == 128 and m.D == 64 and m.H == 12 for m in found)
-    assert all(abs(m.scale - 0.125) < 1e-7 for m in found)
+    assert all(abs(m.ops.scale - 0.125) < 1e-7 and m.ops.mask is None for m in found)
     assert all(len(m.absorbed) == 12 for m in found)  # split, 3 x (reshape, transpose), qk, mul, softmax, pv, merge
     gpt = builders.tiny_gpt()
     optimize(gpt, "O3")
     schedule(gpt)
-    assert attn.find_attention(gpt, plan_memory(gpt, alignment=256)) == []
+    found = attn.find_attention(gpt, plan_memory(gpt, alignment=256))
+    assert len(found) == 2
+    assert all(m.ops.causal and not m.ops.mask_keep and m.ops.fill == -1e4 for m in found)
+
+
+def test_matcher_score_op_forms():
+    """CPU: the score ops the matcher takes, and the ones it leaves unfused."""
+    def ops_of(opt="O3", **case):
+        g, _ = attention_graph(1, 2, 40, 40, 16, True, **case)
+        optimize(g, opt)
+        schedule(g)
+        found = attn.find_attention(g, plan_memory(g, alignment=256))
+        return found[0].ops if found else None
+
+    assert ops_of(divide=True, opt="O0").divide and ops_of(divide=True, opt="O0").scale == 8.0
+    assert not ops_of(divide=True).divide  # O3 turns the division by a constant into a product
+    m = ops_of(mask="causal", keep_true=True)
+    assert m.causal and m.mask_keep
+    m = ops_of(mask="random")
+    assert not m.causal and m.mask is not None and not m.mask_keep
+    assert ops_of(bias="input", opt="O2").bias is not None
+    assert ops_of(bias="const", mask="input").mask is not None
+    # a mask applied before the bias is not the kernel's order
+    g, _ = attention_graph(1, 2, 40, 40, 16, True, mask="causal")
+    w = next(n for n in g.nodes if n.op == "Where")
+    sm = next(n for n in g.nodes if n.op == "Softmax")
+    extra = g.constant(np.full((1, 1, 40, 40), 0.5, np.float32), "late_bias")
+    late = g.add_node("Add", [w.output, extra], 1, {}, name="late_add", output_names=["late"], index=g.nodes.index(sm))
+    g.set_input(sm, 0, late.output)
+    infer_shapes(g)
+    optimize(g, "O2")
+    schedule(g)
+    assert attn.find_attention(g, plan_memory(g, alignment=256)) == []

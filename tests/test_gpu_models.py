@@ -134,6 +134,25 @@ def test_bert_base(batch, hip_cache):
         assert err <= 5e-4
 
 
+@pytest.mark.parametrize("batch", [1, 8])
+def test_gpt2(batch, hip_cache):
+    """GPT-2 small at sequence 128: fused causal attention and the tied 50257-wide head."""
+    print(f"[gpu] gpt2 b{batch}", flush=True)
+    graph = builders.gpt2(batch)
+    feeds = oracle.random_feeds(graph, 8, int_high=50257)
+    model = compile_hip(builders.gpt2(batch), hip_cache)
+    assert model.report.kernels.get("attention") == 12
+    got = model.run(feeds)["logits"]
+    model.release()
+    single = builders.gpt2(1)
+    for i in ([0] if batch == 1 else [0, batch - 1]):
+        expected = oracle.run_graph(single, {"input_ids": feeds["input_ids"][i : i + 1]})["logits"]
+        err, scale = _rel_err(got[i : i + 1], expected)
+        print(f"[gpu] gpt2 b{batch} sequence {i}: max-abs {err:.3e} max|logit| {scale:.3e}", flush=True)
+        assert err <= 5e-4
+        assert np.array_equal(np.argmax(got[i], -1), np.argmax(expected[0], -1))
+
+
 def test_gather_out_of_range_raises(hip_cache):
     from ml_graph_compiler.errors import GraphError
 
