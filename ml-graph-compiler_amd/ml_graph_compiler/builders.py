@@ -175,13 +175,16 @@ def transformer(
     lm_head: bool = True,
     ln_eps: float = 1e-5,
     name: str = "tiny_transformer",
+    separate_qkv: bool = False,
 ) -> Graph:
     """Pre-LN causal tanh-GELU (GPT-2 style) or post-LN erf-GELU (BERT style) encoder.
 
     With the defaults this is the reference's tiny_transformer sample. ``weight_scale`` fixes
     the std of every weight (BERT config: 0.02); ``unit_layer_norm`` makes every LN gamma 1 and
     beta 0; ``embedding_norm`` adds BERT's LayerNorm after the embeddings; ``lm_head`` adds the
-    tied vocabulary projection (otherwise the output is the last hidden state).
+    tied vocabulary projection (otherwise the output is the last hidden state);
+    ``separate_qkv`` projects Q, K and V with three Dense layers, as Hugging Face models export,
+    instead of one Dense and a Split.
     """
     b = GraphBuilder(name, seed)
     ids = b.input("input_ids", "int64", (batch, seq))
@@ -209,8 +212,11 @@ def transformer(
     pre_ln = gelu == "tanh"
     for _ in range(layers):
         h = ln(x) if pre_ln else x
-        qkv = dense(h, d_model, 3 * d_model)
-        q, k, v = b.op("Split", [qkv, b.const(np.asarray([d_model] * 3, np.int64), "split")], 3, axis=-1)
+        if separate_qkv:
+            q, k, v = (dense(h, d_model, d_model) for _ in range(3))
+        else:
+            qkv = dense(h, d_model, 3 * d_model)
+            q, k, v = b.op("Split", [qkv, b.const(np.asarray([d_model] * 3, np.int64), "split")], 3, axis=-1)
 
         def heads_first(t: Value) -> Value:
             return b.op1("Transpose", [_dynamic_reshape(b, t, [heads, dh])], perm=[0, 2, 1, 3])
@@ -368,11 +374,12 @@ def mobilenet_v2(batch: int = 1, classes: int = 1000, seed: int = 0) -> Graph:
     return b.finish([("logits", logits)])
 
 
-def bert_base(batch: int = 1, seq: int = 128, layers: int = 12, seed: int = 0) -> Graph:
+def bert_base(batch: int = 1, seq: int = 128, layers: int = 12, seed: int = 0, separate_qkv: bool = False) -> Graph:
     """Config 5: BERT-base encoder, post-LN, erf GELU, weights ~ N(0, 0.02), LN gamma 1 beta 0.
 
     The embeddings (word + position, then LayerNorm) feed 12 encoder layers; the output is the
-    last hidden state [batch, seq, 768] (no pooler, no vocabulary head).
+    last hidden state [batch, seq, 768] (no pooler, no vocabulary head). ``separate_qkv`` gives
+    the Hugging Face export's three Q/K/V projections instead of the sample's fused one.
     """
     return transformer(
         batch=batch,
@@ -390,6 +397,7 @@ def bert_base(batch: int = 1, seq: int = 128, layers: int = 12, seed: int = 0) -
         lm_head=False,
         ln_eps=1e-12,
         name="bert_base",
+        separate_qkv=separate_qkv,
     )
 
 

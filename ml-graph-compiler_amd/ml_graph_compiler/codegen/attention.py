@@ -84,6 +84,16 @@ class AttentionMatch:
     absorbed: list[Node] = field(default_factory=list)
     staged: bool = False             # output overlaps an operand: write scratch, then copy
     ops: ScoreOps = field(default_factory=ScoreOps)
+    # Q, K and V projected by three FusedGemms of one input (Hugging Face exports): the fused
+    # call runs them as one GEMM with the weights side by side, into a [B*S, 3*H*D] scratch
+    # area that the attention kernel then reads like a fused QKV projection.
+    qkv_gemms: list[Node] = field(default_factory=list)
+
+    def reads(self) -> list[Value]:
+        """Values the fused call reads from memory the plan manages."""
+        if self.qkv_gemms:
+            return [self.qkv_gemms[0].input(0), *self.ops.leaves()]
+        return [self.q.value, self.k.value, self.v.value, *self.ops.leaves()]
 
 
 def _only_user(value: Value, node: Node, graph: Graph) -> bool:
@@ -130,14 +140,16 @@ def find_attention(graph: Graph, plan: MemoryPlan) -> list[AttentionMatch]:
         hi = max(order[id(n)] for n in m.absorbed)
         if m.emit_at is not graph.nodes[hi]:
             continue
-        reads = [m.q.value, m.k.value, m.v.value, *m.ops.leaves()]
+        reads = m.reads()
         ids = {id(n) for n in m.absorbed}
         if not all(_harmless(graph.nodes[i], i, reads, order, plan)
                    for i in range(lo, hi + 1) if id(graph.nodes[i]) not in ids):
             continue
         # The planner may have put the output where a dead operand was (the QKV projection, a
         # bias); the fused call then writes a scratch area past the planned arena and copies.
-        m.staged = any(_overlap(plan, v, m.out) for v in reads)
+        # (A grouped projection's input is consumed by its GEMM before the output is written.)
+        attn_reads = m.ops.leaves() if m.qkv_gemms else reads
+        m.staged = any(_overlap(plan, v, m.out) for v in attn_reads)
         found.append(m)
     return found
 
@@ -346,5 +358,43 @@ def _match(sm: Node, graph: Graph) -> AttentionMatch | None:
         operands = [Operand(qs, 0, HD, S * HD), Operand(ks, 0, HD, Skv * HD), Operand(vs, 0, HD, Skv * HD)]
     if HD % 4:
         return None
-    return AttentionMatch(B=B, H=H, S=S, Skv=Skv, D=D, scale=ops.scale, q=operands[0], k=operands[1],
-                          v=operands[2], out=tr.output, emit_at=tr, absorbed=absorbed, ops=ops)
+    m = AttentionMatch(B=B, H=H, S=S, Skv=Skv, D=D, scale=ops.scale, q=operands[0], k=operands[1],
+                       v=operands[2], out=tr.output, emit_at=tr, absorbed=absorbed, ops=ops)
+    if sp is None or sp.op != "Split":
+        gemms = _qkv_gemms(m, graph)
+        if gemms:
+            m.qkv_gemms = gemms
+            m.absorbed += gemms
+    return m
+
+
+def _gemm_form(node: Node) -> tuple[Any, ...] | None:
+    if node.op != "FusedGemm" or node.optional_input(3) is not None or node.input(1).data is None:
+        return None
+    bias = node.optional_input(2)
+    if bias is not None and (bias.data is None or bias.data.size != node.output.tensor_type.shape[-1]):
+        return None
+    return (id(node.input(0)), int(node.attrs.get("trans_b", 0)), str(node.attrs.get("activation", "none")),
+            float(node.attrs.get("clip_min", 0.0)), float(node.attrs.get("clip_max", 6.0)), bias is None,
+            node.input(1).tensor_type.shape)
+
+
+def _qkv_gemms(m: AttentionMatch, graph: Graph) -> list[Node]:
+    """The three FusedGemms of one input that produce Q, K and V, when their outputs feed only
+    the head-split Reshapes this chain absorbs."""
+    nodes = []
+    for op in (m.q, m.k, m.v):
+        v = op.value
+        p = v.producer
+        if p is None or v in graph.outputs or len(v.users) != 1 or v.users[0].op != "Reshape":
+            return []
+        nodes.append(p)
+    if len({id(n) for n in nodes}) != 3 or m.S != m.Skv:
+        return []
+    forms = [_gemm_form(n) for n in nodes]
+    if forms[0] is None or any(f != forms[0] for f in forms):
+        return []
+    a = nodes[0].input(0)
+    if a.type is None or a.type.dtype != "float32" or a.type.size != m.B * m.S * a.type.shape[-1]:
+        return []
+    return nodes

@@ -255,8 +255,10 @@ class HipEmitter:
         self._attn_skip: dict[int, AttentionMatch] = {}
         # Scratch past the planned arena (the plan's offsets stay as they are) for fused
         # attention outputs that must not be written over their operands.
+        # Layout: [grouped Q/K/V projection output | staged attention output].
         self._scratch_off = (max(self.plan.arena_bytes, ALIGN) + ALIGN - 1) // ALIGN * ALIGN
         self._scratch_bytes = 0
+        qkv_bytes = out_bytes = 0
         if FUSE_ATTENTION:
             for m in find_attention(graph, self.plan):
                 self._attn_emit[id(m.emit_at)] = m
@@ -264,7 +266,12 @@ class HipEmitter:
                     if n is not m.emit_at:
                         self._attn_skip[id(n)] = m
                 if m.staged:
-                    self._scratch_bytes = max(self._scratch_bytes, m.out.tensor_type.nbytes)
+                    out_bytes = max(out_bytes, m.out.tensor_type.nbytes)
+                if m.qkv_gemms:
+                    qkv_bytes = max(qkv_bytes, 3 * m.out.tensor_type.nbytes)
+        self._scratch_qkv_off = self._scratch_off
+        self._scratch_out_off = self._scratch_off + (qkv_bytes + ALIGN - 1) // ALIGN * ALIGN
+        self._scratch_bytes = self._scratch_out_off - self._scratch_off + out_bytes
 
     # -- workspace hook ------------------------------------------------------------------------
     def _gemm_shape(self, node: Node) -> tuple[int, int, int, int] | None:
@@ -829,16 +836,37 @@ class HipEmitter:
         self._gemm_call(m, n, k, self._strided("a", self.ptr(a), k, 1), bspec, self.ptr(node.output), n, batch=batch)
 
     def _attention(self, m: AttentionMatch) -> None:
-        def view(op: Any) -> str:
-            return f"((const float *){self.ptr(op.value)} + {op.col})"
+        HD = m.H * m.D
+        if m.qkv_gemms:
+            # Q, K and V as one GEMM with the three weight matrices side by side, into scratch
+            g0 = m.qkv_gemms[0]
+            a = g0.input(0)
+            trans = int(g0.attrs.get("trans_b", 0))
+            mats = [gm.input(1).data.T if trans else gm.input(1).data for gm in m.qkv_gemms]
+            weights = np.ascontiguousarray(np.concatenate(mats, axis=1), np.float32)
+            k = weights.shape[0]
+            bias, mode = "NULL", 0
+            if g0.optional_input(2) is not None:
+                vec = np.concatenate([gm.input(2).data.reshape(-1) for gm in m.qkv_gemms]).astype(np.float32)
+                bias, mode = f"((const float *)(W + {self.weights.add(vec)}))", 1
+            act, lo, hi = self._act(g0)
+            qkv = f"(A + {self._scratch_qkv_off})"
+            self._gemm_call(m.B * m.S, 3 * HD, k, self._strided("a", self.ptr(a), k, 1),
+                            self._packed_b(weights, ("qkv", *(id(gm.input(1)) for gm in m.qkv_gemms), trans)),
+                            qkv, 3 * HD, bias=bias, bias_mode=mode, act=act, lo=lo, hi=hi)
+            views = [f"((const float *){qkv} + {j * HD})" for j in range(3)]
+            strides = [(m.S * 3 * HD, 3 * HD)] * 3
+        else:
+            views = [f"((const float *){self.ptr(op.value)} + {op.col})" for op in (m.q, m.k, m.v)]
+            strides = [(op.batch_stride, op.row_stride) for op in (m.q, m.k, m.v)]
 
-        out = f"((float *)(A + {self._scratch_off}))" if m.staged else self.fptr(m.out)
-
+        out = f"((float *)(A + {self._scratch_out_off}))" if m.staged else self.fptr(m.out)
+        (qb, qs), (kb, ks), (vb, vs) = strides
         fields = [
             f"t.B = {m.B}; t.H = {m.H}; t.S = {m.S}; t.Skv = {m.Skv}; t.D = {m.D};",
-            f"t.q = {view(m.q)}; t.q_b = {m.q.batch_stride}L; t.q_s = {m.q.row_stride}L; t.q_h = {m.D}L;",
-            f"t.k = {view(m.k)}; t.k_b = {m.k.batch_stride}L; t.k_s = {m.k.row_stride}L; t.k_h = {m.D}L;",
-            f"t.v = {view(m.v)}; t.v_b = {m.v.batch_stride}L; t.v_s = {m.v.row_stride}L; t.v_h = {m.D}L;",
+            f"t.q = {views[0]}; t.q_b = {qb}L; t.q_s = {qs}L; t.q_h = {m.D}L;",
+            f"t.k = {views[1]}; t.k_b = {kb}L; t.k_s = {ks}L; t.k_h = {m.D}L;",
+            f"t.v = {views[2]}; t.v_b = {vb}L; t.v_s = {vs}L; t.v_h = {m.D}L;",
             f"t.o = {out}; t.o_b = {m.S * m.H * m.D}L; t.o_s = {m.H * m.D}L; t.o_h = {m.D}L;",
             f"t.scale = {_f(m.ops.scale)}; t.scale_div = {int(m.ops.divide)};",
         ]
@@ -860,7 +888,7 @@ class HipEmitter:
         self.count("attention")
         if m.staged:
             nbytes = m.out.tensor_type.nbytes
-            self.copy((nbytes,), self.ptr(m.out), [1], 0, f"(A + {self._scratch_off})", [1], 0, 1)
+            self.copy((nbytes,), self.ptr(m.out), [1], 0, f"(A + {self._scratch_out_off})", [1], 0, 1)
 
     @staticmethod
     def _score_strides(value: Value) -> list[int]:

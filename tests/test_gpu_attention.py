@@ -233,3 +233,49 @@ def test_matcher_score_op_forms():
     optimize(g, "O2")
     schedule(g)
     assert attn.find_attention(g, plan_memory(g, alignment=256)) == []
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("causal", [False, True])
+def test_grouped_qkv_projection(causal, hip_cache, monkeypatch):
+    """Separate Q/K/V projections (the Hugging Face export form) run as one GEMM feeding the
+    fused attention: 3 GEMM launches per layer become 1."""
+    def build():
+        return builders.transformer(gelu="tanh" if causal else "erf", causal=causal, separate_qkv=True, seq=40, batch=2)
+
+    feeds = oracle.random_feeds(build(), 3, int_high=100)
+    expected = oracle.run_graph(build(), feeds)
+    got, kernels = _run(build(), feeds, hip_cache)
+    monkeypatch.setattr(hip_codegen, "FUSE_ATTENTION", False)
+    plain, plain_kernels = _run(build(), feeds, hip_cache)
+    assert kernels["attention"] == 2 and kernels["gemm"] == plain_kernels["gemm"] - 2 * 2 - 2 * 2
+    for name, want in expected.items():
+        for out in (got, plain):
+            assert float(np.max(np.abs(out[name].astype(np.float64) - want))) <= 5e-5
+
+
+@pytest.mark.gpu
+def test_bert_base_separate_qkv(hip_cache):
+    graph = builders.bert_base(2, separate_qkv=True)
+    feeds = oracle.random_feeds(graph, 4, int_high=30522)
+    got, kernels = _run(builders.bert_base(2, separate_qkv=True), feeds, hip_cache)
+    assert kernels["attention"] == 12 and kernels["gemm"] == 48
+    for i in (0, 1):
+        want = oracle.run_graph(builders.bert_base(1, separate_qkv=True), {"input_ids": feeds["input_ids"][i : i + 1]})["hidden"]
+        assert float(np.max(np.abs(got["hidden"][i : i + 1].astype(np.float64) - want))) <= 5e-4
+
+
+def test_matcher_groups_separate_qkv_projections():
+    """CPU: the three projections of one input join the match; with two different inputs
+    (cross attention) they do not."""
+    g = builders.bert_base(1, separate_qkv=True)
+    optimize(g, "O3")
+    schedule(g)
+    found = attn.find_attention(g, plan_memory(g, alignment=256))
+    assert len(found) == 12 and all(len(m.qkv_gemms) == 3 and not m.staged for m in found)
+    assert all(m.reads() == [m.qkv_gemms[0].input(0)] for m in found)
+    g, _ = attention_graph(1, 2, 40, 40, 16, False)  # Q, K, V are graph inputs: nothing to group
+    optimize(g, "O3")
+    schedule(g)
+    (m,) = attn.find_attention(g, plan_memory(g, alignment=256))
+    assert m.qkv_gemms == []
