@@ -43,6 +43,7 @@ from ..errors import CodegenError
 from ..ir import Graph, Node, TensorType, Value, comment_text, numpy_dtype
 from ..memory import ALIAS_OPS, MemoryPlan, Strategy, plan_memory
 from .attention import AttentionMatch, find_attention
+from .folding import FoldPlan, plan_folds
 
 ALIGN = 256  # arena offsets, weights chunks and the HBM block are 256-byte aligned
 
@@ -87,6 +88,8 @@ _FLOAT32_OPS = frozenset(EW_OPCODES) | {"Gelu"}
 _FLOAT64_OPS = frozenset({"Add", "Sub", "Mul", "Div", "Neg", "Identity"})
 _INT_OPS = frozenset({"Add", "Sub", "Mul", "Div", "Max", "Min", "Neg", "Abs", "Relu", "Identity", "Clip"})
 
+# Read Transposes through GEMM operand strides (codegen/folding.py); tests turn it off to compare.
+FOLD_TRANSPOSES = True
 # Fuse recognized attention chains into mgc_hip_attention (tests turn it off to compare).
 FUSE_ATTENTION = True
 
@@ -269,6 +272,8 @@ class HipEmitter:
                     out_bytes = max(out_bytes, m.out.tensor_type.nbytes)
                 if m.qkv_gemms:
                     qkv_bytes = max(qkv_bytes, 3 * m.out.tensor_type.nbytes)
+        excluded = set(self._attn_skip) | set(self._attn_emit)
+        self._folds = plan_folds(graph, self.plan, self._workspace_bytes, excluded) if FOLD_TRANSPOSES else FoldPlan()
         self._scratch_qkv_off = self._scratch_off
         self._scratch_out_off = self._scratch_off + (qkv_bytes + ALIGN - 1) // ALIGN * ALIGN
         self._scratch_bytes = self._scratch_out_off - self._scratch_off + out_bytes
@@ -348,6 +353,10 @@ class HipEmitter:
             return
         if id(node) in self._attn_emit:
             self._attention(self._attn_emit[id(node)])
+            return
+        if id(node) in self._folds.skipped:
+            self.emit(f"/* {self._folds.skipped[id(node)]} */")
+            self.count("folded")
             return
         if node.op in ALIAS_OPS:
             if node.op == "Dropout" and len(node.outputs) > 1:
@@ -814,26 +823,54 @@ class HipEmitter:
         self._gemm_call(m, n, k, aspec, bspec, self.ptr(node.output), n, alpha=alpha, bias=bias,
                         bias_mode=mode, res=res, ldr=ldr, beta=beta, workspace=ws, workspace_floats=ws_floats)
 
+    def _operand_view(self, v: Value) -> tuple[str, list[int]]:
+        """Pointer and per-dimension element strides a GEMM reads ``v`` through: a folded
+        Transpose's output is its input read with permuted strides."""
+        t = self._folds.inputs.get(id(v))
+        if t is None:
+            return self.ptr(v), _strides(v.tensor_type.shape)
+        x = t.input(0)
+        src = _strides(x.tensor_type.shape)
+        return self.ptr(x), [src[p] for p in ops.transpose_perm(t, x.tensor_type.rank)]
+
     def op_MatMul(self, node: Node) -> None:
         a, b = node.input(0), node.input(1)
         at, bt = a.tensor_type, b.tensor_type
         self._require_f32(node, at)
-        ashape = (1, *at.shape) if at.rank == 1 else at.shape
-        bshape = (*bt.shape, 1) if bt.rank == 1 else bt.shape
+        ap, ast = self._operand_view(a)
+        bp, bst = self._operand_view(b)
+        ashape, bshape = tuple(at.shape), tuple(bt.shape)
+        if at.rank == 1:  # a row vector [1, k]
+            ashape, ast = (1, *ashape), [at.shape[0], *ast]
+        if bt.rank == 1:  # a column vector [k, 1]
+            bshape, bst = (*bshape, 1), [*bst, 1]
         m, k = ashape[-2], ashape[-1]
         n = bshape[-1]
         batch_shape = tuple(int(d) for d in np.broadcast_shapes(ashape[:-2], bshape[:-2]))
-        a_bs = [s * m * k for s in _broadcast_strides(ashape[:-2], batch_shape)]
-        b_bs = [s * k * n for s in _broadcast_strides(bshape[:-2], batch_shape)]
-        c_bs = [s * m * n for s in _strides(batch_shape)]
+        nb = len(batch_shape)
+
+        def batch_strides(shape: tuple[int, ...], strides: list[int]) -> list[int]:
+            pad = nb - (len(shape) - 2)
+            return [0 if d < pad or shape[d - pad] == 1 else strides[d - pad] for d in range(nb)]
+
+        a_bs, b_bs = batch_strides(ashape, ast), batch_strides(bshape, bst)
+        t = self._folds.outputs.get(id(node))
+        if t is not None:
+            # write the Transpose's output: MatMul dim i is output dim j where perm[j] = i
+            zt = t.output.tensor_type
+            perm = ops.transpose_perm(t, zt.rank)
+            zs = _strides(zt.shape)
+            cst = [zs[perm.index(i)] for i in range(zt.rank)]
+            cptr, ldc, c_bs = self.ptr(t.output), cst[-2], cst[:-2]
+        else:
+            cptr, ldc, c_bs = self.ptr(node.output), n, [s * m * n for s in _strides(batch_shape)]
         dims, (a_c, b_c, c_c) = collapse(batch_shape, [a_bs, b_bs, c_bs])
         batch = [(d, sa, sb, sc, 0) for d, sa, sb, sc in zip(dims, a_c, b_c, c_c)]
-        if b.data is not None and not any(b_c):
-            bmat = b.data.reshape(k, n)
-            bspec = self._packed_b(bmat, ("packed", id(b), 0))
+        if b.data is not None and not any(b_c) and id(b) not in self._folds.inputs:
+            bspec = self._packed_b(b.data.reshape(k, n), ("packed", id(b), 0))
         else:
-            bspec = self._strided("b", self.ptr(b), n, 1)
-        self._gemm_call(m, n, k, self._strided("a", self.ptr(a), k, 1), bspec, self.ptr(node.output), n, batch=batch)
+            bspec = self._strided("b", bp, bst[-2], bst[-1])
+        self._gemm_call(m, n, k, self._strided("a", ap, ast[-2], ast[-1]), bspec, cptr, ldc, batch=batch)
 
     def _attention(self, m: AttentionMatch) -> None:
         HD = m.H * m.D
