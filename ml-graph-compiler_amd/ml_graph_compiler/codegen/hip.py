@@ -44,6 +44,7 @@ from ..ir import Graph, Node, TensorType, Value, comment_text, numpy_dtype
 from ..memory import ALIAS_OPS, MemoryPlan, Strategy, plan_memory
 from .attention import AttentionMatch, find_attention
 from .folding import FoldPlan, plan_folds
+from .folding import _overlap as fold_overlap
 
 ALIGN = 256  # arena offsets, weights chunks and the HBM block are 256-byte aligned
 
@@ -90,6 +91,8 @@ _INT_OPS = frozenset({"Add", "Sub", "Mul", "Div", "Max", "Min", "Neg", "Abs", "R
 
 # Read Transposes through GEMM operand strides (codegen/folding.py); tests turn it off to compare.
 FOLD_TRANSPOSES = True
+# Run stride-2 convolutions over few channels on a space-to-depth copy of the input.
+SPACE_TO_DEPTH = True
 # Fuse recognized attention chains into mgc_hip_attention (tests turn it off to compare).
 FUSE_ATTENTION = True
 
@@ -277,6 +280,20 @@ class HipEmitter:
         self._scratch_qkv_off = self._scratch_off
         self._scratch_out_off = self._scratch_off + (qkv_bytes + ALIGN - 1) // ALIGN * ALIGN
         self._scratch_bytes = self._scratch_out_off - self._scratch_off + out_bytes
+        # Stride-2 convolutions over few channels (the ResNet stem) run as stride-1
+        # convolutions over a space-to-depth copy of their input, written to the scratch area
+        # (scratch contents live only within one node's launches, so every use shares it).
+        self._s2d: dict[int, Value | None] = {}
+        self._s2d_skip: set[int] = set()
+        if SPACE_TO_DEPTH:
+            order = {id(n): i for i, n in enumerate(graph.nodes)}
+            for n in graph.nodes:
+                if id(n) in excluded or self._s2d_geometry(n) is None:
+                    continue
+                self._s2d[id(n)] = self._s2d_source(n, order, excluded)
+                if self._s2d[id(n)] is not None:
+                    self._s2d_skip.add(id(n.input(0).producer))
+                self._scratch_bytes = max(self._scratch_bytes, n.input(0).tensor_type.nbytes)
 
     # -- workspace hook ------------------------------------------------------------------------
     def _gemm_shape(self, node: Node) -> tuple[int, int, int, int] | None:
@@ -289,6 +306,12 @@ class HipEmitter:
             a = node.input(0).tensor_type
             k = a.shape[0] if int(node.attrs.get("transA", 0)) else a.shape[1]
             return out.shape[0], out.shape[1], k, 1
+        if node.op in ("Conv", "FusedConv") and ops.conv_layout(node) == "NHWC" and not self.depthwise(node):
+            # the implicit GEMM of one group (groups run one after another on the same workspace)
+            out, w = node.output.tensor_type, node.input(1).tensor_type
+            kh, kw, cg, kout = w.shape
+            group = int(node.attrs.get("group", 1))
+            return out.shape[0] * out.shape[1] * out.shape[2], kout // group, kh * kw * cg, 1
         return None
 
     def _workspace_bytes(self, node: Node) -> int:
@@ -356,6 +379,10 @@ class HipEmitter:
             return
         if id(node) in self._folds.skipped:
             self.emit(f"/* {self._folds.skipped[id(node)]} */")
+            self.count("folded")
+            return
+        if id(node) in self._s2d_skip:
+            self.emit("/* read in NCHW by the space-to-depth copy of the convolution it feeds */")
             self.count("folded")
             return
         if node.op in ALIAS_OPS:
@@ -981,6 +1008,9 @@ class HipEmitter:
             )
             self.count("depthwise")
             return
+        if id(node) in self._s2d:
+            self._conv_space_to_depth(node, bias, res, act, lo, hi)
+            return
         kg = kout // group
         geo = (f"g.{{f}}.H = {h}; g.{{f}}.W = {wd}; g.{{f}}.C = {c}; g.{{f}}.KH = {kh}; g.{{f}}.KW = {kw}; "
                f"g.{{f}}.SH = {g.strides[0]}; g.{{f}}.SW = {g.strides[1]}; g.{{f}}.DH = {g.dilations[0]}; "
@@ -997,10 +1027,12 @@ class HipEmitter:
                     aspec = self._strided("a", xp, c, 1)
                 else:
                     aspec = [f"g.a.kind = MGC_OP_CONV_NHWC; g.a.p = {xp}; " + geo.format(f="a")]
+                ws, ws_floats = self._workspace(node)
                 self._gemm_call(
                     nb * oh * ow, kg, kh * kw * cg, aspec, bspec, f"({self.fptr(node.output)} + {gi * kg})", kout,
                     bias=gbias, bias_mode=1 if bias != "NULL" else 0,
                     res=f"({res} + {gi * kg})" if res != "NULL" else "NULL", ldr=kout, act=act, lo=lo, hi=hi,
+                    workspace=ws, workspace_floats=ws_floats,
                 )
             else:
                 wmat = np.ascontiguousarray(wv.data[gi * kg : (gi + 1) * kg].reshape(kg, cg * kh * kw), np.float32)
@@ -1014,6 +1046,89 @@ class HipEmitter:
                     batch=batch, bias=gbias, bias_mode=2 if bias != "NULL" else 0,
                     res=f"({res} + {gi * kg * plane})" if res != "NULL" else "NULL", ldr=plane, act=act, lo=lo, hi=hi,
                 )
+
+    # -- space-to-depth convolution -------------------------------------------------------------
+    @staticmethod
+    def _s2d_geometry(node: Node) -> dict[str, int] | None:
+        """A stride-2 NHWC convolution whose channel count rules out the 16-byte operand path
+        (C % 4 != 0, e.g. an RGB stem) as a stride-1 convolution over the space-to-depth input
+        x2[b, i, j, (dy, dx, c)] = x[b, 2i + dy, 2j + dx, c]: tap (t, u) of the new kernel with
+        sub-pixel (dy, dx) is tap (2t + dy - 2P + pt, 2u + dx - 2Q + pl) of the original, where
+        P = ceil(pt / 2), Q = ceil(pl / 2) are the new top/left pads (zero where that tap is
+        outside the original kernel)."""
+        if node.op not in ("Conv", "FusedConv") or ops.conv_layout(node) != "NHWC":
+            return None
+        if int(node.attrs.get("group", 1)) != 1 or node.input(1).data is None:
+            return None
+        xt, wt = node.input(0).tensor_type, node.input(1).tensor_type
+        if xt.dtype != "float32" or xt.rank != 4:
+            return None
+        nb, h, wd, c = xt.shape
+        kh, kw, cg, kout = wt.shape
+        g = ops.window_geometry(node, (h, wd), (kh, kw))
+        if tuple(g.strides) != (2, 2) or tuple(g.dilations) != (1, 1) or c % 4 == 0 or h % 2 or wd % 2:
+            return None
+        pt, pl = g.pads[0], g.pads[1]
+        P, Q = (pt + 1) // 2, (pl + 1) // 2
+        return dict(nb=nb, h=h, w=wd, c=c, kh=kh, kw=kw, kout=kout, pt=pt, pl=pl, P=P, Q=Q,
+                    KH=-(-(kh + 2 * P - pt) // 2), KW=-(-(kw + 2 * Q - pl) // 2),
+                    oh=g.out_hw[0], ow=g.out_hw[1])
+
+    def _s2d_source(self, conv: Node, order: dict[int, int], excluded: set[int]) -> Value | None:
+        """The NCHW tensor the space-to-depth copy can read directly when the convolution's
+        input is an NCHW -> NHWC Transpose used by nothing else (the Transpose then emits
+        nothing), provided nothing between the two overwrites that tensor."""
+        x = conv.input(0)
+        t = x.producer
+        if t is None or t.op != "Transpose" or id(t) in excluded or id(t) in self._folds.skipped:
+            return None
+        if x in self.graph.outputs or x.users != [conv] or ops.transpose_perm(t, 4) != [0, 2, 3, 1]:
+            return None
+        src = t.input(0)
+        for n in self.graph.nodes[order[id(t)] + 1 : order[id(conv)]]:
+            if any(fold_overlap(self.plan, o, src) for o in n.outputs):
+                return None
+            if id(n) in self.plan.workspaces:
+                return None
+        return src
+
+    def _conv_space_to_depth(self, node: Node, bias: str, res: str, act: str, lo: float, hi: float) -> None:
+        s2 = self._s2d_geometry(node)
+        assert s2 is not None
+        nb, h, wd, c, kout = s2["nb"], s2["h"], s2["w"], s2["c"], s2["kout"]
+        h2, w2, c4 = h // 2, wd // 2, 4 * c
+        dst = f"(A + {self._scratch_off})"
+        src = self._s2d[id(node)]
+        if src is not None:  # NCHW source [b, c, 2i + dy, 2j + dx]
+            in_ptr, in_st = self.ptr(src), [c * h * wd, 2 * wd, 2, wd, 1, h * wd]
+        else:                # NHWC source [b, 2i + dy, 2j + dx, c]
+            in_ptr, in_st = self.ptr(node.input(0)), [h * wd * c, 2 * wd * c, 2 * c, wd * c, c, 1]
+        shape = [nb, h2, w2, 2, 2, c]
+        self.copy(shape, dst, _strides(shape), 0, in_ptr, in_st, 0, 4)
+        self.count("space_to_depth")
+        w = node.input(1).data
+        KH, KW = s2["KH"], s2["KW"]
+        w2m = np.zeros((KH, KW, 2, 2, c, kout), np.float32)
+        for t in range(KH):
+            for dy in range(2):
+                r = 2 * t + dy - 2 * s2["P"] + s2["pt"]
+                if not 0 <= r < s2["kh"]:
+                    continue
+                for u in range(KW):
+                    for dx in range(2):
+                        q = 2 * u + dx - 2 * s2["Q"] + s2["pl"]
+                        if 0 <= q < s2["kw"]:
+                            w2m[t, u, dy, dx] = w[r, q]
+        kdim = KH * KW * c4
+        bspec = self._packed_b(w2m.reshape(kdim, kout), ("s2d", id(node.input(1))))
+        oh, ow = s2["oh"], s2["ow"]
+        geo = (f"g.a.H = {h2}; g.a.W = {w2}; g.a.C = {c4}; g.a.KH = {KH}; g.a.KW = {KW}; g.a.SH = 1; "
+               f"g.a.SW = 1; g.a.DH = 1; g.a.DW = 1; g.a.PT = {s2['P']}; g.a.PL = {s2['Q']}; "
+               f"g.a.OH = {oh}; g.a.OW = {ow}; g.a.cg = {c4};")
+        aspec = [f"g.a.kind = MGC_OP_CONV_NHWC; g.a.p = (const float *){dst}; " + geo]
+        self._gemm_call(nb * oh * ow, kout, kdim, aspec, bspec, self.ptr(node.output), kout,
+                        bias=bias, bias_mode=1 if bias != "NULL" else 0, res=res, ldr=kout,
+                        act=act, lo=lo, hi=hi)
 
     def _pool(self, node: Node, is_max: int) -> None:
         xv = node.input(0)

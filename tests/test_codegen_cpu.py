@@ -74,15 +74,25 @@ def test_model_library_exports_the_model_abi(hip_cache):
         ("tiny-cnn", {"depthwise": 1, "gemm": 9, "pool": 1, "reduce": 1, "transpose": 1, "view": 1}, None),
     ],
 )
-def test_kernel_mix_matches_reference(name, kernels, arena):
+def test_kernel_mix_matches_reference(name, kernels, arena, monkeypatch):
     """Reference kernel mixes at O3: ResNet-50 gemm 54, pool 1, reduce 1, transpose 1, view 1;
     MobileNetV2 gemm 36, depthwise 17 (benchmarks/results/ablation_cnn.json:759-830,1468-1540);
-    tiny-cnn gemm 9, depthwise 1 (tests/test_codegen.py:638-647)."""
+    tiny-cnn gemm 9, depthwise 1 (tests/test_codegen.py:638-647). With the space-to-depth stem
+    the input Transpose folds into the stem's copy; the planned arena is the same either way."""
+    from ml_graph_compiler.codegen import hip as hip_codegen
+
     make = builders.SAMPLES.get(name) or builders.CONFIGS[name]
+    monkeypatch.setattr(hip_codegen, "SPACE_TO_DEPTH", False)
     gen = generate_hip(o3(make()))
     assert gen.kernels == kernels
     if arena is not None:
-        assert gen.arena_bytes == arena
+        assert gen.arena_bytes == arena == gen.plan.arena_bytes
+    monkeypatch.setattr(hip_codegen, "SPACE_TO_DEPTH", True)
+    s2d = generate_hip(o3(make()))
+    moved = dict(kernels, folded=1, space_to_depth=1)
+    del moved["transpose"]
+    assert s2d.kernels == moved
+    assert s2d.plan.arena_bytes == gen.plan.arena_bytes
     assert gen.weights.nbytes % 256 == 0 and len(gen.weights.digest()) == 24
     assert "mgc_forward" in gen.source and "int mgc_run(" in gen.source
 
