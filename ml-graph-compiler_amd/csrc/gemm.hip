@@ -4,7 +4,7 @@
 // mgc_gemm (src/ml_graph_compiler/codegen/runtime/mgc_kernels.c:282-396), with operands read as
 // strided matrices or through implicit im2col of an NHWC (A) or NCHW (B) image.
 //
-// Three kernels share the MFMA core (MI355X-first, not a translation of the reference's
+// Two kernels share the MFMA core (MI355X-first, not a translation of the reference's
 // Goto/BLIS CPU blocking). A workgroup of 256 threads (4 waves of 64) owns a BM x BN output
 // tile; each wave owns a WM x WN sub-tile of 32x32 MFMA blocks (16 accumulators per block).
 // K advances 32 per stage; the 32x32x2 MFMA consumes two k per instruction, one per half-wave,
@@ -12,25 +12,22 @@
 // (a permutation of the summation order applied identically to A and B), so a lane's
 // operands are contiguous 16-byte LDS reads.
 //
-//  * gemm_dma_kernel / gemm_stream_kernel (k-contiguous operands: packed weights, NHWC
-//    activations, row-major matrices — every convolution and linear layer). Tiles travel
-//    from HBM to LDS with buffer_load_dwordx4 ... lds (no register staging) through a ring of
-//    stages; masked elements use an offset past the end of the buffer resource, which the
-//    hardware reads as zero. The LDS row layout is fixed by the DMA (a wave's 64 lanes write
-//    1 KB of consecutive LDS), so bank spreading comes from which k-chunk each lane fetches
-//    (an XOR swizzle). Barriers wait only for LDS traffic, so the loads of later stages stay
-//    in flight. Implicit-im2col offsets are advanced incrementally and divisions by shape
-//    constants use host-computed magic numbers.
-//    gemm_stream_kernel is persistent: each workgroup walks a list of tiles and its operand
-//    pipeline runs across tile boundaries, so small-K GEMMs (1x1 convolutions over large
-//    images) overlap the next tile's loads with the current tile's epilogue, which writes
-//    16-byte chunks straight from the accumulators.
+//  * gemm_dma_kernel (k-contiguous operands: packed weights, NHWC activations, row-major
+//    matrices — every convolution and linear layer). Tiles travel from HBM to LDS with
+//    buffer_load_dwordx4 ... lds (no register staging) through a ring of stages; masked
+//    elements use an offset past the end of the buffer resource, which the hardware reads as
+//    zero. The LDS row layout is fixed by the DMA (a wave's 64 lanes write 1 KB of consecutive
+//    LDS), so bank spreading comes from which k-chunk each lane fetches (an XOR swizzle).
+//    Barriers wait only for LDS traffic, so the loads of later stages stay in flight.
+//    Implicit-im2col offsets are advanced incrementally and divisions by shape constants use
+//    host-computed magic numbers.
 //  * gemm_mfma_kernel: every other operand form (transposed or strided A, NCHW im2col B,
 //    dynamic k-major B), staged through registers into double-buffered LDS.
 //  * The workgroup id is remapped so each of the 8 XCDs (each with its own L2) works on a
 //    contiguous range of tiles, N fastest: tiles that share A rows share an L2.
-//  * Few-tile problems split K over extra workgroups into a planner-provided workspace, then
-//    a reduction applies the epilogue.
+//  * Tiles are 64 x 64 (see choose_tiles); K is split over extra workgroups into a
+//    planner-provided workspace when the tiles alone cannot balance the CUs, and a reduction
+//    then applies the epilogue.
 #include "mgc_device.h"
 
 namespace mgc {
@@ -74,7 +71,6 @@ struct GemmDev {
     int vec_out;
     FastDiv div_ow, div_ohw, div_cg, div_kw;  // A as NHWC image: OW, OH * OW, cg, KW
     long a_bytes, b_bytes;  // bytes of A and B reachable from a.p / b.p (all batch elements)
-    long c_bytes, r_bytes, ws_bytes;  // and of C, the residual and the split-K workspace
     int nbatch;                       // batch elements  // 16-byte epilogue accesses are aligned (ldc, ldr, pointers)
 };
 
@@ -732,334 +728,6 @@ __global__ void __launch_bounds__(256) gemm_dma_kernel(const GemmDev p) {
     gemm_store_tile<BM, BN, WGM>(p, smem, acc, m0, n0, ks, co, ro);
 }
 
-// ------------------------------------------------------------------------------------------
-// Persistent streaming GEMM for k-contiguous operands (the hot path: convolutions, linear
-// layers). Each workgroup walks a list of output tiles; the operand pipeline (buffer -> LDS
-// DMA through a STAGES-deep ring, swizzled as in gemm_dma_kernel) runs continuously across
-// tile boundaries, so the next tile's first stages load while the current tile's epilogue
-// runs. The epilogue works straight from the accumulators (no LDS round trip) with buffer
-// stores whose out-of-range offsets are dropped by the hardware.
-// ------------------------------------------------------------------------------------------
-struct TileWork {
-    int m0, n0, kbeg, kend, nk;
-    long ao, bo, co, ro;
-    int ks;
-};
-
-__device__ __forceinline__ void decode_work(const GemmDev &p, int w, int BM_, int BN_, int BK_,
-                                            TileWork &o) {
-    const int tiles = p.tiles_m * p.tiles_n;
-    const int slice = w / tiles;
-    const int t = w - slice * tiles;
-    const int tm = t / p.tiles_n;
-    const int tn = t - tm * p.tiles_n;
-    const int bz = slice / p.split;
-    o.ks = slice - bz * p.split;
-    o.m0 = tm * BM_;
-    o.n0 = tn * BN_;
-    o.kbeg = o.ks * p.kchunk;
-    o.kend = min(p.K, o.kbeg + p.kchunk);
-    o.nk = o.kend > o.kbeg ? (o.kend - o.kbeg + BK_ - 1) / BK_ : 0;
-    batch_offsets(p, bz, o.ao, o.bo, o.co, o.ro);
-}
-
-template <int BM, int BN, int WGM, int STAGES, int AMODE, bool GEN_ACT>
-__global__ void __launch_bounds__(256) gemm_stream_kernel(const GemmDev p) {
-    constexpr int BK = 32;
-    constexpr int WGN = 4 / WGM;
-    constexpr int WM = BM / WGM;
-    constexpr int WN = BN / WGN;
-    constexpr int RM = WM / 32;
-    constexpr int RN = WN / 32;
-    static_assert(RM >= 1 && RN >= 1 && WGM * WGN == 4, "bad tile");
-    static_assert(STAGES >= 2 && STAGES <= 4, "stages");
-    static_assert(AMODE == AM_VEC || AMODE == AM_CONV_VEC, "vector A only");
-    constexpr int AI = BM / 32;
-    constexpr int BI = BN / 32;
-    constexpr int STAGE = (BM + BN) * BK;
-    constexpr int PER_STAGE = AI + BI;
-    constexpr unsigned OOB = 0x80000000u;
-
-    __shared__ __attribute__((aligned(16))) float smem[STAGES * STAGE];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave / WGN, wn = wave - (wave / WGN) * WGN;
-    const int li = lane & 31;
-    const int lh = lane >> 5;
-
-    const int total = p.tiles_m * p.tiles_n * p.nbatch * p.split;
-    const int G = gridDim.x;
-    // Work item j of this workgroup is first + j * G. Workgroup ids are dealt round-robin to the
-    // 8 XCDs; XCD x takes the contiguous range [x * G / 8, (x + 1) * G / 8) of every round, so
-    // tiles that share rows of A share an L2.
-    int first = blockIdx.x;
-    if ((G & 7) == 0) first = (first & 7) * (G >> 3) + (first >> 3);
-    if (first >= total) return;
-
-    // ---- loader state (the work item whose stages are being fetched) ----------------------
-    const int q4 = ((lane & 7) ^ (lane >> 3) ^ (wave & 1)) * 4;
-    const int rsub = lane >> 3;
-    const int ohw = p.a.OH * p.a.OW;
-    int lw = first;
-    TileWork L;
-    decode_work(p, lw, BM, BN, BK, L);
-    int lkt = 0;
-    bool loading = true;
-    __amdgpu_buffer_rsrc_t ra, rb;
-    unsigned aoff[AI], boff[BI];
-    int aih[AI], aiw[AI];
-    int knext = 0, cc = 0, ckw = 0, ckh = 0;
-
-    auto setup_load = [&]() __attribute__((always_inline)) {
-        ra = __builtin_amdgcn_make_buffer_rsrc((void *)(p.a.p + L.ao), (short)0,
-                                               (int)(p.a_bytes - L.ao * 4), 0x00020000);
-        rb = __builtin_amdgcn_make_buffer_rsrc((void *)(p.b.p + L.bo), (short)0,
-                                               (int)(p.b_bytes - L.bo * 4), 0x00020000);
-#pragma unroll
-        for (int i = 0; i < AI; ++i) {
-            const int m = L.m0 + (i * 4 + wave) * 8 + rsub;
-            aoff[i] = OOB;
-            aih[i] = aiw[i] = -0x40000000;
-            if (m < p.M) {
-                if (AMODE == AM_CONV_VEC) {
-                    const int n = fdiv(m, p.div_ohw), rr = m - n * ohw;
-                    const int oh = fdiv(rr, p.div_ow), ow = rr - oh * p.a.OW;
-                    aih[i] = oh * p.a.SH - p.a.PT;
-                    aiw[i] = ow * p.a.SW - p.a.PL;
-                    aoff[i] = (unsigned)(((n * p.a.H + aih[i]) * p.a.W + aiw[i]) * p.a.C) * 4u;
-                } else {
-                    aoff[i] = (unsigned)m * (unsigned)p.a.rs * 4u;
-                }
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < BI; ++i) {
-            const int n = L.n0 + (i * 4 + wave) * 8 + rsub;
-            boff[i] = n < p.N ? (unsigned)n * (unsigned)p.b.cs * 4u : OOB;
-        }
-        knext = L.kbeg + q4;
-        if (AMODE == AM_CONV_VEC) {
-            const int t = fdiv(knext, p.div_cg);
-            cc = knext - t * p.a.cg;
-            ckh = fdiv(t, p.div_kw);
-            ckw = t - ckh * p.a.KW;
-        }
-    };
-    // Move the loader to the next work item that has stages (or stop).
-    auto next_load_item = [&]() __attribute__((always_inline)) {
-        do {
-            lw += G;
-            if (lw >= total) {
-                loading = false;
-                return;
-            }
-            decode_work(p, lw, BM, BN, BK, L);
-        } while (L.nk == 0);
-        lkt = 0;
-        setup_load();
-    };
-    if (L.nk == 0) {
-        next_load_item();
-    } else {
-        setup_load();
-    }
-
-    auto issue = [&](int buf) __attribute__((always_inline)) {
-        const int k = knext;
-        const bool kok = k < L.kend;
-        float *sa = smem + buf * STAGE;
-        float *sb = sa + BM * BK;
-        if constexpr (AMODE == AM_VEC) {
-#pragma unroll
-            for (int i = 0; i < AI; ++i)
-                dma16_buf(ra, kok ? aoff[i] + (unsigned)k * 4u : OOB, sa + (i * 4 + wave) * 8 * BK);
-        } else {
-            const int dh = ckh * p.a.DH, dw = ckw * p.a.DW;
-            const unsigned koff = (unsigned)((dh * p.a.W + dw) * p.a.C + cc) * 4u;
-#pragma unroll
-            for (int i = 0; i < AI; ++i) {
-                const bool ok = kok && (unsigned)(aih[i] + dh) < (unsigned)p.a.H &&
-                                (unsigned)(aiw[i] + dw) < (unsigned)p.a.W;
-                dma16_buf(ra, ok ? aoff[i] + koff : OOB, sa + (i * 4 + wave) * 8 * BK);
-            }
-            cc += BK;
-            while (cc >= p.a.cg) {
-                cc -= p.a.cg;
-                if (++ckw == p.a.KW) {
-                    ckw = 0;
-                    ++ckh;
-                }
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < BI; ++i)
-            dma16_buf(rb, kok ? boff[i] + (unsigned)k * 4u : OOB, sb + (i * 4 + wave) * 8 * BK);
-        knext = k + BK;
-        if (++lkt == L.nk) next_load_item();
-    };
-
-    // ---- consumer state (the work item being multiplied) ----------------------------------
-    int cw = first;
-    TileWork C;
-    decode_work(p, cw, BM, BN, BK, C);
-    int ckt = 0;
-
-    floatx16 acc[RM][RN];
-#pragma unroll
-    for (int i = 0; i < RM; ++i)
-#pragma unroll
-        for (int j = 0; j < RN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-    const bool split_out = p.split > 1;
-    const int bmode = split_out ? 0 : p.bias_mode;
-    // Scalars read once: keeps the compiler from copying the argument block to scratch.
-    const float alpha = p.alpha, beta = p.beta, lo = p.lo, hi = p.hi;
-    const float *const bias = p.bias;
-    const int act = p.act;
-    const bool has_res = !split_out && p.res != nullptr;
-    const bool clampit = p.act != MGC_ACT_NONE;
-
-    // Epilogue of work item C from the accumulators. The MFMA takes B as its first operand, so
-    // block (i, j) holds C^T: lane (li, lh) owns row m0 + wm * WM + i * 32 + li and, in
-    // registers 4g .. 4g + 3, the four consecutive columns n0 + wn * WN + j * 32 + 8g + 4lh + 0..3.
-    // Residual loads and output stores are therefore 16 bytes wide.
-    const f4 zero4 = {0.f, 0.f, 0.f, 0.f};
-    auto epilogue = [&]() __attribute__((always_inline)) {
-        const long cofs = split_out ? (long)C.ks * p.M * p.N : C.co;
-        float *cptr = (split_out ? p.ws : p.c) + cofs;
-        const unsigned ldc = split_out ? (unsigned)p.N : (unsigned)p.ldc;
-        const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
-            (void *)cptr, (short)0, (int)((split_out ? p.ws_bytes : p.c_bytes) - cofs * 4),
-            0x00020000);
-        __amdgpu_buffer_rsrc_t rr = rc;
-        if (has_res)
-            rr = __builtin_amdgcn_make_buffer_rsrc((void *)(p.res + C.ro), (short)0,
-                                                   (int)(p.r_bytes - C.ro * 4), 0x00020000);
-        const int cbase = C.n0 + wn * WN + 4 * lh;
-        {
-#pragma unroll
-            for (int i = 0; i < RM; ++i) {
-                const int row = C.m0 + wm * WM + i * 32 + li;
-                const bool rok = row < p.M;
-                const float rbias = (bmode == 2 && rok) ? ldg(bias + row) : 0.0f;
-#pragma unroll
-                for (int j = 0; j < RN; ++j) {
-                    f4 rv[4], cb[4];
-#pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const int col = cbase + j * 32 + 8 * g;
-                        cb[g] = (bmode == 1 && col < p.N) ? ldg4(bias + col) : zero4;
-                        rv[g] = zero4;
-                        if (has_res) {
-                            const unsigned off =
-                                rok && col < p.N
-                                    ? ((unsigned)row * (unsigned)p.ldr + (unsigned)col) * 4u
-                                    : OOB;
-                            rv[g] = __builtin_bit_cast(
-                                f4, __builtin_amdgcn_raw_buffer_load_b128(rr, (int)off, 0, 0));
-                        }
-                    }
-#pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const int col = cbase + j * 32 + 8 * g;
-                        f4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                                acc[i][j][4 * g + 3]};
-                        if (!split_out) {
-                            v = v * alpha + cb[g] + rbias;
-                            if (has_res) v += beta * rv[g];
-                            if constexpr (GEN_ACT) {
-#pragma unroll
-                                for (int e = 0; e < 4; ++e) v[e] = apply_act(v[e], act, lo, hi);
-                            } else if (clampit) {
-#pragma unroll
-                                for (int e = 0; e < 4; ++e) v[e] = fminf(fmaxf(v[e], lo), hi);
-                            }
-                        }
-                        const unsigned off =
-                            rok && col < p.N ? ((unsigned)row * ldc + (unsigned)col) * 4u : OOB;
-                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uint4_t, v), rc,
-                                                               (int)off, 0, 0);
-                    }
-                }
-            }
-        }
-    };
-
-    // ---- pipeline -----------------------------------------------------------------------
-    int issued = 0, consumed = 0;
-#pragma unroll
-    for (int s = 0; s < STAGES - 1; ++s) {
-        if (loading) {
-            issue(s);
-            ++issued;
-        }
-    }
-    while (true) {
-        if (C.nk > 0) {
-            // Step `consumed` has landed once only the later steps' loads are outstanding.
-            const int ahead = issued - consumed - 1;
-            if (STAGES >= 4 && ahead >= 2) {
-                wait_vmcnt<(STAGES >= 4 ? 2 : 0) * PER_STAGE>();
-            } else if (STAGES >= 3 && ahead >= 1) {
-                wait_vmcnt<PER_STAGE>();
-            } else {
-                wait_vmcnt<0>();
-            }
-            barrier_lds();
-            if (loading) {
-                issue(issued % STAGES);
-                ++issued;
-            }
-            const float *as = smem + (consumed % STAGES) * STAGE;
-            const float *bs = as + BM * BK;
-            const int sw = (li & 7) ^ ((li >> 3) & 1);
-            f4 af[RM][4], bf[RN][4];
-#pragma unroll
-            for (int i = 0; i < RM; ++i)
-#pragma unroll
-                for (int s = 0; s < 4; ++s)
-                    af[i][s] = *reinterpret_cast<const f4 *>(
-                        &as[(wm * WM + i * 32 + li) * BK + (((lh * 4 + s) ^ sw) << 2)]);
-#pragma unroll
-            for (int j = 0; j < RN; ++j)
-#pragma unroll
-                for (int s = 0; s < 4; ++s)
-                    bf[j][s] = *reinterpret_cast<const f4 *>(
-                        &bs[(wn * WN + j * 32 + li) * BK + (((lh * 4 + s) ^ sw) << 2)]);
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-#pragma unroll
-                    for (int i = 0; i < RM; ++i)
-#pragma unroll
-                        for (int j = 0; j < RN; ++j)
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                                bf[j][s][e], af[i][s][e], acc[i][j], 0, 0, 0);
-            ++consumed;
-            ++ckt;
-        }
-        if (ckt >= C.nk) {
-            // Work item done (or one without stages: an empty K split writes zeros).
-            epilogue();
-#pragma unroll
-            for (int i = 0; i < RM; ++i)
-#pragma unroll
-                for (int j = 0; j < RN; ++j)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-            cw += G;
-            if (cw >= total) return;
-            decode_work(p, cw, BM, BN, BK, C);
-            ckt = 0;
-        }
-    }
-}
-
 // Sum the split-K partials and apply the epilogue (one batch element).
 __global__ void gemm_splitk_reduce(const GemmDev p) {
     const long total = (long)p.M * p.N;
@@ -1104,50 +772,45 @@ static GemmKernel pick_dma(int am) {
                         : &gemm_dma_kernel<BM, BN, WGM, 2, AM_CONV_VEC>;
 }
 
-static GemmKernel pick_stream(int am, bool gen_act) {
-    if (gen_act)
-        return am == AM_VEC ? &gemm_stream_kernel<128, 64, 2, 2, AM_VEC, true>
-                            : &gemm_stream_kernel<128, 64, 2, 2, AM_CONV_VEC, true>;
-    return am == AM_VEC ? &gemm_stream_kernel<128, 64, 2, 2, AM_VEC, false>
-                        : &gemm_stream_kernel<128, 64, 2, 2, AM_CONV_VEC, false>;
-}
-
 struct TileChoice {
     int bm, bn, split;
 };
 
 static const int kCUs = 256;
 
-// Tile shape and K split for one GEMM. Larger tiles reuse more data per LDS stage; the chip
-// needs several hundred workgroups in flight, so small problems drop to 64-wide tiles and,
-// failing that, split K.
+// Tile shape and K split for one GEMM. 64 x 64 tiles throughout: a two-stage ring is 32 KB of
+// LDS and the kernel fits five workgroups per CU, whose interleaved waves hide each other's
+// load latency. Measured on every ResNet-50 b32 GEMM this beats 128 x 64 and 128 x 128 tiles
+// (which fit one or two workgroups per CU) and a persistent tile-streaming kernel.
+//
+// K is split over extra workgroups when the tiles alone leave CUs idle or badly balanced:
+// with W workgroups on the 256 CUs the busiest CU runs ceil(W / 256) of them while the
+// average is W / 256, so the split is raised until that ratio reaches 0.9 (one resident wave
+// of at most five workgroups per CU, at least 256 k per split). Balancing alone pays only for
+// long K (>= 2048): the partial results cost a write and a read of split * M * N floats.
 static TileChoice choose_tiles(int M, int N, int K, int batch) {
     TileChoice t;
-    t.bn = N <= 64 ? 64 : 128;
-    t.bm = 128;
-    long tiles = (long)((M + 127) / 128) * ((N + t.bn - 1) / t.bn) * batch;
-    if (tiles < 2 * kCUs) {
-        t.bm = 64;
-        t.bn = 64;
-    }
-    tiles = (long)((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn) * batch;
+    t.bm = 64;
+    t.bn = 64;
     t.split = 1;
-    if (batch == 1 && tiles < kCUs && K >= 512) {
-        int want = (int)((2 * kCUs + tiles - 1) / tiles);
-        int max_split = K / 256;
-        t.split = want < max_split ? want : max_split;
-        if (t.split < 1) t.split = 1;
+    const long tiles = (long)((M + 63) / 64) * ((N + 63) / 64) * batch;
+    if (batch != 1 || K < 512 || !(tiles < kCUs || (K >= 2048 && tiles < 2 * kCUs))) return t;
+    auto balance = [&](int s) {
+        const long w = tiles * s;
+        return (double)w / (double)(((w + kCUs - 1) / kCUs) * kCUs);
+    };
+    const int max_split = K / 256 < 8 ? K / 256 : 8;
+    double best = balance(1);
+    for (int s = 2; s <= max_split && tiles * s <= 5L * kCUs && best < 0.9; ++s) {
+        const double e = balance(s);
+        if (e > best + 0.05) {
+            best = e;
+            t.split = s;
+        }
     }
+    // too few tiles to fill the chip even once: use every split K allows
+    if (tiles * t.split < kCUs && max_split > t.split) t.split = max_split;
     return t;
-}
-
-// The streaming kernel pays off where each tile has little K to multiply (1x1 convolutions
-// over large images): with K <= 256 a tile is at most 8 stages, and the overlap of one tile's
-// epilogue with the next tile's loads matters. It needs enough 128 x 64 tiles to keep every
-// workgroup slot busy for several tiles.
-static bool prefer_stream(int M, int N, int K, int batch) {
-    const long tiles = (long)((M + 127) / 128) * ((N + 63) / 64) * batch;
-    return K <= 256 && tiles >= 4L * kCUs;
 }
 
 }  // namespace mgc
@@ -1243,18 +906,12 @@ extern "C" void mgc_hip_gemm(mgc_hip_exec *x, const mgc_hip_gemm_args *g) {
         a_ext = (long)(p.M - 1) * p.a.rs + (long)(p.K - 1) * p.a.cs + 1;
     }
     b_ext = (long)(p.K - 1) * p.b.rs + (long)(p.N - 1) * p.b.cs + 1;
-    long c_ext = (long)(p.M - 1) * p.ldc + p.N, r_ext = p.res ? (long)(p.M - 1) * p.ldr + p.N : 0;
     for (int d = 0; d < p.batch_rank; ++d) {
         a_ext += (long)(p.bdims[d] - 1) * p.a_bs[d];
         b_ext += (long)(p.bdims[d] - 1) * p.b_bs[d];
-        c_ext += (long)(p.bdims[d] - 1) * p.c_bs[d];
-        if (p.res) r_ext += (long)(p.bdims[d] - 1) * p.r_bs[d];
     }
     p.a_bytes = a_ext * 4;
     p.b_bytes = b_ext * 4;
-    p.c_bytes = c_ext * 4;
-    p.r_bytes = r_ext * 4;
-    p.ws_bytes = p.split > 1 ? (long)p.split * p.M * p.N * 4 : 0;
     p.nbatch = batch;
     const long kMaxRes = 0x7fffffffL;  // buffer offsets past this mean "masked"
     bool nonneg = p.a.rs >= 0 && p.a.cs >= 0 && p.b.rs >= 0 && p.b.cs >= 0 && p.ldc >= 0 &&
@@ -1264,44 +921,9 @@ extern "C" void mgc_hip_gemm(mgc_hip_exec *x, const mgc_hip_gemm_args *g) {
     const bool dma_ok = nonneg && (am == AM_VEC || am == AM_CONV_VEC) && bm == BD_NK_VEC && p.K > 0 &&
                         p.a_bytes > 0 && p.a_bytes < kMaxRes && p.b_bytes > 0 &&
                         p.b_bytes < kMaxRes;
-    const bool stream_ok = dma_ok && p.N % 4 == 0 && (p.split > 1 || p.vec_out) &&
-                           p.c_bytes < kMaxRes && p.r_bytes < kMaxRes && p.ws_bytes < kMaxRes;
 
-    GemmKernel kern;
-    dim3 grid;
-    if (stream_ok && t.split == 1 && prefer_stream(p.M, p.N, p.K, batch)) {
-        if (p.act == MGC_ACT_RELU) {  // ReLU as a clamp to [0, inf)
-            p.lo = 0.0f;
-            p.hi = __builtin_huge_valf();
-        }
-        const bool gen_act =
-            !(p.act == MGC_ACT_NONE || p.act == MGC_ACT_RELU || p.act == MGC_ACT_CLIP);
-        p.tiles_m = (p.M + 127) / 128;
-        p.tiles_n = (p.N + 63) / 64;
-        // Two 128 x 64 workgroups fit a CU (2 x 48 KB of LDS ring, 2 waves per SIMD).
-        const long items = (long)p.tiles_m * p.tiles_n * batch;
-        const long slots = 2L * kCUs;
-        kern = pick_stream(am, gen_act);
-        grid = dim3((unsigned)(items < slots ? items : slots));
-    } else {
-        p.tiles_m = (p.M + t.bm - 1) / t.bm;
-        p.tiles_n = (p.N + t.bn - 1) / t.bn;
-        if (dma_ok) {
-            if (t.bm == 128 && t.bn == 128)
-                kern = pick_dma<128, 128, 2>(am);
-            else if (t.bm == 128 && t.bn == 64)
-                kern = pick_dma<128, 64, 2>(am);
-            else
-                kern = pick_dma<64, 64, 2>(am);
-        } else if (t.bm == 128 && t.bn == 128) {
-            kern = pick_kernel<128, 128, 2>(am, bm);
-        } else if (t.bm == 128 && t.bn == 64) {
-            kern = pick_kernel<128, 64, 2>(am, bm);
-        } else {
-            kern = pick_kernel<64, 64, 2>(am, bm);
-        }
-        grid = dim3((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)(batch * p.split));
-    }
+    const GemmKernel kern = dma_ok ? pick_dma<64, 64, 2>(am) : pick_kernel<64, 64, 2>(am, bm);
+    const dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)(batch * p.split));
     MGC_LAUNCH(x, kern, grid, dim3(256), 0, p);
     if (p.split > 1) {
         MGC_LAUNCH(x, gemm_splitk_reduce, dim3(blocks_for((long)p.M * p.N, 256, 4096)), dim3(256),
