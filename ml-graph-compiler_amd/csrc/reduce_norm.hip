@@ -29,6 +29,62 @@ __global__ void reduce_mid_strided(int is_max, long outer, long n, long inner, c
     }
 }
 
+// inner % 4 == 0 (global pooling over NHWC): workgroup (x, o) owns 64 column quads of row
+// block o; its four waves each walk every fourth of the n rows with 16-byte loads, then the
+// four partial results meet in LDS. Many more loads are in flight per CU than with one thread
+// per output walking all n rows.
+__global__ void __launch_bounds__(256) reduce_mid_vec4(int is_max, int n, int inner4, const float4 *in,
+                                                       float4 *out) {
+    const int lane = threadIdx.x & 63, part = threadIdx.x >> 6;
+    const int col = blockIdx.x * 64 + lane;
+    const long o = blockIdx.y;
+    const float init = is_max ? -INFINITY : 0.0f;
+    float4 acc = make_float4(init, init, init, init);
+    if (col < inner4) {
+        const float4 *src = in + o * n * inner4 + col;
+        for (int k = part; k < n; k += 4) {
+            const float4 v = src[(long)k * inner4];
+            if (is_max) {
+                acc.x = v.x > acc.x ? v.x : acc.x;
+                acc.y = v.y > acc.y ? v.y : acc.y;
+                acc.z = v.z > acc.z ? v.z : acc.z;
+                acc.w = v.w > acc.w ? v.w : acc.w;
+            } else {
+                acc.x += v.x;
+                acc.y += v.y;
+                acc.z += v.z;
+                acc.w += v.w;
+            }
+        }
+    }
+    __shared__ float4 partial[4][64];
+    partial[part][lane] = acc;
+    __syncthreads();
+    if (part != 0 || col >= inner4) return;
+    for (int q = 1; q < 4; ++q) {
+        const float4 v = partial[q][lane];
+        if (is_max) {
+            acc.x = v.x > acc.x ? v.x : acc.x;
+            acc.y = v.y > acc.y ? v.y : acc.y;
+            acc.z = v.z > acc.z ? v.z : acc.z;
+            acc.w = v.w > acc.w ? v.w : acc.w;
+        } else {
+            acc.x += v.x;
+            acc.y += v.y;
+            acc.z += v.z;
+            acc.w += v.w;
+        }
+    }
+    if (!is_max) {
+        const float s = n > 0 ? 1.0f / (float)n : 0.0f;
+        acc.x *= s;
+        acc.y *= s;
+        acc.z *= s;
+        acc.w *= s;
+    }
+    out[o * inner4 + col] = acc;
+}
+
 // inner == 1: one wavefront per row.
 __global__ void reduce_mid_rows(int is_max, long outer, long n, const float *in, float *out) {
     const int lane = threadIdx.x & 63;
@@ -291,6 +347,53 @@ __global__ void pool_nhwc(const PoolGeo g, const float *in, float *out) {
     }
 }
 
+// NHWC with C % 4 == 0: one thread per output channel quad, 16-byte loads and stores, 32-bit
+// index arithmetic with host-computed divisors (the element count is below 2^31).
+__global__ void pool_nhwc_vec4(const PoolGeo g, FastDiv div_c4, FastDiv div_ow, FastDiv div_oh,
+                               int total, const float *in, float *out) {
+    const int C4 = g.C >> 2;
+    for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += gridDim.x * blockDim.x) {
+        int t = fdiv(idx, div_c4);
+        const int c4 = idx - t * C4;
+        int t2 = fdiv(t, div_ow);
+        const int ow = t - t2 * g.OW;
+        const int n = fdiv(t2, div_oh);
+        const int oh = t2 - n * g.OH;
+        const float *img = in + (long)n * g.H * g.W * g.C + c4 * 4;
+        const float init = g.is_max ? -INFINITY : 0.0f;
+        float4 acc = make_float4(init, init, init, init);
+        for (int kh = 0; kh < g.KH; ++kh) {
+            const int ih = oh * g.SH - g.PT + kh * g.DH;
+            if (ih < 0 || ih >= g.H) continue;
+            for (int kw = 0; kw < g.KW; ++kw) {
+                const int iw = ow * g.SW - g.PL + kw * g.DW;
+                if (iw < 0 || iw >= g.W) continue;
+                const float4 v = *reinterpret_cast<const float4 *>(img + (long)(ih * g.W + iw) * g.C);
+                if (g.is_max) {
+                    acc.x = v.x > acc.x ? v.x : acc.x;
+                    acc.y = v.y > acc.y ? v.y : acc.y;
+                    acc.z = v.z > acc.z ? v.z : acc.z;
+                    acc.w = v.w > acc.w ? v.w : acc.w;
+                } else {
+                    acc.x += v.x;
+                    acc.y += v.y;
+                    acc.z += v.z;
+                    acc.w += v.w;
+                }
+            }
+        }
+        if (!g.is_max) {
+            const int cnt = window_count(g, oh, ow);
+            const float s = cnt > 0 ? 1.0f / (float)cnt : 0.0f;
+            acc.x *= s;
+            acc.y *= s;
+            acc.z *= s;
+            acc.w *= s;
+        }
+        reinterpret_cast<float4 *>(out)[idx] = acc;
+    }
+}
+
 __global__ void pool_nchw(const PoolGeo g, const float *in, float *out) {
     const long total = (long)g.N * g.C * g.OH * g.OW;
     for (long idx = blockIdx.x * (long)blockDim.x + threadIdx.x; idx < total;
@@ -440,6 +543,11 @@ extern "C" void mgc_hip_reduce_mid(mgc_hip_exec *x, int is_max, long outer, long
     if (inner == 1 && n >= 64) {
         MGC_LAUNCH(x, reduce_mid_rows, dim3(blocks_for(outer * 64, 256, 8192)), dim3(256), 0,
                    is_max, outer, n, in, out);
+    } else if (inner % 4 == 0 && outer <= 65535 && n < 0x7fffffffL && inner < 0x7fffffffL &&
+               (((uintptr_t)in | (uintptr_t)out) & 15) == 0) {
+        const int inner4 = (int)(inner / 4);
+        MGC_LAUNCH(x, reduce_mid_vec4, dim3((unsigned)((inner4 + 63) / 64), (unsigned)outer), dim3(256),
+                   0, is_max, (int)n, inner4, (const float4 *)in, (float4 *)out);
     } else {
         MGC_LAUNCH(x, reduce_mid_strided, dim3(blocks_for(outer * inner, 256, 8192)), dim3(256),
                    0, is_max, outer, n, inner, in, out);
@@ -532,10 +640,18 @@ extern "C" void mgc_hip_pool(mgc_hip_exec *x, int nhwc, int is_max, int N, int H
     long total = (long)N * OH * OW * C;
     if (total <= 0) return;
     dim3 grid(blocks_for(total, 256, 16384));
-    if (nhwc)
+    const bool vec = nhwc && C % 4 == 0 && total < 0x7fffffffL && (long)N * H * W * C < 0x7fffffffL &&
+                     (((uintptr_t)in | (uintptr_t)out) & 15) == 0;
+    if (vec) {
+        const int quads = (int)(total / 4);
+        MGC_LAUNCH(x, pool_nhwc_vec4, dim3(blocks_for(quads, 256, 16384)), dim3(256), 0, g,
+                   make_fastdiv((unsigned)(C / 4)), make_fastdiv((unsigned)OW), make_fastdiv((unsigned)OH),
+                   quads, in, out);
+    } else if (nhwc) {
         MGC_LAUNCH(x, pool_nhwc, grid, dim3(256), 0, g, in, out);
-    else
+    } else {
         MGC_LAUNCH(x, pool_nchw, grid, dim3(256), 0, g, in, out);
+    }
 }
 
 extern "C" void mgc_hip_depthwise(mgc_hip_exec *x, int nhwc, int N, int H, int W, int C, int KH,

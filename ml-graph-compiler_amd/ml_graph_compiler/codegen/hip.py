@@ -1099,12 +1099,17 @@ class HipEmitter:
         h2, w2, c4 = h // 2, wd // 2, 4 * c
         dst = f"(A + {self._scratch_off})"
         src = self._s2d[id(node)]
-        if src is not None:  # NCHW source [b, c, 2i + dy, 2j + dx]
-            in_ptr, in_st = self.ptr(src), [c * h * wd, 2 * wd, 2, wd, 1, h * wd]
-        else:                # NHWC source [b, 2i + dy, 2j + dx, c]
-            in_ptr, in_st = self.ptr(node.input(0)), [h * wd * c, 2 * wd * c, 2 * c, wd * c, c, 1]
-        shape = [nb, h2, w2, 2, 2, c]
-        self.copy(shape, dst, _strides(shape), 0, in_ptr, in_st, 0, 4)
+        out_st = _strides([nb, h2, w2, 2, 2, c])  # x2[b, i, j, dy, dx, c]
+        if src is not None:
+            # NCHW source [b, c, 2i + dy, 2j + dx]; walked as (b, i, c, dy, j, dx) so that
+            # neighbouring threads read neighbouring source elements
+            order = [0, 1, 5, 3, 2, 4]
+            in_st = [c * h * wd, 2 * wd, 2, wd, 1, h * wd]
+            self.copy([[nb, h2, w2, 2, 2, c][d] for d in order], dst, [out_st[d] for d in order], 0,
+                      self.ptr(src), [in_st[d] for d in order], 0, 4)
+        else:  # NHWC source [b, 2i + dy, 2j + dx, c]
+            in_st = [h * wd * c, 2 * wd * c, 2 * c, wd * c, c, 1]
+            self.copy([nb, h2, w2, 2, 2, c], dst, out_st, 0, self.ptr(node.input(0)), in_st, 0, 4)
         self.count("space_to_depth")
         w = node.input(1).data
         KH, KW = s2["KH"], s2["KW"]
