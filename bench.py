@@ -289,7 +289,7 @@ def main() -> int:
     model.release()
 
     b1 = None
-    if args.workload in ("resnet50", "bottleneck", "mobilenet_v2", "bert_base") and not args.no_b1 and batch != 1:
+    if args.workload in ("resnet50", "bottleneck", "mobilenet_v2", "bert_base", "gpt2") and not args.no_b1 and batch != 1:
         g1, m1 = compile_workload(args.workload, 1, cache)
         m1.upload(feeds_for(g1))
         m1.launch(args.warmup)
@@ -303,7 +303,7 @@ def main() -> int:
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.workload)
     unit = {"resnet50": "img/s", "bottleneck": "img/s", "mobilenet_v2": "img/s", "bert_base": "seq/s",
-            "single_gemm": "calls/s"}[args.workload]
+            "gpt2": "seq/s", "single_gemm": "calls/s"}[args.workload]
     line = {
         "metric": "ResNet-50 fp32 img/s at b1/b32; achieved TFLOP/s vs fp32 MFMA peak"
         if args.workload == "resnet50" else f"{args.workload} fp32 {unit}",
