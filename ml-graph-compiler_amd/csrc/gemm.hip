@@ -744,6 +744,26 @@ __global__ void gemm_splitk_reduce(const GemmDev p) {
     }
 }
 
+// The same for N % 4 == 0 with 16-byte aligned output rows: four columns per thread, 16-byte
+// partial loads and stores (element sums in the same split order as above).
+__global__ void gemm_splitk_reduce_vec4(const GemmDev p, FastDiv div_n4) {
+    const int N4 = p.N >> 2;
+    const int total4 = p.M * N4;
+    const long total = (long)p.M * p.N;
+    const f4 *ws4 = reinterpret_cast<const f4 *>(p.ws);
+    for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total4; idx += gridDim.x * blockDim.x) {
+        const int row = fdiv(idx, div_n4);
+        const int col = (idx - row * N4) * 4;
+        f4 v = ws4[idx];
+        for (int s = 1; s < p.split; ++s) v += ws4[(long)s * (total >> 2) + idx];
+        v = v * p.alpha;
+        if (p.bias && p.bias_mode == 2) v += p.bias[row];
+        if (p.bias && p.bias_mode == 1) v += ldg4(p.bias + col);
+        if (p.res) v += p.beta * ldg4(p.res + (long)row * p.ldr + col);
+        *reinterpret_cast<f4 *>(p.c + (long)row * p.ldc + col) = act4(v, p.act, p.lo, p.hi);
+    }
+}
+
 static bool aligned16(const void *ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
 static bool bs_div4(const long *bs, int rank) {
@@ -926,7 +946,12 @@ extern "C" void mgc_hip_gemm(mgc_hip_exec *x, const mgc_hip_gemm_args *g) {
     const dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)(batch * p.split));
     MGC_LAUNCH(x, kern, grid, dim3(256), 0, p);
     if (p.split > 1) {
-        MGC_LAUNCH(x, gemm_splitk_reduce, dim3(blocks_for((long)p.M * p.N, 256, 4096)), dim3(256),
-                   0, p);
+        const long total = (long)p.M * p.N;
+        if (p.vec_out && p.N % 4 == 0 && total < 0x7fffffffL && aligned16(p.ws)) {
+            MGC_LAUNCH(x, gemm_splitk_reduce_vec4, dim3(blocks_for(total / 4, 256, 4096)), dim3(256), 0,
+                       p, make_fastdiv((unsigned)(p.N / 4)));
+        } else {
+            MGC_LAUNCH(x, gemm_splitk_reduce, dim3(blocks_for(total, 256, 4096)), dim3(256), 0, p);
+        }
     }
 }
