@@ -1125,7 +1125,8 @@ class HipEmitter:
                         if 0 <= q < s2["kw"]:
                             w2m[t, u, dy, dx] = w[r, q]
         kdim = KH * KW * c4
-        bspec = self._packed_b(w2m.reshape(kdim, kout), ("s2d", id(node.input(1))))
+        # the rearranged weights depend on the pads too, so those are part of the blob key
+        bspec = self._packed_b(w2m.reshape(kdim, kout), ("s2d", id(node.input(1)), s2["pt"], s2["pl"]))
         oh, ow = s2["oh"], s2["ow"]
         geo = (f"g.a.H = {h2}; g.a.W = {w2}; g.a.C = {c4}; g.a.KH = {KH}; g.a.KW = {KW}; g.a.SH = 1; "
                f"g.a.SW = 1; g.a.DH = 1; g.a.DW = 1; g.a.PT = {s2['P']}; g.a.PL = {s2['Q']}; "
