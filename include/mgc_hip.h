@@ -15,6 +15,7 @@
  *   mgc_hip_softmax         <- mgc_softmax (mgc_runtime.h:196)
  *   mgc_hip_layer_norm      <- mgc_layer_norm (mgc_runtime.h:199-200)
  *   mgc_hip_elementwise     <- the loop nests CEmitter.elementwise/loops emit (codegen/c.py:360-529)
+ *   mgc_hip_space_to_depth  <- no counterpart (feeds the stem convolution's stride-1 form)
  *   mgc_hip_copy            <- the identity-body loop nests of op_Transpose/Expand/Tile/Slice/
  *                              Concat/Split/Pad (codegen/c.py:558-660) and output copies (c.py:1283)
  *   mgc_hip_fill            <- constant loops of _write_constant/op_ConstantOfShape (c.py:690-722)
@@ -261,6 +262,13 @@ typedef struct {
 } mgc_hip_copy_args;
 
 void mgc_hip_copy(mgc_hip_exec *x, const mgc_hip_copy_args *c);
+
+/* Space-to-depth of an NCHW float image for a stride-2 convolution over few channels:
+ * out[b][i][j][(dy * 2 + dx) * C + c] = in[b][c][2 i + dy][2 j + dx], out contiguous
+ * [N][H/2][W/2][4 C]. Requires even H and W and 1 <= C <= 8 (returns without launching and
+ * sets the launch error otherwise). No counterpart in the reference: the hip emitter uses it to
+ * run the network's stem convolution as a stride-1 convolution with 16-byte operand loads. */
+void mgc_hip_space_to_depth(mgc_hip_exec *x, int N, int C, int H, int W, const float *in, float *out);
 
 /* Fill n elements of elem_bytes each with the bit pattern `bits`. */
 void mgc_hip_fill(mgc_hip_exec *x, void *out, long n, int elem_bytes, uint64_t bits);

@@ -534,6 +534,32 @@ __global__ void __launch_bounds__(256) copy_kernel(const mgc_hip_copy_args c) {
     }
 }
 
+// One thread per output pixel (b, i, j): two 8-byte reads per channel and row of the 2 x 2
+// block (neighbouring threads read neighbouring pairs), C 16-byte writes of the pixel's 4 C
+// values (neighbouring threads write neighbouring 16 C-byte groups).
+__global__ void space_to_depth_kernel(int C, int H2, int W2, int total, FastDiv div_w2, FastDiv div_h2,
+                                      const float *in, float *out) {
+    const int H = 2 * H2, W = 2 * W2;
+    for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += gridDim.x * blockDim.x) {
+        const int t = fdiv(idx, div_w2);
+        const int j = idx - t * W2;
+        const int b = fdiv(t, div_h2);
+        const int i = t - b * H2;
+        float v[32];
+        const float *src = in + (long)b * C * H * W + (long)(2 * i) * W + 2 * j;
+        for (int c = 0; c < C; ++c) {
+#pragma unroll
+            for (int dy = 0; dy < 2; ++dy) {
+                const float2 pr = *reinterpret_cast<const float2 *>(src + (long)c * H * W + dy * W);
+                v[(dy * 2) * C + c] = pr.x;
+                v[(dy * 2 + 1) * C + c] = pr.y;
+            }
+        }
+        float4 *dst = reinterpret_cast<float4 *>(out + (long)idx * 4 * C);
+        for (int q = 0; q < C; ++q) dst[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+    }
+}
+
 template <typename T>
 __global__ void fill_kernel(T *out, long n, T v) {
     for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < n;
@@ -629,6 +655,19 @@ extern "C" void mgc_hip_copy(mgc_hip_exec *x, const mgc_hip_copy_args *c) {
     case 8: MGC_LAUNCH(x, copy_kernel<unsigned long long>, grid, dim3(256), 0, a); break;
     default: MGC_LAUNCH(x, copy_kernel<uint4>, grid, dim3(256), 0, a); break;
     }
+}
+
+extern "C" void mgc_hip_space_to_depth(mgc_hip_exec *x, int N, int C, int H, int W, const float *in,
+                                       float *out) {
+    const long total = (long)N * (H / 2) * (W / 2);
+    if (N <= 0 || C < 1 || C > 8 || H % 2 || W % 2 || H <= 0 || W <= 0 ||
+        total * 4 * C >= 0x7fffffffL || (((uintptr_t)in & 7) | ((uintptr_t)out & 15))) {
+        x->launch_error = (int)hipErrorInvalidValue;
+        set_error("mgc_hip_space_to_depth: unsupported shape or alignment", hipErrorInvalidValue);
+        return;
+    }
+    MGC_LAUNCH(x, space_to_depth_kernel, dim3(blocks_for(total, 256, 16384)), dim3(256), 0, C, H / 2,
+               W / 2, (int)total, make_fastdiv((unsigned)(W / 2)), make_fastdiv((unsigned)(H / 2)), in, out);
 }
 
 extern "C" void mgc_hip_fill(mgc_hip_exec *x, void *out, long n, int elem_bytes, uint64_t bits) {

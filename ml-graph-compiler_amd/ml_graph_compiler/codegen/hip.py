@@ -1100,9 +1100,12 @@ class HipEmitter:
         dst = f"(A + {self._scratch_off})"
         src = self._s2d[id(node)]
         out_st = _strides([nb, h2, w2, 2, 2, c])  # x2[b, i, j, dy, dx, c]
-        if src is not None:
-            # NCHW source [b, c, 2i + dy, 2j + dx]; walked as (b, i, c, dy, j, dx) so that
-            # neighbouring threads read neighbouring source elements
+        if src is not None and c <= 8:
+            # NCHW source [b, c, 2i + dy, 2j + dx]: a thread per output pixel, paired reads
+            self.emit(f"mgc_hip_space_to_depth(x, {nb}, {c}, {h}, {wd}, (const float *){self.ptr(src)}, (float *){dst});")
+        elif src is not None:
+            # walked as (b, i, c, dy, j, dx) so that neighbouring threads read neighbouring
+            # source elements
             order = [0, 1, 5, 3, 2, 4]
             in_st = [c * h * wd, 2 * wd, 2, wd, 1, h * wd]
             self.copy([[nb, h2, w2, 2, 2, c][d] for d in order], dst, [out_st[d] for d in order], 0,
