@@ -50,6 +50,16 @@ __device__ __forceinline__ int fdiv(int n, const FastDiv &f) {
     return (int)((__umulhi((unsigned)n, f.m) + (unsigned)n) >> f.s);
 }
 
+// Workgroup ids of a 1-D grid are dealt round-robin to the 8 XCDs, each with its own L2. This
+// renumbering (a permutation of 0..gridDim.x-1) gives XCD x a contiguous range of logical
+// blocks, so neighbouring blocks that read overlapping input rows share one L2 instead of each
+// XCD fetching the rows from HBM again.
+__device__ __forceinline__ int xcd_block() {
+    const int nb = gridDim.x, b = blockIdx.x;
+    const int per = nb >> 3, rem = nb & 7, x = b & 7, i = b >> 3;
+    return x < rem ? x * (per + 1) + i : rem * (per + 1) + (x - rem) * per + i;
+}
+
 // ------------------------------------------------------------------------------------------
 // device math. exp/log/sqrt/tanh come from the HIP device library; erf uses the rational
 // approximation the reference's interpreter and C runtime share (ops.py:201-229,

@@ -296,6 +296,62 @@ __global__ void __launch_bounds__(256) layer_norm_rows(long rows, long cols, con
     }
 }
 
+// cols % 4 == 0 and cols <= 1024 with 16-byte aligned rows (the hidden sizes of transformer
+// encoders): one wavefront per row holds the row in registers as up to four float4 per lane, so
+// the row is read once and written once with 16-byte accesses and three times fewer load
+// instructions than the scalar kernel.
+__global__ void __launch_bounds__(256) layer_norm_rows_vec4(int rows, int cols4, const float4 *in,
+                                                            const float4 *scale, const float4 *bias,
+                                                            float eps, float4 *out) {
+    const int lane = threadIdx.x & 63;
+    const int r = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    if (r >= rows) return;
+    const float4 *src = in + (long)r * cols4;
+    float4 *dst = out + (long)r * cols4;
+    const float cols = (float)(cols4 * 4);
+    float4 v[4];
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int k = lane + 64 * j;
+        v[j] = k < cols4 ? src[k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        sum += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+    }
+    const float mean = wave_sum(sum) / cols;
+    float var = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (lane + 64 * j < cols4) {
+            const float dx = v[j].x - mean, dy = v[j].y - mean, dz = v[j].z - mean, dw = v[j].w - mean;
+            var += (dx * dx + dy * dy) + (dz * dz + dw * dw);
+        }
+    }
+    const float inv = 1.0f / sqrtf(wave_sum(var) / cols + eps);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int k = lane + 64 * j;
+        if (k < cols4) {
+            float4 y = make_float4((v[j].x - mean) * inv, (v[j].y - mean) * inv,
+                                   (v[j].z - mean) * inv, (v[j].w - mean) * inv);
+            if (scale) {
+                const float4 s = scale[k];
+                y.x *= s.x;
+                y.y *= s.y;
+                y.z *= s.z;
+                y.w *= s.w;
+            }
+            if (bias) {
+                const float4 b = bias[k];
+                y.x += b.x;
+                y.y += b.y;
+                y.z += b.z;
+                y.w += b.w;
+            }
+            dst[k] = y;
+        }
+    }
+}
+
 // ---- pooling -----------------------------------------------------------------------------------
 struct PoolGeo {
     int N, H, W, C, KH, KW, SH, SW, DH, DW, PT, PL, PB, PR, OH, OW, include_pad, is_max;
@@ -352,7 +408,7 @@ __global__ void pool_nhwc(const PoolGeo g, const float *in, float *out) {
 __global__ void pool_nhwc_vec4(const PoolGeo g, FastDiv div_c4, FastDiv div_ow, FastDiv div_oh,
                                int total, const float *in, float *out) {
     const int C4 = g.C >> 2;
-    for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += gridDim.x * blockDim.x) {
+    for (int idx = xcd_block() * blockDim.x + threadIdx.x; idx < total; idx += gridDim.x * blockDim.x) {
         int t = fdiv(idx, div_c4);
         const int c4 = idx - t * C4;
         int t2 = fdiv(t, div_ow);
@@ -429,40 +485,40 @@ struct DwGeo {
     float lo, hi;
 };
 
-// NHWC, four channels per thread (C % 4 == 0): float4 loads of input, weights and bias.
-__global__ void depthwise_nhwc_vec4(const DwGeo g, const float *in, const float *w,
-                                    const float *bias, const float *res, float *out) {
+// NHWC, four channels per thread (C % 4 == 0): float4 loads of input, weights and bias, and
+// 32-bit index arithmetic with host-computed divisors (the quad count is below 2^31): 64-bit
+// division chains would make this bandwidth-bound kernel ALU-bound. Blocks run in XCD order.
+__global__ void depthwise_nhwc_vec4(const DwGeo g, FastDiv div_c4, FastDiv div_ow, FastDiv div_oh,
+                                    int total, const float *in, const float *w, const float *bias,
+                                    const float *res, float *out) {
     const int C4 = g.C >> 2;
-    const long total = (long)g.N * g.OH * g.OW * C4;
-    for (long idx = blockIdx.x * (long)blockDim.x + threadIdx.x; idx < total;
-         idx += (long)gridDim.x * blockDim.x) {
-        long t = idx;
-        const int c4 = (int)(t % C4);
-        t /= C4;
-        const int ow = (int)(t % g.OW);
-        t /= g.OW;
-        const int oh = (int)(t % g.OH);
-        const int n = (int)(t / g.OH);
+    for (int idx = xcd_block() * blockDim.x + threadIdx.x; idx < total; idx += gridDim.x * blockDim.x) {
+        const int t = fdiv(idx, div_c4);
+        const int c4 = idx - t * C4;
+        const int t2 = fdiv(t, div_ow);
+        const int ow = t - t2 * g.OW;
+        const int n = fdiv(t2, div_oh);
+        const int oh = t2 - n * g.OH;
         const int c = c4 * 4;
         float4 acc = bias ? *reinterpret_cast<const float4 *>(bias + c) : make_float4(0, 0, 0, 0);
         const float *img = in + (long)n * g.H * g.W * g.C + c;
         for (int kh = 0; kh < g.KH; ++kh) {
-            int ih = oh * g.SH - g.PT + kh * g.DH;
+            const int ih = oh * g.SH - g.PT + kh * g.DH;
             if (ih < 0 || ih >= g.H) continue;
             for (int kw = 0; kw < g.KW; ++kw) {
-                int iw = ow * g.SW - g.PL + kw * g.DW;
+                const int iw = ow * g.SW - g.PL + kw * g.DW;
                 if (iw < 0 || iw >= g.W) continue;
-                float4 xv = *reinterpret_cast<const float4 *>(img + ((long)ih * g.W + iw) * g.C);
-                float4 wv = *reinterpret_cast<const float4 *>(w + ((long)kh * g.KW + kw) * g.C + c);
+                const float4 xv = *reinterpret_cast<const float4 *>(img + (long)(ih * g.W + iw) * g.C);
+                const float4 wv = *reinterpret_cast<const float4 *>(w + (kh * g.KW + kw) * g.C + c);
                 acc.x = fmaf(xv.x, wv.x, acc.x);
                 acc.y = fmaf(xv.y, wv.y, acc.y);
                 acc.z = fmaf(xv.z, wv.z, acc.z);
                 acc.w = fmaf(xv.w, wv.w, acc.w);
             }
         }
-        const long o = idx * 4;
+        const long o = (long)idx * 4;
         if (res) {
-            float4 rv = *reinterpret_cast<const float4 *>(res + o);
+            const float4 rv = *reinterpret_cast<const float4 *>(res + o);
             acc.x += rv.x;
             acc.y += rv.y;
             acc.z += rv.z;
@@ -473,6 +529,83 @@ __global__ void depthwise_nhwc_vec4(const DwGeo g, const float *in, const float 
         acc.z = apply_act(acc.z, g.act, g.lo, g.hi);
         acc.w = apply_act(acc.w, g.act, g.lo, g.hi);
         *reinterpret_cast<float4 *>(out + o) = acc;
+    }
+}
+
+// 3x3, dilation 1, horizontal stride SW (1 or 2), C % 4 == 0: each thread computes four
+// channels of T neighbouring output pixels of one row. The ((T - 1) * SW + 3) input columns
+// those outputs share are loaded once per kernel row and the weights once per thread, so the
+// cache traffic per output quad drops from 18 float4 loads (nine input taps and nine weights)
+// to (3 * ((T - 1) * SW + 3) + 9) / T. Blocks run in XCD order (xcd_block), so the three input
+// rows an output row needs are mostly fetched into one L2 once. Taps are accumulated in the
+// same order as the general kernel (bias, then row-major over the window), and out-of-image
+// taps are skipped, not multiplied.
+template <int SW, int T>
+__global__ void __launch_bounds__(256) depthwise3x3_nhwc_vec4(const DwGeo g, FastDiv div_c4, FastDiv div_owb,
+                                                              FastDiv div_oh, int total, const float *in,
+                                                              const float *w, const float *bias,
+                                                              const float *res, float *out) {
+    constexpr int NCOL = (T - 1) * SW + 3;
+    const int C4 = g.C >> 2, OWB = (g.OW + T - 1) / T;
+    for (int idx = xcd_block() * blockDim.x + threadIdx.x; idx < total; idx += gridDim.x * blockDim.x) {
+        const int t = fdiv(idx, div_c4);
+        const int c4 = idx - t * C4;
+        const int t2 = fdiv(t, div_owb);
+        const int owb = t - t2 * OWB;
+        const int n = fdiv(t2, div_oh);
+        const int oh = t2 - n * g.OH;
+        const int c = c4 * 4, ow0 = owb * T, iw0 = ow0 * SW - g.PL;
+        const float4 b = bias ? *reinterpret_cast<const float4 *>(bias + c) : make_float4(0, 0, 0, 0);
+        float4 acc[T];
+#pragma unroll
+        for (int j = 0; j < T; ++j) acc[j] = b;
+        const float *img = in + (long)n * g.H * g.W * g.C + c;
+#pragma unroll
+        for (int kh = 0; kh < 3; ++kh) {
+            const int ih = oh * g.SH - g.PT + kh;
+            if (ih < 0 || ih >= g.H) continue;
+            const float *row = img + (long)ih * g.W * g.C;
+            float4 xs[NCOL];
+#pragma unroll
+            for (int q = 0; q < NCOL; ++q) {
+                const int iw = iw0 + q;
+                xs[q] = iw >= 0 && iw < g.W ? *reinterpret_cast<const float4 *>(row + (long)iw * g.C)
+                                            : make_float4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int kw = 0; kw < 3; ++kw) {
+                const float4 wv = *reinterpret_cast<const float4 *>(w + (kh * 3 + kw) * g.C + c);
+#pragma unroll
+                for (int j = 0; j < T; ++j) {
+                    const int iw = iw0 + j * SW + kw;
+                    if (iw < 0 || iw >= g.W) continue;
+                    const float4 xv = xs[j * SW + kw];
+                    acc[j].x = fmaf(xv.x, wv.x, acc[j].x);
+                    acc[j].y = fmaf(xv.y, wv.y, acc[j].y);
+                    acc[j].z = fmaf(xv.z, wv.z, acc[j].z);
+                    acc[j].w = fmaf(xv.w, wv.w, acc[j].w);
+                }
+            }
+        }
+        const long base = ((long)(n * g.OH + oh) * g.OW + ow0) * g.C + c;
+#pragma unroll
+        for (int j = 0; j < T; ++j) {
+            if (ow0 + j >= g.OW) break;
+            const long o = base + (long)j * g.C;
+            float4 v = acc[j];
+            if (res) {
+                const float4 rv = *reinterpret_cast<const float4 *>(res + o);
+                v.x += rv.x;
+                v.y += rv.y;
+                v.z += rv.z;
+                v.w += rv.w;
+            }
+            v.x = apply_act(v.x, g.act, g.lo, g.hi);
+            v.y = apply_act(v.y, g.act, g.lo, g.hi);
+            v.z = apply_act(v.z, g.act, g.lo, g.hi);
+            v.w = apply_act(v.w, g.act, g.lo, g.hi);
+            *reinterpret_cast<float4 *>(out + o) = v;
+        }
     }
 }
 
@@ -627,6 +760,14 @@ extern "C" void mgc_hip_softmax(mgc_hip_exec *x, long outer, long n, long inner,
 extern "C" void mgc_hip_layer_norm(mgc_hip_exec *x, long rows, long cols, const float *in,
                                    const float *scale, const float *bias, float eps, float *out) {
     if (rows <= 0 || cols <= 0) return;
+    const bool vec = cols % 4 == 0 && cols <= 1024 && rows < (1L << 25) &&
+                     (((uintptr_t)in | (uintptr_t)out | (uintptr_t)scale | (uintptr_t)bias) & 15) == 0;
+    if (vec) {
+        MGC_LAUNCH(x, layer_norm_rows_vec4, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, (int)rows,
+                   (int)(cols / 4), (const float4 *)in, (const float4 *)scale, (const float4 *)bias, eps,
+                   (float4 *)out);
+        return;
+    }
     MGC_LAUNCH(x, layer_norm_rows, dim3(blocks_for(rows * 64, 256, 16384)), dim3(256), 0, rows,
                cols, in, scale, bias, eps, out);
 }
@@ -654,6 +795,12 @@ extern "C" void mgc_hip_pool(mgc_hip_exec *x, int nhwc, int is_max, int N, int H
     }
 }
 
+// Output pixels per thread of the 3x3 depthwise kernel: four on wide stride-1 rows, else two
+// (four would leave too few threads and waste a partial tile on every narrow row; at stride 2
+// four outputs share fewer of their nine columns). Chosen by timing MobileNetV2's 17 depthwise
+// layers at batch 32 with each choice.
+static int dw3_tile(int OW, int SW) { return SW == 1 && OW >= 28 ? 4 : 2; }
+
 extern "C" void mgc_hip_depthwise(mgc_hip_exec *x, int nhwc, int N, int H, int W, int C, int KH,
                                   int KW, int SH, int SW, int DH, int DW, int PT, int PL, int OH,
                                   int OW, const float *in, const float *w, const float *bias,
@@ -662,11 +809,22 @@ extern "C" void mgc_hip_depthwise(mgc_hip_exec *x, int nhwc, int N, int H, int W
     long total = (long)N * OH * OW * C;
     if (total <= 0) return;
     if (nhwc) {
-        bool vec = C % 4 == 0 && (((uintptr_t)in | (uintptr_t)w | (uintptr_t)out |
-                                   (uintptr_t)bias | (uintptr_t)res) & 15) == 0;
-        if (vec)
+        bool vec = C % 4 == 0 && total / 4 < 0x7fffffffL && (long)N * H * W * C < 0x7fffffffL &&
+                   (((uintptr_t)in | (uintptr_t)w | (uintptr_t)out | (uintptr_t)bias | (uintptr_t)res) & 15) == 0;
+        const bool k3 = KH == 3 && KW == 3 && DH == 1 && DW == 1 && (SW == 1 || SW == 2);
+        if (vec && k3) {
+            const int tile = dw3_tile(OW, SW);
+            const int owb = (OW + tile - 1) / tile;
+            const int quads = (int)((long)N * OH * owb * (C / 4));
+            auto kern = SW == 2 ? depthwise3x3_nhwc_vec4<2, 2>
+                                : (tile == 4 ? depthwise3x3_nhwc_vec4<1, 4> : depthwise3x3_nhwc_vec4<1, 2>);
+            MGC_LAUNCH(x, kern, dim3(blocks_for(quads, 256, 16384)), dim3(256), 0, g,
+                       make_fastdiv((unsigned)(C / 4)), make_fastdiv((unsigned)owb), make_fastdiv((unsigned)OH),
+                       quads, in, w, bias, res, out);
+        } else if (vec)
             MGC_LAUNCH(x, depthwise_nhwc_vec4, dim3(blocks_for(total / 4, 256, 16384)), dim3(256),
-                       0, g, in, w, bias, res, out);
+                       0, g, make_fastdiv((unsigned)(C / 4)), make_fastdiv((unsigned)OW),
+                       make_fastdiv((unsigned)OH), (int)(total / 4), in, w, bias, res, out);
         else
             MGC_LAUNCH(x, depthwise_nhwc, dim3(blocks_for(total, 256, 16384)), dim3(256), 0, g, in,
                        w, bias, res, out);

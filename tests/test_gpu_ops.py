@@ -138,6 +138,12 @@ def test_layer_and_batch_norm(hip_cache):
     check_hip(*op_graph("LayerNormalization", [f32(2, 5, 16), pos(16), f32(16)], const={1, 2},
                         attrs={"axis": -1, "epsilon": 1e-5}), hip_cache)
     check_hip(*op_graph("LayerNormalization", [f32(2, 3, 4), pos(3, 4)], attrs={"axis": 1}), hip_cache)
+    # rows of 768 and 1000 (several float4 per lane, the last partly filled), 1024 (the widest
+    # row held in registers), 1028 and 10 (the scalar kernel), and a row without bias
+    for cols in (768, 1000, 1024, 1028, 10):
+        check_hip(*op_graph("LayerNormalization", [f32(37, cols) * 3 + 1, pos(cols), f32(cols)], const={1, 2},
+                            attrs={"axis": -1, "epsilon": 1e-5}), hip_cache)
+    check_hip(*op_graph("LayerNormalization", [f32(5, 768), np.ones(768, np.float32)], const={1}), hip_cache)
     check_hip(*op_graph("BatchNormalization", [f32(2, 3, 4, 5), pos(3), f32(3), f32(3), pos(3)], const={1, 2, 3, 4}),
               hip_cache)
 
@@ -194,6 +200,18 @@ CONV_CASES = [
     ({"kernel_shape": [3, 3], "auto_pad": "SAME_UPPER", "strides": [2, 2]}, (1, 3, 8, 8), (4, 3, 3, 3)),
     ({"kernel_shape": [3, 3], "pads": [1, 1, 1, 1]}, (2, 64, 10, 12), (96, 64, 3, 3)),
     ({"kernel_shape": [3, 3], "pads": [1, 1, 1, 1], "group": 32}, (2, 32, 9, 9), (32, 1, 3, 3)),
+    # depthwise over NHWC at O3 (C % 4 == 0): the 3x3 kernel with four output pixels per thread
+    # (output widths that are not a multiple of four, strides 1 and 2 on either axis, asymmetric
+    # pads) and the general kernel (dilation, 5x5)
+    ({"kernel_shape": [3, 3], "pads": [1, 1, 1, 1], "group": 16}, (2, 16, 7, 13), (16, 1, 3, 3)),
+    ({"kernel_shape": [3, 3], "pads": [1, 1, 1, 1], "group": 16, "strides": [2, 2]}, (2, 16, 15, 15), (16, 1, 3, 3)),
+    ({"kernel_shape": [3, 3], "pads": [0, 1, 2, 0], "group": 8, "strides": [2, 2]}, (1, 8, 10, 10), (8, 1, 3, 3)),
+    ({"kernel_shape": [3, 3], "pads": [2, 0, 0, 2], "group": 8, "strides": [1, 2]}, (1, 8, 6, 11), (8, 1, 3, 3)),
+    ({"kernel_shape": [3, 3], "group": 12, "strides": [2, 1]}, (1, 12, 9, 6), (12, 1, 3, 3)),
+    ({"kernel_shape": [3, 3], "pads": [1, 1, 1, 1], "group": 8}, (1, 8, 5, 30), (8, 1, 3, 3)),   # four per thread
+    ({"kernel_shape": [3, 3], "pads": [1, 0, 1, 1], "group": 8, "strides": [2, 2]}, (1, 8, 9, 62), (8, 1, 3, 3)),
+    ({"kernel_shape": [3, 3], "pads": [2, 2, 2, 2], "group": 8, "dilations": [2, 2]}, (1, 8, 9, 9), (8, 1, 3, 3)),
+    ({"kernel_shape": [5, 5], "pads": [2, 2, 2, 2], "group": 8}, (1, 8, 9, 9), (8, 1, 5, 5)),
 ]
 
 
@@ -202,6 +220,27 @@ CONV_CASES = [
 def test_conv(attrs, x_shape, w_shape, opt, hip_cache):
     g, feeds = op_graph("Conv", [f32(*x_shape), f32(*w_shape) * 0.3, f32(w_shape[0])], const={1, 2}, attrs=attrs)
     check_hip(g, feeds, hip_cache, opt=opt)
+
+
+def test_depthwise_with_residual_and_clip(hip_cache):
+    """Depthwise 3x3 with the residual Add and the ReLU6 Clip fused into its epilogue (O3)."""
+    from ml_graph_compiler.ir import Graph, TensorType
+    from ml_graph_compiler.shape_inference import infer_shapes
+
+    for stride, hw in ((1, 10), (1, 7)):
+        g = Graph("dw_res")
+        x = g.add_input("x", TensorType("float32", (2, 16, hw, hw)))
+        w = g.constant(f32(16, 1, 3, 3) * 0.3, "w")
+        b = g.constant(f32(16), "b")
+        y = g.add_node("Conv", [x, w, b], 1, {"kernel_shape": [3, 3], "pads": [1, 1, 1, 1], "group": 16,
+                                               "strides": [stride, stride]}, name="dw").output
+        y = g.add_node("Add", [y, x], 1, {}, name="res").output
+        lo = g.constant(np.asarray(0.0, np.float32), "lo")
+        hi = g.constant(np.asarray(6.0, np.float32), "hi")
+        y = g.add_node("Clip", [y, lo, hi], 1, {}, name="clip").output
+        g.add_output(y, "y")
+        infer_shapes(g)
+        check_hip(g, {"x": f32(2, 16, hw, hw) * 3}, hip_cache, opt="O3")
 
 
 POOL_CASES = [
