@@ -88,7 +88,8 @@ def gemm_roofline(graph, model, replays: int) -> dict:
     secs = 0.0
     launches = 0
     for (op, _name, sec), node, f in zip(prof, graph.nodes, model.node_flops):
-        if op in ("FusedConv", "Conv", "FusedGemm", "Gemm", "MatMul") and not _is_depthwise(node):
+        # f == 0: a GEMM node absorbed into a fused attention call (its work is timed there)
+        if op in ("FusedConv", "Conv", "FusedGemm", "Gemm", "MatMul") and not _is_depthwise(node) and f > 0:
             flops += f * replays
             secs += sec
             launches += replays
@@ -173,25 +174,35 @@ def pmc_probe(workload: str, batch: int, cache: Path) -> None:
     log("pmc probe done: calibration copy, then one eager forward")
 
 
-def pmc_summary(fetch_dir: Path, write_dir: Path, workload: str, batch: int) -> str:
-    """Markdown summary of the FETCH_SIZE and WRITE_SIZE runs over --pmc-probe."""
+def per_dispatch(d: Path, counter: str) -> list[tuple[str, float]]:
+    """(kernel name, counter value) of every dispatch of a rocprofv3 --pmc run, in dispatch order."""
     import csv
 
-    def per_dispatch(d: Path, counter: str) -> list[tuple[str, float]]:
-        rows = []
-        for f in sorted(d.rglob("*counter_collection.csv")):
-            for r in csv.DictReader(open(f)):
-                if r["Counter_Name"] == counter:
-                    rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
-        rows.sort()
-        return [(name, v) for _, name, v in rows]
+    rows = []
+    for f in sorted(d.rglob("*counter_collection.csv")):
+        for r in csv.DictReader(open(f)):
+            if r["Counter_Name"] == counter:
+                rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
+    rows.sort()
+    return [(name, v) for _, name, v in rows]
 
-    fetch = per_dispatch(fetch_dir, "FETCH_SIZE")
-    write = per_dispatch(write_dir, "WRITE_SIZE")
+
+def calibration(fetch: list[tuple[str, float]], write: list[tuple[str, float]]) -> tuple[float, float, float, float]:
+    """Bytes per counter KiB for FETCH_SIZE and WRITE_SIZE, from the probe's calibration copy
+    (the first copy_kernel dispatch), and the raw counter values of that copy."""
     nbytes = 4 * CALIBRATION_FLOATS
     cal_f = next(v for name, v in fetch if "copy_kernel" in name)
     cal_w = next(v for name, v in write if "copy_kernel" in name)
-    kf, kw = nbytes / (cal_f * 1024.0), nbytes / (cal_w * 1024.0)
+    return nbytes / cal_f, nbytes / cal_w, cal_f, cal_w
+
+
+def pmc_summary(fetch_dir: Path, write_dir: Path, workload: str, batch: int) -> str:
+    """Markdown summary of the FETCH_SIZE and WRITE_SIZE runs over --pmc-probe."""
+    fetch = per_dispatch(fetch_dir, "FETCH_SIZE")
+    write = per_dispatch(write_dir, "WRITE_SIZE")
+    nbytes = 4 * CALIBRATION_FLOATS
+    bf, bw, cal_f, cal_w = calibration(fetch, write)
+    kf, kw = bf / 1024.0, bw / 1024.0
 
     def is_gemm(name: str) -> bool:
         return "gemm_" in name and "reduce" not in name
@@ -239,6 +250,104 @@ def pmc_summary(fetch_dir: Path, write_dir: Path, workload: str, batch: int) -> 
     ])
 
 
+HBM_PEAK_GBS = 8000.0
+
+
+def _short_kernel(name: str) -> str:
+    """Kernel name without its parameter list and namespace (template arguments kept)."""
+    name = name.replace("(anonymous namespace)::", "")
+    return name.split("(", 1)[0].replace("void ", "").replace("mgc::", "").strip()
+
+
+def hbm_summary(fetch_dir: Path, write_dir: Path, trace_dir: Path, workload: str, batch: int) -> str:
+    """Achieved HBM bandwidth of every kernel of one eager forward: the calibrated FETCH_SIZE +
+    WRITE_SIZE bytes of each dispatch (two --pmc runs over --pmc-probe) over the dispatch's
+    duration in a third, kernel-trace-only run of the same program. The three runs launch the
+    same kernels in the same order; dispatches are matched by position and checked by name."""
+    import csv
+
+    fetch = per_dispatch(fetch_dir, "FETCH_SIZE")
+    write = per_dispatch(write_dir, "WRITE_SIZE")
+    trace = []
+    for f in sorted(trace_dir.rglob("*kernel_trace.csv")):
+        for r in csv.DictReader(open(f)):
+            trace.append((int(r["Dispatch_Id"]), r["Kernel_Name"],
+                          (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-9))
+    trace.sort()
+    bf, bw, _, _ = calibration(fetch, write)
+
+    def from_calibration(rows):
+        i = next(k for k, r in enumerate(rows) if "copy_kernel" in r[1 if len(r) == 3 else 0])
+        return rows[i + 1:]
+
+    def kernels_only(rows):  # the runtime's own blit kernels (uploads) are not the model's
+        return [r for r in rows if not r[1 if len(r) == 3 else 0].startswith("__amd_rocclr")]
+
+    fetch, write = kernels_only(from_calibration(fetch)), kernels_only(from_calibration(write))
+    trace = kernels_only(from_calibration(trace))
+    n = min(len(fetch), len(write), len(trace))
+    mismatched = sum(1 for i in range(n) if not (fetch[i][0] == write[i][0] == trace[i][1]))
+    if mismatched or not (len(fetch) == len(write) == len(trace)):
+        raise SystemExit(f"runs differ: {len(fetch)}/{len(write)}/{len(trace)} dispatches, {mismatched} names differ")
+    rows = []
+    for i in range(n):
+        name = _short_kernel(trace[i][1])
+        fb, wb, sec = fetch[i][1] * bf, write[i][1] * bw, trace[i][2]
+        rows.append((name, fb, wb, sec))
+
+    def bound(name: str) -> str:
+        if "gemm_" in name and "reduce" not in name:
+            return "MFMA"
+        return "MFMA/latency" if "attention" in name else "HBM"
+
+    fam: dict[str, list] = {}
+    for name, fb, wb, sec in rows:
+        a = fam.setdefault(name, [0, 0.0, 0.0])
+        a[0] += 1
+        a[1] += fb + wb
+        a[2] += sec
+    total_sec = sum(r[3] for r in rows)
+    cmd_base = "$GRAFT_REPO_ROOT/bench.py --pmc-probe --workload {w} --batch {b}".format(w=workload, b=batch)
+    out = [
+        f"# Achieved HBM bandwidth per kernel: {workload} b{batch} forward (hip backend, -O3)",
+        "",
+        "Commands (repo root, on the MI355X box; one counter per run, then a kernel trace):",
+        "",
+        "```",
+        "cd /tmp && export TMPDIR=/tmp",
+        f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d $GRAFT_REPO_ROOT/gpurun_out/hbm_fetch -o p -- python3 {cmd_base}",
+        f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d $GRAFT_REPO_ROOT/gpurun_out/hbm_write -o p -- python3 {cmd_base}",
+        f"rocprofv3 --kernel-trace --output-format csv -d $GRAFT_REPO_ROOT/gpurun_out/hbm_trace -o p -- python3 {cmd_base}",
+        f"python3 bench.py --hbm-summary gpurun_out/hbm_fetch gpurun_out/hbm_write gpurun_out/hbm_trace --workload {workload} --batch {batch}",
+        "```",
+        "",
+        f"Bytes are FETCH_SIZE and WRITE_SIZE (KiB) scaled by a plain 256 MiB copy in the same program "
+        f"(x{bf / 1024:.4f} and x{bw / 1024:.4f}); durations are the kernel trace's "
+        f"end - start of the same dispatch. {n} dispatches, {total_sec * 1e6:.1f} us of kernel time. "
+        f"GB/s = (fetched + written bytes) / duration; peak {HBM_PEAK_GBS:.0f} GB/s.",
+        "",
+        "| kernel | bound | launches | MB per launch | avg us | GB/s | % of HBM peak | % of time |",
+        "|---|---|---:|---:|---:|---:|---:|---:|",
+    ]
+    for name, (cnt, nbytes, sec) in sorted(fam.items(), key=lambda kv: -kv[1][2]):
+        gbs = nbytes / sec / 1e9
+        out.append(f"| `{name}` | {bound(name)} | {cnt} | {nbytes / cnt / 1e6:.2f} | {sec / cnt * 1e6:.2f} | "
+                   f"{gbs:.0f} | {100 * gbs / HBM_PEAK_GBS:.1f} | {100 * sec / total_sec:.1f} |")
+    out += ["", "Memory-bound dispatches of more than 4 MB, in launch order:", "",
+            "| # | kernel | MB fetched | MB written | us | GB/s | % of peak |", "|---:|---|---:|---:|---:|---:|---:|"]
+    for i, (name, fb, wb, sec) in enumerate(rows):
+        if bound(name) == "HBM" and fb + wb > 4e6:
+            gbs = (fb + wb) / sec / 1e9
+            out.append(f"| {i} | `{name}` | {fb / 1e6:.2f} | {wb / 1e6:.2f} | {sec * 1e6:.2f} | {gbs:.0f} | "
+                       f"{100 * gbs / HBM_PEAK_GBS:.1f} |")
+    hb = [(fb + wb, sec) for name, fb, wb, sec in rows if bound(name) == "HBM"]
+    if hb:
+        nb, ns = sum(b for b, _ in hb), sum(t for _, t in hb)
+        out += ["", f"All memory-bound dispatches together: {nb / 1e6:.1f} MB in {ns * 1e6:.1f} us = "
+                    f"{nb / ns / 1e9:.0f} GB/s ({100 * nb / ns / 1e9 / HBM_PEAK_GBS:.1f}% of peak).", ""]
+    return "\n".join(out)
+
+
 def main() -> int:
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
@@ -253,7 +362,16 @@ def main() -> int:
     p.add_argument("--pmc-probe", action="store_true", help="run the counter-run program and exit")
     p.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                    help="summarize the FETCH_SIZE / WRITE_SIZE runs into profiles/ and exit")
+    p.add_argument("--hbm-summary", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "TRACE_DIR"),
+                   help="per-kernel achieved HBM GB/s from two counter runs and a kernel trace of "
+                        "--pmc-probe, written to profiles/ and printed")
     args = p.parse_args()
+    if args.hbm_summary:
+        batch = 128 if args.workload == "single_gemm" else args.batch
+        text = hbm_summary(*map(Path, args.hbm_summary), args.workload, batch)
+        (ROOT / "profiles" / f"{args.workload}_b{batch}_hbm_bandwidth.md").write_text(text)
+        print(text)
+        return 0
     if args.pmc_summary:
         text = pmc_summary(Path(args.pmc_summary[0]), Path(args.pmc_summary[1]), args.workload, args.batch)
         traffic_file(args.workload, args.batch).write_text(text)

@@ -40,6 +40,9 @@ from ..ir import Graph, Node, Value
 from ..memory import MemoryPlan
 
 ATT_DMAX = 64   # head dim limit of the kernel (csrc/attention.hip)
+# Run the Q/K/V projection GEMM(s) inside the fused call, into scratch (tests turn it off to
+# exercise the staged output of a plain match).
+ABSORB_QKV = True
 SCORE_OPS = ("Mul", "Div", "Add", "Where")
 
 
@@ -84,9 +87,10 @@ class AttentionMatch:
     absorbed: list[Node] = field(default_factory=list)
     staged: bool = False             # output overlaps an operand: write scratch, then copy
     ops: ScoreOps = field(default_factory=ScoreOps)
-    # Q, K and V projected by three FusedGemms of one input (Hugging Face exports): the fused
-    # call runs them as one GEMM with the weights side by side, into a [B*S, 3*H*D] scratch
-    # area that the attention kernel then reads like a fused QKV projection.
+    # Q, K and V projected by three FusedGemms of one input (Hugging Face exports), or by one
+    # FusedGemm whose output only the absorbed Split reads: the fused call runs them as one GEMM
+    # with the weights side by side, into a [B*S, 3*H*D] scratch area that the attention kernel
+    # then reads like a fused QKV projection.
     qkv_gemms: list[Node] = field(default_factory=list)
 
     def reads(self) -> list[Value]:
@@ -360,12 +364,30 @@ def _match(sm: Node, graph: Graph) -> AttentionMatch | None:
         return None
     m = AttentionMatch(B=B, H=H, S=S, Skv=Skv, D=D, scale=ops.scale, q=operands[0], k=operands[1],
                        v=operands[2], out=tr.output, emit_at=tr, absorbed=absorbed, ops=ops)
-    if sp is None or sp.op != "Split":
+    if not ABSORB_QKV:
+        gemms = []
+    elif sp is None or sp.op != "Split":
         gemms = _qkv_gemms(m, graph)
-        if gemms:
-            m.qkv_gemms = gemms
-            m.absorbed += gemms
+    else:
+        gemms = _fused_qkv_gemm(sp, m, graph)
+    if gemms:
+        m.qkv_gemms = gemms
+        m.absorbed += gemms
     return m
+
+
+def _fused_qkv_gemm(sp: Node, m: AttentionMatch, graph: Graph) -> list[Node]:
+    """The FusedGemm whose [B, S, 3HD] output only the absorbed Split reads (a model with Q, K
+    and V weights already side by side): it runs as part of the fused call, into scratch, so the
+    attention output never shares memory with its operands and needs no staging copy."""
+    src = sp.input(0)
+    p = src.producer
+    if p is None or src in graph.outputs or len(src.users) != 1 or _gemm_form(p) is None:
+        return []
+    a = p.input(0)
+    if a.type is None or a.type.dtype != "float32" or a.type.size != m.B * m.S * a.type.shape[-1]:
+        return []
+    return [p]
 
 
 def _gemm_form(node: Node) -> tuple[Any, ...] | None:

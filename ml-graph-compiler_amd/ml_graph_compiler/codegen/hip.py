@@ -1261,8 +1261,19 @@ class HipEmitter:
             plan=self.plan,
             lines=source.count("\n"),
             kernels=dict(sorted(self.kernels.items())),
-            node_flops=[ops.flops(n) for n in self.graph.nodes],
+            node_flops=self._node_flops(),
         )
+
+    def _node_flops(self) -> list[int]:
+        """FLOPs per node, with the nodes a fused attention call absorbs (among them a QKV
+        projection GEMM) counted at the node that emits the call, whose launches do that work."""
+        index = {id(n): i for i, n in enumerate(self.graph.nodes)}
+        flops = [ops.flops(n) for n in self.graph.nodes]
+        for nid, m in self._attn_skip.items():
+            i = index[nid]
+            flops[index[id(m.emit_at)]] += flops[i]
+            flops[i] = 0
+        return flops
 
 
 def generate_hip(

@@ -187,8 +187,10 @@ def test_fused_and_unfused_samples_agree(sample, hip_cache, monkeypatch):
 
 
 def test_matcher_finds_every_bert_and_gpt_layer():
-    """CPU: all 12 BERT-base layers match (staged: the planner put the context where the dead
-    QKV projection was); the causal GPT sample's Where mask is recognized as causal."""
+    """CPU: all 12 BERT-base layers match, each with its QKV projection absorbed (the fused
+    call runs it into scratch, so the context, which the planner put where the dead projection
+    was, is written in place without staging); the causal GPT sample's Where mask is
+    recognized as causal."""
     g = builders.bert_base(1)
     optimize(g, "O3")
     schedule(g)
@@ -196,13 +198,37 @@ def test_matcher_finds_every_bert_and_gpt_layer():
     assert len(found) == 12
     assert all(m.S == 128 and m.Skv == 128 and m.D == 64 and m.H == 12 for m in found)
     assert all(abs(m.ops.scale - 0.125) < 1e-7 and m.ops.mask is None for m in found)
-    assert all(len(m.absorbed) == 12 for m in found)  # split, 3 x (reshape, transpose), qk, mul, softmax, pv, merge
+    # split, 3 x (reshape, transpose), qk, mul, softmax, pv, merge + the QKV FusedGemm
+    assert all(len(m.absorbed) == 13 and len(m.qkv_gemms) == 1 and not m.staged for m in found)
     gpt = builders.tiny_gpt()
     optimize(gpt, "O3")
     schedule(gpt)
     found = attn.find_attention(gpt, plan_memory(gpt, alignment=256))
     assert len(found) == 2
     assert all(m.ops.causal and not m.ops.mask_keep and m.ops.fill == -1e4 for m in found)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("sample", ["tiny-bert", "tiny-gpt"])
+def test_staged_output(sample, hip_cache, monkeypatch):
+    """With the QKV projection left as its own GEMM, the planner puts each layer's context where
+    the dead projection was: the fused call writes scratch and a copy moves the result into
+    place. Both builds must match the oracle."""
+    g = builders.SAMPLES[sample]()
+    optimize(g, "O3")
+    schedule(g)
+    monkeypatch.setattr(attn, "ABSORB_QKV", False)
+    found = attn.find_attention(g, plan_memory(g, alignment=256))
+    assert found and all(m.staged and not m.qkv_gemms for m in found)
+    build = builders.SAMPLES[sample]
+    feeds = oracle.random_feeds(build(), 2, int_high=50)
+    expected = oracle.run_graph(build(), feeds)
+    for absorb in (False, True):
+        monkeypatch.setattr(attn, "ABSORB_QKV", absorb)
+        got, kernels = _run(build(), feeds, hip_cache)
+        assert kernels.get("attention") == len(found), kernels
+        for name, want in expected.items():
+            assert float(np.max(np.abs(got[name].astype(np.float64) - want))) <= 5e-5
 
 
 def test_matcher_score_op_forms():
