@@ -348,6 +348,98 @@ def hbm_summary(fetch_dir: Path, write_dir: Path, trace_dir: Path, workload: str
     return "\n".join(out)
 
 
+MI355X_CLOCK_HZ = 2.4e9
+MI355X_SIMDS = 256 * 4
+MFMA_COUNTERS = "SQ_INSTS_VALU_MFMA_MOPS_F32 SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CU_CYCLES GRBM_GUI_ACTIVE"
+
+
+def mfma_summary(pmc_dir: Path, trace_dir: Path, workload: str, batch: int) -> str:
+    """MFMA work and utilisation of every matrix-core dispatch of one eager forward: one counter
+    run over --pmc-probe (MFMA_COUNTERS) and the kernel-trace run of the same program for
+    durations, matched by position and checked by name. SQ_INSTS_VALU_MFMA_MOPS_F32 counts fp32
+    MFMA work in units of 512 FLOP; SQ_VALU_MFMA_BUSY_CYCLES counts matrix-core busy cycles,
+    reported here per CU per GPU-active cycle (GRBM_GUI_ACTIVE)."""
+    import csv
+
+    counters: dict[int, dict] = {}
+    for f in sorted(pmc_dir.rglob("*counter_collection.csv")):
+        for r in csv.DictReader(open(f)):
+            d = counters.setdefault(int(r["Dispatch_Id"]), {"name": r["Kernel_Name"]})
+            d[r["Counter_Name"]] = float(r["Counter_Value"])
+    trace = []
+    for f in sorted(trace_dir.rglob("*kernel_trace.csv")):
+        for r in csv.DictReader(open(f)):
+            trace.append((int(r["Dispatch_Id"]), r["Kernel_Name"],
+                          (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-9))
+    trace.sort()
+    rows = [counters[k] for k in sorted(counters)]
+
+    def model_only(seq, name_of):
+        i = next(k for k, r in enumerate(seq) if "copy_kernel" in name_of(r))
+        return [r for r in seq[i + 1:] if not name_of(r).startswith("__amd_rocclr")]
+
+    rows = model_only(rows, lambda r: r["name"])
+    trace = model_only(trace, lambda r: r[1])
+    if len(rows) != len(trace) or any(a["name"] != b[1] for a, b in zip(rows, trace)):
+        raise SystemExit(f"runs differ: {len(rows)} counter dispatches vs {len(trace)} traced")
+    fam: dict[str, list] = {}
+    tot_flop = tot_sec = 0.0
+    for r, (_, name, sec) in zip(rows, trace):
+        flop = 512.0 * r.get("SQ_INSTS_VALU_MFMA_MOPS_F32", 0.0)
+        if flop <= 0:
+            continue
+        busy = r.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / (sec * MI355X_CLOCK_HZ * MI355X_SIMDS)
+        a = fam.setdefault(_short_kernel(name), [0, 0.0, 0.0, 0.0])
+        a[0] += 1
+        a[1] += flop
+        a[2] += sec
+        a[3] += busy * sec
+        tot_flop += flop
+        tot_sec += sec
+    base = f"$GRAFT_REPO_ROOT/bench.py --pmc-probe --workload {workload} --batch {batch}"
+    out = [
+        f"# MFMA work and utilisation: {workload} b{batch} forward (hip backend, -O3)",
+        "",
+        "Commands (repo root, on the MI355X box; one counter run, then a kernel trace):",
+        "",
+        "```",
+        "cd /tmp && export TMPDIR=/tmp",
+        f"rocprofv3 --pmc {MFMA_COUNTERS} --output-format csv -d $GRAFT_REPO_ROOT/gpurun_out/mfma_pmc -o p -- python3 {base}",
+        f"rocprofv3 --kernel-trace --output-format csv -d $GRAFT_REPO_ROOT/gpurun_out/hbm_trace -o p -- python3 {base}",
+        f"python3 bench.py --mfma-summary gpurun_out/mfma_pmc gpurun_out/hbm_trace --workload {workload} --batch {batch}",
+        "```",
+        "",
+        "FLOP = 512 x SQ_INSTS_VALU_MFMA_MOPS_F32 (the fp32 MFMA work the matrix cores executed, "
+        "padding of partial tiles included); TFLOP/s = that over the traced duration; % of peak "
+        f"against {MFMA_FP32_PEAK_TFLOPS} TFLOP/s. MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES over the "
+        "traced duration x 2.4 GHz x 1024 SIMDs (256 CUs x 4), time-weighted: the fraction of "
+        "matrix-core cycles in use. (GRBM_GUI_ACTIVE, summed over the 8 XCDs and stretched by the "
+        "counter collection, is not used as the time base.)",
+        "",
+        "| kernel | launches | GFLOP per launch | avg us | TFLOP/s | % of peak | MFMA busy per SIMD |",
+        "|---|---:|---:|---:|---:|---:|---:|",
+    ]
+    for name, (cnt, flop, sec, busy_sec) in sorted(fam.items(), key=lambda kv: -kv[1][2]):
+        tf = flop / sec / 1e12
+        out.append(f"| `{name}` | {cnt} | {flop / cnt / 1e9:.3f} | {sec / cnt * 1e6:.2f} | {tf:.1f} | "
+                   f"{100 * tf / MFMA_FP32_PEAK_TFLOPS:.1f} | {busy_sec / sec:.3f} |")
+    if tot_sec > 0:
+        tf = tot_flop / tot_sec / 1e12
+        out += ["", f"All MFMA dispatches: {tot_flop / 1e9:.1f} GFLOP in {tot_sec * 1e6:.1f} us = {tf:.1f} TFLOP/s "
+                    f"({100 * tf / MFMA_FP32_PEAK_TFLOPS:.1f}% of peak)."]
+        from ml_graph_compiler import ops
+        from ml_graph_compiler.passes import optimize
+
+        g = build_graph(workload, batch)
+        optimize(g, "O3")
+        algo = sum(ops.flops(n) for n in g.nodes
+                   if n.op in ("FusedConv", "Conv", "FusedGemm", "Gemm", "MatMul") and not _is_depthwise(n))
+        out += [f"Algorithmic FLOPs of the graph's contractions (2 per multiply-add): {algo / 1e9:.1f} GFLOP; "
+                f"the matrix cores executed {tot_flop / algo:.3f}x that (partial-tile padding, the stem's "
+                "space-to-depth zero taps).", ""]
+    return "\n".join(out)
+
+
 def main() -> int:
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
@@ -365,7 +457,16 @@ def main() -> int:
     p.add_argument("--hbm-summary", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "TRACE_DIR"),
                    help="per-kernel achieved HBM GB/s from two counter runs and a kernel trace of "
                         "--pmc-probe, written to profiles/ and printed")
+    p.add_argument("--mfma-summary", nargs=2, metavar=("PMC_DIR", "TRACE_DIR"),
+                   help="per-kernel MFMA FLOP, TFLOP/s and busy cycles from a counter run and a "
+                        "kernel trace of --pmc-probe, written to profiles/ and printed")
     args = p.parse_args()
+    if args.mfma_summary:
+        batch = 128 if args.workload == "single_gemm" else args.batch
+        text = mfma_summary(*map(Path, args.mfma_summary), args.workload, batch)
+        (ROOT / "profiles" / f"{args.workload}_b{batch}_mfma_utilisation.md").write_text(text)
+        print(text)
+        return 0
     if args.hbm_summary:
         batch = 128 if args.workload == "single_gemm" else args.batch
         text = hbm_summary(*map(Path, args.hbm_summary), args.workload, batch)

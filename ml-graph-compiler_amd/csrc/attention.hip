@@ -10,7 +10,9 @@
 // One workgroup of 256 threads (4 waves) owns 64 query rows of one (batch, head) and streams
 // the keys in blocks of 64 with a running ("online") softmax, so neither S nor Skv is bounded:
 //  1. the Q rows go to LDS ([row][d], d contiguous) once;
-//  2. per key block, K goes to LDS as [key][d] and V transposed as [d][key]; each wave
+//  2. per key block, K goes to LDS as [key][d] and V transposed as [d][key] from registers
+//     loaded while the previous block was being multiplied (the next block's loads are issued
+//     right after, so HBM latency is paid once per workgroup, not once per block); each wave
 //     multiplies a 32x32 block of the scores with v_mfma_f32_32x32x2f32 and writes it, scaled,
 //     biased and masked as the graph says, into an LDS tile;
 //  3. four threads per row take the block's row maximum, raise the running maximum m, turn the
@@ -85,12 +87,53 @@ __global__ void __launch_bounds__(256) attention_kernel(const AttnDev p) {
     const int srow = tid >> 2, part = tid & 3;
     float m_run = NEG_INF, l_run = 0.f;
 
-    // 1. Q rows (rows past S and columns past D are zero)
-    for (int e = tid; e < ATT_BQ * (ATT_DMAX / 4); e += 256) {
-        const int r = e / (ATT_DMAX / 4), c4 = e - r * (ATT_DMAX / 4);
-        f4 v = zero4;
-        if (q0 + r < p.S && c4 < D4) v = *reinterpret_cast<const f4 *>(qbase + (long)(q0 + r) * p.q_s + c4 * 4);
-        *reinterpret_cast<f4 *>(&Qs[r * ATT_P + c4 * 4]) = v;
+    // Tiles of 64 rows x 16 float quads are moved as 4 quads per thread. Q and K: thread t takes
+    // row e >> 4, quad e & 15 of e = t + 256 i (16 lanes read one row's 256 contiguous bytes).
+    // V: row e & 63, quad e >> 6, so a wave's 64 lanes hold 64 consecutive keys of one quad and
+    // the transposed LDS stores [d][key] hit 64 consecutive words (no bank conflicts).
+    constexpr int QUADS = ATT_BQ * (ATT_DMAX / 4) / 256;
+    static_assert(ATT_BQ == ATT_BK && QUADS == 4, "tile moves assume 64 x 64 tiles");
+    f4 kst[QUADS], vst[QUADS];
+    // Issue the global loads of key block k0 into registers (zero past Skv and past D); they
+    // stay in flight while the current block is multiplied.
+    auto load_kv = [&](int k0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < QUADS; ++i) {
+            const int e = tid + 256 * i;
+            const int r = e >> 4, c4 = e & 15;
+            kst[i] = zero4;
+            if (k0 + r < p.Skv && c4 < D4) kst[i] = *reinterpret_cast<const f4 *>(kbase + (long)(k0 + r) * p.k_s + c4 * 4);
+            const int rv = e & 63, cv = e >> 6;
+            vst[i] = zero4;
+            if (k0 + rv < p.Skv && cv < D4) vst[i] = *reinterpret_cast<const f4 *>(vbase + (long)(k0 + rv) * p.v_s + cv * 4);
+        }
+    };
+    auto store_kv = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < QUADS; ++i) {
+            const int e = tid + 256 * i;
+            *reinterpret_cast<f4 *>(&Ks[(e >> 4) * ATT_P + (e & 15) * 4]) = kst[i];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) Vt[((e >> 6) * 4 + j) * ATT_P + (e & 63)] = vst[i][j];
+        }
+    };
+
+    // 1. Q rows (rows past S and columns past D are zero), requested with the first key block
+    {
+        f4 qst[QUADS];
+#pragma unroll
+        for (int i = 0; i < QUADS; ++i) {
+            const int e = tid + 256 * i;
+            const int r = e >> 4, c4 = e & 15;
+            qst[i] = zero4;
+            if (q0 + r < p.S && c4 < D4) qst[i] = *reinterpret_cast<const f4 *>(qbase + (long)(q0 + r) * p.q_s + c4 * 4);
+        }
+        load_kv(0);
+#pragma unroll
+        for (int i = 0; i < QUADS; ++i) {
+            const int e = tid + 256 * i;
+            *reinterpret_cast<f4 *>(&Qs[(e >> 4) * ATT_P + (e & 15) * 4]) = qst[i];
+        }
     }
 
     floatx16 oacc;
@@ -105,19 +148,10 @@ __global__ void __launch_bounds__(256) attention_kernel(const AttnDev p) {
             if (__syncthreads_and(zero_terms)) break;
         }
         __syncthreads();  // Ks, Vt, Ps and rowscale free; Qs visible
-        // 2. K block [key][d], V block transposed [d][key] (zero past Skv and past D)
-        for (int e = tid; e < ATT_BK * (ATT_DMAX / 4); e += 256) {
-            const int r = e / (ATT_DMAX / 4), c4 = e - r * (ATT_DMAX / 4);
-            const int key = k0 + r;
-            f4 kv = zero4, vv = zero4;
-            if (key < p.Skv && c4 < D4) {
-                kv = *reinterpret_cast<const f4 *>(kbase + (long)key * p.k_s + c4 * 4);
-                vv = *reinterpret_cast<const f4 *>(vbase + (long)key * p.v_s + c4 * 4);
-            }
-            *reinterpret_cast<f4 *>(&Ks[r * ATT_P + c4 * 4]) = kv;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) Vt[(c4 * 4 + j) * ATT_P + r] = vv[j];
-        }
+        // 2. K block [key][d], V block transposed [d][key], from the registers loaded one block
+        // ahead; then the next block's loads go out
+        store_kv();
+        if (kb + 1 < kblocks) load_kv(k0 + ATT_BK);
         __syncthreads();
         floatx16 acc;
 #pragma unroll

@@ -833,6 +833,15 @@ static TileChoice choose_tiles(int M, int N, int K, int batch) {
     return t;
 }
 
+// 128 x 32 tiles (four waves stacked along M) instead of 64 x 64 when they pad N less: the
+// pointwise convolutions of MobileNet-style networks have 16 to 160 output channels, where a
+// 64-wide tile leaves up to 3/4 of the matrix-core work and of the epilogue on padding. Only
+// without a K split (the workspace size depends on the tile count) and for the DMA kernel.
+static bool narrow_tiles(int N, int split) {
+    const long pad64 = (N + 63) / 64 * 64, pad32 = (N + 31) / 32 * 32;
+    return split == 1 && pad32 < pad64;
+}
+
 }  // namespace mgc
 
 using namespace mgc;
@@ -912,8 +921,6 @@ extern "C" void mgc_hip_gemm(mgc_hip_exec *x, const mgc_hip_gemm_args *g) {
     p.div_ohw = make_fastdiv((unsigned)(p.a.OH * p.a.OW > 0 ? p.a.OH * p.a.OW : 1));
     p.div_cg = make_fastdiv((unsigned)(p.a.cg > 0 ? p.a.cg : 1));
     p.div_kw = make_fastdiv((unsigned)(p.a.KW > 0 ? p.a.KW : 1));
-    p.tiles_m = (p.M + t.bm - 1) / t.bm;
-    p.tiles_n = (p.N + t.bn - 1) / t.bn;
 
     // Reachable extents of the operands from their base pointers: the DMA kernels address them
     // through buffer resources with 32-bit offsets.
@@ -942,7 +949,13 @@ extern "C" void mgc_hip_gemm(mgc_hip_exec *x, const mgc_hip_gemm_args *g) {
                         p.a_bytes > 0 && p.a_bytes < kMaxRes && p.b_bytes > 0 &&
                         p.b_bytes < kMaxRes;
 
-    const GemmKernel kern = dma_ok ? pick_dma<64, 64, 2>(am) : pick_kernel<64, 64, 2>(am, bm);
+    const bool narrow = dma_ok && narrow_tiles(p.N, p.split);
+    t.bm = narrow ? 128 : 64;
+    t.bn = narrow ? 32 : 64;
+    p.tiles_m = (p.M + t.bm - 1) / t.bm;
+    p.tiles_n = (p.N + t.bn - 1) / t.bn;
+    const GemmKernel kern = narrow ? pick_dma<128, 32, 4>(am)
+                            : dma_ok ? pick_dma<64, 64, 2>(am) : pick_kernel<64, 64, 2>(am, bm);
     const dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)(batch * p.split));
     MGC_LAUNCH(x, kern, grid, dim3(256), 0, p);
     if (p.split > 1) {

@@ -162,6 +162,12 @@ def test_layer_and_batch_norm(hip_cache):
         ((33, 65), (65, 29), True),
         ((200, 136), (136, 264), True),
         ((3, 130, 68), (3, 68, 132), False),
+        # narrow outputs take 128 x 32 tiles (N = 24, 96, 160, 16); N = 40 pads the same either way
+        ((300, 64), (64, 24), True),
+        ((257, 96), (96, 96), True),
+        ((129, 128), (128, 160), True),
+        ((64, 16), (16, 16), True),
+        ((130, 32), (32, 40), True),
     ],
 )
 def test_matmul(a_shape, b_shape, const_b, hip_cache):
@@ -212,6 +218,9 @@ CONV_CASES = [
     ({"kernel_shape": [3, 3], "pads": [1, 0, 1, 1], "group": 8, "strides": [2, 2]}, (1, 8, 9, 62), (8, 1, 3, 3)),
     ({"kernel_shape": [3, 3], "pads": [2, 2, 2, 2], "group": 8, "dilations": [2, 2]}, (1, 8, 9, 9), (8, 1, 3, 3)),
     ({"kernel_shape": [5, 5], "pads": [2, 2, 2, 2], "group": 8}, (1, 8, 9, 9), (8, 1, 5, 5)),
+    # narrow output channels (128 x 32 tiles at O3): pointwise and 3x3
+    ({"kernel_shape": [1, 1]}, (2, 32, 9, 9), (24, 32, 1, 1)),
+    ({"kernel_shape": [3, 3], "pads": [1, 1, 1, 1]}, (1, 16, 12, 12), (96, 16, 3, 3)),
 ]
 
 
@@ -241,6 +250,24 @@ def test_depthwise_with_residual_and_clip(hip_cache):
         g.add_output(y, "y")
         infer_shapes(g)
         check_hip(g, {"x": f32(2, 16, hw, hw) * 3}, hip_cache, opt="O3")
+
+
+def test_narrow_pointwise_with_residual(hip_cache):
+    """A 24-channel pointwise convolution (128 x 32 tiles) with the residual Add and ReLU in its
+    epilogue (O3), over an image whose pixel count is not a multiple of the tile height."""
+    from ml_graph_compiler.ir import Graph, TensorType
+    from ml_graph_compiler.shape_inference import infer_shapes
+
+    g = Graph("pw_res")
+    x = g.add_input("x", TensorType("float32", (3, 24, 10, 9)))
+    w = g.constant(f32(24, 24, 1, 1) * 0.3, "w")
+    b = g.constant(f32(24), "b")
+    y = g.add_node("Conv", [x, w, b], 1, {"kernel_shape": [1, 1]}, name="pw").output
+    y = g.add_node("Add", [y, x], 1, {}, name="res").output
+    y = g.add_node("Relu", [y], 1, {}, name="relu").output
+    g.add_output(y, "y")
+    infer_shapes(g)
+    check_hip(g, {"x": f32(3, 24, 10, 9)}, hip_cache, opt="O3")
 
 
 POOL_CASES = [
