@@ -14,6 +14,7 @@
  *   mgc_hip_reduce_mid      <- mgc_reduce_mid (mgc_runtime.h:193)
  *   mgc_hip_softmax         <- mgc_softmax (mgc_runtime.h:196)
  *   mgc_hip_layer_norm      <- mgc_layer_norm (mgc_runtime.h:199-200)
+ *   mgc_hip_gemm_layer_norm <- mgc_gemm then mgc_layer_norm, fused (mgc_runtime.h:120-161, 199-200)
  *   mgc_hip_elementwise     <- the loop nests CEmitter.elementwise/loops emit (codegen/c.py:360-529)
  *   mgc_hip_space_to_depth  <- no counterpart (feeds the stem convolution's stride-1 form)
  *   mgc_hip_copy            <- the identity-body loop nests of op_Transpose/Expand/Tile/Slice/
@@ -128,6 +129,25 @@ void mgc_hip_gemm(mgc_hip_exec *x, const mgc_hip_gemm_args *g);
 /* Workspace floats mgc_hip_gemm wants for a GEMM of this shape (0 = none). The emitter asks
  * at compile time and reserves it through the memory planner's workspace hook. */
 long mgc_hip_gemm_workspace(int M, int N, int K, int batch);
+
+/* A GEMM (batch_rank 0) whose output rows then go through a LayerNorm: out = LayerNorm(C) with
+ * C = act(alpha A B + bias + beta R) as mgc_hip_gemm computes it. K is always split (at least
+ * in two) and the split-K reduction applies the epilogue, stores C when g->c is not NULL and
+ * normalizes each row from registers (two-pass float mean and variance, then * ln_scale +
+ * ln_bias; either may be NULL), so C is not read back and the LayerNorm has no launch of its
+ * own. Needs N % 4 == 0, N <= 1024, M < 2^25, 16-byte aligned pointers and row strides, and
+ * g->workspace of mgc_hip_gemm_layer_norm_workspace(M, N, K) floats; sets the launch error
+ * otherwise. Replaces mgc_gemm followed by mgc_layer_norm
+ * (src/ml_graph_compiler/codegen/runtime/mgc_kernels.c:328-396, 657-679) for a FusedGemm the
+ * schedule puts right before the LayerNormalization of its output. */
+void mgc_hip_gemm_layer_norm(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const float *ln_scale,
+                             const float *ln_bias, float eps, float *ln_out);
+
+/* Workspace floats mgc_hip_gemm_layer_norm needs (0 when the shape is outside its limits). */
+long mgc_hip_gemm_layer_norm_workspace(int M, int N, int K);
+
+/* 1 when mgc_hip_gemm_layer_norm takes an M x N output. */
+int mgc_hip_gemm_layer_norm_supported(int M, int N);
 
 /* ---------------------------------------------------------------------------------------- */
 /* memory-bound kernels                                                                      */

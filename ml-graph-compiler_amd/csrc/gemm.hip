@@ -764,6 +764,56 @@ __global__ void gemm_splitk_reduce_vec4(const GemmDev p, FastDiv div_n4) {
     }
 }
 
+// The same reduction for a GEMM whose output feeds a LayerNorm over its rows (N % 4 == 0,
+// N <= 1024): one wavefront per row sums the partials, applies the epilogue exactly as
+// gemm_splitk_reduce_vec4 does, stores the GEMM output when p.c is set (other readers need it)
+// and normalizes the row from registers (layer_norm_row_vec4, as the LayerNorm kernel does), so
+// the row makes no second trip through HBM and the LayerNorm needs no launch of its own.
+__global__ void __launch_bounds__(256) gemm_splitk_layer_norm(const GemmDev p, const float4 *ln_scale,
+                                                              const float4 *ln_bias, float eps, float4 *ln_out) {
+    const int lane = threadIdx.x & 63;
+    const int row = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    if (row >= p.M) return;
+    const int N4 = p.N >> 2;
+    const long total4 = ((long)p.M * p.N) >> 2;
+    const f4 *ws4 = reinterpret_cast<const f4 *>(p.ws) + (long)row * N4;
+    // partials summed in split order, as gemm_splitk_reduce_vec4 does; the loads of one split
+    // for all of the lane's columns go out together
+    f4 acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int k = lane + 64 * j;
+        acc[j] = k < N4 ? ws4[k] : f4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int s = 1; s < p.split; ++s) {
+        f4 part[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int k = lane + 64 * j;
+            part[j] = k < N4 ? ws4[(long)s * total4 + k] : f4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] += part[j];
+    }
+    float4 y[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int k = lane + 64 * j;
+        y[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (k < N4) {
+            const int col = k * 4;
+            f4 v = acc[j] * p.alpha;
+            if (p.bias && p.bias_mode == 2) v += p.bias[row];
+            if (p.bias && p.bias_mode == 1) v += ldg4(p.bias + col);
+            if (p.res) v += p.beta * ldg4(p.res + (long)row * p.ldr + col);
+            v = act4(v, p.act, p.lo, p.hi);
+            if (p.c) *reinterpret_cast<f4 *>(p.c + (long)row * p.ldc + col) = v;
+            y[j] = make_float4(v[0], v[1], v[2], v[3]);
+        }
+    }
+    layer_norm_row_vec4(y, lane, N4, ln_scale, ln_bias, eps, ln_out + (long)row * N4);
+}
+
 static bool aligned16(const void *ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
 static bool bs_div4(const long *bs, int rank) {
@@ -851,7 +901,56 @@ extern "C" long mgc_hip_gemm_workspace(int M, int N, int K, int batch) {
     return t.split > 1 ? (long)t.split * M * N : 0;
 }
 
-extern "C" void mgc_hip_gemm(mgc_hip_exec *x, const mgc_hip_gemm_args *g) {
+// LayerNorm that ends a split-K GEMM (mgc_hip_gemm_layer_norm).
+struct LnTail {
+    const float *scale, *bias;
+    float eps;
+    float *out;
+};
+
+// K splits of a GEMM whose reduction ends in a LayerNorm: the library's own choice, and at
+// least two, since the reduction is where the LayerNorm runs.
+static int ln_split(int M, int N, int K) {
+    const TileChoice t = choose_tiles(M, N, K, 1);
+    return t.split > 1 ? t.split : 2;
+}
+
+static void gemm_launch(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const LnTail *ln);
+
+extern "C" void mgc_hip_gemm(mgc_hip_exec *x, const mgc_hip_gemm_args *g) { gemm_launch(x, g, nullptr); }
+
+extern "C" int mgc_hip_gemm_layer_norm_supported(int M, int N) {
+    return M >= 1 && M < (1 << 25) && N >= 4 && N % 4 == 0 && N <= 1024;
+}
+
+extern "C" long mgc_hip_gemm_layer_norm_workspace(int M, int N, int K) {
+    if (!mgc_hip_gemm_layer_norm_supported(M, N) || K < 1) return 0;
+    return (long)ln_split(M, N, K) * M * N;
+}
+
+extern "C" void mgc_hip_gemm_layer_norm(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const float *ln_scale,
+                                        const float *ln_bias, float eps, float *ln_out) {
+    if (g->M <= 0) return;
+    const int split = ln_split(g->M, g->N, g->K);
+    const bool ok = mgc_hip_gemm_layer_norm_supported(g->M, g->N) && g->batch_rank == 0 &&
+                    g->workspace != nullptr && g->workspace_floats >= (long)split * g->M * g->N &&
+                    aligned16(g->workspace) && aligned16(ln_out) && aligned16(ln_scale) &&
+                    aligned16(ln_bias) && (!g->c || (aligned16(g->c) && g->ldc % 4 == 0)) &&
+                    (!g->res || (aligned16(g->res) && g->ldr % 4 == 0)) &&
+                    (!g->bias || g->bias_mode != 1 || aligned16(g->bias));
+    if (!ok) {
+        x->launch_error = (int)hipErrorInvalidValue;
+        set_error("mgc_hip_gemm_layer_norm: shape, alignment or workspace outside its limits",
+                  hipErrorInvalidValue);
+        return;
+    }
+    mgc_hip_gemm_args a = *g;
+    a.split_k = split;
+    const LnTail tail{ln_scale, ln_bias, eps, ln_out};
+    gemm_launch(x, &a, &tail);
+}
+
+static void gemm_launch(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const LnTail *ln) {
     if (g->M <= 0 || g->N <= 0) return;
     GemmDev p;
     p.M = g->M;
@@ -957,8 +1056,19 @@ extern "C" void mgc_hip_gemm(mgc_hip_exec *x, const mgc_hip_gemm_args *g) {
     const GemmKernel kern = narrow ? pick_dma<128, 32, 4>(am)
                             : dma_ok ? pick_dma<64, 64, 2>(am) : pick_kernel<64, 64, 2>(am, bm);
     const dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)(batch * p.split));
+    if (ln && p.split < 2) {  // the workspace did not allow the split the reduction needs
+        x->launch_error = (int)hipErrorInvalidValue;
+        set_error("mgc_hip_gemm_layer_norm: no K split", hipErrorInvalidValue);
+        return;
+    }
     MGC_LAUNCH(x, kern, grid, dim3(256), 0, p);
-    if (p.split > 1) {
+    if (ln) {
+        // a wavefront per row; one-wave workgroups when there are few rows, to spread them over CUs
+        const int rows_per_block = p.M >= 1024 ? 4 : 1;
+        MGC_LAUNCH(x, gemm_splitk_layer_norm, dim3((unsigned)((p.M + rows_per_block - 1) / rows_per_block)),
+                   dim3(64 * rows_per_block), 0, p, (const float4 *)ln->scale, (const float4 *)ln->bias, ln->eps,
+                   (float4 *)ln->out);
+    } else if (p.split > 1) {
         const long total = (long)p.M * p.N;
         if (p.vec_out && p.N % 4 == 0 && total < 0x7fffffffL && aligned16(p.ws)) {
             MGC_LAUNCH(x, gemm_splitk_reduce_vec4, dim3(blocks_for(total / 4, 256, 4096)), dim3(256), 0,

@@ -120,6 +120,52 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// LayerNorm of one row held by a wavefront as up to four float4 per lane (v[j] is column quad
+// lane + 64 j, zero where that is >= cols4): two-pass mean and variance in float, then
+// (x - mean) / sqrt(var + eps) * scale + bias written to dst (scale, bias may be null). Every
+// lane of the wave must call it. Shared by the LayerNorm kernel and the split-K reduction that
+// ends in a LayerNorm, so both round identically.
+__device__ __forceinline__ void layer_norm_row_vec4(const float4 (&v)[4], int lane, int cols4, const float4 *scale,
+                                                    const float4 *bias, float eps, float4 *dst) {
+    const float cols = (float)(cols4 * 4);
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sum += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+    const float mean = wave_sum(sum) / cols;
+    float var = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (lane + 64 * j < cols4) {
+            const float dx = v[j].x - mean, dy = v[j].y - mean, dz = v[j].z - mean, dw = v[j].w - mean;
+            var += (dx * dx + dy * dy) + (dz * dz + dw * dw);
+        }
+    }
+    const float inv = 1.0f / sqrtf(wave_sum(var) / cols + eps);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int k = lane + 64 * j;
+        if (k < cols4) {
+            float4 y = make_float4((v[j].x - mean) * inv, (v[j].y - mean) * inv, (v[j].z - mean) * inv,
+                                   (v[j].w - mean) * inv);
+            if (scale) {
+                const float4 s = scale[k];
+                y.x *= s.x;
+                y.y *= s.y;
+                y.z *= s.z;
+                y.w *= s.w;
+            }
+            if (bias) {
+                const float4 b = bias[k];
+                y.x += b.x;
+                y.y += b.y;
+                y.z += b.z;
+                y.w += b.w;
+            }
+            dst[k] = y;
+        }
+    }
+}
+
 __device__ __forceinline__ double wave_sum_d(double v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);

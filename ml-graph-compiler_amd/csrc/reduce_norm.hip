@@ -307,49 +307,13 @@ __global__ void __launch_bounds__(256) layer_norm_rows_vec4(int rows, int cols4,
     const int r = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     if (r >= rows) return;
     const float4 *src = in + (long)r * cols4;
-    float4 *dst = out + (long)r * cols4;
-    const float cols = (float)(cols4 * 4);
     float4 v[4];
-    float sum = 0.0f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int k = lane + 64 * j;
         v[j] = k < cols4 ? src[k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        sum += (v[j].x + v[j].y) + (v[j].z + v[j].w);
     }
-    const float mean = wave_sum(sum) / cols;
-    float var = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        if (lane + 64 * j < cols4) {
-            const float dx = v[j].x - mean, dy = v[j].y - mean, dz = v[j].z - mean, dw = v[j].w - mean;
-            var += (dx * dx + dy * dy) + (dz * dz + dw * dw);
-        }
-    }
-    const float inv = 1.0f / sqrtf(wave_sum(var) / cols + eps);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int k = lane + 64 * j;
-        if (k < cols4) {
-            float4 y = make_float4((v[j].x - mean) * inv, (v[j].y - mean) * inv,
-                                   (v[j].z - mean) * inv, (v[j].w - mean) * inv);
-            if (scale) {
-                const float4 s = scale[k];
-                y.x *= s.x;
-                y.y *= s.y;
-                y.z *= s.z;
-                y.w *= s.w;
-            }
-            if (bias) {
-                const float4 b = bias[k];
-                y.x += b.x;
-                y.y += b.y;
-                y.z += b.z;
-                y.w += b.w;
-            }
-            dst[k] = y;
-        }
-    }
+    layer_norm_row_vec4(v, lane, cols4, scale, bias, eps, out + (long)r * cols4);
 }
 
 // ---- pooling -----------------------------------------------------------------------------------

@@ -109,6 +109,8 @@ def load_kernel_library() -> ctypes.CDLL:
         lib = ctypes.CDLL(str(kernel_library_path()), mode=ctypes.RTLD_GLOBAL)
         lib.mgc_hip_gemm_workspace.restype = ctypes.c_long
         lib.mgc_hip_gemm_workspace.argtypes = [ctypes.c_int] * 4
+        lib.mgc_hip_gemm_layer_norm_workspace.restype = ctypes.c_long
+        lib.mgc_hip_gemm_layer_norm_workspace.argtypes = [ctypes.c_int] * 3
         lib.mgc_hip_last_error.restype = ctypes.c_char_p
         lib.mgc_hip_version.restype = ctypes.c_char_p
         lib.mgc_hip_device_count.restype = ctypes.c_int
@@ -119,6 +121,12 @@ def load_kernel_library() -> ctypes.CDLL:
 def gemm_workspace_floats(m: int, n: int, k: int, batch: int) -> int:
     """Workspace the kernel library wants for one GEMM (asked at compile time)."""
     return int(load_kernel_library().mgc_hip_gemm_workspace(m, n, k, batch))
+
+
+def gemm_layer_norm_workspace_floats(m: int, n: int, k: int) -> int:
+    """Split-K workspace of a GEMM whose reduction also runs the LayerNorm of its rows (0: the
+    library cannot fuse that shape)."""
+    return int(load_kernel_library().mgc_hip_gemm_layer_norm_workspace(m, n, k))
 
 
 def _file_digest(path: Path) -> str:

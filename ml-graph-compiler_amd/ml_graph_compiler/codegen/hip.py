@@ -95,6 +95,9 @@ FOLD_TRANSPOSES = True
 SPACE_TO_DEPTH = True
 # Fuse recognized attention chains into mgc_hip_attention (tests turn it off to compare).
 FUSE_ATTENTION = True
+# Run a LayerNormalization that directly follows the FusedGemm producing its input inside that
+# GEMM's split-K reduction (mgc_hip_gemm_layer_norm); tests turn it off to compare.
+FUSE_GEMM_LAYER_NORM = True
 
 MAX_RANK = 6
 MAX_LEAVES = 16
@@ -238,6 +241,7 @@ class HipEmitter:
         inplace: bool = True,
         profile: bool = False,
         gemm_workspace: Callable[[int, int, int, int], int] | None = None,
+        gemm_ln_workspace: Callable[[int, int, int], int] | None = None,
     ) -> None:
         unsupported = sorted({n.op for n in graph.nodes} - self.SUPPORTED)
         if unsupported:
@@ -294,6 +298,68 @@ class HipEmitter:
                 if self._s2d[id(n)] is not None:
                     self._s2d_skip.add(id(n.input(0).producer))
                 self._scratch_bytes = max(self._scratch_bytes, n.input(0).tensor_type.nbytes)
+        # FusedGemm -> LayerNormalization of its rows, scheduled back to back: the LayerNorm runs
+        # in the GEMM's split-K reduction. id(gemm) -> (LayerNorm, partials in scratch?)
+        self._gemm_ln: dict[int, tuple[Node, bool]] = {}
+        self._ln_skip: dict[int, Node] = {}
+        if FUSE_GEMM_LAYER_NORM and gemm_ln_workspace is not None:
+            taken = excluded | set(self._folds.skipped) | self._s2d_skip | set(self._s2d)
+            for node, ln in zip(graph.nodes, graph.nodes[1:]):
+                shape = self._gemm_ln_shape(node, ln, taken)
+                if shape is None:
+                    continue
+                need = 4 * int(gemm_ln_workspace(*shape))
+                if need <= 0:
+                    continue
+                off = self.plan.workspaces.get(id(node))
+                in_scratch = not (off is not None and self._workspace_bytes(node) >= need
+                                  and not (self.plan.location(ln.output).kind == "arena"
+                                           and self._region_overlap(ln.output, off, need)))
+                if in_scratch:
+                    self._scratch_bytes = max(self._scratch_bytes, need)
+                self._gemm_ln[id(node)] = (ln, in_scratch)
+                self._ln_skip[id(ln)] = node
+
+    def _gemm_ln_shape(self, node: Node, ln: Node, taken: set[int]) -> tuple[int, int, int] | None:
+        """(M, N, K) when the LayerNorm ``ln`` can run in ``node``'s split-K reduction: a float
+        FusedGemm whose output ``ln`` normalizes over exactly the N output columns, constant
+        LayerNorm parameters, and an ``ln`` output that does not overlap the residual the
+        reduction reads (an exact alias is fine: each row is read before it is written)."""
+        if node.op != "FusedGemm" or ln.op != "LayerNormalization" or ln.input(0) is not node.output:
+            return None
+        if id(node) in taken or id(ln) in taken:
+            return None
+        at, bt, ot = node.input(0).tensor_type, node.input(1).tensor_type, node.output.tensor_type
+        if ot.dtype != "float32" or ln.output.tensor_type.dtype != "float32" or ot.rank < 1:
+            return None
+        trans = int(node.attrs.get("trans_b", 0))
+        k, n = (bt.shape[1], bt.shape[0]) if trans else bt.shape
+        axis = int(ln.attrs.get("axis", -1))
+        axis = axis + ot.rank if axis < 0 else axis
+        if axis != ot.rank - 1 or ot.shape[-1] != n or n % 4:
+            return None
+        if any(v is not None and v.data is None for v in ln.inputs[1:3]):
+            return None
+        res = node.optional_input(3)
+        if res is not None and self._overlap(res, ln.output) and not self._same_storage(res, ln.output):
+            return None
+        return at.size // max(k, 1), n, k
+
+    def _overlap(self, a: Value, b: Value) -> bool:
+        la, lb = self.plan.location(a), self.plan.location(b)
+        if la.kind != lb.kind or la.kind == "const":
+            return False
+        if la.kind in ("input", "output"):
+            return la.index == lb.index
+        return la.index < lb.index + b.tensor_type.nbytes and lb.index < la.index + a.tensor_type.nbytes
+
+    def _same_storage(self, a: Value, b: Value) -> bool:
+        la, lb = self.plan.location(a), self.plan.location(b)
+        return la.kind == lb.kind and la.index == lb.index and a.tensor_type.nbytes == b.tensor_type.nbytes
+
+    def _region_overlap(self, v: Value, off: int, nbytes: int) -> bool:
+        loc = self.plan.location(v)
+        return loc.index < off + nbytes and off < loc.index + v.tensor_type.nbytes
 
     # -- workspace hook ------------------------------------------------------------------------
     def _gemm_shape(self, node: Node) -> tuple[int, int, int, int] | None:
@@ -384,6 +450,9 @@ class HipEmitter:
         if id(node) in self._s2d_skip:
             self.emit("/* read in NCHW by the space-to-depth copy of the convolution it feeds */")
             self.count("folded")
+            return
+        if id(node) in self._ln_skip:
+            self.emit(f"/* computed in the split-K reduction of {comment_text(self._ln_skip[id(node)].name)} */")
             return
         if node.op in ALIAS_OPS:
             if node.op == "Dropout" and len(node.outputs) > 1:
@@ -759,7 +828,10 @@ class HipEmitter:
                    batch: Sequence[tuple[int, int, int, int, int]] = (), alpha: float = 1.0,
                    bias: str = "NULL", bias_mode: int = 0, res: str = "NULL", ldr: int = 0,
                    beta: float = 1.0, act: str = "none", lo: float = 0.0, hi: float = 6.0,
-                   workspace: str = "NULL", workspace_floats: int = 0) -> None:
+                   workspace: str = "NULL", workspace_floats: int = 0,
+                   layer_norm: tuple[str, str, str, str] | None = None) -> None:
+        """One mgc_hip_gemm call; ``layer_norm`` = (scale, bias, eps, out) makes it an
+        mgc_hip_gemm_layer_norm call whose split-K reduction also normalizes the rows."""
         if len(batch) > MAX_BATCH_RANK:
             raise CodegenError(f"GEMM with {len(batch)} batch dimensions is not supported")
         parts = ["mgc_hip_gemm_args g; memset(&g, 0, sizeof g);", f"g.M = {m}; g.N = {n}; g.K = {k};"]
@@ -772,9 +844,15 @@ class HipEmitter:
             for d, (dim, abs_, bbs, cbs, rbs) in enumerate(batch):
                 parts.append(f"g.batch_dims[{d}] = {dim}; g.a_bs[{d}] = {abs_}L; g.b_bs[{d}] = {bbs}L; g.c_bs[{d}] = {cbs}L; g.r_bs[{d}] = {rbs}L;")
         parts.append(f"g.workspace = {workspace}; g.workspace_floats = {workspace_floats}L;")
-        parts.append("mgc_hip_gemm(x, &g);")
+        if layer_norm is not None:
+            scale, lbias, eps, out = layer_norm
+            parts.append(f"mgc_hip_gemm_layer_norm(x, &g, {scale}, {lbias}, {eps}, {out});")
+        else:
+            parts.append("mgc_hip_gemm(x, &g);")
         self.emit("{ " + " ".join(parts) + " }")
         self.count("gemm")
+        if layer_norm is not None:
+            self.count("gemm_layer_norm")
 
     @staticmethod
     def _strided(field_: str, p: str, rs: int, cs: int) -> list[str]:
@@ -810,12 +888,23 @@ class HipEmitter:
         bias_v, res_v = node.optional_input(2), node.optional_input(3)
         act, lo, hi = self._act(node)
         ws, ws_floats = self._workspace(node)
+        out, layer_norm = self.ptr(node.output), None
+        if id(node) in self._gemm_ln:
+            ln, in_scratch = self._gemm_ln[id(node)]
+            if in_scratch:
+                ws, ws_floats = f"(float *)(A + {self._scratch_off})", self._scratch_bytes // 4
+            y = node.output
+            if not (y in self.graph.outputs or len(y.users) > 1):
+                out = "NULL"  # only the LayerNorm reads the GEMM output
+            layer_norm = (self._vector_ptr(ln.optional_input(1), n, "LayerNormalization scale"),
+                          self._vector_ptr(ln.optional_input(2), n, "LayerNormalization bias"),
+                          _f(float(ln.attrs.get("epsilon", 1e-5))), self.fptr(ln.output))
         self._gemm_call(
-            m, n, k, self._strided("a", self.ptr(a), k, 1), bspec, self.ptr(node.output), n,
+            m, n, k, self._strided("a", self.ptr(a), k, 1), bspec, out, n,
             bias=self._vector_ptr(bias_v, n, "FusedGemm bias") if bias_v is not None else "NULL",
             bias_mode=1 if bias_v is not None else 0,
             res=self.fptr(res_v) if res_v is not None else "NULL", ldr=n, act=act, lo=lo, hi=hi,
-            workspace=ws, workspace_floats=ws_floats,
+            workspace=ws, workspace_floats=ws_floats, layer_norm=layer_norm,
         )
 
     def op_Gemm(self, node: Node) -> None:
@@ -1282,6 +1371,9 @@ def generate_hip(
     inplace: bool = True,
     profile: bool = False,
     gemm_workspace: Callable[[int, int, int, int], int] | None = None,
+    gemm_ln_workspace: Callable[[int, int, int], int] | None = None,
 ) -> GeneratedModel:
-    """Generate the host source and weights blob of a scheduled graph for the hip backend."""
-    return HipEmitter(graph, strategy, inplace, profile, gemm_workspace).generate()
+    """Generate the host source and weights blob of a scheduled graph for the hip backend.
+    ``gemm_workspace`` / ``gemm_ln_workspace`` ask the kernel library for split-K workspace
+    sizes (without the second, no LayerNorm is fused into a GEMM)."""
+    return HipEmitter(graph, strategy, inplace, profile, gemm_workspace, gemm_ln_workspace).generate()

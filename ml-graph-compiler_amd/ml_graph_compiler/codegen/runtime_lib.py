@@ -29,7 +29,8 @@ import numpy as np
 from ..errors import CodegenError, GraphError, ModelImportError
 from ..ir import Graph, TensorType, numpy_dtype
 from ..memory import Strategy
-from .build import BuildOptions, BuildResult, build_model_library, gemm_workspace_floats, load_kernel_library
+from .build import (BuildOptions, BuildResult, build_model_library, gemm_layer_norm_workspace_floats,
+                    gemm_workspace_floats, load_kernel_library)
 from .hip import GeneratedModel, generate_hip
 
 BACKENDS = ("hip",)
@@ -333,7 +334,8 @@ def compile_graph(
     if backend not in BACKENDS:
         raise CodegenError(f"backend {backend!r} is not part of this build (available: {', '.join(BACKENDS)})")
     t0 = time.perf_counter()
-    generated: GeneratedModel = generate_hip(graph, strategy, inplace, profile, gemm_workspace_floats)
+    generated: GeneratedModel = generate_hip(graph, strategy, inplace, profile, gemm_workspace_floats,
+                                             gemm_layer_norm_workspace_floats)
     codegen_seconds = time.perf_counter() - t0
     t0 = time.perf_counter()
     built: BuildResult = build_model_library(
