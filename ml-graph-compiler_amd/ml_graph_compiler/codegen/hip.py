@@ -329,6 +329,8 @@ class HipEmitter:
             return None
         if id(node) in taken or id(ln) in taken:
             return None
+        if any(o.users or o in self.graph.outputs for o in ln.outputs[1:]):  # Mean / InvStdDev wanted
+            return None
         at, bt, ot = node.input(0).tensor_type, node.input(1).tensor_type, node.output.tensor_type
         if ot.dtype != "float32" or ln.output.tensor_type.dtype != "float32" or ot.rank < 1:
             return None
