@@ -129,6 +129,9 @@ def _check(g, feeds, hip_cache, opt="O3", fused=True):
         (2, 2, 256, 256, 32, True),  # D of one MFMA column block
         (1, 2, 16, 300, 16, False),  # keys past the old 256 limit
         (1, 3, 700, 700, 64, True),  # long sequence: 11 query blocks x 11 key blocks
+        # many (batch, head) pairs: 576 and 512 workgroups, more than two per CU
+        (4, 16, 520, 520, 64, True),
+        (2, 32, 500, 500, 48, False),
     ],
 )
 def test_fused_attention_matches_oracle(B, H, S, Skv, D, fused_qkv, hip_cache):
@@ -160,6 +163,15 @@ def test_masked_and_biased_attention(case, opt, hip_cache):
 @pytest.mark.gpu
 def test_causal_long_sequence(hip_cache):
     g, feeds = attention_graph(1, 2, 1030, 1030, 64, True, mask="causal", fill=-np.inf)
+    _check(g, feeds, hip_cache)
+
+
+@pytest.mark.gpu
+def test_causal_and_biased_many_heads(hip_cache):
+    """Score ops with 64 (batch, head) pairs of 520 queries (ragged last query block)."""
+    g, feeds = attention_graph(2, 32, 520, 520, 64, True, mask="causal", fill=-np.inf)
+    _check(g, feeds, hip_cache)
+    g, feeds = attention_graph(2, 32, 520, 520, 64, True, bias="input")
     _check(g, feeds, hip_cache)
 
 
