@@ -103,8 +103,11 @@ def test_every_sample_and_config_generates_and_builds(hip_cache):
             g = make()
             optimize(g, level)
             schedule(g)
-            gen = generate_hip(g, gemm_workspace=native.gemm_workspace_floats)
+            gen = generate_hip(g, gemm_workspace=native.gemm_workspace_floats,
+                               gemm_ln_workspace=native.gemm_layer_norm_workspace_floats)
             native.build_model_library(gen.source, cache_dir=hip_cache, name="m")
+            if name == "tiny-bert" and level == "O3":  # the fused GEMM + LayerNorm call compiles too
+                assert gen.kernels.get("gemm_layer_norm", 0) > 0, gen.kernels
 
 
 def test_split_k_workspace_is_planned():
