@@ -153,6 +153,40 @@ def test_gpt2(batch, hip_cache):
         assert np.array_equal(np.argmax(got[i], -1), np.argmax(expected[0], -1))
 
 
+@pytest.mark.parametrize(
+    "name, kwargs",
+    [
+        # BERT-large width (hidden 1024 = the widest row the fused GEMM + LayerNorm takes, 16 heads)
+        ("bert_large_2l", dict(batch=2, seq=256, d_model=1024, heads=16, layers=2, vocab=1000, gelu="erf",
+                               causal=False, weight_scale=0.02, unit_layer_norm=True, embedding_norm=True,
+                               lm_head=False, ln_eps=1e-12)),
+        # GPT-2-medium width, a ragged causal sequence and a vocabulary head
+        ("gpt2_medium_2l", dict(batch=2, seq=200, d_model=1024, heads=16, layers=2, vocab=3000, gelu="tanh",
+                                causal=True, weight_scale=0.02)),
+        # hidden 1280 (GPT-2 large): wider than the fused GEMM + LayerNorm, so it stays unfused
+        ("gpt2_large_width_1l", dict(batch=1, seq=64, d_model=1280, heads=20, layers=1, vocab=500, gelu="tanh",
+                                     causal=True, weight_scale=0.02)),
+    ],
+)
+def test_wider_transformers(name, kwargs, hip_cache):
+    print(f"[gpu] {name}", flush=True)
+    graph = builders.transformer(name=name, **kwargs)
+    feeds = oracle.random_feeds(graph, 12, int_high=kwargs["vocab"])
+    expected = oracle.run_graph(graph, feeds)
+    model = compile_hip(builders.transformer(name=name, **kwargs), hip_cache)
+    kernels = dict(model.report.kernels)
+    try:
+        got = model.run(feeds)
+    finally:
+        model.release()
+    assert kernels.get("attention") == kwargs["layers"], kernels
+    assert (kernels.get("gemm_layer_norm", 0) > 0) == (kwargs["d_model"] <= 1024), kernels
+    for k, want in expected.items():
+        err, scale = _rel_err(got[k], want)
+        print(f"[gpu] {name} {k}: max-abs {err:.3e} max|ref| {scale:.3e}", flush=True)
+        assert err <= 5e-4
+
+
 def test_gather_out_of_range_raises(hip_cache):
     from ml_graph_compiler.errors import GraphError
 
