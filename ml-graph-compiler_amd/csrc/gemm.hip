@@ -878,8 +878,14 @@ static TileChoice choose_tiles(int M, int N, int K, int batch) {
             t.split = s;
         }
     }
-    // too few tiles to fill the chip even once: use every split K allows
-    if (tiles * t.split < kCUs && max_split > t.split) t.split = max_split;
+    // too few tiles to fill the chip even once: split further, as far as K allows without
+    // spilling into a second round (tiles * split <= kCUs), where the CUs that run two
+    // workgroups would double the time
+    if (tiles * t.split < kCUs) {
+        const int fill = (int)(kCUs / tiles);
+        const int s = fill < max_split ? fill : max_split;
+        if (s > t.split) t.split = s;
+    }
     return t;
 }
 
