@@ -1,5 +1,6 @@
 // Model runtime of libmgc_hip.so: one HBM block per model, weights uploaded once, the forward
-// captured into a hipGraph on first use and replayed after, a device error flag for Gather.
+// captured into a hipGraph on first use and replayed after, a device error flag for Gather
+// (zeroed at init, cleared again only after a check finds it set).
 //
 // Mirrors what the reference does around its generated mgc_run (allocate the arena once,
 // serialize calls, map status 1 to a Gather error: src/ml_graph_compiler/codegen/
@@ -39,10 +40,6 @@ struct ModelState {
     int host_flag = 0;
 };
 
-__global__ void clear_flag_kernel(int *flag) {
-    if (threadIdx.x == 0 && blockIdx.x == 0) *flag = 0;
-}
-
 int fail(const char *where, hipError_t err) {
     mgc::set_error(where, err);
     return MGC_ERR_HIP;
@@ -56,11 +53,12 @@ int fail(const char *where, hipError_t err) {
 
 ModelState *state(mgc_hip_model *m) { return static_cast<ModelState *>(m->state); }
 
-// Enqueue one forward pass (flag reset first) on the model stream.
+// Enqueue one forward pass on the model stream. The Gather error flag is not cleared here: it
+// is zero from init and only a bad index sets it, so it stays zero until finish() reads it set
+// and clears it (outside any captured graph). No kernel of the replayed graph spends a launch
+// on it, and an error in a forward that nobody checked is reported by the next check.
 int enqueue_forward(mgc_hip_model *m, ModelState *s, const void *const *in, void *const *out) {
     s->exec.launch_error = 0;
-    hipLaunchKernelGGL(clear_flag_kernel, dim3(1), dim3(64), 0, s->stream, s->flag);
-    mgc::note_launch(&s->exec);
     m->forward(&s->exec, in, out, s->A, s->W);
     if (s->exec.launch_error) return fail("kernel launch", (hipError_t)s->exec.launch_error);
     return MGC_OK;
@@ -87,7 +85,10 @@ int finish(ModelState *s) {
     MGC_CHECK(hipMemcpyAsync(&s->host_flag, s->flag, sizeof(int), hipMemcpyDeviceToHost,
                              s->stream));
     MGC_CHECK(hipStreamSynchronize(s->stream));
-    return s->host_flag ? MGC_ERR_GATHER_INDEX : MGC_OK;
+    if (!s->host_flag) return MGC_OK;
+    MGC_CHECK(hipMemsetAsync(s->flag, 0, sizeof(int), s->stream));
+    MGC_CHECK(hipStreamSynchronize(s->stream));
+    return MGC_ERR_GATHER_INDEX;
 }
 
 int ensure_staged_graph(mgc_hip_model *m, ModelState *s) {
@@ -176,6 +177,13 @@ int mgc_hip_model_init(mgc_hip_model *m, const unsigned char *weights_host, unsi
     for (size_t o : in_off) s->in_stage.push_back(s->block + o);
     for (size_t o : out_off) s->out_stage.push_back(s->block + o);
     s->flag = reinterpret_cast<int *>(s->block + flag_off);
+    err = hipMemset(s->flag, 0, sizeof(int));
+    if (err != hipSuccess) {
+        hipFree(s->block);
+        hipStreamDestroy(s->stream);
+        delete s;
+        return fail("mgc_hip_model_init", err);
+    }
     if (m->weights_bytes) {
         err = hipMemcpy(s->W, weights_host, m->weights_bytes, hipMemcpyHostToDevice);
         if (err != hipSuccess) {

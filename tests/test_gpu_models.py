@@ -197,7 +197,16 @@ def test_gather_out_of_range_raises(hip_cache):
         model.run({})
     with pytest.raises(GraphError, match="expected"):
         model.run({"input_ids": np.zeros((1, 8), np.int32)})
-    # the flag is cleared by the next run
+    # the flag was cleared when the error was reported
     ok = model.run({"input_ids": np.zeros((1, 8), np.int64)})
     assert np.isfinite(ok["logits"]).all()
+    # replays without a check: the error of any of them is reported by the next check, once
+    model.upload({"input_ids": np.full((1, 8), 99, np.int64)})
+    model.launch(2)
+    model.upload({"input_ids": np.zeros((1, 8), np.int64)})
+    model.launch(1)
+    with pytest.raises(GraphError, match="Gather"):
+        model.sync()
+    model.launch(1)
+    model.sync()
     model.release()
