@@ -373,6 +373,29 @@ __global__ void __launch_bounds__(256) ew_f32_kernel(const EwF32Args e) {
     }
 }
 
+// Merges adjacent dimensions that every operand walks contiguously (stride[d] ==
+// stride[d + 1] * dims[d + 1] for the output and every leaf, broadcast leaves included), so the
+// kernel splits each index over fewer dimensions: [16, 128, 768] + [1, 128, 768] becomes
+// [16, 98304] + [1, 98304].
+static void ew_coalesce(mgc_hip_ew_args &e) {
+    int d = e.rank - 2;
+    while (d >= 0) {
+        bool ok = e.out_strides[d] == e.out_strides[d + 1] * e.dims[d + 1];
+        for (int l = 0; l < e.n_leaves && ok; ++l)
+            ok = e.leaf[l].strides[d] == e.leaf[l].strides[d + 1] * e.dims[d + 1];
+        if (ok) {
+            e.dims[d + 1] *= e.dims[d];
+            for (int k = d; k + 1 < e.rank; ++k) {
+                e.dims[k] = e.dims[k + 1];
+                e.out_strides[k] = e.out_strides[k + 1];
+                for (int l = 0; l < e.n_leaves; ++l) e.leaf[l].strides[k] = e.leaf[l].strides[k + 1];
+            }
+            --e.rank;
+        }
+        --d;
+    }
+}
+
 // Builds the float32 fast-path arguments, or returns false when the program does not qualify.
 static bool ew_f32_plan(const mgc_hip_ew_args *e, EwF32Args &f, bool &vec) {
     if (e->out_dtype != MGC_F32 || e->rank < 1 || e->rank > EWF_RANK || e->n_leaves < 1 ||
@@ -603,10 +626,13 @@ __global__ void range_kernel(const T *start, const T *delta, long n, T *out) {
 
 using namespace mgc;
 
-extern "C" void mgc_hip_elementwise(mgc_hip_exec *x, const mgc_hip_ew_args *e) {
+extern "C" void mgc_hip_elementwise(mgc_hip_exec *x, const mgc_hip_ew_args *args) {
     long total = 1;
-    for (int d = 0; d < e->rank; ++d) total *= e->dims[d];
+    for (int d = 0; d < args->rank; ++d) total *= args->dims[d];
     if (total <= 0) return;
+    mgc_hip_ew_args coalesced = *args;
+    ew_coalesce(coalesced);
+    const mgc_hip_ew_args *e = &coalesced;
     EwF32Args f;
     bool vec = false;
     if (ew_f32_plan(e, f, vec)) {
