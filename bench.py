@@ -34,6 +34,91 @@ import numpy as np  # noqa: E402
 
 MFMA_FP32_PEAK_TFLOPS = 157.3
 HBM_PEAK_GBS = 8000.0
+
+
+def _membench_cases():
+    """Single-operator graphs at bandwidth-bound sizes (hundreds of MB per launch) for every
+    memory-bound kernel family: (label, graph, feeds, op of the node to time)."""
+    from ml_graph_compiler.ir import Graph, TensorType
+    from ml_graph_compiler.shape_inference import infer_shapes
+
+    rng = np.random.default_rng(0)
+
+    def f32(*shape):
+        return rng.standard_normal(shape, dtype=np.float32)
+
+    cases = []
+
+    def single(label, op, inputs, attrs=None, consts=(), n_out=1, time_op=None):
+        g = Graph(label.replace(" ", "_"))
+        vals, feeds = [], {}
+        for i, arr in enumerate(inputs):
+            if i in consts:
+                vals.append(g.constant(arr, f"c{i}"))
+            else:
+                vals.append(g.add_input(f"x{i}", TensorType("float32", arr.shape)))
+                feeds[f"x{i}"] = arr
+        node = g.add_node(op, vals, n_out, attrs or {}, name="op")
+        for j, o in enumerate(node.outputs):
+            g.add_output(o, f"y{j}")
+        infer_shapes(g)
+        cases.append((label, g, feeds, time_op or op))
+
+    rows = 1 << 17
+    single("LayerNorm 131072 x 768", "LayerNormalization", [f32(rows, 768), f32(768), f32(768)], {"axis": -1}, consts=(1, 2))
+    single("Softmax 65536 x 1024", "Softmax", [f32(1 << 16, 1024)], {"axis": -1})
+    single("Add 64M + 64M", "Add", [f32(1 << 26), f32(1 << 26)])
+    single("Add 16 x 4096 x 1024 + bias row", "Add", [f32(16, 4096, 1024), f32(1024)])
+    single("Gelu 64M", "Gelu", [f32(1 << 26)])
+    single("Transpose 8192 x 8192", "Transpose", [f32(8192, 8192)], {"perm": [1, 0]})
+    single("Transpose head split 64 x 512 x 12 x 64", "Transpose", [f32(64, 512, 12, 64)], {"perm": [0, 2, 1, 3]})
+    single("Depthwise 3x3 s1 32 x 144 x 112 x 112", "Conv",
+           [f32(32, 144, 112, 112), f32(144, 1, 3, 3), f32(144)],
+           {"kernel_shape": [3, 3], "pads": [1, 1, 1, 1], "group": 144}, consts=(1, 2), time_op="FusedConv")
+    single("Depthwise 3x3 s2 32 x 144 x 112 x 112", "Conv",
+           [f32(32, 144, 112, 112), f32(144, 1, 3, 3), f32(144)],
+           {"kernel_shape": [3, 3], "pads": [1, 1, 1, 1], "strides": [2, 2], "group": 144}, consts=(1, 2),
+           time_op="FusedConv")
+    single("MaxPool 3x3 s2 32 x 128 x 112 x 112", "MaxPool", [f32(32, 128, 112, 112)],
+           {"kernel_shape": [3, 3], "strides": [2, 2], "pads": [1, 1, 1, 1]})
+    single("GlobalAveragePool 64 x 2048 x 14 x 14", "GlobalAveragePool", [f32(64, 2048, 14, 14)])
+    return cases
+
+
+def membench(cache: Path, replays: int = 5) -> str:
+    """Achieved bandwidth of each memory-bound kernel family at bandwidth-bound sizes: the timed
+    node's input + output bytes over its hipEvent duration (eager, best of ``replays``)."""
+    from ml_graph_compiler.codegen import compile_graph
+    from ml_graph_compiler.ir import numpy_dtype
+    from ml_graph_compiler.passes import optimize
+    from ml_graph_compiler.schedule import schedule
+
+    def nbytes(v):
+        return int(np.prod(v.type.shape)) * np.dtype(numpy_dtype(v.type.dtype)).itemsize
+
+    out = ["| case | timed node | MB moved | us | GB/s | % of 8 TB/s |", "|---|---|---:|---:|---:|---:|"]
+    for label, g, feeds, op in _membench_cases():
+        log(f"membench {label}")
+        optimize(g, "O3")
+        schedule(g)
+        model = compile_graph(g, cache_dir=cache, name="membench", profile=True)
+        try:
+            model.upload(feeds)
+            model.profile_reset()
+            model.profile_run(1)  # warm
+            best = None
+            for _ in range(replays):
+                model.profile_reset()
+                model.profile_run(1)
+                t = next(sec for (o, _name, sec), node in zip(model.profile(), g.nodes) if o == op)
+                best = t if best is None else min(best, t)
+        finally:
+            model.release()
+        node = next(n for n in g.nodes if n.op == op)
+        moved = sum(nbytes(v) for v in node.inputs if v is not None) + sum(nbytes(v) for v in node.outputs)
+        gbs = moved / best / 1e9
+        out.append(f"| {label} | {op} | {moved / 1e6:.1f} | {best * 1e6:.1f} | {gbs:.0f} | {100 * gbs / HBM_PEAK_GBS:.1f} |")
+    return "\n".join(out)
 WORKLOADS = ("resnet50", "bottleneck", "mobilenet_v2", "bert_base", "gpt2", "single_gemm")
 
 
@@ -460,7 +545,12 @@ def main() -> int:
     p.add_argument("--mfma-summary", nargs=2, metavar=("PMC_DIR", "TRACE_DIR"),
                    help="per-kernel MFMA FLOP, TFLOP/s and busy cycles from a counter run and a "
                         "kernel trace of --pmc-probe, written to profiles/ and printed")
+    p.add_argument("--membench", action="store_true",
+                   help="achieved HBM bandwidth of every memory-bound kernel family at large sizes; prints a table")
     args = p.parse_args()
+    if args.membench:
+        print(membench(Path(args.cache)))
+        return 0
     if args.mfma_summary:
         batch = 128 if args.workload == "single_gemm" else args.batch
         text = mfma_summary(*map(Path, args.mfma_summary), args.workload, batch)

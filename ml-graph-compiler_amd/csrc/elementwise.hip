@@ -312,13 +312,17 @@ __device__ __forceinline__ float ewf_op(const EwF32Instr &in, float a, float b, 
     }
 }
 
-template <bool VEC>
+// NL leaves and NI instructions at most: the register file of a work item is NL + NI values
+// per lane of the unit; small programs (one Add, one activation) take the small instantiation,
+// whose few registers let twice as many waves, and so twice as many loads, be in flight.
+template <bool VEC, int NL, int NI>
 __global__ void __launch_bounds__(256) ew_f32_kernel(const EwF32Args e) {
     constexpr int W = VEC ? 4 : 1;
+    constexpr int NR = NL + NI;
     for (int u = blockIdx.x * 256 + threadIdx.x; u < e.units; u += gridDim.x * 256) {
-        int off[EWF_LEAVES];
+        int off[NL];
 #pragma unroll
-        for (int l = 0; l < EWF_LEAVES; ++l) off[l] = 0;
+        for (int l = 0; l < NL; ++l) off[l] = 0;
         int ooff = 0;
         int rem = u;
 #pragma unroll
@@ -330,12 +334,12 @@ __global__ void __launch_bounds__(256) ew_f32_kernel(const EwF32Args e) {
                 if (d == e.rank - 1) c *= W;
                 ooff += c * e.ost[d];
 #pragma unroll
-                for (int l = 0; l < EWF_LEAVES; ++l) off[l] += c * e.lst[l][d];
+                for (int l = 0; l < NL; ++l) off[l] += c * e.lst[l][d];
             }
         }
-        float R0[EWF_REGS], R1[EWF_REGS], R2[EWF_REGS], R3[EWF_REGS];
+        float R0[NR], R1[NR], R2[NR], R3[NR];
 #pragma unroll
-        for (int l = 0; l < EWF_LEAVES; ++l) {
+        for (int l = 0; l < NL; ++l) {
             float v0 = 0.f, v1 = 0.f, v2 = 0.f, v3 = 0.f;
             if (l < e.n_leaves) {
                 const float *src = e.leaf[l] + off[l];
@@ -349,9 +353,11 @@ __global__ void __launch_bounds__(256) ew_f32_kernel(const EwF32Args e) {
             R0[l] = v0; R1[l] = v1; R2[l] = v2; R3[l] = v3;
         }
 #pragma unroll
-        for (int r = EWF_LEAVES; r < EWF_REGS; ++r) R0[r] = R1[r] = R2[r] = R3[r] = 0.f;
+        for (int r = NL; r < NR; ++r) R0[r] = R1[r] = R2[r] = R3[r] = 0.f;
         float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
-        for (int i = 0; i < e.n_instr; ++i) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            if (i >= e.n_instr) break;
             const EwF32Instr &in = e.ins[i];
             const int ia = in.a, ib = in.b >= 0 ? in.b : 0, ic = in.c >= 0 ? in.c : 0;
             o0 = ewf_op(in, R0[ia], R0[ib], R0[ic]);
@@ -360,10 +366,10 @@ __global__ void __launch_bounds__(256) ew_f32_kernel(const EwF32Args e) {
                 o2 = ewf_op(in, R2[ia], R2[ib], R2[ic]);
                 o3 = ewf_op(in, R3[ia], R3[ib], R3[ic]);
             }
-            R0[EWF_LEAVES + i] = o0;
-            R1[EWF_LEAVES + i] = o1;
-            R2[EWF_LEAVES + i] = o2;
-            R3[EWF_LEAVES + i] = o3;
+            R0[NL + i] = o0;
+            R1[NL + i] = o1;
+            R2[NL + i] = o2;
+            R3[NL + i] = o3;
         }
         if (VEC) {
             *reinterpret_cast<float4 *>(e.out + ooff) = make_float4(o0, o1, o2, o3);
@@ -397,7 +403,8 @@ static void ew_coalesce(mgc_hip_ew_args &e) {
 }
 
 // Builds the float32 fast-path arguments, or returns false when the program does not qualify.
-static bool ew_f32_plan(const mgc_hip_ew_args *e, EwF32Args &f, bool &vec) {
+// ``nl``: the leaf count of the kernel instantiation, where instruction results start.
+static bool ew_f32_plan(const mgc_hip_ew_args *e, EwF32Args &f, bool &vec, int nl) {
     if (e->out_dtype != MGC_F32 || e->rank < 1 || e->rank > EWF_RANK || e->n_leaves < 1 ||
         e->n_leaves > EWF_LEAVES || e->n_instr < 1 || e->n_instr > EWF_INSTR)
         return false;
@@ -462,8 +469,8 @@ static bool ew_f32_plan(const mgc_hip_ew_args *e, EwF32Args &f, bool &vec) {
             f.lst[l][d] = (l < e->n_leaves && d < e->rank) ? (int)e->leaf[l].strides[d] : 0;
     }
     // Registers: leaves 0 .. n_leaves - 1 keep their numbers; instruction i's result, register
-    // MGC_EW_MAX_LEAVES + i in the generic encoding, becomes EWF_LEAVES + i.
-    auto remap = [&](int a) { return a < 0 ? -1 : (a < MGC_EW_MAX_LEAVES ? a : a - MGC_EW_MAX_LEAVES + EWF_LEAVES); };
+    // MGC_EW_MAX_LEAVES + i in the generic encoding, becomes nl + i.
+    auto remap = [&](int a) { return a < 0 ? -1 : (a < MGC_EW_MAX_LEAVES ? a : a - MGC_EW_MAX_LEAVES + nl); };
     for (int i = 0; i < EWF_INSTR; ++i) {
         EwF32Instr &o = f.ins[i];
         if (i < e->n_instr) {
@@ -557,6 +564,78 @@ __global__ void __launch_bounds__(256) copy_kernel(const mgc_hip_copy_args c) {
     }
 }
 
+// A copy that moves the input's contiguous dim p to a strided output position while the
+// output's contiguous dim q reads the input with a stride (a transpose of p and q): 64 x 64
+// tiles through LDS, read with consecutive lanes along p and written with consecutive lanes
+// along q, so both sides are coalesced (the element-wise copy would touch one element per
+// 64-byte line on one side). blockIdx.z enumerates the other (batch) dims, at most two.
+struct TransposeGeo {
+    int np, nq;               // extents of p (input-contiguous) and q (output-contiguous)
+    long in_q, out_p;         // the non-unit strides: input along q, output along p
+    int nb0, nb1;             // batch extents (nb0 outermost)
+    long in_b0, in_b1, out_b0, out_b1;
+    long in_base, out_base;
+};
+
+template <typename T>
+__global__ void __launch_bounds__(256) transpose_tiled_kernel(const TransposeGeo g, const T *in, T *out) {
+    __shared__ T tile[64][65];
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    const int q0 = blockIdx.x * 64, p0 = blockIdx.y * 64;
+    const int b1 = blockIdx.z % g.nb1, b0 = blockIdx.z / g.nb1;
+    const T *src = in + g.in_base + b0 * g.in_b0 + b1 * g.in_b1;
+    T *dst = out + g.out_base + b0 * g.out_b0 + b1 * g.out_b1;
+    const int p = p0 + tx;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int ql = ty + 4 * i, q = q0 + ql;
+        if (p < g.np && q < g.nq) tile[ql][tx] = src[(long)q * g.in_q + p];
+    }
+    __syncthreads();
+    const int q = q0 + tx;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int pl = ty + 4 * i, pp = p0 + pl;
+        if (pp < g.np && q < g.nq) dst[(long)pp * g.out_p + q] = tile[tx][pl];
+    }
+}
+
+// The tiled transpose applies when the output's innermost dim q is read with a stride while
+// another dim p is the input's contiguous one, both at least 32 long, with no modulus and at
+// most two other dims; fills g and the grid and returns true then.
+static bool transpose_plan(const mgc_hip_copy_args &c, TransposeGeo &g, dim3 &grid) {
+    const int r = c.rank;
+    if (r < 2 || r > 4 || (c.elem_bytes != 4 && c.elem_bytes != 8)) return false;
+    const int q = r - 1;
+    if (c.out_strides[q] != 1 || c.in_strides[q] == 1) return false;
+    int p = -1;
+    for (int d = 0; d < r; ++d) {
+        if (c.in_mod[d] != 0) return false;
+        if (d != q && c.in_strides[d] == 1) p = d;
+    }
+    if (p < 0 || c.dims[p] < 32 || c.dims[q] < 32 || c.dims[p] > 0x7fffffff || c.dims[q] > 0x7fffffff)
+        return false;
+    int batch[2] = {-1, -1}, nb = 0;
+    for (int d = 0; d < r; ++d)
+        if (d != p && d != q) batch[nb++] = d;
+    g.np = (int)c.dims[p];
+    g.nq = (int)c.dims[q];
+    g.in_q = c.in_strides[q];
+    g.out_p = c.out_strides[p];
+    g.nb0 = batch[0] >= 0 ? (int)c.dims[batch[0]] : 1;
+    g.nb1 = batch[1] >= 0 ? (int)c.dims[batch[1]] : 1;
+    g.in_b0 = batch[0] >= 0 ? c.in_strides[batch[0]] : 0;
+    g.out_b0 = batch[0] >= 0 ? c.out_strides[batch[0]] : 0;
+    g.in_b1 = batch[1] >= 0 ? c.in_strides[batch[1]] : 0;
+    g.out_b1 = batch[1] >= 0 ? c.out_strides[batch[1]] : 0;
+    g.in_base = c.in_base;
+    g.out_base = c.out_base;
+    const long nbatch = (long)g.nb0 * g.nb1;
+    if (nbatch < 1 || nbatch > 65535) return false;
+    grid = dim3((unsigned)((g.nq + 63) / 64), (unsigned)((g.np + 63) / 64), (unsigned)nbatch);
+    return grid.y <= 65535;
+}
+
 // One thread per output pixel (b, i, j): two 8-byte reads per channel and row of the 2 x 2
 // block (neighbouring threads read neighbouring pairs), C 16-byte writes of the pixel's 4 C
 // values (neighbouring threads write neighbouring 16 C-byte groups).
@@ -635,11 +714,19 @@ extern "C" void mgc_hip_elementwise(mgc_hip_exec *x, const mgc_hip_ew_args *args
     const mgc_hip_ew_args *e = &coalesced;
     EwF32Args f;
     bool vec = false;
-    if (ew_f32_plan(e, f, vec)) {
-        if (vec)
-            MGC_LAUNCH(x, ew_f32_kernel<true>, dim3(blocks_for(f.units, 256, 8192)), dim3(256), 0, f);
-        else
-            MGC_LAUNCH(x, ew_f32_kernel<false>, dim3(blocks_for(f.units, 256, 8192)), dim3(256), 0, f);
+    const int nl = e->n_leaves <= 2 && e->n_instr <= 1 ? 2 : e->n_leaves <= 3 && e->n_instr <= 2 ? 3 : EWF_LEAVES;
+    if (ew_f32_plan(e, f, vec, nl)) {
+        const dim3 grid(blocks_for(f.units, 256, 8192));
+        if (nl == 2) {
+            if (vec) MGC_LAUNCH(x, (ew_f32_kernel<true, 2, 1>), grid, dim3(256), 0, f);
+            else MGC_LAUNCH(x, (ew_f32_kernel<false, 2, 1>), grid, dim3(256), 0, f);
+        } else if (nl == 3) {
+            if (vec) MGC_LAUNCH(x, (ew_f32_kernel<true, 3, 2>), grid, dim3(256), 0, f);
+            else MGC_LAUNCH(x, (ew_f32_kernel<false, 3, 2>), grid, dim3(256), 0, f);
+        } else {
+            if (vec) MGC_LAUNCH(x, (ew_f32_kernel<true, EWF_LEAVES, EWF_INSTR>), grid, dim3(256), 0, f);
+            else MGC_LAUNCH(x, (ew_f32_kernel<false, EWF_LEAVES, EWF_INSTR>), grid, dim3(256), 0, f);
+        }
         return;
     }
     MGC_LAUNCH(x, ew_program_kernel, dim3(blocks_for(total, 256, 8192)), dim3(256), 0, *e);
@@ -650,6 +737,17 @@ extern "C" void mgc_hip_copy(mgc_hip_exec *x, const mgc_hip_copy_args *c) {
     for (int d = 0; d < c->rank; ++d) total *= c->dims[d];
     if (total <= 0) return;
     mgc_hip_copy_args a = *c;
+    TransposeGeo tg;
+    dim3 tgrid;
+    if (transpose_plan(a, tg, tgrid)) {
+        if (a.elem_bytes == 4)
+            MGC_LAUNCH(x, transpose_tiled_kernel<unsigned>, tgrid, dim3(256), 0, tg,
+                       static_cast<const unsigned *>(a.in), static_cast<unsigned *>(a.out));
+        else
+            MGC_LAUNCH(x, transpose_tiled_kernel<unsigned long long>, tgrid, dim3(256), 0, tg,
+                       static_cast<const unsigned long long *>(a.in), static_cast<unsigned long long *>(a.out));
+        return;
+    }
     // Move 16-byte units when the innermost dim is contiguous on both sides, a multiple of the
     // unit, and every stride and base keeps the unit aligned.
     int r = a.rank;

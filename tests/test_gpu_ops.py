@@ -91,6 +91,12 @@ def test_integer_clip(hip_cache):
     [
         ("Transpose", [f32(2, 3, 4, 5)], set(), {"perm": [0, 2, 3, 1]}),
         ("Transpose", [f32(3, 4)], set(), {}),
+        # the LDS-tiled transpose (the contiguous dim moves; both dims >= 32): ragged tiles,
+        # one and two batch dims, 8-byte elements
+        ("Transpose", [f32(70, 90)], set(), {"perm": [1, 0]}),
+        ("Transpose", [f32(4, 64, 33)], set(), {"perm": [0, 2, 1]}),
+        ("Transpose", [f32(2, 3, 40, 48)], set(), {"perm": [1, 0, 3, 2]}),
+        ("Transpose", [np.arange(40 * 50, dtype=np.int64).reshape(40, 50)], set(), {"perm": [1, 0]}),
         ("Expand", [f32(3, 1), np.asarray([2, 3, 4], np.int64)], {1}, {}),
         ("Tile", [f32(2, 3), np.asarray([2, 2], np.int64)], {1}, {}),
         ("Slice", [f32(6, 8), np.asarray([1, -6], np.int64), np.asarray([5, 100], np.int64),
