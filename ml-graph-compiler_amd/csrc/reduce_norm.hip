@@ -369,9 +369,13 @@ __global__ void pool_nhwc(const PoolGeo g, const float *in, float *out) {
 
 // NHWC with C % 4 == 0: one thread per output channel quad, 16-byte loads and stores, 32-bit
 // index arithmetic with host-computed divisors (the element count is below 2^31).
+// K > 0: a K x K window with its taps unrolled, so all K * K loads are requested before the
+// first is combined; K == 0: any window.
+template <int K>
 __global__ void pool_nhwc_vec4(const PoolGeo g, FastDiv div_c4, FastDiv div_ow, FastDiv div_oh,
                                int total, const float *in, float *out) {
     const int C4 = g.C >> 2;
+    const int KH = K > 0 ? K : g.KH, KW = K > 0 ? K : g.KW;
     for (int idx = xcd_block() * blockDim.x + threadIdx.x; idx < total; idx += gridDim.x * blockDim.x) {
         int t = fdiv(idx, div_c4);
         const int c4 = idx - t * C4;
@@ -382,10 +386,12 @@ __global__ void pool_nhwc_vec4(const PoolGeo g, FastDiv div_c4, FastDiv div_ow, 
         const float *img = in + (long)n * g.H * g.W * g.C + c4 * 4;
         const float init = g.is_max ? -INFINITY : 0.0f;
         float4 acc = make_float4(init, init, init, init);
-        for (int kh = 0; kh < g.KH; ++kh) {
+#pragma unroll
+        for (int kh = 0; kh < KH; ++kh) {
             const int ih = oh * g.SH - g.PT + kh * g.DH;
             if (ih < 0 || ih >= g.H) continue;
-            for (int kw = 0; kw < g.KW; ++kw) {
+#pragma unroll
+            for (int kw = 0; kw < KW; ++kw) {
                 const int iw = ow * g.SW - g.PL + kw * g.DW;
                 if (iw < 0 || iw >= g.W) continue;
                 const float4 v = *reinterpret_cast<const float4 *>(img + (long)(ih * g.W + iw) * g.C);
@@ -749,7 +755,8 @@ extern "C" void mgc_hip_pool(mgc_hip_exec *x, int nhwc, int is_max, int N, int H
                      (((uintptr_t)in | (uintptr_t)out) & 15) == 0;
     if (vec) {
         const int quads = (int)(total / 4);
-        MGC_LAUNCH(x, pool_nhwc_vec4, dim3(blocks_for(quads, 256, 16384)), dim3(256), 0, g,
+        auto kern = KH == 3 && KW == 3 ? pool_nhwc_vec4<3> : pool_nhwc_vec4<0>;
+        MGC_LAUNCH(x, kern, dim3(blocks_for(quads, 256, 16384)), dim3(256), 0, g,
                    make_fastdiv((unsigned)(C / 4)), make_fastdiv((unsigned)OW), make_fastdiv((unsigned)OH),
                    quads, in, out);
     } else if (nhwc) {

@@ -294,6 +294,9 @@ def test_pooling(op, attrs, opt, hip_cache):
         attrs = {k: v for k, v in attrs.items() if k != "count_include_pad"}
     g, feeds = op_graph(op, [f32(2, 3, 9, 10)], attrs=attrs)
     check_hip(g, feeds, hip_cache, opt=opt)
+    # eight channels: at O3 the NHWC 16-byte kernel (3x3 windows unrolled, other windows generic)
+    g, feeds = op_graph(op, [f32(2, 8, 9, 10)], attrs=attrs)
+    check_hip(g, feeds, hip_cache, opt=opt)
 
 
 @pytest.mark.parametrize("op", ["GlobalAveragePool", "GlobalMaxPool"])
