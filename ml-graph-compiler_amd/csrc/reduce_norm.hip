@@ -579,6 +579,82 @@ __global__ void __launch_bounds__(256) depthwise3x3_nhwc_vec4(const DwGeo g, Fas
     }
 }
 
+// 3x3, dilation 1, stride S, C % 4 == 0, staged through LDS: a workgroup owns an 8 x 8 block
+// of output pixels over 8 channel quads. It loads the ((8 - 1) S + 3)^2 input pixels of those
+// quads once (zeros outside the image: 16-byte loads, 128 contiguous bytes per pixel), then
+// each thread computes two output quads from LDS. Every input quad crosses L2 -> CU once per
+// tile (the halo adds (7 S + 3)^2 / (8 S)^2 - 1) instead of once per window that covers it.
+// Taps accumulate after the bias in row-major order, as in the other depthwise kernels; taps
+// outside the image contribute zero products.
+template <int S>
+__global__ void __launch_bounds__(256) depthwise3x3_nhwc_lds(const DwGeo g, int tiles_w, int tiles_h, int cgroups,
+                                                             const float *in, const float *w, const float *bias,
+                                                             const float *res, float *out) {
+    constexpr int T = 8, CQ = 8, IT = (T - 1) * S + 3;
+    __shared__ float4 tile[IT * IT * CQ];
+    int b = xcd_block();
+    const int cg = b % cgroups;
+    b /= cgroups;
+    const int tw = b % tiles_w;
+    b /= tiles_w;
+    const int th = b % tiles_h;
+    const int n = b / tiles_h;
+    const int C4 = g.C >> 2;
+    const int c4base = cg * CQ;
+    const int oh0 = th * T, ow0 = tw * T;
+    const int ih0 = oh0 * S - g.PT, iw0 = ow0 * S - g.PL;
+    const float4 *img = reinterpret_cast<const float4 *>(in) + (long)n * g.H * g.W * C4;
+    const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int e = threadIdx.x; e < IT * IT * CQ; e += 256) {
+        const int q = e % CQ, pix = e / CQ;
+        const int r = pix / IT, col = pix - r * IT;
+        const int ih = ih0 + r, iw = iw0 + col, c4 = c4base + q;
+        float4 v = zero;
+        if (ih >= 0 && ih < g.H && iw >= 0 && iw < g.W && c4 < C4) v = img[((long)ih * g.W + iw) * C4 + c4];
+        tile[e] = v;
+    }
+    __syncthreads();
+    const int q = threadIdx.x % CQ, c4 = c4base + q;
+    if (c4 >= C4) return;
+    const float4 *w4 = reinterpret_cast<const float4 *>(w);
+    float4 wv[9];
+#pragma unroll
+    for (int t = 0; t < 9; ++t) wv[t] = w4[t * C4 + c4];
+    const float4 bv = bias ? reinterpret_cast<const float4 *>(bias)[c4] : zero;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int p = threadIdx.x / CQ + 32 * k;
+        const int ohl = p / T, owl = p % T;
+        const int oh = oh0 + ohl, ow = ow0 + owl;
+        if (oh >= g.OH || ow >= g.OW) continue;
+        float4 acc = bv;
+#pragma unroll
+        for (int kh = 0; kh < 3; ++kh)
+#pragma unroll
+            for (int kw = 0; kw < 3; ++kw) {
+                const float4 xv = tile[((ohl * S + kh) * IT + owl * S + kw) * CQ + q];
+                const float4 wt = wv[kh * 3 + kw];
+                acc.x = fmaf(xv.x, wt.x, acc.x);
+                acc.y = fmaf(xv.y, wt.y, acc.y);
+                acc.z = fmaf(xv.z, wt.z, acc.z);
+                acc.w = fmaf(xv.w, wt.w, acc.w);
+            }
+        const long o = ((long)(n * g.OH + oh) * g.OW + ow) * C4 + c4;
+        if (res) {
+            const float4 rv = reinterpret_cast<const float4 *>(res)[o];
+            acc.x += rv.x;
+            acc.y += rv.y;
+            acc.z += rv.z;
+            acc.w += rv.w;
+        }
+        acc.x = apply_act(acc.x, g.act, g.lo, g.hi);
+        acc.y = apply_act(acc.y, g.act, g.lo, g.hi);
+        acc.z = apply_act(acc.z, g.act, g.lo, g.hi);
+        acc.w = apply_act(acc.w, g.act, g.lo, g.hi);
+        reinterpret_cast<float4 *>(out)[o] = acc;
+    }
+}
+
 __global__ void depthwise_nhwc(const DwGeo g, const float *in, const float *w, const float *bias,
                                const float *res, float *out) {
     const long total = (long)g.N * g.OH * g.OW * g.C;
@@ -772,6 +848,16 @@ extern "C" void mgc_hip_pool(mgc_hip_exec *x, int nhwc, int is_max, int N, int H
 // layers at batch 32 with each choice.
 static int dw3_tile(int OW, int SW) { return SW == 1 && OW >= 28 ? 4 : 2; }
 
+// The LDS-tiled 3x3 kernel (equal strides) for launches of at most 2^18 output quads: there a
+// workgroup's three loads per thread, all issued before the first is used, beat the per-thread
+// column kernel (MobileNetV2 at batch 1: 0.404 vs 0.428 ms per forward). On large launches it
+// measured slower (the 112 x 112 x 144 s1 layer of 32 images at 32% of HBM peak instead of 47%:
+// its 128-byte channel slices of 576-byte pixels straddle cache lines and the tile does not
+// overlap its loads with its arithmetic), so those keep the column kernel.
+static bool dw3_lds(int N, int OH, int OW, int C) {
+    return (long)N * OH * OW * (C / 4) <= (1L << 18);
+}
+
 extern "C" void mgc_hip_depthwise(mgc_hip_exec *x, int nhwc, int N, int H, int W, int C, int KH,
                                   int KW, int SH, int SW, int DH, int DW, int PT, int PL, int OH,
                                   int OW, const float *in, const float *w, const float *bias,
@@ -783,7 +869,14 @@ extern "C" void mgc_hip_depthwise(mgc_hip_exec *x, int nhwc, int N, int H, int W
         bool vec = C % 4 == 0 && total / 4 < 0x7fffffffL && (long)N * H * W * C < 0x7fffffffL &&
                    (((uintptr_t)in | (uintptr_t)w | (uintptr_t)out | (uintptr_t)bias | (uintptr_t)res) & 15) == 0;
         const bool k3 = KH == 3 && KW == 3 && DH == 1 && DW == 1 && (SW == 1 || SW == 2);
-        if (vec && k3) {
+        const int tiles_w = (OW + 7) / 8, tiles_h = (OH + 7) / 8, cgroups = (C / 4 + 7) / 8;
+        const long blocks = (long)N * tiles_h * tiles_w * cgroups;
+        const bool lds = vec && k3 && SH == SW && dw3_lds(N, OH, OW, C) && blocks < 0x7fffffffL;
+        if (lds) {
+            auto kern = SW == 2 ? depthwise3x3_nhwc_lds<2> : depthwise3x3_nhwc_lds<1>;
+            MGC_LAUNCH(x, kern, dim3((unsigned)blocks), dim3(256), 0, g, tiles_w, tiles_h, cgroups, in, w, bias,
+                       res, out);
+        } else if (vec && k3) {
             const int tile = dw3_tile(OW, SW);
             const int owb = (OW + tile - 1) / tile;
             const int quads = (int)((long)N * OH * owb * (C / 4));

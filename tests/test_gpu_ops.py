@@ -258,6 +258,23 @@ def test_depthwise_with_residual_and_clip(hip_cache):
         check_hip(g, {"x": f32(2, 16, hw, hw) * 3}, hip_cache, opt="O3")
 
 
+@pytest.mark.parametrize(
+    "x_shape, stride",
+    [
+        ((1, 32, 30, 30), 1),     # at most 2^18 output quads: the LDS-tiled kernel
+        ((1, 48, 61, 61), 2),
+        ((2, 64, 120, 120), 1),   # more: the column kernel, four outputs per thread
+        ((2, 64, 240, 240), 2),   # ... stride 2, two outputs per thread
+        ((64, 64, 20, 20), 1),    # ... a narrow image, two outputs per thread
+    ],
+)
+def test_depthwise_kernels_by_launch_size(x_shape, stride, hip_cache):
+    c = x_shape[1]
+    attrs = {"kernel_shape": [3, 3], "pads": [1, 1, 1, 1], "group": c, "strides": [stride, stride]}
+    g, feeds = op_graph("Conv", [f32(*x_shape), f32(c, 1, 3, 3) * 0.3, f32(c)], const={1, 2}, attrs=attrs)
+    check_hip(g, feeds, hip_cache, opt="O3")
+
+
 def test_narrow_pointwise_with_residual(hip_cache):
     """A 24-channel pointwise convolution (128 x 32 tiles) with the residual Add and ReLU in its
     epilogue (O3), over an image whose pixel count is not a multiple of the tile height."""
