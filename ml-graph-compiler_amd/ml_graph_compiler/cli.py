@@ -62,9 +62,29 @@ def load_model(args: argparse.Namespace) -> Graph:
     return from_onnx(Path(args.model), _parse_shapes(args.shape), _parse_dims(args.dim))
 
 
+_INDEX_PASSTHROUGH = ("Reshape", "Flatten", "Squeeze", "Unsqueeze", "Identity", "Cast")
+
+
+def _gather_bound(value, depth: int = 0) -> int | None:
+    """The smallest extent a Gather indexes with ``value`` (directly or through reshapes and
+    casts), so random token ids stay in range; None when nothing gathers with it."""
+    bound = None
+    for u in value.users:
+        if u.op == "Gather" and len(u.inputs) > 1 and u.inputs[1] is value and u.input(0).type is not None:
+            data = u.input(0).tensor_type
+            axis = int(u.attrs.get("axis", 0))
+            size = int(data.shape[axis + data.rank if axis < 0 else axis])
+            bound = size if bound is None else min(bound, size)
+        elif u.op in _INDEX_PASSTHROUGH and depth < 4:
+            inner = _gather_bound(u.output, depth + 1)
+            if inner is not None:
+                bound = inner if bound is None else min(bound, inner)
+    return bound
+
+
 def random_inputs(graph: Graph, seed: int = 0, int_high: int = 100) -> dict[str, np.ndarray]:
-    """Random feeds for every graph input: standard normal floats, integers in [0, int_high),
-    random booleans."""
+    """Random feeds for every graph input: standard normal floats, integers in [0, int_high)
+    (or below the extent a Gather indexes with them, if smaller), random booleans."""
     rng = np.random.default_rng(seed)
     feeds: dict[str, np.ndarray] = {}
     for v in graph.inputs:
@@ -73,7 +93,9 @@ def random_inputs(graph: Graph, seed: int = 0, int_high: int = 100) -> dict[str,
         if dt == np.bool_:
             feeds[v.name] = rng.random(t.shape) < 0.5
         elif dt.kind in "iu":
-            feeds[v.name] = rng.integers(0, int_high, t.shape).astype(dt)
+            bound = _gather_bound(v)
+            high = int_high if bound is None else max(1, min(int_high, bound))
+            feeds[v.name] = rng.integers(0, high, t.shape).astype(dt)
         else:
             feeds[v.name] = rng.standard_normal(t.shape).astype(dt)
     return feeds

@@ -435,3 +435,16 @@ def test_cli_inspect_dims_shapes_and_export(tmp_path, capsys):
     assert "arena by strategy" in capsys.readouterr().out
     assert cli_main(["inspect", "no-such-model"]) == 2
     assert "neither a file nor a bundled sample" in capsys.readouterr().err
+
+
+def test_cli_random_token_ids_stay_in_range():
+    """Integer inputs that index a Gather (directly or through reshapes and casts) are drawn
+    below the gathered extent, so `compile --check/--bench` does not trip the index check."""
+    from ml_graph_compiler import builders
+    from ml_graph_compiler.cli import random_inputs
+
+    g = from_onnx(GOLDEN / "tiny_gpt.onnx")
+    vocab = next(n for n in g.nodes if n.op == "Gather").input(0).tensor_type.shape[0]
+    assert random_inputs(g, int_high=10**6)["ids"].max() < vocab
+    assert random_inputs(builders.bert_base(1), int_high=10**6)["input_ids"].max() < 30522
+    assert random_inputs(builders.bert_base(1), int_high=7)["input_ids"].max() < 7
