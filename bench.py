@@ -208,7 +208,10 @@ def cpu_baseline(workload: str, seconds_budget: float = 20.0) -> dict | None:
         log(f"cpu baseline unavailable: {exc}")
         return None
     try:
-        return cbackend.time_baseline(workload, seconds_budget=seconds_budget)
+        base = cbackend.time_baseline(workload, seconds_budget=seconds_budget)
+        one = cbackend.time_baseline(workload, seconds_budget=seconds_budget / 2, threads=1)
+        base["sample"] += f"; on 1 thread: {one['value']} {one['unit']} ({one['sample'].split('(')[1].split(')')[0]})"
+        return base
     except Exception as exc:
         log(f"cpu baseline failed: {exc}")
         return None

@@ -579,7 +579,10 @@ def time_baseline(workload: str, seconds_budget: float = 20.0, threads: int | No
     from ml_graph_compiler.builders import random_feeds
 
     model, g, meta = load_baseline(workload)
-    n_threads = threads or int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count() or 1
+    if threads:  # the reference runtime's own thread knob (mgc_kernels.c:34-70)
+        model.lib.mgc_set_num_threads(int(threads))
+    model.lib.mgc_get_max_threads.restype = ctypes.c_int
+    n_threads = int(model.lib.mgc_get_max_threads())
     feeds = random_feeds(g, 0, int_high=30522 if workload == "bert_base" else 100)
     model.run(feeds)
     times = []
