@@ -600,6 +600,47 @@ __global__ void __launch_bounds__(256) transpose_tiled_kernel(const TransposeGeo
     }
 }
 
+// The same transpose with 16-byte global accesses (V = 16 / sizeof(T) elements per lane) when
+// both extents, every stride and both bases are multiples of V and the pointers are 16-byte
+// aligned: a wave moves 1 KB per load or store instruction instead of 256 bytes, which the
+// address units, not HBM, limited. Lanes read V consecutive p of a q row into LDS, then V
+// consecutive q of a p column out of it; with the 65-element row pitch both phases spread a
+// wave's 64 lanes over all banks.
+template <typename T>
+__global__ void __launch_bounds__(256) transpose_tiled_vec_kernel(const TransposeGeo g, const T *in, T *out) {
+    constexpr int V = 16 / sizeof(T), LP = 64 / V, RP = 256 / LP;
+    __shared__ T tile[64][65];
+    const int lx = threadIdx.x % LP, ly = threadIdx.x / LP;
+    const int q0 = blockIdx.x * 64, p0 = blockIdx.y * 64;
+    const int b1 = blockIdx.z % g.nb1, b0 = blockIdx.z / g.nb1;
+    const T *src = in + g.in_base + b0 * g.in_b0 + b1 * g.in_b1;
+    T *dst = out + g.out_base + b0 * g.out_b0 + b1 * g.out_b1;
+    const int p = p0 + lx * V;
+#pragma unroll
+    for (int i = 0; i < 64 / RP; ++i) {
+        const int ql = ly + RP * i, q = q0 + ql;
+        if (p < g.np && q < g.nq) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(src + (long)q * g.in_q + p);
+            const T *e = reinterpret_cast<const T *>(&v);
+#pragma unroll
+            for (int k = 0; k < V; ++k) tile[ql][lx * V + k] = e[k];
+        }
+    }
+    __syncthreads();
+    const int q = q0 + lx * V;
+#pragma unroll
+    for (int i = 0; i < 64 / RP; ++i) {
+        const int pl = ly + RP * i, pp = p0 + pl;
+        if (pp < g.np && q < g.nq) {
+            uint4 v;
+            T *e = reinterpret_cast<T *>(&v);
+#pragma unroll
+            for (int k = 0; k < V; ++k) e[k] = tile[lx * V + k][pl];
+            *reinterpret_cast<uint4 *>(dst + (long)pp * g.out_p + q) = v;
+        }
+    }
+}
+
 // The tiled transpose applies when the output's innermost dim q is read with a stride while
 // another dim p is the input's contiguous one, both at least 32 long, with no modulus and at
 // most two other dims; fills g and the grid and returns true then.
@@ -740,7 +781,18 @@ extern "C" void mgc_hip_copy(mgc_hip_exec *x, const mgc_hip_copy_args *c) {
     TransposeGeo tg;
     dim3 tgrid;
     if (transpose_plan(a, tg, tgrid)) {
-        if (a.elem_bytes == 4)
+        const long per = 16 / a.elem_bytes;
+        const bool vec = tg.np % per == 0 && tg.nq % per == 0 && tg.in_q % per == 0 && tg.out_p % per == 0 &&
+                         tg.in_b0 % per == 0 && tg.in_b1 % per == 0 && tg.out_b0 % per == 0 &&
+                         tg.out_b1 % per == 0 && tg.in_base % per == 0 && tg.out_base % per == 0 &&
+                         (((uintptr_t)a.in | (uintptr_t)a.out) & 15) == 0;
+        if (vec && a.elem_bytes == 4)
+            MGC_LAUNCH(x, transpose_tiled_vec_kernel<unsigned>, tgrid, dim3(256), 0, tg,
+                       static_cast<const unsigned *>(a.in), static_cast<unsigned *>(a.out));
+        else if (vec)
+            MGC_LAUNCH(x, transpose_tiled_vec_kernel<unsigned long long>, tgrid, dim3(256), 0, tg,
+                       static_cast<const unsigned long long *>(a.in), static_cast<unsigned long long *>(a.out));
+        else if (a.elem_bytes == 4)
             MGC_LAUNCH(x, transpose_tiled_kernel<unsigned>, tgrid, dim3(256), 0, tg,
                        static_cast<const unsigned *>(a.in), static_cast<unsigned *>(a.out));
         else

@@ -42,6 +42,21 @@ def test_binary_broadcast(op, shapes, hip_cache):
     check_hip(g, feeds, hip_cache)
 
 
+@pytest.mark.parametrize(
+    "op, shapes",
+    [
+        ("Add", ((3, 1000, 3001), (3, 1000, 3001))),  # one element per item, 9M items
+        ("Add", ((4, 2048, 2560), (2560,))),           # four per item: 5.2M items, a bias row
+        ("Gelu", ((3, 1024, 3000),)),
+    ],
+)
+def test_elementwise_several_items_per_thread(op, shapes, hip_cache):
+    """Launches of more work items than the grid has threads (the grid-stride loop runs
+    several trips, the last one partial)."""
+    g, feeds = op_graph(op, [f32(*s) for s in shapes])
+    check_hip(g, feeds, hip_cache)
+
+
 @pytest.mark.parametrize("op", ["Equal", "Less", "Greater", "LessOrEqual", "GreaterOrEqual"])
 def test_compare(op, hip_cache):
     a = rng.integers(0, 3, (3, 4)).astype(np.float32)
@@ -97,6 +112,10 @@ def test_integer_clip(hip_cache):
         ("Transpose", [f32(4, 64, 33)], set(), {"perm": [0, 2, 1]}),
         ("Transpose", [f32(2, 3, 40, 48)], set(), {"perm": [1, 0, 3, 2]}),
         ("Transpose", [np.arange(40 * 50, dtype=np.int64).reshape(40, 50)], set(), {"perm": [1, 0]}),
+        # ... with 16-byte accesses (extents, strides and bases multiples of 16 bytes), ragged tiles
+        ("Transpose", [f32(2, 3, 100, 72)], set(), {"perm": [0, 1, 3, 2]}),
+        ("Transpose", [f32(36, 5, 68)], set(), {"perm": [2, 1, 0]}),
+        ("Transpose", [np.arange(66 * 98, dtype=np.int64).reshape(66, 98)], set(), {"perm": [1, 0]}),
         ("Expand", [f32(3, 1), np.asarray([2, 3, 4], np.int64)], {1}, {}),
         ("Tile", [f32(2, 3), np.asarray([2, 2], np.int64)], {1}, {}),
         ("Slice", [f32(6, 8), np.asarray([1, -6], np.int64), np.asarray([5, 100], np.int64),
@@ -263,7 +282,8 @@ def test_depthwise_with_residual_and_clip(hip_cache):
     [
         ((1, 32, 30, 30), 1),     # at most 2^18 output quads: the LDS-tiled kernel
         ((1, 48, 61, 61), 2),
-        ((2, 64, 120, 120), 1),   # more: the column kernel, four outputs per thread
+        ((2, 64, 112, 112), 1),   # more: the column kernel, eight outputs per thread
+        ((2, 64, 60, 60), 1),     # ... four outputs per thread (60 is not a multiple of 8)
         ((2, 64, 240, 240), 2),   # ... stride 2, two outputs per thread
         ((64, 64, 20, 20), 1),    # ... a narrow image, two outputs per thread
     ],
