@@ -123,26 +123,17 @@ __device__ __forceinline__ f4 act4(f4 v, int act, float lo, float hi) {
     }
 }
 
-// Epilogue shared by the GEMM kernels: the accumulator tile goes through LDS (smem, at least
-// BM * (BN + 8) floats, free when this is called) and leaves as 16-byte chunks with alpha, bias,
-// residual and activation applied, or raw into the split-K workspace.
-// Pass 2 gives each thread one fixed 16-byte column chunk of the tile and the rows
-// r0, r0 + RSTEP, ..., so the column bias is read once per thread.
-template <int BM, int BN, int WGM, int RM, int RN>
-__device__ __forceinline__ void gemm_store_tile(const GemmDev &p, float *smem,
-                                                     const floatx16 (&acc)[RM][RN], int m0, int n0,
-                                                     int ks, long co, long ro) {
-    constexpr int WGN = 4 / WGM;
-    constexpr int WM = BM / WGM;
-    constexpr int WN = BN / WGN;
+// Epilogue shared by the GEMM kernels, pass 2: the BM x BN tile, staged in LDS at Cs with row
+// pitch BN + 8 floats, leaves as 16-byte chunks with alpha, bias, residual and activation
+// applied, or raw into the split-K workspace. Each thread owns one fixed 16-byte column chunk
+// of the tile and the rows r0, r0 + RSTEP, ..., so the column bias is read once per thread.
+// Every one of the 256 threads calls it (no barrier inside).
+template <int BM, int BN>
+__device__ __forceinline__ void gemm_lds_to_global(const GemmDev &p, const float *Cs, int m0, int n0, int ks,
+                                                   long co, long ro) {
     constexpr int LDC = BN + 8;
     const f4 zero4 = {0.f, 0.f, 0.f, 0.f};
     const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave / WGN, wn = wave - (wave / WGN) * WGN;
-    const int li = lane & 31;
-    const int lh = lane >> 5;
     constexpr int C4 = BN / 4;
     static_assert(256 % C4 == 0, "column chunks must divide the workgroup");
     constexpr int RSTEP = 256 / C4;
@@ -172,19 +163,6 @@ __device__ __forceinline__ void gemm_store_tile(const GemmDev &p, float *smem,
             for (int e = 0; e < ncol; ++e) cbias[e] = ldg(bias + col + e);
         }
     }
-    // pass 1: registers -> LDS tile. Block (i, j) register r holds tile row
-    // 8 * (r / 4) + 4 * lh + r % 4 and column li of that 32x32 block.
-    float *const Cs = smem;
-#pragma unroll
-    for (int i = 0; i < RM; ++i)
-#pragma unroll
-        for (int j = 0; j < RN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-                Cs[(wm * WM + i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3)) * LDC + wn * WN + j * 32 +
-                   li] = acc[i][j][r];
-    __syncthreads();
-
     // pass 2: LDS tile -> epilogue -> memory, 16 bytes per access, G rows per step with their
     // residual chunks (and row biases) requested together.
     if (!col_ok) return;
@@ -232,6 +210,38 @@ __device__ __forceinline__ void gemm_store_tile(const GemmDev &p, float *smem,
 }
 
 
+
+
+// The whole epilogue: pass 1 moves the accumulators to LDS (smem, at least BM * (BN + 8)
+// floats, free when this is called), then gemm_lds_to_global.
+template <int BM, int BN, int WGM, int RM, int RN>
+__device__ __forceinline__ void gemm_store_tile(const GemmDev &p, float *smem,
+                                                     const floatx16 (&acc)[RM][RN], int m0, int n0,
+                                                     int ks, long co, long ro) {
+    constexpr int WGN = 4 / WGM;
+    constexpr int WM = BM / WGM;
+    constexpr int WN = BN / WGN;
+    constexpr int LDC = BN + 8;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave / WGN, wn = wave - (wave / WGN) * WGN;
+    const int li = lane & 31;
+    const int lh = lane >> 5;
+    // pass 1: registers -> LDS tile. Block (i, j) register r holds tile row
+    // 8 * (r / 4) + 4 * lh + r % 4 and column li of that 32x32 block.
+    float *const Cs = smem;
+#pragma unroll
+    for (int i = 0; i < RM; ++i)
+#pragma unroll
+        for (int j = 0; j < RN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                Cs[(wm * WM + i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3)) * LDC + wn * WN + j * 32 +
+                   li] = acc[i][j][r];
+    __syncthreads();
+    gemm_lds_to_global<BM, BN>(p, Cs, m0, n0, ks, co, ro);
+}
 
 template <int BM, int BN, int WGM, int AMODE, int BMODE>
 __global__ void __launch_bounds__(256) gemm_mfma_kernel(const GemmDev p) {
@@ -728,6 +738,177 @@ __global__ void __launch_bounds__(256) gemm_dma_kernel(const GemmDev p) {
     gemm_store_tile<BM, BN, WGM>(p, smem, acc, m0, n0, ks, co, ro);
 }
 
+// GEMM / implicit-GEMM convolution on 32 x 32 output tiles whose K range is dealt out to the
+// workgroup's four waves (wave w takes the 32-wide K stages w, w + 4, ...), each with its own
+// two-stage DMA ring in LDS; the four partial tiles are summed through LDS in wave order before
+// the shared epilogue. For GEMMs whose 64 x 64 tiles are too few to occupy the CUs (small M at
+// batch 1), where the alternative is a K split over workgroups and a second kernel that adds
+// the partials: this kernel spreads the same work over four times as many tiles and finishes
+// in one launch. The waves synchronise only around the epilogue; in the main loop each wave
+// waits for its own loads (s_waitcnt), since it alone reads what it loaded. Operand forms as
+// gemm_dma_kernel (k-contiguous A or an NHWC image, packed [N][K] B). Row r of a wave's
+// 32-row block keeps k-chunk q at position q ^ (r & 7), so the eight lanes that read one chunk
+// of eight consecutive rows hit eight different positions.
+template <int AMODE>
+__global__ void __launch_bounds__(256) gemm_dma_wsplit_kernel(const GemmDev p) {
+    constexpr int BK = 32, T = 32;
+    constexpr int STAGE = 2 * T * BK;  // one wave's A and B blocks of one stage (floats)
+    constexpr int RING = 2 * STAGE;    // two stages per wave
+    constexpr int LDC = T + 8;
+    constexpr int SMEM = 4 * RING;     // 64 KB; the epilogue uses 5 * T * LDC floats of it
+    static_assert(5 * T * LDC <= SMEM, "epilogue staging");
+    static_assert(AMODE == AM_VEC || AMODE == AM_CONV_VEC, "vector A only");
+
+    __shared__ __attribute__((aligned(16))) float smem[SMEM];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    const int nb = gridDim.x;
+    const int full = nb & ~7;
+    int lin = blockIdx.x;
+    if (lin < full) {
+        const int per = full >> 3;
+        lin = (lin & 7) * per + (lin >> 3);
+    }
+    const int tm = lin / p.tiles_n;
+    const int tn = lin - tm * p.tiles_n;
+    const int m0 = tm * T, n0 = tn * T;
+
+    const int bz = blockIdx.z / p.split;
+    const int ks = blockIdx.z - bz * p.split;
+    long ao, bo, co, ro;
+    batch_offsets(p, bz, ao, bo, co, ro);
+    const float *abase = p.a.p + ao;
+    const float *bbase = p.b.p + bo;
+    const int kbeg = ks * p.kchunk;
+    const int kend = min(p.K, kbeg + p.kchunk);
+    const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+    const int nkw = nk > wave ? (nk - 1 - wave) / 4 + 1 : 0;  // this wave's stages
+
+    const int rsub = lane >> 3;
+    const int q4 = ((lane & 7) ^ rsub) * 4;  // this lane's k offset within a stage
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)abase, (short)0, (int)(p.a_bytes - ao * 4), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)bbase, (short)0, (int)(p.b_bytes - bo * 4), 0x00020000);
+    constexpr unsigned OOB = 0x80000000u;
+    unsigned aoff[4];
+    int aih[4], aiw[4];
+    const int ohw = p.a.OH * p.a.OW;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = m0 + i * 8 + rsub;
+        aoff[i] = OOB;
+        aih[i] = aiw[i] = -0x40000000;
+        if (m < p.M) {
+            if (AMODE == AM_CONV_VEC) {
+                const int n = fdiv(m, p.div_ohw), rr = m - n * ohw;
+                const int oh = fdiv(rr, p.div_ow), ow = rr - oh * p.a.OW;
+                aih[i] = oh * p.a.SH - p.a.PT;
+                aiw[i] = ow * p.a.SW - p.a.PL;
+                aoff[i] = (unsigned)(((n * p.a.H + aih[i]) * p.a.W + aiw[i]) * p.a.C) * 4u;
+            } else {
+                aoff[i] = (unsigned)m * (unsigned)p.a.rs * 4u;
+            }
+        }
+    }
+    unsigned boff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int n = n0 + i * 8 + rsub;
+        boff[i] = n < p.N ? (unsigned)n * (unsigned)p.b.cs * 4u : OOB;
+    }
+    int knext = kbeg + wave * BK + q4;
+    int cc = 0, ckw = 0, ckh = 0;
+    if (AMODE == AM_CONV_VEC) {
+        const int t = fdiv(knext, p.div_cg);
+        cc = knext - t * p.a.cg;
+        ckh = fdiv(t, p.div_kw);
+        ckw = t - ckh * p.a.KW;
+    }
+    float *const ring = smem + wave * RING;
+
+    auto issue = [&](int buf) __attribute__((always_inline)) {
+        const int k = knext;
+        const bool kok = k < kend;
+        float *sa = ring + buf * STAGE;
+        float *sb = sa + T * BK;
+        if constexpr (AMODE == AM_VEC) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dma16_buf(ra, kok ? aoff[i] + (unsigned)k * 4u : OOB, sa + i * 8 * BK);
+        } else {
+            const int dh = ckh * p.a.DH, dw = ckw * p.a.DW;
+            const unsigned koff = (unsigned)((dh * p.a.W + dw) * p.a.C + cc) * 4u;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const bool ok = kok && (unsigned)(aih[i] + dh) < (unsigned)p.a.H &&
+                                (unsigned)(aiw[i] + dw) < (unsigned)p.a.W;
+                dma16_buf(ra, ok ? aoff[i] + koff : OOB, sa + i * 8 * BK);
+            }
+            cc += 4 * BK;
+            while (cc >= p.a.cg) {
+                cc -= p.a.cg;
+                if (++ckw == p.a.KW) {
+                    ckw = 0;
+                    ++ckh;
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dma16_buf(rb, kok ? boff[i] + (unsigned)k * 4u : OOB, sb + i * 8 * BK);
+        knext = k + 4 * BK;
+    };
+
+    floatx16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    const int li = lane & 31;
+    const int lh = lane >> 5;
+    const int sw = li & 7;
+
+    if (nkw > 0) issue(0);
+    for (int kt = 0; kt < nkw; ++kt) {
+        // this wave's stage kt has landed in LDS; its reads of the other buffer (stage kt - 1)
+        // are complete before the next stage's DMA overwrites it
+        wait_vmcnt<0>();
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (kt + 1 < nkw) issue((kt + 1) & 1);
+        const float *as = ring + (kt & 1) * STAGE;
+        const float *bs = as + T * BK;
+        f4 af[4], bf[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            af[s] = *reinterpret_cast<const f4 *>(&as[li * BK + (((lh * 4 + s) ^ sw) << 2)]);
+            bf[s] = *reinterpret_cast<const f4 *>(&bs[li * BK + (((lh * 4 + s) ^ sw) << 2)]);
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[s][e], bf[s][e], acc, 0, 0, 0);
+    }
+    __syncthreads();
+    // partial tiles -> LDS slots (register r of a 32 x 32 block holds row 8 (r / 4) + 4 lh + r % 4,
+    // column li), then each thread adds one 16-byte chunk of the four slots in wave order
+    float *const slot = smem + wave * (T * LDC);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) slot[((r >> 2) * 8 + lh * 4 + (r & 3)) * LDC + li] = acc[r];
+    __syncthreads();
+    float *const Cs = smem + 4 * T * LDC;
+    {
+        const int row = tid >> 3, c = (tid & 7) * 4;
+        const int o = row * LDC + c;
+        f4 v = *reinterpret_cast<const f4 *>(&smem[o]);
+        v += *reinterpret_cast<const f4 *>(&smem[T * LDC + o]);
+        v += *reinterpret_cast<const f4 *>(&smem[2 * T * LDC + o]);
+        v += *reinterpret_cast<const f4 *>(&smem[3 * T * LDC + o]);
+        *reinterpret_cast<f4 *>(&Cs[o]) = v;
+    }
+    __syncthreads();
+    gemm_lds_to_global<T, T>(p, Cs, m0, n0, ks, co, ro);
+}
+
 // Sum the split-K partials and apply the epilogue (one batch element).
 __global__ void gemm_splitk_reduce(const GemmDev p) {
     const long total = (long)p.M * p.N;
@@ -842,6 +1023,10 @@ static GemmKernel pick_dma(int am) {
                         : &gemm_dma_kernel<BM, BN, WGM, 2, AM_CONV_VEC>;
 }
 
+static GemmKernel pick_wsplit(int am) {
+    return am == AM_VEC ? &gemm_dma_wsplit_kernel<AM_VEC> : &gemm_dma_wsplit_kernel<AM_CONV_VEC>;
+}
+
 struct TileChoice {
     int bm, bn, split;
 };
@@ -887,6 +1072,22 @@ static TileChoice choose_tiles(int M, int N, int K, int batch) {
         if (s > t.split) t.split = s;
     }
     return t;
+}
+
+// The wave-split kernel (32 x 32 tiles, K dealt to the four waves of a workgroup) in place of
+// a K split over 64 x 64 tiles plus the reduction kernel, when its tiles fit one workgroup per
+// CU and each of its waves runs at most four K stages more than a wave of the split launch
+// (about what the reduction launch and the partials' round trip cost). Batch-1 convolutions at
+// 56 x 56 and 28 x 28 qualify; deep-K layers on 14 x 14 and 7 x 7 images keep the K split, whose
+// extra workgroups the 32 x 32 tiles cannot match.
+static bool wave_split(int M, int N, int K, int batch) {
+    const TileChoice t = choose_tiles(M, N, K, batch);
+    if (batch != 1 || t.split < 2) return false;
+    const long tiles32 = (long)((M + 31) / 32) * ((N + 31) / 32);
+    const int kchunk = ((K + t.split - 1) / t.split + 31) / 32 * 32;
+    const int stages_split = kchunk / 32;
+    const int stages_wave = ((K + 31) / 32 + 3) / 4;
+    return tiles32 <= kCUs && stages_wave <= stages_split + 4;
 }
 
 // 128 x 32 tiles (four waves stacked along M) instead of 64 x 64 when they pad N less: the
@@ -1054,13 +1255,20 @@ static void gemm_launch(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const LnTai
                         p.a_bytes > 0 && p.a_bytes < kMaxRes && p.b_bytes > 0 &&
                         p.b_bytes < kMaxRes;
 
-    const bool narrow = dma_ok && narrow_tiles(p.N, p.split);
-    t.bm = narrow ? 128 : 64;
-    t.bn = narrow ? 32 : 64;
+    const bool wsplit = dma_ok && !ln && g->split_k <= 0 && wave_split(p.M, p.N, p.K, batch);
+    if (wsplit) {
+        p.split = 1;
+        p.kchunk = (p.K + 31) / 32 * 32;
+    }
+    const bool narrow = dma_ok && !wsplit && narrow_tiles(p.N, p.split);
+    t.bm = wsplit ? 32 : narrow ? 128 : 64;
+    t.bn = wsplit || narrow ? 32 : 64;
     p.tiles_m = (p.M + t.bm - 1) / t.bm;
     p.tiles_n = (p.N + t.bn - 1) / t.bn;
-    const GemmKernel kern = narrow ? pick_dma<128, 32, 4>(am)
-                            : dma_ok ? pick_dma<64, 64, 2>(am) : pick_kernel<64, 64, 2>(am, bm);
+    const GemmKernel kern = wsplit   ? pick_wsplit(am)
+                            : narrow ? pick_dma<128, 32, 4>(am)
+                            : dma_ok ? pick_dma<64, 64, 2>(am)
+                                     : pick_kernel<64, 64, 2>(am, bm);
     const dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)(batch * p.split));
     if (ln && p.split < 2) {  // the workspace did not allow the split the reduction needs
         x->launch_error = (int)hipErrorInvalidValue;
