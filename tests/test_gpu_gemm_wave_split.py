@@ -2,7 +2,7 @@
 the library runs them on the wave-split kernel (32 x 32 tiles, the K range dealt to the four
 waves of a workgroup, partial tiles summed in LDS) instead of a K split plus a reduction
 launch. Shapes chosen so that the selection applies: K of at least 512, a K split that the
-64 x 64 tiling would take, at most 256 tiles of 32 x 32. Ragged M, N and K, a partial last K
+64 x 64 tiling would take, at most 512 tiles of 32 x 32. Ragged M, N and K, a partial last K
 stage, bias / residual / activation epilogues, strided and dilated windows; compared with the
 oracle (rtol 1e-4)."""
 from __future__ import annotations
@@ -23,6 +23,7 @@ pytestmark = pytest.mark.gpu
         (128, 256, 1024, "bias_relu"),
         (100, 50, 600, "none"),          # ragged tiles, N not a multiple of 4, partial K stage
         (300, 96, 800, "residual"),
+        (128, 2304, 768, "bias_relu"),   # 288 tiles: two workgroups per CU
         (1, 1000, 2048, "bias_relu"),    # deep K over few rows: stays on the K split
     ],
 )
