@@ -1075,22 +1075,33 @@ static TileChoice choose_tiles(int M, int N, int K, int batch) {
 }
 
 // The wave-split kernel (32 x 32 tiles, K dealt to the four waves of a workgroup) in place of
-// a K split over 64 x 64 tiles plus the reduction kernel, when its tiles fit in one round of
-// two workgroups per CU (its LDS allows two) and each of its waves runs at most four K stages
-// more than a wave of the split launch (about what the reduction launch and the partials'
-// round trip cost). Batch-1 convolutions at 56 x 56 and 28 x 28 and the 128-row QKV and FFN
-// GEMMs of a sequence qualify; deep-K layers on 14 x 14 and 7 x 7 images keep the K split,
-// whose extra workgroups the 32 x 32 tiles cannot match. Measured at batch 1 against one
-// workgroup per CU: BERT-base 0.955 vs 1.113 ms, ResNet-50 and MobileNetV2 unchanged; margins
-// of 2, 8 and 16 stages instead of 4: ResNet-50 0.557, 0.561, 0.580 vs 0.556 ms.
-static bool wave_split(int M, int N, int K, int batch) {
+// the 64 x 64 tiles for a GEMM that the latter would split over K: returns the wave-split
+// launch's own K split (1: none, so no reduction launch) or 0 to keep the 64 x 64 tiles. Cost
+// of a launch = the K stages one wave runs, plus six when a reduction launch follows (about
+// what that launch and the partials' round trip cost); the wave-split launch may use up to the
+// 64 x 64 launch's split (the workspace is sized for it) while its tiles fit one round of two
+// workgroups per CU (its LDS allows two). Ties go to the wave-split kernel, the smaller split.
+// Batch-1 convolutions at 56 x 56 and 28 x 28 and the 128-row QKV and FFN GEMMs of a sequence
+// take it without a split; deep-K layers on 14 x 14 and 7 x 7 images with one, four times as
+// many waves sharing K as the 64 x 64 split launch. Measured at batch 1 with the no-split form
+// only, two workgroups per CU against one: BERT-base 0.955 vs 1.113 ms, ResNet-50 and
+// MobileNetV2 unchanged; a reduction cost of 2, 8 and 16 stages instead of 4: ResNet-50 0.557,
+// 0.561, 0.580 vs 0.556 ms.
+static int wave_split(int M, int N, int K, int batch) {
     const TileChoice t = choose_tiles(M, N, K, batch);
-    if (batch != 1 || t.split < 2) return false;
+    if (batch != 1 || t.split < 2) return 0;
     const long tiles32 = (long)((M + 31) / 32) * ((N + 31) / 32);
-    const int kchunk = ((K + t.split - 1) / t.split + 31) / 32 * 32;
-    const int stages_split = kchunk / 32;
-    const int stages_wave = ((K + 31) / 32 + 3) / 4;
-    return tiles32 <= 2 * kCUs && stages_wave <= stages_split + 4;
+    auto chunk_stages = [&](int s) { return ((K + s - 1) / s + 31) / 32; };
+    constexpr int kReduce = 6;
+    int best = 0, best_cost = chunk_stages(t.split) + kReduce;
+    for (int s = 1; s <= t.split && tiles32 * s <= 2 * kCUs; ++s) {
+        const int cost = (chunk_stages(s) + 3) / 4 + (s > 1 ? kReduce : 0);
+        if (cost < best_cost || (best == 0 && cost == best_cost)) {
+            best = s;
+            best_cost = cost;
+        }
+    }
+    return best;
 }
 
 // 128 x 32 tiles (four waves stacked along M) instead of 64 x 64 when they pad N less: the
@@ -1258,10 +1269,12 @@ static void gemm_launch(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const LnTai
                         p.a_bytes > 0 && p.a_bytes < kMaxRes && p.b_bytes > 0 &&
                         p.b_bytes < kMaxRes;
 
-    const bool wsplit = dma_ok && !ln && g->split_k <= 0 && wave_split(p.M, p.N, p.K, batch);
+    int wsk = dma_ok && !ln && g->split_k <= 0 ? wave_split(p.M, p.N, p.K, batch) : 0;
+    if (wsk > 1 && (g->workspace == nullptr || g->workspace_floats < (long)wsk * p.M * p.N)) wsk = 1;
+    const bool wsplit = wsk > 0;
     if (wsplit) {
-        p.split = 1;
-        p.kchunk = (p.K + 31) / 32 * 32;
+        p.split = wsk;
+        p.kchunk = ((p.K + wsk - 1) / wsk + 31) / 32 * 32;
     }
     const bool narrow = dma_ok && !wsplit && narrow_tiles(p.N, p.split);
     t.bm = wsplit ? 32 : narrow ? 128 : 64;

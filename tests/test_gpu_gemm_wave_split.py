@@ -1,8 +1,9 @@
 """GEMMs and convolutions shaped like batch-1 layers whose 64 x 64 tiles are too few for the CUs:
 the library runs them on the wave-split kernel (32 x 32 tiles, the K range dealt to the four
 waves of a workgroup, partial tiles summed in LDS) instead of a K split plus a reduction
-launch. Shapes chosen so that the selection applies: K of at least 512, a K split that the
-64 x 64 tiling would take, at most 512 tiles of 32 x 32. Ragged M, N and K, a partial last K
+launch (or, for deep K over few rows, with a K split of its own, four times as many waves
+sharing K). Shapes chosen so that the selection applies: K of at least 512, a K split that the
+64 x 64 tiling would take, at most 512 tiles of 32 x 32 (times the split). Ragged M, N and K, a partial last K
 stage, bias / residual / activation epilogues, strided and dilated windows; compared with the
 oracle (rtol 1e-4)."""
 from __future__ import annotations
@@ -24,7 +25,7 @@ pytestmark = pytest.mark.gpu
         (100, 50, 600, "none"),          # ragged tiles, N not a multiple of 4, partial K stage
         (300, 96, 800, "residual"),
         (128, 2304, 768, "bias_relu"),   # 288 tiles: two workgroups per CU
-        (1, 1000, 2048, "bias_relu"),    # deep K over few rows: stays on the K split
+        (1, 1000, 2048, "bias_relu"),    # deep K over one row: wave split plus a K split
     ],
 )
 def test_wave_split_gemm(m, n, k, epilogue, hip_cache):
@@ -54,6 +55,8 @@ def test_wave_split_gemm(m, n, k, epilogue, hip_cache):
         (128, 128, 28, 1, 1, True),   # stage 2, with the residual Add
         (64, 96, 57, 2, 1, False),    # strided, ragged output
         (64, 64, 20, 1, 2, True),     # dilated
+        (256, 256, 14, 1, 1, False),  # deep K (2304): the wave-split launch splits K as well
+        (512, 512, 7, 1, 1, True),    # K 4608 over 49 pixels
     ],
 )
 def test_wave_split_conv(cin, cout, hw, stride, dil, residual, hip_cache):
