@@ -1091,8 +1091,16 @@ static TileChoice choose_tiles(int M, int N, int K, int batch) {
 // by less than 0.3%.
 static int wave_split(int M, int N, int K, int batch) {
     const TileChoice t = choose_tiles(M, N, K, batch);
-    if (batch != 1 || t.split < 2) return 0;
+    if (batch != 1) return 0;
     const long tiles32 = (long)((M + 31) / 32) * ((N + 31) / 32);
+    if (t.split < 2) {
+        // K too short to split (< 512) on too few 64 x 64 tiles: four times the tiles with a
+        // quarter of the stages per wave, when that is fewer stages (the 1 x 1 convolutions of
+        // 28 x 28 and 14 x 14 images at batch 1)
+        const long tiles64 = (long)((M + 63) / 64) * ((N + 63) / 64);
+        const int st = (K + 31) / 32;
+        return tiles64 < kCUs && tiles32 <= 2 * kCUs && (st + 3) / 4 < st ? 1 : 0;
+    }
     auto chunk_stages = [&](int s) { return ((K + s - 1) / s + 31) / 32; };
     constexpr int kReduce = 6;
     int best = 0, best_cost = chunk_stages(t.split) + kReduce;

@@ -25,6 +25,7 @@ pytestmark = pytest.mark.gpu
         (100, 50, 600, "none"),          # ragged tiles, N not a multiple of 4, partial K stage
         (300, 96, 800, "residual"),
         (128, 2304, 768, "bias_relu"),   # 288 tiles: two workgroups per CU
+        (196, 1024, 256, "bias_relu"),   # K below the split threshold on 64 too few tiles
         (1, 1000, 2048, "bias_relu"),    # deep K over one row: wave split plus a K split
     ],
 )
@@ -49,24 +50,27 @@ def test_wave_split_gemm(m, n, k, epilogue, hip_cache):
 
 
 @pytest.mark.parametrize(
-    "cin, cout, hw, stride, dil, residual",
+    "cin, cout, hw, stride, dil, residual, ksize",
     [
-        (64, 64, 56, 1, 1, False),    # the ResNet-50 stage-1 3 x 3 layer at batch 1
-        (128, 128, 28, 1, 1, True),   # stage 2, with the residual Add
-        (64, 96, 57, 2, 1, False),    # strided, ragged output
-        (64, 64, 20, 1, 2, True),     # dilated
-        (256, 256, 14, 1, 1, False),  # deep K (2304): the wave-split launch splits K as well
-        (512, 512, 7, 1, 1, True),    # K 4608 over 49 pixels
+        (64, 64, 56, 1, 1, False, 3),    # the ResNet-50 stage-1 3 x 3 layer at batch 1
+        (128, 128, 28, 1, 1, True, 3),   # stage 2, with the residual Add
+        (64, 96, 57, 2, 1, False, 3),    # strided, ragged output
+        (64, 64, 20, 1, 2, True, 3),     # dilated
+        (256, 256, 14, 1, 1, False, 3),  # deep K (2304): the wave-split launch splits K as well
+        (512, 512, 7, 1, 1, True, 3),    # K 4608 over 49 pixels
+        (256, 1024, 14, 1, 1, False, 1), # 1 x 1, K 256: no split, a quarter of the stages
+        (256, 512, 56, 2, 1, False, 1),  # 1 x 1 stride-2 downsample to 28 x 28
     ],
 )
-def test_wave_split_conv(cin, cout, hw, stride, dil, residual, hip_cache):
+def test_wave_split_conv(cin, cout, hw, stride, dil, residual, ksize, hip_cache):
     rng = np.random.default_rng(cin + cout + hw)
     g = Graph("ws_conv")
     x = g.add_input("x", TensorType("float32", (1, cin, hw, hw)))
     feeds = {"x": rng.standard_normal((1, cin, hw, hw)).astype(np.float32)}
-    wt = g.constant((rng.standard_normal((cout, cin, 3, 3)) / np.sqrt(cin * 9)).astype(np.float32), "w")
+    wt = g.constant((rng.standard_normal((cout, cin, ksize, ksize)) / np.sqrt(cin * ksize * ksize)).astype(np.float32), "w")
     b = g.constant(rng.standard_normal(cout).astype(np.float32) * 0.1, "b")
-    attrs = {"kernel_shape": [3, 3], "pads": [dil] * 4, "strides": [stride, stride], "dilations": [dil, dil]}
+    attrs = {"kernel_shape": [ksize, ksize], "pads": [dil * (ksize // 2)] * 4, "strides": [stride, stride],
+             "dilations": [dil, dil]}
     y = g.add_node("Conv", [x, wt, b], 1, attrs, name="conv").output
     if residual:
         y = g.add_node("Add", [y, x], 1, {}, name="res").output
