@@ -1114,6 +1114,24 @@ static int wave_split(int M, int N, int K, int batch) {
     return best;
 }
 
+// The same choice for a GEMM whose split-K reduction ends in a LayerNorm (the split is
+// required, at least 2 and at most the 64 x 64 launch's): the wave-split launch with the split
+// that needs the fewest K stages per wave, when that beats the 64 x 64 launch; 0 to keep the
+// 64 x 64 tiles. Both end in the same reduction launch, so stages alone decide.
+static int wave_split_ln(int M, int N, int K, int split) {
+    const long tiles32 = (long)((M + 31) / 32) * ((N + 31) / 32);
+    auto chunk_stages = [&](int s) { return ((K + s - 1) / s + 31) / 32; };
+    int best = 0, best_cost = chunk_stages(split);
+    for (int s = 2; s <= split && tiles32 * s <= 2 * kCUs; ++s) {
+        const int cost = (chunk_stages(s) + 3) / 4;
+        if (cost < best_cost) {
+            best = s;
+            best_cost = cost;
+        }
+    }
+    return best;
+}
+
 // 128 x 32 tiles (four waves stacked along M) instead of 64 x 64 when they pad N less: the
 // pointwise convolutions of MobileNet-style networks have 16 to 160 output channels, where a
 // 64-wide tile leaves up to 3/4 of the matrix-core work and of the epilogue on padding. Only
@@ -1281,6 +1299,7 @@ static void gemm_launch(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const LnTai
 
     int wsk = dma_ok && !ln && g->split_k <= 0 ? wave_split(p.M, p.N, p.K, batch) : 0;
     if (wsk > 1 && (g->workspace == nullptr || g->workspace_floats < (long)wsk * p.M * p.N)) wsk = 1;
+    if (dma_ok && ln && batch == 1 && p.split >= 2) wsk = wave_split_ln(p.M, p.N, p.K, p.split);
     const bool wsplit = wsk > 0;
     if (wsplit) {
         p.split = wsk;
