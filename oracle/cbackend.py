@@ -59,7 +59,10 @@ EXPR = {"Add": "({0} + {1})", "Sub": "({0} - {1})", "Mul": "({0} * {1})", "Div":
         "Sqrt": "sqrtf({0})", "Exp": "mgc_expf({0})", "Neg": "(-{0})", "Identity": "{0}",
         "Pow": "powf({0}, {1})", "Abs": "fabsf({0})", "Reciprocal": "(1.0f / {0})"}
 
-BASELINES = {"resnet50": 1, "bottleneck": 1, "mobilenet_v2": 1, "bert_base": 1, "single_gemm": 128}
+# workload -> the batches a library is prebuilt for: batch 1 and the GPU batch of each BASELINE
+# config (the single GEMM is one call of 128 rows)
+BASELINES = {"resnet50": (1, 32), "bottleneck": (1, 32), "mobilenet_v2": (1, 32), "bert_base": (1, 16),
+             "single_gemm": (1,)}
 
 
 class CBackendError(Exception):
@@ -524,37 +527,47 @@ def compile_c(graph: Graph, out: Path) -> CModel:
     return CModel(out, graph, em.blob.bytes())
 
 
-def _baseline_graph(workload: str):
+def _baseline_graph(workload: str, batch: int):
     from ml_graph_compiler import builders
     from ml_graph_compiler.passes import optimize
     from ml_graph_compiler.schedule import schedule
 
-    g = builders.single_gemm() if workload == "single_gemm" else builders.CONFIGS[workload](batch=BASELINES[workload])
+    g = builders.single_gemm() if workload == "single_gemm" else builders.CONFIGS[workload](batch=batch)
     optimize(g, "O3")
     schedule(g)
     return g
 
 
+def baseline_path(workload: str, batch: int) -> Path:
+    return REF_OUT / f"{workload}_b{batch}_cref.so"
+
+
 def build_baselines(workloads=tuple(BASELINES)) -> list[Path]:
-    """Prebuild the per-workload C libraries into oracle/_ref (run where /root/reference is)."""
+    """Prebuild the per-workload C libraries, at every batch of BASELINES, into oracle/_ref (run
+    where /root/reference is)."""
     built = []
     REF_OUT.mkdir(exist_ok=True)
     for wl in workloads:
-        g = _baseline_graph(wl)
-        em = CEmitter(g)
-        source = em.generate()
-        lib = REF_OUT / f"{wl}_cref.so"
-        build_library(source, lib)
-        meta = {"workload": wl, "batch": BASELINES[wl], "weights_digest": blob_digest(em.blob.bytes())}
-        (REF_OUT / f"{wl}_cref.json").write_text(json.dumps(meta))
-        built.append(lib)
+        for batch in BASELINES[wl]:
+            g = _baseline_graph(wl, batch)
+            em = CEmitter(g)
+            source = em.generate()
+            lib = baseline_path(wl, batch)
+            build_library(source, lib)
+            meta = {"workload": wl, "batch": batch, "weights_digest": blob_digest(em.blob.bytes())}
+            lib.with_suffix(".json").write_text(json.dumps(meta))
+            built.append(lib)
     return built
 
 
-def load_baseline(workload: str) -> tuple[CModel, Graph, dict]:
-    lib = REF_OUT / f"{workload}_cref.so"
-    meta = json.loads((REF_OUT / f"{workload}_cref.json").read_text())
-    g = _baseline_graph(workload)
+def load_baseline(workload: str, batch: int = 1) -> tuple[CModel, Graph, dict]:
+    """A prebuilt baseline library with its O3 graph and regenerated weights. Raises
+    CBackendError (never skips) when the library was not built or its weights differ."""
+    lib = baseline_path(workload, batch)
+    if not lib.exists() or not lib.with_suffix(".json").exists():
+        raise CBackendError(f"{lib.name} is not built: run __graft_entry__.build() where /root/reference exists")
+    meta = json.loads(lib.with_suffix(".json").read_text())
+    g = _baseline_graph(workload, batch)
     em = CEmitter(g)
     em.generate()
     blob = em.blob.bytes()

@@ -70,9 +70,12 @@ def check_hip(
     opt: str = "O0",
     rtol: float = 1e-4,
     atol: float = 1e-5,
+    exact: bool = False,
 ) -> dict[str, np.ndarray]:
     """Compile ``graph`` with the hip backend at ``opt``, run it and compare every output with
-    the oracle run on the unoptimized graph; returns the hip outputs."""
+    the oracle run on the unoptimized graph; returns the hip outputs. Integer and bool outputs
+    always compare bit for bit; ``exact`` makes float outputs do so too (pure data movement:
+    Gather, Transpose, Slice, ...)."""
     expected = oracle.run_graph(graph, feeds)
     model = compile_hip(graph, cache, opt)
     try:
@@ -83,7 +86,7 @@ def check_hip(
     for name, value in expected.items():
         assert got[name].shape == value.shape, (name, got[name].shape, value.shape)
         assert got[name].dtype == value.dtype, (name, got[name].dtype, value.dtype)
-        if np.issubdtype(value.dtype, np.floating):
+        if np.issubdtype(value.dtype, np.floating) and not exact:
             np.testing.assert_allclose(got[name], value, rtol=rtol, atol=atol, err_msg=name)
         else:
             np.testing.assert_array_equal(got[name], value, err_msg=name)

@@ -54,68 +54,85 @@ def test_single_gemm(hip_cache):
     model.release()
 
 
-@pytest.mark.parametrize("batch", [1, 2])
+def _per_item_error(got: np.ndarray, expected: np.ndarray) -> np.ndarray:
+    """Max-abs error of every batch element (axis 0)."""
+    diff = np.abs(got.astype(np.float64) - np.asarray(expected, np.float64))
+    return diff.reshape(diff.shape[0], -1).max(axis=1)
+
+
+def _check_batch(label: str, got: np.ndarray, expected: np.ndarray, tol: float, top1: bool) -> np.ndarray:
+    """Every element of a batched run against the oracle run on the whole batch: max-abs per
+    element within ``tol`` and, for logits, the arg-max of every row (every image, every
+    sequence position) identical (the reference's parity harness, benchmarks/parity.py:104-125)."""
+    assert got.shape == expected.shape and got.dtype == np.float32
+    errs = _per_item_error(got, expected)
+    worst = int(np.argmax(errs))
+    print(f"[gpu] {label}: max-abs {errs.max():.3e} (element {worst} of {len(errs)}), "
+          f"max|ref| {np.abs(expected).max():.3e}", flush=True)
+    assert np.all(errs <= tol), (label, errs.tolist())
+    if top1:
+        same = np.argmax(got, axis=-1) == np.argmax(expected, axis=-1)
+        print(f"[gpu] {label}: top-1 agreement {same.mean():.4f} over {same.size} rows", flush=True)
+        assert same.all()
+    return errs
+
+
+@pytest.mark.parametrize("batch", [1, 2, 32])
 def test_bottleneck(batch, hip_cache):
+    """Config 2 at batch 1 and 32 (and 2): the batched-offset path of the implicit-GEMM
+    convolutions (reference c.py:1144-1167), every image against the oracle."""
     print(f"[gpu] bottleneck b{batch}", flush=True)
     g0 = builders.bottleneck(batch)
     feeds = oracle.random_feeds(g0, 1)
-    expected = oracle.run_graph(g0, feeds)["y"]
     model = compile_hip(builders.bottleneck(batch), hip_cache)
     got = model.run(feeds)["y"]
-    err = float(np.max(np.abs(got.astype(np.float64) - expected)))
-    print(f"[gpu] bottleneck b{batch} max-abs {err:.3e} max|ref| {np.abs(expected).max():.3e}", flush=True)
-    assert err <= 1e-4
     model.release()
-
-
-def _rel_err(got, expected):
-    err = float(np.max(np.abs(got.astype(np.float64) - expected)))
-    scale = float(np.max(np.abs(expected)))
-    return err, scale
+    expected = oracle.run_graph(g0, feeds)["y"]
+    _check_batch(f"bottleneck b{batch}", got, expected, 1e-4, top1=False)
 
 
 # ResNet-50 with random He-normal weights and BatchNorm statistics that do not renormalize grows
 # activations block by block: |logits| reach ~4e4, where one fp32 ulp is ~4e-3, so an absolute
-# 1e-4 bound is below float resolution. The bound is relative to max|logit| instead: the
-# reference's own C backend sits at ~5e-7 of max|logit| against the same oracle
-# (tests/test_oracle.py), and the hip result must stay within 1e-5 with identical top-1.
-RESNET_REL_TOL = 1e-5
+# 1e-4 bound is below float resolution. The gate is the reference's own C backend instead: run in
+# the same test on the same inputs and weights, its error against the oracle is the fp32 floor,
+# and the hip error may be at most twice that floor.
+RESNET_FLOOR_FACTOR = 2.0
 
 
 @pytest.mark.parametrize("batch", [1, 32])
 def test_resnet50(batch, hip_cache):
+    from oracle import cbackend
+
     print(f"[gpu] resnet50 b{batch}", flush=True)
     graph = builders.resnet50(batch)
     feeds = oracle.random_feeds(graph, 3)
     model = compile_hip(builders.resnet50(batch), hip_cache)
     got = model.run(feeds)["logits"]
     model.release()
-    # the oracle on every image of b1, on the first and last image of b32 (batch independence)
-    images = [0] if batch == 1 else [0, batch - 1]
-    single = builders.resnet50(1)
-    for i in images:
-        expected = oracle.run_graph(single, {"image": feeds["image"][i : i + 1]})["logits"]
-        err, scale = _rel_err(got[i : i + 1], expected)
-        print(f"[gpu] resnet50 b{batch} image {i}: max-abs {err:.3e} max|logit| {scale:.3e} "
-              f"rel {err / scale:.2e}", flush=True)
-        assert err <= RESNET_REL_TOL * scale
-        assert int(np.argmax(got[i])) == int(np.argmax(expected[0]))
+    print(f"[gpu] resnet50 b{batch}: reference C backend", flush=True)
+    cmodel, _, _ = cbackend.load_baseline("resnet50", batch)
+    cref = cmodel.run(feeds)["logits"]
+    print(f"[gpu] resnet50 b{batch}: oracle", flush=True)
+    expected = oracle.run_graph(graph, feeds)["logits"]
+    c_errs = _per_item_error(cref, expected)
+    floor = float(c_errs.max())
+    print(f"[gpu] resnet50 b{batch}: reference C backend max-abs {floor:.3e} "
+          f"(rel {floor / np.abs(expected).max():.2e})", flush=True)
+    errs = _check_batch(f"resnet50 b{batch}", got, expected, RESNET_FLOOR_FACTOR * floor, top1=True)
+    print(f"[gpu] resnet50 b{batch}: hip / C error {errs.max() / floor:.2f}", flush=True)
+    assert np.array_equal(np.argmax(cref, -1), np.argmax(expected, -1))
 
 
 @pytest.mark.parametrize("batch", [1, 32])
 def test_mobilenet_v2(batch, hip_cache):
     print(f"[gpu] mobilenet_v2 b{batch}", flush=True)
-    feeds = oracle.random_feeds(builders.mobilenet_v2(batch), 5)
+    graph = builders.mobilenet_v2(batch)
+    feeds = oracle.random_feeds(graph, 5)
     model = compile_hip(builders.mobilenet_v2(batch), hip_cache)
     got = model.run(feeds)["logits"]
     model.release()
-    single = builders.mobilenet_v2(1)
-    for i in ([0] if batch == 1 else [0, batch - 1]):
-        expected = oracle.run_graph(single, {"image": feeds["image"][i : i + 1]})["logits"]
-        err, scale = _rel_err(got[i : i + 1], expected)
-        print(f"[gpu] mobilenet_v2 b{batch} image {i}: max-abs {err:.3e} max|logit| {scale:.3e}", flush=True)
-        assert err <= 1e-4
-        assert int(np.argmax(got[i])) == int(np.argmax(expected[0]))
+    expected = oracle.run_graph(graph, feeds)["logits"]
+    _check_batch(f"mobilenet_v2 b{batch}", got, expected, 1e-4, top1=True)
 
 
 @pytest.mark.parametrize("batch", [1, 16])
@@ -126,17 +143,14 @@ def test_bert_base(batch, hip_cache):
     model = compile_hip(builders.bert_base(batch), hip_cache)
     got = model.run(feeds)["hidden"]
     model.release()
-    single = builders.bert_base(1)
-    for i in ([0] if batch == 1 else [0, batch - 1]):
-        expected = oracle.run_graph(single, {"input_ids": feeds["input_ids"][i : i + 1]})["hidden"]
-        err, scale = _rel_err(got[i : i + 1], expected)
-        print(f"[gpu] bert_base b{batch} sequence {i}: max-abs {err:.3e} max|h| {scale:.3e}", flush=True)
-        assert err <= 5e-4
+    expected = oracle.run_graph(graph, feeds)["hidden"]
+    _check_batch(f"bert_base b{batch}", got, expected, 5e-4, top1=False)
 
 
 @pytest.mark.parametrize("batch", [1, 8])
 def test_gpt2(batch, hip_cache):
-    """GPT-2 small at sequence 128: fused causal attention and the tied 50257-wide head."""
+    """GPT-2 small at sequence 128: fused causal attention and the tied 50257-wide head; the
+    next-token arg-max of every position of every sequence must agree."""
     print(f"[gpu] gpt2 b{batch}", flush=True)
     graph = builders.gpt2(batch)
     feeds = oracle.random_feeds(graph, 8, int_high=50257)
@@ -144,13 +158,8 @@ def test_gpt2(batch, hip_cache):
     assert model.report.kernels.get("attention") == 12
     got = model.run(feeds)["logits"]
     model.release()
-    single = builders.gpt2(1)
-    for i in ([0] if batch == 1 else [0, batch - 1]):
-        expected = oracle.run_graph(single, {"input_ids": feeds["input_ids"][i : i + 1]})["logits"]
-        err, scale = _rel_err(got[i : i + 1], expected)
-        print(f"[gpu] gpt2 b{batch} sequence {i}: max-abs {err:.3e} max|logit| {scale:.3e}", flush=True)
-        assert err <= 5e-4
-        assert np.array_equal(np.argmax(got[i], -1), np.argmax(expected[0], -1))
+    expected = oracle.run_graph(graph, feeds)["logits"]
+    _check_batch(f"gpt2 b{batch}", got, expected, 5e-4, top1=True)
 
 
 @pytest.mark.parametrize(
@@ -182,9 +191,7 @@ def test_wider_transformers(name, kwargs, hip_cache):
     assert kernels.get("attention") == kwargs["layers"], kernels
     assert (kernels.get("gemm_layer_norm", 0) > 0) == (kwargs["d_model"] <= 1024), kernels
     for k, want in expected.items():
-        err, scale = _rel_err(got[k], want)
-        print(f"[gpu] {name} {k}: max-abs {err:.3e} max|ref| {scale:.3e}", flush=True)
-        assert err <= 5e-4
+        _check_batch(f"{name} {k}", got[k], want, 5e-4, top1=False)
 
 
 def test_gather_out_of_range_raises(hip_cache):

@@ -149,7 +149,53 @@ def test_integer_clip(hip_cache):
 )
 def test_data_movement_and_reductions(op, inputs, const, attrs, hip_cache):
     g, feeds = op_graph(op, inputs, const=const, attrs=attrs)
-    check_hip(g, feeds, hip_cache)
+    check_hip(g, feeds, hip_cache, exact=op in COPY_OPS)
+
+
+# operators that only move data: their outputs must equal the oracle's bit for bit
+COPY_OPS = {"Transpose", "Expand", "Tile", "Slice", "Concat", "Pad", "Gather", "Shape", "Size", "ConstantOfShape",
+            "Flatten", "Unsqueeze", "Squeeze", "Identity", "ReduceMax", "ReduceMin", "ArgMax"}
+
+
+@pytest.mark.parametrize(
+    "table, indices, axis, const_table",
+    [
+        # the embedding lookup of BERT-base: a [30522, 768] table and [2, 128] int64 ids with
+        # negative ids counting from the end (reference ops.py:596-603 wraps them)
+        ("f32", (30522, 768), 0, True),
+        ("f32", (10, 4), 0, False),
+        ("f32", (3, 10, 2), 1, True),
+        ("f32", (2, 3, 11), 2, False),
+        ("f32", (2, 3, 11), -1, False),
+        ("i64", (50, 6), 0, True),       # an int64 table, gathered rows of 48 bytes
+        ("i64", (4, 50), 1, False),
+        ("i32", (7, 9, 3), 1, False),
+        ("f32", (9, 5), 0, False),       # a scalar index: the axis disappears
+    ],
+)
+@pytest.mark.parametrize("index_dtype", [np.int64, np.int32])
+def test_gather_bit_exact(table, indices, axis, const_table, index_dtype, hip_cache):
+    """Gather is a pure copy: every output bit equals the oracle's (np.take), for float32,
+    int64 and int32 tables, int64 and int32 indices, negative indices, every axis."""
+    shape = indices
+    if table == "f32":
+        data = (rng.standard_normal(shape) * 1e3).astype(np.float32)
+        data.flat[:: max(1, data.size // 7)] = np.float32(np.nan)   # NaN payloads copy unchanged
+    elif table == "i64":
+        data = rng.integers(-(2**62), 2**62, shape, dtype=np.int64)
+    else:
+        data = rng.integers(-(2**31), 2**31 - 1, shape, dtype=np.int64).astype(np.int32)
+    dim = shape[axis]
+    if shape == (9, 5):
+        idx = np.asarray(-3, index_dtype)
+    elif shape == (30522, 768):
+        idx = rng.integers(-dim, dim, (2, 128)).astype(index_dtype)
+    else:
+        idx = rng.integers(-dim, dim, (3, 4)).astype(index_dtype)
+    g, feeds = op_graph("Gather", [data, idx], const={0} if const_table else set(), attrs={"axis": axis})
+    got = check_hip(g, feeds, hip_cache, exact=True)
+    want = np.take(data, np.where(idx < 0, idx + dim, idx), axis=axis)
+    assert got["out0"].tobytes() == want.tobytes()
 
 
 def test_split_and_dropout(hip_cache):
