@@ -130,6 +130,21 @@ void mgc_hip_gemm(mgc_hip_exec *x, const mgc_hip_gemm_args *g);
  * at compile time and reserves it through the memory planner's workspace hook. */
 long mgc_hip_gemm_workspace(int M, int N, int K, int batch);
 
+/* Floats of device scratch the library holds per GPU for mgc_hip_gemm_noalloc (32 MiB). */
+#define MGC_HIP_NOALLOC_SCRATCH_FLOATS (1L << 23)
+
+/* mgc_hip_gemm for callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc). No counterpart in the reference: its C
+ * backend allocates nothing to begin with. Computes exactly what mgc_hip_gemm computes with a
+ * sufficient workspace, but keeps the K-split partials in the library's own per-GPU device
+ * array of MGC_HIP_NOALLOC_SCRATCH_FLOATS floats: g->workspace and g->workspace_floats are
+ * ignored, and the call allocates nothing. `stream` is a hipStream_t (NULL = the null stream);
+ * the call only enqueues work. Returns MGC_OK, MGC_ERR_ARGS (no arguments, or a GEMM whose
+ * K split needs more than MGC_HIP_NOALLOC_SCRATCH_FLOATS floats; see mgc_hip_last_error) or
+ * MGC_ERR_HIP (launch or runtime failure). Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (different streams without ordering) race on it. */
+int mgc_hip_gemm_noalloc(void *stream, const mgc_hip_gemm_args *g);
+
 /* A GEMM (batch_rank 0) whose output rows then go through a LayerNorm: out = LayerNorm(C) with
  * C = act(alpha A B + bias + beta R) as mgc_hip_gemm computes it. K is always split (at least
  * in two) and the split-K reduction applies the epilogue, stores C when g->c is not NULL and

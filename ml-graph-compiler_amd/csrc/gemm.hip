@@ -28,6 +28,10 @@
 //  * Tiles are 64 x 64 (see choose_tiles); K is split over extra workgroups into a
 //    planner-provided workspace when the tiles alone cannot balance the CUs, and a reduction
 //    then applies the epilogue.
+#include <stdio.h>
+
+#include <mutex>
+
 #include "mgc_device.h"
 
 namespace mgc {
@@ -1167,6 +1171,83 @@ static int ln_split(int M, int N, int K) {
 static void gemm_launch(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const LnTail *ln);
 
 extern "C" void mgc_hip_gemm(mgc_hip_exec *x, const mgc_hip_gemm_args *g) { gemm_launch(x, g, nullptr); }
+
+// ---------------------------------------------------------------------------------------------
+// mgc_hip_gemm_noalloc: mgc_hip_gemm with the K-split partials in the library's own device
+// array instead of a caller workspace, for callers that cannot allocate device memory.
+//
+// `scratch` is a file-scope device array; every GPU the library runs on holds its own copy
+// (MGC_HIP_NOALLOC_SCRATCH_FLOATS floats) until the process ends. Host code never passes the
+// array's name to a kernel (on the host it is only a stand-in symbol): the first call on a
+// device, with that device current, asks the runtime for that device's address of the array
+// and keeps it; kernels get that pointer. Every call on a GPU shares its array, so calls that
+// overlap on one GPU (different streams, or threads without ordering) race on it; calls on one
+// stream are ordered and safe. Nothing in it must start at zero: each K split writes its whole
+// partial tile (zeros for an empty K range) before the reduction reads it.
+static __device__ __align__(256) float scratch[MGC_HIP_NOALLOC_SCRATCH_FLOATS];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+float *g_scratch_ptr[kMaxDevices] = {};
+
+// This device's address of `scratch`, looked up once per device (with the device current).
+hipError_t scratch_for_current_device(float **out) {
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return err;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void *ptr = nullptr;
+        err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (err != hipSuccess) return err;
+        g_scratch_ptr[dev] = static_cast<float *>(ptr);
+    }
+    *out = g_scratch_ptr[dev];
+    return hipSuccess;
+}
+}  // namespace
+
+extern "C" int mgc_hip_gemm_noalloc(void *stream, const mgc_hip_gemm_args *g) {
+    if (!g) {
+        set_error("mgc_hip_gemm_noalloc: no arguments", hipErrorInvalidValue);
+        return MGC_ERR_ARGS;
+    }
+    int batch = 1;
+    for (int d = 0; d < g->batch_rank && d < 4; ++d) batch *= g->batch_dims[d];
+    // the partials this call needs: the split mgc_hip_gemm takes when its workspace allows
+    // (the wave-split kernel's own K split never needs more), or the caller's explicit split
+    long need = 0;
+    if (g->M > 0 && g->N > 0 && g->K > 0 && batch > 0) {
+        if (g->split_k > 1 && batch == 1)
+            need = (long)g->split_k * g->M * g->N;
+        else if (g->split_k <= 0)
+            need = mgc_hip_gemm_workspace(g->M, g->N, g->K, batch);
+    }
+    if (need > MGC_HIP_NOALLOC_SCRATCH_FLOATS) {
+        char msg[200];
+        snprintf(msg, sizeof msg,
+                 "mgc_hip_gemm_noalloc: this GEMM needs %ld floats of K-split scratch, more than "
+                 "the %ld the library holds",
+                 need, (long)MGC_HIP_NOALLOC_SCRATCH_FLOATS);
+        set_error(msg, hipErrorInvalidValue);
+        return MGC_ERR_ARGS;
+    }
+    float *ws = nullptr;
+    const hipError_t err = scratch_for_current_device(&ws);
+    if (err != hipSuccess) {
+        set_error("mgc_hip_gemm_noalloc: hipGetSymbolAddress(scratch)", err);
+        return MGC_ERR_HIP;
+    }
+    mgc_hip_gemm_args a = *g;
+    a.workspace = ws;
+    a.workspace_floats = MGC_HIP_NOALLOC_SCRATCH_FLOATS;
+    mgc_hip_exec x{};
+    x.stream = static_cast<hipStream_t>(stream);
+    gemm_launch(&x, &a, nullptr);
+    return x.launch_error ? MGC_ERR_HIP : MGC_OK;
+}
 
 extern "C" int mgc_hip_gemm_layer_norm_supported(int M, int N) {
     return M >= 1 && M < (1 << 25) && N >= 4 && N % 4 == 0 && N <= 1024;

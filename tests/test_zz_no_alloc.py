@@ -1,0 +1,165 @@
+"""mgc_hip_gemm_noalloc against mgc_hip_gemm, both through the C ABI.
+
+mgc_hip_gemm_noalloc keeps its K-split partials in the library's own per-GPU device array
+instead of a caller workspace. The existing entry point, mgc_hip_gemm, runs inside a compiled
+model (the emitter's call, with the planner's workspace); the new one is called directly with
+device buffers this test allocates for the operands (the caller still owns inputs and outputs).
+Two calls in a row on the same GPU, the second with a smaller input, must each match the
+compiled model bit for bit (same kernels, same K split) and the oracle within the single-GEMM
+tolerance (1e-4 max-abs). A GEMM whose K split needs more than the scratch holds is rejected.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from ml_graph_compiler.codegen import compile_graph
+from ml_graph_compiler.codegen.build import load_kernel_library
+from ml_graph_compiler.ir import Graph, TensorType
+from ml_graph_compiler.passes import optimize
+from ml_graph_compiler.schedule import schedule
+from ml_graph_compiler.shape_inference import infer_shapes
+from oracle import interpreter as oracle
+
+pytestmark = pytest.mark.gpu
+
+MGC_OP_STRIDED, MGC_ACT_RELU = 0, 1
+MGC_OK, MGC_ERR_ARGS = 0, 3
+SCRATCH_FLOATS = 1 << 23
+
+
+class Operand(ctypes.Structure):
+    _fields_ = [("kind", ctypes.c_int), ("p", ctypes.c_void_p), ("rs", ctypes.c_long), ("cs", ctypes.c_long)] + [
+        (n, ctypes.c_int) for n in ("H", "W", "C", "KH", "KW", "SH", "SW", "DH", "DW", "PT", "PL", "OH", "OW", "cg")
+    ]
+
+
+class GemmArgs(ctypes.Structure):
+    """mgc_hip_gemm_args (include/mgc_hip.h)."""
+
+    _fields_ = [
+        ("M", ctypes.c_int), ("N", ctypes.c_int), ("K", ctypes.c_int),
+        ("a", Operand), ("b", Operand),
+        ("c", ctypes.c_void_p), ("ldc", ctypes.c_long),
+        ("alpha", ctypes.c_float), ("beta", ctypes.c_float),
+        ("bias", ctypes.c_void_p), ("bias_mode", ctypes.c_int),
+        ("res", ctypes.c_void_p), ("ldr", ctypes.c_long),
+        ("act", ctypes.c_int), ("lo", ctypes.c_float), ("hi", ctypes.c_float),
+        ("batch_rank", ctypes.c_int), ("batch_dims", ctypes.c_int * 4),
+        ("a_bs", ctypes.c_long * 4), ("b_bs", ctypes.c_long * 4), ("c_bs", ctypes.c_long * 4), ("r_bs", ctypes.c_long * 4),
+        ("workspace", ctypes.c_void_p), ("workspace_floats", ctypes.c_long),
+        ("split_k", ctypes.c_int),
+    ]
+
+
+class Hip:
+    """The few HIP runtime calls the test needs for its own operand buffers."""
+
+    def __init__(self) -> None:
+        self.lib = ctypes.CDLL("libamdhip64.so.7", mode=ctypes.RTLD_GLOBAL)  # the runtime libmgc_hip.so links
+        self.lib.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+        self.lib.hipFree.argtypes = [ctypes.c_void_p]
+        self.lib.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+        self.buffers: list[ctypes.c_void_p] = []
+
+    def check(self, code: int, what: str) -> None:
+        assert code == 0, f"{what} failed with {code}"
+
+    def upload(self, array: np.ndarray) -> int:
+        array = np.ascontiguousarray(array)
+        ptr = ctypes.c_void_p()
+        self.check(self.lib.hipMalloc(ctypes.byref(ptr), max(array.nbytes, 4)), "hipMalloc")
+        self.buffers.append(ptr)
+        self.check(self.lib.hipMemcpy(ptr, array.ctypes.data, array.nbytes, 1), "hipMemcpy H2D")
+        return ptr.value
+
+    def empty(self, nbytes: int) -> int:
+        return self.upload(np.full(nbytes // 4, np.nan, np.float32))
+
+    def download(self, ptr: int, shape, dtype=np.float32) -> np.ndarray:
+        out = np.empty(shape, dtype)
+        self.check(self.lib.hipDeviceSynchronize(), "hipDeviceSynchronize")
+        self.check(self.lib.hipMemcpy(out.ctypes.data, ctypes.c_void_p(ptr), out.nbytes, 2), "hipMemcpy D2H")
+        return out
+
+    def free(self) -> None:
+        for ptr in self.buffers:
+            self.lib.hipFree(ptr)
+        self.buffers.clear()
+
+
+def _graph(m: int, n: int, k: int, seed: int):
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((k, n)) / np.sqrt(k)).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32)
+    g = Graph("noalloc_ref")
+    x = g.add_input("x", TensorType("float32", (m, k)))
+    y = g.add_node("MatMul", [x, g.constant(w, "w")], 1, {}, name="mm").output
+    y = g.add_node("Add", [y, g.constant(bias, "b")], 1, {}, name="bias").output
+    y = g.add_node("Relu", [y], 1, {}, name="relu").output
+    g.add_output(y, "y")
+    infer_shapes(g)
+    feeds = {"x": rng.standard_normal((m, k)).astype(np.float32)}
+    return g, w, bias, feeds
+
+
+def _noalloc(lib, hip: Hip, m: int, n: int, k: int, x: np.ndarray, w: np.ndarray, bias: np.ndarray,
+             split_k: int = 0) -> tuple[int, np.ndarray | None]:
+    args = GemmArgs()
+    args.M, args.N, args.K = m, n, k
+    args.a = Operand(kind=MGC_OP_STRIDED, p=hip.upload(x), rs=k, cs=1)
+    # B stored [N][K] (k contiguous), the layout the emitter packs constant weights in
+    args.b = Operand(kind=MGC_OP_STRIDED, p=hip.upload(np.ascontiguousarray(w.T)), rs=1, cs=k)
+    c = hip.empty(m * n * 4)
+    args.c, args.ldc = c, n
+    args.alpha, args.beta = 1.0, 1.0
+    args.bias, args.bias_mode = hip.upload(bias), 1
+    args.act, args.lo, args.hi = MGC_ACT_RELU, 0.0, 6.0
+    args.split_k = split_k
+    code = lib.mgc_hip_gemm_noalloc(None, ctypes.byref(args))
+    return code, (hip.download(c, (m, n)) if code == MGC_OK else None)
+
+
+def test_noalloc_gemm_matches_mgc_hip_gemm(hip_cache):
+    lib = load_kernel_library()
+    lib.mgc_hip_gemm_noalloc.restype = ctypes.c_int
+    lib.mgc_hip_gemm_noalloc.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    lib.mgc_hip_gemm_workspace.restype = ctypes.c_long
+    lib.mgc_hip_gemm_workspace.argtypes = [ctypes.c_int] * 4
+    lib.mgc_hip_last_error.restype = ctypes.c_char_p
+    hip = Hip()
+    try:
+        # two calls in a row, the second smaller; both shapes split K (the scratch holds
+        # partials of the first when the second runs)
+        for m, n, k, seed in ((256, 1024, 4096, 1), (64, 768, 3072, 2)):
+            need = int(lib.mgc_hip_gemm_workspace(m, n, k, 1))
+            print(f"[gpu] noalloc GEMM {m}x{n}x{k}: K-split scratch {need} floats", flush=True)
+            assert 0 < need <= SCRATCH_FLOATS
+            g, w, bias, feeds = _graph(m, n, k, seed)
+            expected = oracle.run_graph(g, feeds)["y"]
+            optimize(g, "O3")
+            schedule(g)
+            model = compile_graph(g, cache_dir=hip_cache, name=f"noalloc_ref_{m}")
+            try:
+                want = model.run(feeds)["y"]
+            finally:
+                model.release()
+            code, got = _noalloc(lib, hip, m, n, k, feeds["x"], w, bias)
+            assert code == MGC_OK, lib.mgc_hip_last_error()
+            err = float(np.max(np.abs(got.astype(np.float64) - expected)))
+            same = bool(np.array_equal(got, want))
+            print(f"[gpu] noalloc {m}x{n}x{k}: max-abs vs oracle {err:.3e}, identical to mgc_hip_gemm: {same}",
+                  flush=True)
+            assert err <= 1e-4
+            np.testing.assert_array_equal(got, want)
+        # an explicit split whose partials exceed the scratch is refused, before any launch
+        m, n, k = 2048, 4096, 256
+        code, _ = _noalloc(lib, hip, m, n, k, np.zeros((m, k), np.float32), np.zeros((k, n), np.float32),
+                           np.zeros(n, np.float32), split_k=2)
+        assert code == MGC_ERR_ARGS
+        assert b"more than" in lib.mgc_hip_last_error()
+    finally:
+        hip.free()
