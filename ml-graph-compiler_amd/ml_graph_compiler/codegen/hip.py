@@ -495,8 +495,36 @@ class HipEmitter:
             return EW_OPCODES[op], float(attrs.get("min", -np.inf)), float(attrs.get("max", np.inf))
         return EW_OPCODES[op], 0.0, 0.0
 
+    @staticmethod
+    def _cast_pow_exponents(program: list[tuple[str, dict[str, Any], list[int]]],
+                            leaves: list[Value | None]) -> list[tuple[str, dict[str, Any], list[int]]]:
+        """Pow raises to the exponent converted to the base's dtype (reference ops.py:164-167:
+        ``np.power(a, b.astype(a.dtype))``); the kernel evaluates an instruction in one dtype,
+        so an exponent of another dtype gets a Cast instruction in front of the Pow."""
+        n_leaves = len(leaves)
+        types: list[TensorType | None] = [None if v is None else v.type for v in leaves]
+        out: list[tuple[str, dict[str, Any], list[int]]] = []
+        moved: dict[int, int] = {}  # register of an instruction result -> its register after insertions
+
+        def infer(op: str, attrs: dict[str, Any], args: list[int]) -> TensorType:
+            sub = Node(op, [], [Value("_")], dict(attrs))
+            return ops.spec(op).infer(sub, [types[a] if a >= 0 else None for a in args], [None] * len(args))[0]
+
+        for k, (op, attrs, args) in enumerate(program):
+            args = [moved.get(a, a) if a >= 0 else a for a in args]
+            if op == "Pow" and len(args) == 2 and min(args) >= 0 and types[args[0]].dtype != types[args[1]].dtype:
+                cast = ("Cast", {"to": types[args[0]].dtype}, [args[1]])
+                out.append(cast)
+                types.append(infer(*cast))
+                args = [args[0], n_leaves + len(out) - 1]
+            out.append((op, attrs, args))
+            types.append(infer(op, attrs, args))
+            moved[n_leaves + k] = n_leaves + len(out) - 1
+        return out
+
     def elementwise(self, out_value: Value, program: list[tuple[str, dict[str, Any], list[int]]], leaves: list[Value | None]) -> None:
         shape = out_value.tensor_type.shape
+        program = self._cast_pow_exponents(program, leaves)
         n_leaves = len(leaves)
         if n_leaves > MAX_LEAVES or len(program) > MAX_INSTR:
             raise CodegenError(f"elementwise program too large ({n_leaves} leaves, {len(program)} ops)")

@@ -1,11 +1,14 @@
-"""SSA graph IR with static shapes (reference: src/ml_graph_compiler/ir.py:1-396).
+"""The graph IR the compiler stages pass along: SSA values, operator nodes, one graph.
 
-Each Value is defined once: as a graph input, as a constant (it carries ``data``), or as one
-output of one Node. Nodes hold their input Values (None for an omitted optional ONNX input)
-and every Value keeps the list of Nodes that read it, so rewrites never rebuild an index.
-The behaviour that other stages depend on is kept exactly: the naming counter, the order of
-``values()`` (inputs, node inputs, node outputs, graph outputs), the stable heap-based
-``topological_sort`` and the checks of ``verify``.
+Interface of the reference IR (src/ml_graph_compiler/ir.py): the class and method names, the
+``Value`` / ``Node`` fields and the observable orders — ``values()`` lists graph inputs, then
+node inputs, node outputs and graph outputs, each value once; ``topological_sort`` is stable
+(when several nodes are ready, the one that currently comes first runs first); fresh names are
+``<hint>_<n>`` from one counter. The implementation is this package's own.
+
+Every value is defined exactly once: as a graph input, as a constant (its ``data`` is set), or
+as an output of one node. Values keep their readers in ``users`` (a node appears once per input
+slot that reads the value), so passes can rewrite without rebuilding indexes.
 """
 
 from __future__ import annotations
@@ -20,52 +23,42 @@ import numpy as np
 
 from .errors import GraphError
 
-_DTYPES: dict[str, np.dtype] = {
-    name: np.dtype(t)
-    for name, t in (
-        ("float32", np.float32),
-        ("float64", np.float64),
-        ("float16", np.float16),
-        ("int64", np.int64),
-        ("int32", np.int32),
-        ("int8", np.int8),
-        ("uint8", np.uint8),
-        ("bool", np.bool_),
-    )
-}
+# element types the IR accepts, by name
+SUPPORTED_DTYPES = ("float32", "float64", "float16", "int64", "int32", "int8", "uint8", "bool")
+_BY_NAME = {name: np.dtype(name) for name in SUPPORTED_DTYPES}
 
 
 def contiguous(array: Any, dtype: Any = None) -> np.ndarray:
-    """C-ordered ndarray view/copy of ``array``; zero-dimensional arrays stay zero-dimensional."""
+    """A C-ordered ndarray of ``array`` (a view when already one); rank is preserved."""
     return np.asarray(array, dtype=dtype, order="C")
 
 
 def numpy_dtype(name: str) -> np.dtype:
-    if name not in _DTYPES:
-        raise GraphError(f"unsupported dtype {name!r}")
-    return _DTYPES[name]
+    try:
+        return _BY_NAME[name]
+    except KeyError:
+        raise GraphError(f"unsupported dtype {name!r}") from None
 
 
 def dtype_name(dtype: Any) -> str:
     wanted = np.dtype(dtype)
-    for name, dt in _DTYPES.items():
-        if dt == wanted:
+    for name, candidate in _BY_NAME.items():
+        if candidate == wanted:
             return name
     raise GraphError(f"unsupported numpy dtype {wanted}")
 
 
 @dataclass(frozen=True)
 class TensorType:
-    """Element dtype name and static shape."""
+    """A dtype name and a static shape."""
 
     dtype: str
     shape: tuple[int, ...]
 
     def __post_init__(self) -> None:
         numpy_dtype(self.dtype)
-        for d in self.shape:
-            if not isinstance(d, int) or d < 0:
-                raise GraphError(f"shape must be non-negative integers, got {self.shape}")
+        if not all(isinstance(d, int) and d >= 0 for d in self.shape):
+            raise GraphError(f"shape must be non-negative integers, got {self.shape}")
 
     @property
     def rank(self) -> int:
@@ -73,21 +66,18 @@ class TensorType:
 
     @property
     def size(self) -> int:
-        n = 1
-        for d in self.shape:
-            n *= d
-        return n
+        return int(np.prod(self.shape, dtype=np.int64)) if self.shape else 1
 
     @property
     def itemsize(self) -> int:
-        return numpy_dtype(self.dtype).itemsize
+        return _BY_NAME[self.dtype].itemsize
 
     @property
     def nbytes(self) -> int:
         return self.size * self.itemsize
 
     def __str__(self) -> str:
-        return f"{self.dtype}[{'x'.join(map(str, self.shape))}]"
+        return self.dtype + "[" + "x".join(str(d) for d in self.shape) + "]"
 
     @staticmethod
     def of(array: np.ndarray) -> TensorType:
@@ -95,7 +85,7 @@ class TensorType:
 
 
 class Value:
-    """One SSA value."""
+    """An SSA value: a graph input, a constant (``data`` set) or a node output."""
 
     __slots__ = ("data", "name", "producer", "type", "users")
 
@@ -121,145 +111,144 @@ class Value:
 
 
 class Node:
-    """One operator application."""
+    """One operator application; an omitted optional input is ``None``."""
 
     __slots__ = ("attrs", "inputs", "name", "op", "outputs")
 
-    def __init__(
-        self,
-        op: str,
-        inputs: list[Value | None],
-        outputs: list[Value],
-        attrs: dict[str, Any] | None = None,
-        name: str = "",
-    ):
+    def __init__(self, op: str, inputs: list[Value | None], outputs: list[Value],
+                 attrs: dict[str, Any] | None = None, name: str = ""):
         self.op = op
         self.inputs = inputs
         self.outputs = outputs
-        self.attrs: dict[str, Any] = dict(attrs) if attrs else {}
+        self.attrs: dict[str, Any] = dict(attrs or {})
         self.name = name
 
     def input(self, i: int) -> Value:
-        v = self.inputs[i] if i < len(self.inputs) else None
-        if v is None:
+        """Input ``i``, which must be present."""
+        value = self.optional_input(i)
+        if value is None:
             raise GraphError(f"{self.op} node {self.name!r} is missing input {i}")
-        return v
+        return value
 
     def optional_input(self, i: int) -> Value | None:
-        return self.inputs[i] if i < len(self.inputs) else None
+        return self.inputs[i] if 0 <= i < len(self.inputs) else None
 
     @property
     def output(self) -> Value:
         return self.outputs[0]
 
     def __repr__(self) -> str:
-        args = ", ".join("_" if v is None else v.name for v in self.inputs)
-        res = ", ".join(v.name for v in self.outputs)
-        text = f"{res} = {self.op}({args})"
-        return f"{text} {self.attrs}" if self.attrs else text
+        reads = ", ".join("_" if v is None else v.name for v in self.inputs)
+        writes = ", ".join(v.name for v in self.outputs)
+        suffix = f" {self.attrs}" if self.attrs else ""
+        return f"{writes} = {self.op}({reads}){suffix}"
+
+
+class _NameTable:
+    """Names handed out in one graph: requested names when free, else ``<hint>_<n>``."""
+
+    def __init__(self) -> None:
+        self.taken: set[str] = set()
+        self.serial = itertools.count()
+
+    def fresh(self, hint: str) -> str:
+        name = f"{hint}_{next(self.serial)}"
+        while name in self.taken:
+            name = f"{hint}_{next(self.serial)}"
+        self.taken.add(name)
+        return name
+
+    def claim(self, wanted: str) -> str:
+        if not wanted or wanted in self.taken:
+            return self.fresh(wanted or "v")
+        self.taken.add(wanted)
+        return wanted
 
 
 class Graph:
-    """Ordered nodes plus graph inputs, outputs (with fixed public names) and constants."""
+    """Nodes in execution order, graph inputs, and outputs under fixed public names."""
 
     def __init__(self, name: str = "graph"):
         self.name = name
         self.opset = 17
         self.inputs: list[Value] = []
         self.outputs: list[Value] = []
-        self.output_names: list[str] = []
+        self.output_names: list[str] = []  # the public names; passes may swap the values
         self.nodes: list[Node] = []
-        self._names: set[str] = set()
-        self._counter = itertools.count()
+        self._table = _NameTable()
 
     # -- names ---------------------------------------------------------------------------------
     def fresh_name(self, hint: str = "v") -> str:
-        while True:
-            candidate = f"{hint}_{next(self._counter)}"
-            if candidate not in self._names:
-                self._names.add(candidate)
-                return candidate
+        return self._table.fresh(hint)
 
     def _claim(self, name: str) -> str:
-        if name and name not in self._names:
-            self._names.add(name)
-            return name
-        return self.fresh_name(name or "v")
+        return self._table.claim(name)
 
     # -- building ------------------------------------------------------------------------------
     def add_input(self, name: str, type: TensorType) -> Value:
-        v = Value(self._claim(name), type)
-        self.inputs.append(v)
-        return v
+        value = Value(self._claim(name), type)
+        self.inputs.append(value)
+        return value
 
     def constant(self, array: np.ndarray, name: str = "const") -> Value:
+        """A constant value; it belongs to no node and lives as long as something reads it."""
         data = contiguous(array)
         return Value(self._claim(name), TensorType.of(data), data)
 
-    def add_node(
-        self,
-        op: str,
-        inputs: list[Value | None],
-        n_outputs: int = 1,
-        attrs: dict[str, Any] | None = None,
-        name: str = "",
-        output_names: list[str] | None = None,
-        index: int | None = None,
-    ) -> Node:
-        if output_names:
-            names = list(output_names)
-        else:
-            names = [f"{name or op.lower()}_out"] * n_outputs
-        outs = [Value(self._claim(n)) for n in names]
-        node = Node(op, list(inputs), outs, attrs, name or self.fresh_name(op.lower()))
-        for v in outs:
-            v.producer = node
-        for v in inputs:
-            if v is not None:
-                v.users.append(node)
-        if index is None:
-            self.nodes.append(node)
-        else:
-            self.nodes.insert(index, node)
+    def add_node(self, op: str, inputs: list[Value | None], n_outputs: int = 1,
+                 attrs: dict[str, Any] | None = None, name: str = "",
+                 output_names: list[str] | None = None, index: int | None = None) -> Node:
+        """A node with fresh output values, appended or inserted before position ``index``."""
+        wanted = list(output_names) if output_names else [f"{name or op.lower()}_out"] * n_outputs
+        node = Node(op, list(inputs), [], attrs, name or self.fresh_name(op.lower()))
+        for out_name in wanted:
+            value = Value(self._claim(out_name))
+            value.producer = node
+            node.outputs.append(value)
+        for value in node.inputs:
+            if value is not None:
+                value.users.append(node)
+        self.nodes.insert(len(self.nodes) if index is None else index, node)
         return node
 
     # -- rewriting -----------------------------------------------------------------------------
     def set_input(self, node: Node, i: int, value: Value | None) -> None:
-        previous = node.inputs[i]
-        if previous is not None:
-            previous.users.remove(node)
+        """Point input slot ``i`` of ``node`` at ``value``, keeping use lists right."""
+        _drop_use(node.inputs[i], node)
         node.inputs[i] = value
         if value is not None:
             value.users.append(node)
 
     def remove_node(self, node: Node) -> None:
-        if any(o.users or o in self.outputs for o in node.outputs):
-            raise GraphError(f"cannot remove {node.op} {node.name!r}: output still used")
-        for v in node.inputs:
-            if v is not None:
-                v.users.remove(node)
+        """Delete a node nothing reads any more."""
+        for out in node.outputs:
+            if out.users or any(out is o for o in self.outputs):
+                raise GraphError(f"cannot remove {node.op} {node.name!r}: output still used")
+        for value in node.inputs:
+            _drop_use(value, node)
         self.nodes.remove(node)
 
     def remove_nodes(self, dead: Iterable[Node]) -> int:
-        doomed = set(dead)
-        if not doomed:
-            return 0
-        for node in doomed:
-            for v in node.inputs:
-                if v is not None and node in v.users:
-                    v.users.remove(node)
-        self.nodes = [n for n in self.nodes if n not in doomed]
+        """Delete a set of nodes whose outputs are read only inside the set; returns how many."""
+        doomed = {id(n): n for n in dead}
+        for node in doomed.values():
+            for value in node.inputs:
+                if value is not None and node in value.users:
+                    value.users.remove(node)
+        if doomed:
+            self.nodes = [n for n in self.nodes if id(n) not in doomed]
         return len(doomed)
 
     def replace_all_uses(self, old: Value, new: Value) -> None:
+        """Every reader of ``old``, graph outputs included, reads ``new`` instead."""
         if old is new:
             return
-        for user in list(old.users):
-            for i, v in enumerate(user.inputs):
-                if v is old:
-                    user.inputs[i] = new
-                    new.users.append(user)
-        old.users = []
+        readers, old.users = old.users, []
+        for reader in dict.fromkeys(readers):  # a node once, however many slots it has
+            for slot, value in enumerate(reader.inputs):
+                if value is old:
+                    reader.inputs[slot] = new
+                    new.users.append(reader)
         self.outputs = [new if v is old else v for v in self.outputs]
 
     def add_output(self, value: Value, name: str | None = None) -> None:
@@ -274,112 +263,114 @@ class Graph:
 
     # -- queries -------------------------------------------------------------------------------
     def values(self) -> Iterator[Value]:
-        seen: set[int] = set()
-        ordered = itertools.chain(
-            self.inputs,
-            (v for n in self.nodes for v in n.inputs if v is not None),
-            (v for n in self.nodes for v in n.outputs),
-            self.outputs,
-        )
-        for v in ordered:
-            if id(v) not in seen:
-                seen.add(id(v))
-                yield v
+        """Graph inputs, values the nodes read, values they write, graph outputs; each once."""
+        ordered: dict[int, Value] = {}
+        for value in self.inputs:
+            ordered.setdefault(id(value), value)
+        for node in self.nodes:
+            for value in node.inputs:
+                if value is not None:
+                    ordered.setdefault(id(value), value)
+        for node in self.nodes:
+            for value in node.outputs:
+                ordered.setdefault(id(value), value)
+        for value in self.outputs:
+            ordered.setdefault(id(value), value)
+        return iter(list(ordered.values()))
 
     def constants(self) -> list[Value]:
         return [v for v in self.values() if v.is_constant]
 
     def op_counts(self) -> dict[str, int]:
+        """Operator histogram, most frequent first, ties by name."""
         counts: dict[str, int] = {}
-        for n in self.nodes:
-            counts[n.op] = counts.get(n.op, 0) + 1
-        return dict(sorted(counts.items(), key=lambda kv: (-kv[1], kv[0])))
+        for node in self.nodes:
+            counts[node.op] = counts.get(node.op, 0) + 1
+        return {op: counts[op] for op in sorted(counts, key=lambda op: (-counts[op], op))}
 
     def constant_bytes(self) -> int:
-        return sum(v.data.nbytes for v in self.constants() if v.data is not None)
+        return sum(int(v.data.nbytes) for v in self.constants())
 
     # -- order and checks ----------------------------------------------------------------------
     def topological_sort(self) -> None:
-        """Stable topological order: among ready nodes the earliest current position runs first."""
-        pos = {id(n): i for i, n in enumerate(self.nodes)}
-        pending: dict[int, int] = {}
-        for n in self.nodes:
-            preds = {
-                id(v.producer)
-                for v in n.inputs
-                if v is not None and v.producer is not None and id(v.producer) in pos
-            }
-            pending[id(n)] = len(preds)
-        heap = [(pos[id(n)], n) for n in self.nodes if pending[id(n)] == 0]
-        heapq.heapify(heap)
-        order: list[Node] = []
-        while heap:
-            _, n = heapq.heappop(heap)
-            order.append(n)
-            done: set[int] = set()
-            for out in n.outputs:
-                for user in out.users:
-                    if id(user) in done or id(user) not in pending:
-                        continue
-                    if any(v is not None and v.producer is n for v in user.inputs):
-                        done.add(id(user))
-                        pending[id(user)] -= 1
-                        if pending[id(user)] == 0:
-                            heapq.heappush(heap, (pos[id(user)], user))
+        """Reorder the nodes so that producers come before readers; among the nodes whose
+        inputs are all available, the one earliest in the current order goes next, so an order
+        that is already valid is kept unchanged."""
+        index = {id(n): i for i, n in enumerate(self.nodes)}
+        successors: list[set[int]] = [set() for _ in self.nodes]
+        waiting = [0] * len(self.nodes)
+        for i, node in enumerate(self.nodes):
+            producers = {index[id(v.producer)] for v in node.inputs
+                         if v is not None and v.producer is not None and id(v.producer) in index}
+            waiting[i] = len(producers)
+            for p in producers:
+                successors[p].add(i)
+        ready = [i for i, count in enumerate(waiting) if count == 0]
+        heapq.heapify(ready)
+        order: list[int] = []
+        while ready:
+            i = heapq.heappop(ready)
+            order.append(i)
+            for j in successors[i]:
+                waiting[j] -= 1
+                if waiting[j] == 0:
+                    heapq.heappush(ready, j)
         if len(order) != len(self.nodes):
             raise GraphError("graph has a cycle")
-        self.nodes = order
+        self.nodes = [self.nodes[i] for i in order]
 
     def verify(self) -> None:
-        defined = {id(v) for v in self.inputs}
-        produced: set[int] = set()
-        for n in self.nodes:
-            for v in n.inputs:
-                if v is None:
+        """Raise GraphError unless the graph is in SSA form, ordered, and its use lists agree."""
+        available = {id(v) for v in self.inputs}
+        for node in self.nodes:
+            for value in node.inputs:
+                if value is None:
                     continue
-                if not v.is_constant and id(v) not in defined:
-                    raise GraphError(f"{n.op} {n.name!r} uses undefined {v.name!r}")
-                if n not in v.users:
-                    raise GraphError(f"use list of {v.name!r} misses {n.name!r}")
-            for out in n.outputs:
-                if id(out) in produced or id(out) in defined:
-                    raise GraphError(f"value {out.name!r} is defined twice")
-                if out.producer is not n:
-                    raise GraphError(f"producer of {out.name!r} is wrong")
-                produced.add(id(out))
-                defined.add(id(out))
-        alive = {id(n) for n in self.nodes}
-        for v in self.values():
-            for user in v.users:
-                if id(user) not in alive:
-                    raise GraphError(f"{v.name!r} lists removed user {user.name!r}")
-        for v in self.outputs:
-            if not v.is_constant and id(v) not in defined:
-                raise GraphError(f"graph output {v.name!r} is undefined")
+                if not (value.is_constant or id(value) in available):
+                    raise GraphError(f"{node.op} {node.name!r} uses undefined {value.name!r}")
+                if node not in value.users:
+                    raise GraphError(f"use list of {value.name!r} misses {node.name!r}")
+            for value in node.outputs:
+                if id(value) in available:
+                    raise GraphError(f"value {value.name!r} is defined twice")
+                if value.producer is not node:
+                    raise GraphError(f"producer of {value.name!r} is wrong")
+                available.add(id(value))
+        present = {id(n) for n in self.nodes}
+        for value in self.values():
+            stale = next((u for u in value.users if id(u) not in present), None)
+            if stale is not None:
+                raise GraphError(f"{value.name!r} lists removed user {stale.name!r}")
+        for value in self.outputs:
+            if not value.is_constant and id(value) not in available:
+                raise GraphError(f"graph output {value.name!r} is undefined")
 
     def summary(self) -> dict[str, Any]:
         return {
             "name": self.name,
             "nodes": len(self.nodes),
             "inputs": {v.name: str(v.type) for v in self.inputs},
-            "outputs": {name: str(v.type) for name, v in self.named_outputs()},
+            "outputs": {n: str(v.type) for n, v in self.named_outputs()},
             "constants": len(self.constants()),
             "constant_bytes": self.constant_bytes(),
             "ops": self.op_counts(),
         }
 
     def __str__(self) -> str:
-        lines = [f"graph {self.name}("]
-        lines.extend(f"  {v.name}: {v.type}," for v in self.inputs)
-        lines.append(") {")
-        for n in self.nodes:
-            lines.append(f"  {n!r}  -> {', '.join(str(o.type) for o in n.outputs)}")
-        lines.append("  return " + ", ".join(f"{k}={v.name}" for k, v in self.named_outputs()))
-        lines.append("}")
-        return "\n".join(lines)
+        body = [f"  {v.name}: {v.type}," for v in self.inputs]
+        body.append(") {")
+        body += [f"  {n!r}  -> {', '.join(str(o.type) for o in n.outputs)}" for n in self.nodes]
+        body.append("  return " + ", ".join(f"{k}={v.name}" for k, v in self.named_outputs()))
+        return "\n".join([f"graph {self.name}(", *body, "}"])
+
+
+def _drop_use(value: Value | None, node: Node) -> None:
+    if value is not None:
+        value.users.remove(node)
 
 
 def comment_text(text: str) -> str:
-    """Model-supplied text made safe inside a C/C++ comment: no line breaks, no comment ends."""
-    printable = "".join(c if c.isprintable() else " " for c in text)
-    return printable.replace("*/", "* /").replace("/*", "/ *")
+    """Model-supplied text made safe inside a generated C/C++ comment: non-printable
+    characters become spaces and comment delimiters are broken apart."""
+    safe = "".join(ch if ch.isprintable() else " " for ch in text)
+    return safe.replace("*/", "* /").replace("/*", "/ *")

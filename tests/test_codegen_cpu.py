@@ -182,3 +182,25 @@ def test_other_backends_and_onnx_paths_are_rejected(hip_cache):
 def test_depthwise_detection():
     g = o3(builders.tiny_cnn())
     assert sum(HipEmitter.depthwise(n) for n in g.nodes) == 1
+
+
+def test_reference_vector_cases_the_backend_rejects():
+    """The reference-generated operator cases that neither the reference's C backend nor this
+    backend compiles (Trilu; MatMul on int64) fail at generation with a CodegenError naming
+    the cause; every other case compiles (tests/test_gpu_reference_vectors.py runs them)."""
+    from test_gpu_reference_vectors import UNSUPPORTED
+    from test_reference_op_vectors import MANIFEST, decode_attrs, load_case
+
+    with np.load(ROOT / "tests" / "golden" / "reference_ops.npz") as data:
+        arrays = {k: data[k] for k in data.files}
+    for case in MANIFEST:
+        inputs, _ = load_case(case, arrays)
+        g, _ = op_graph(case["op"], inputs, const=set(case["const"]), attrs=decode_attrs(case["attrs"]),
+                        n_outputs=case["outputs"])
+        optimize(g, "O0")
+        schedule(g)
+        if case["name"] in UNSUPPORTED:
+            with pytest.raises(CodegenError, match=UNSUPPORTED[case["name"]]):
+                generate_hip(g)
+        else:
+            generate_hip(g)
