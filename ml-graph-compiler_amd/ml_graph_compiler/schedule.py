@@ -1,10 +1,18 @@
-"""Memory-aware list scheduling and dataflow analysis (reference: src/ml_graph_compiler/schedule.py).
+"""Node order: a memory-aware topological order, plus dataflow statistics.
 
-``memory_aware_order`` keeps the set of ready nodes and repeatedly runs the one whose execution
-grows the live footprint least, delta(n) = bytes(outputs of n) - bytes(inputs whose last
-remaining user is n), ties broken by program order. ``wavefronts`` gives ASAP levels (the
-operator-level parallelism a multi-stream executor could use) and ``critical_path_flops`` the
-FLOP-weighted longest path.
+Every topological order computes the same values; orders differ in how many bytes of
+intermediate tensors are alive at once, and the planner's arena follows that peak. The order the
+reference compiler picks (src/ml_graph_compiler/schedule.py) — which the planner offsets pinned
+by tests/golden/reference_plans.json depend on — is a greedy list schedule: among the nodes
+whose producers have all run, take the one that grows the live set least,
+
+    growth(n) = bytes written by n - bytes of the inputs whose last remaining reader is n
+
+(views write nothing; constants and graph outputs never free), the earliest in the current
+order on ties. The new order is kept only when it lowers the peak of live bytes.
+
+Live bytes count storage owners: a view (Reshape, Flatten, ...) owns nothing and keeps its
+source alive while it is read. A node's inputs and outputs are alive together while it runs.
 """
 
 from __future__ import annotations
@@ -19,98 +27,115 @@ from .ir import Graph, Node, Value
 VIEW_OPS = frozenset({"Reshape", "Flatten", "Squeeze", "Unsqueeze", "Identity", "Dropout"})
 
 
-def _bytes(value: Value) -> int:
+def _nbytes(value: Value) -> int:
     return 0 if value.is_constant or value.type is None else value.type.nbytes
 
 
-def _storage_root(value: Value) -> Value:
+def _owner(value: Value) -> Value:
+    """The value whose storage ``value`` uses (itself unless it is a view's output)."""
     while value.producer is not None and value.producer.op in VIEW_OPS:
         value = value.producer.input(0)
     return value
 
 
-def peak_live_bytes(graph: Graph, order: Sequence[Node] | None = None) -> int:
-    """Peak live bytes of a schedule; a node's inputs and outputs count together, views own no
-    storage, graph outputs live to the end."""
-    nodes = list(graph.nodes if order is None else order)
-    last: dict[int, int] = {}
-    for i, node in enumerate(nodes):
-        for v in node.inputs:
-            if v is not None and not v.is_constant:
-                last[id(_storage_root(v))] = i
-    for v in graph.outputs:
-        last[id(_storage_root(v))] = len(nodes)
-    live = sum(_bytes(v) for v in graph.inputs)
-    peak = live
-    dying: dict[int, list[Value]] = {}
-    for v in graph.inputs:
-        dying.setdefault(last.get(id(v), -1), []).append(v)
-    live -= sum(_bytes(v) for v in dying.pop(-1, []))
-    for i, node in enumerate(nodes):
-        if node.op not in VIEW_OPS:
-            for out in node.outputs:
-                live += _bytes(out)
-                dying.setdefault(last.get(id(out), i), []).append(out)
-        peak = max(peak, live)
-        live -= sum(_bytes(v) for v in dying.pop(i, []))
-    return peak
-
-
-def _unique_inputs(node: Node) -> list[Value]:
+def _distinct_inputs(node: Node) -> list[Value]:
     return list({id(v): v for v in node.inputs if v is not None}.values())
 
 
-def memory_aware_order(graph: Graph) -> list[Node]:
-    nodes = list(graph.nodes)
-    members = {id(n) for n in nodes}
-    index = {id(n): i for i, n in enumerate(nodes)}
-    waiting = {
-        id(n): len({id(v.producer) for v in n.inputs if v is not None and v.producer is not None and id(v.producer) in members})
-        for n in nodes
-    }
-    uses_left: dict[int, int] = {}
-    for n in nodes:
-        for v in _unique_inputs(n):
-            uses_left[id(v)] = uses_left.get(id(v), 0) + 1
-    outputs = {id(v) for v in graph.outputs}
+def peak_live_bytes(graph: Graph, order: Sequence[Node] | None = None) -> int:
+    """Peak of live bytes over ``order`` (default: the graph's order). Graph inputs are alive
+    from the start until their last read (unread inputs only at the very start), a node's
+    outputs from its step to their storage's last read, graph outputs to the end."""
+    steps = list(graph.nodes if order is None else order)
+    n = len(steps)
+    last_read: dict[int, int] = {}
+    for i, node in enumerate(steps):
+        for v in node.inputs:
+            if v is not None and not v.is_constant:
+                last_read[id(_owner(v))] = i
+    for v in graph.outputs:
+        last_read[id(_owner(v))] = n
+    # bytes alive at each step: +size at the first step, -size after the last
+    delta = [0] * (n + 2)
+    at_start = 0
+    for v in graph.inputs:
+        size = _nbytes(v)
+        at_start += size
+        last = last_read.get(id(v), -1)
+        if last >= 0:
+            delta[0] += size
+            delta[last + 1] -= size
+    for i, node in enumerate(steps):
+        if node.op in VIEW_OPS:
+            continue
+        for out in node.outputs:
+            size = _nbytes(out)
+            delta[i] += size
+            delta[max(last_read.get(id(out), i), i) + 1] -= size
+    peak, live = at_start, 0
+    for i in range(n):
+        live += delta[i]
+        peak = max(peak, live)
+    return peak
 
-    def delta(node: Node) -> int:
+
+class _ListScheduler:
+    """Greedy list scheduling by live-set growth (see the module docstring)."""
+
+    def __init__(self, graph: Graph):
+        self.graph = graph
+        self.nodes = list(graph.nodes)
+        self.rank = {id(n): i for i, n in enumerate(self.nodes)}
+        self.graph_outputs = {id(v) for v in graph.outputs}
+        self.readers_left: dict[int, int] = {}  # distinct reader nodes not yet scheduled
+        self.blocked: dict[int, int] = {}       # distinct producers not yet scheduled
+        self.followers: dict[int, list[Node]] = {id(n): [] for n in self.nodes}
+        for node in self.nodes:
+            for v in _distinct_inputs(node):
+                self.readers_left[id(v)] = self.readers_left.get(id(v), 0) + 1
+            producers = {id(v.producer): v.producer for v in node.inputs
+                         if v is not None and v.producer is not None and id(v.producer) in self.rank}
+            self.blocked[id(node)] = len(producers)
+            for p in producers.values():
+                self.followers[id(p)].append(node)
+
+    def growth(self, node: Node) -> int:
         if node.op in VIEW_OPS:
             return 0
-        grown = sum(_bytes(o) for o in node.outputs)
-        freed = sum(
-            _bytes(v) for v in _unique_inputs(node) if uses_left.get(id(v)) == 1 and id(v) not in outputs
-        )
-        return grown - freed
+        freed = sum(_nbytes(v) for v in _distinct_inputs(node)
+                    if self.readers_left.get(id(v)) == 1 and id(v) not in self.graph_outputs)
+        return sum(_nbytes(o) for o in node.outputs) - freed
 
-    ready = [n for n in nodes if waiting[id(n)] == 0]
-    order: list[Node] = []
-    while ready:
-        best = min(ready, key=lambda n: (delta(n), index[id(n)]))
-        ready.remove(best)
-        order.append(best)
-        for v in _unique_inputs(best):
-            uses_left[id(v)] -= 1
-        released: set[int] = set()
-        for out in best.outputs:
-            for user in out.users:
-                if id(user) in members and id(user) not in released:
-                    released.add(id(user))
-                    waiting[id(user)] -= 1
-                    if waiting[id(user)] == 0:
-                        ready.append(user)
-    if len(order) != len(nodes):
-        raise GraphError("graph has a cycle")
-    return order
+    def run(self) -> list[Node]:
+        ready = {id(n): n for n in self.nodes if self.blocked[id(n)] == 0}
+        order: list[Node] = []
+        while ready:
+            pick = min(ready.values(), key=lambda n: (self.growth(n), self.rank[id(n)]))
+            del ready[id(pick)]
+            order.append(pick)
+            for v in _distinct_inputs(pick):
+                self.readers_left[id(v)] -= 1
+            for follower in self.followers[id(pick)]:
+                self.blocked[id(follower)] -= 1
+                if self.blocked[id(follower)] == 0:
+                    ready[id(follower)] = follower
+        if len(order) != len(self.nodes):
+            raise GraphError("graph has a cycle")
+        return order
+
+
+def memory_aware_order(graph: Graph) -> list[Node]:
+    """A topological order that keeps the live set small (greedy; see the module docstring)."""
+    return _ListScheduler(graph).run()
 
 
 def apply_order(graph: Graph, order: Iterable[Node]) -> None:
-    """Replace the node order with a topological permutation of the same nodes."""
-    new = list(order)
-    if len(new) != len(graph.nodes) or {id(n) for n in new} != {id(n) for n in graph.nodes}:
+    """Install ``order`` (a permutation of the nodes); the graph is left unchanged when the
+    order is not a permutation or not topological."""
+    proposed = list(order)
+    if len(proposed) != len(graph.nodes) or {id(n) for n in proposed} != {id(n) for n in graph.nodes}:
         raise GraphError("schedule is not a permutation of the graph's nodes")
-    previous = graph.nodes
-    graph.nodes = new
+    previous, graph.nodes = graph.nodes, proposed
     try:
         graph.verify()
     except GraphError:
@@ -118,30 +143,33 @@ def apply_order(graph: Graph, order: Iterable[Node]) -> None:
         raise
 
 
-def wavefronts(graph: Graph) -> list[list[Node]]:
-    """ASAP levels: level(n) = 1 + max level of its producers."""
-    level: dict[int, int] = {}
-    levels: list[list[Node]] = []
+def _depths(graph: Graph) -> dict[int, int]:
+    """ASAP level of every node: one more than its deepest producer, 0 without producers."""
+    depth: dict[int, int] = {}
     for node in graph.nodes:
-        preds = [level[id(v.producer)] for v in node.inputs if v is not None and v.producer is not None]
-        lv = 1 + max(preds) if preds else 0
-        level[id(node)] = lv
-        while len(levels) <= lv:
-            levels.append([])
-        levels[lv].append(node)
+        above = [depth[id(v.producer)] for v in node.inputs if v is not None and v.producer is not None]
+        depth[id(node)] = max(above) + 1 if above else 0
+    return depth
+
+
+def wavefronts(graph: Graph) -> list[list[Node]]:
+    """Nodes grouped by ASAP level; the nodes of one level are independent of each other."""
+    depth = _depths(graph)
+    levels: list[list[Node]] = [[] for _ in range(max(depth.values(), default=-1) + 1)]
+    for node in graph.nodes:
+        levels[depth[id(node)]].append(node)
     return levels
 
 
 def critical_path_flops(graph: Graph) -> tuple[int, int]:
-    """(FLOPs on the longest FLOP-weighted path, total FLOPs)."""
-    longest: dict[int, int] = {}
-    total = 0
+    """(FLOPs of the heaviest producer-to-consumer path, total FLOPs); their ratio bounds what
+    running independent operators concurrently can gain."""
+    heaviest: dict[int, int] = {}
     for node in graph.nodes:
-        f = ops.flops(node)
-        total += f
-        preds = [longest[id(v.producer)] for v in node.inputs if v is not None and v.producer is not None]
-        longest[id(node)] = f + (max(preds) if preds else 0)
-    return (max(longest.values()) if longest else 0), total
+        above = [heaviest[id(v.producer)] for v in node.inputs if v is not None and v.producer is not None]
+        heaviest[id(node)] = ops.flops(node) + max(above, default=0)
+    total = sum(ops.flops(n) for n in graph.nodes)
+    return max(heaviest.values(), default=0), total
 
 
 @dataclass
@@ -156,7 +184,7 @@ class ScheduleReport:
 
 
 def schedule(graph: Graph) -> ScheduleReport:
-    """Reorder with memory_aware_order when that lowers the peak live bytes."""
+    """Reorder ``graph`` by ``memory_aware_order`` when that lowers its peak live bytes."""
     before = peak_live_bytes(graph)
     order = memory_aware_order(graph)
     after = peak_live_bytes(graph, order)
@@ -165,13 +193,7 @@ def schedule(graph: Graph) -> ScheduleReport:
     else:
         after = before
     levels = wavefronts(graph)
-    crit, total = critical_path_flops(graph)
-    return ScheduleReport(
-        nodes=len(graph.nodes),
-        peak_before=before,
-        peak_after=after,
-        levels=len(levels),
-        max_width=max((len(lv) for lv in levels), default=0),
-        critical_flops=crit,
-        total_flops=total,
-    )
+    critical, total = critical_path_flops(graph)
+    return ScheduleReport(nodes=len(graph.nodes), peak_before=before, peak_after=after, levels=len(levels),
+                          max_width=max((len(level) for level in levels), default=0),
+                          critical_flops=critical, total_flops=total)
