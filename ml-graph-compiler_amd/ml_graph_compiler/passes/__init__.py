@@ -1,6 +1,13 @@
-"""Optimization passes and the pass manager (reference: src/ml_graph_compiler/passes/__init__.py).
+"""Graph optimization passes and the pass manager.
 
-Pipelines are cumulative; each level adds one group of passes. O3 = loop fusion level.
+Pass names and cumulative pipelines are the reference's interface
+(src/ml_graph_compiler/passes/__init__.py): ``O0`` runs nothing, ``O1`` = ``simplify``,
+``O2`` = ``fuse``, ``O3`` = ``loopfuse`` (NHWC layout plus loop fusion). ``optimize`` runs a
+pipeline in place, verifies the graph after every pass and reports what each pass did.
+
+Modules: ``cleanup`` (fold, dce, cse), ``algebra`` (simplify), ``patterns`` (LayerNorm and
+GELU recognition), ``epilogue`` (Conv/GEMM fusion with bias, residual and activation),
+``nhwc`` (layout), ``loops`` (elementwise loop fusion), ``graph_tools`` (shared helpers).
 """
 
 from __future__ import annotations
@@ -12,14 +19,20 @@ from typing import Any
 
 from ..errors import CompilerError
 from ..ir import Graph
-from .basic import eliminate_common_subexpressions, eliminate_dead_code, fold_constants
-from .fusion import fuse
-from .layout import to_nhwc
-from .loopfuse import fuse_elementwise
-from .simplify import simplify
+from .algebra import simplify
+from .cleanup import eliminate_common_subexpressions, eliminate_dead_code, fold_constants
+from .epilogue import fuse_conv, fuse_gemm
+from .loops import fuse_elementwise
+from .nhwc import to_nhwc
+from .patterns import fuse_gelu, fuse_layer_norm
+
+
+def fuse(graph: Graph) -> int:
+    """LayerNorm and GELU recognition, then Conv and GEMM fusion; returns the rewrites."""
+    return fuse_layer_norm(graph) + fuse_gelu(graph) + fuse_conv(graph) + fuse_gemm(graph)
+
 
 PassFn = Callable[[Graph], int]
-
 PASSES: dict[str, PassFn] = {
     "fold": fold_constants,
     "dce": eliminate_dead_code,
@@ -30,25 +43,27 @@ PASSES: dict[str, PassFn] = {
     "loopfuse": fuse_elementwise,
 }
 
-_FOLD = ["fold", "dce"]
-_CSE = [*_FOLD, "cse", "dce"]
-_SIMPLIFY = ["fold", "dce", "cse", "simplify", "fold", "cse", "dce"]
-_FUSE = ["fold", "dce", "cse", "simplify", "fold", "cse", "fuse", "simplify", "dce"]
-_LAYOUT = ["fold", "dce", "cse", "simplify", "fold", "cse", "fuse", "simplify", "layout", "cse", "dce"]
-_LOOPFUSE = [*_LAYOUT, "loopfuse", "dce"]
 
-PIPELINES: dict[str, list[str]] = {
-    "O0": [],
-    "fold": _FOLD,
-    "cse": _CSE,
-    "simplify": _SIMPLIFY,
-    "fuse": _FUSE,
-    "layout": _LAYOUT,
-    "loopfuse": _LOOPFUSE,
-    "O1": _SIMPLIFY,
-    "O2": _FUSE,
-    "O3": _LOOPFUSE,
-}
+def _levels() -> dict[str, list[str]]:
+    """Each level extends the one before it."""
+    front = ["fold", "dce", "cse"]
+    simplified = front + ["simplify", "fold", "cse"]
+    fused = simplified + ["fuse", "simplify"]
+    layout = fused + ["layout", "cse", "dce"]
+    levels = {
+        "O0": [],
+        "fold": ["fold", "dce"],
+        "cse": front + ["dce"],
+        "simplify": simplified + ["dce"],
+        "fuse": fused + ["dce"],
+        "layout": layout,
+        "loopfuse": layout + ["loopfuse", "dce"],
+    }
+    levels.update(O1=levels["simplify"], O2=levels["fuse"], O3=levels["loopfuse"])
+    return levels
+
+
+PIPELINES: dict[str, list[str]] = _levels()
 
 
 @dataclass
@@ -69,15 +84,12 @@ class PassReport:
         return self.records[-1].nodes_after if self.records else self.nodes_before
 
     def to_dict(self) -> dict[str, Any]:
-        return {
-            "nodes_before": self.nodes_before,
-            "nodes_after": self.nodes_after,
-            "passes": [r.__dict__ for r in self.records],
-        }
+        return {"nodes_before": self.nodes_before, "nodes_after": self.nodes_after,
+                "passes": [vars(r) for r in self.records]}
 
 
 def resolve(passes: str | Sequence[str]) -> list[str]:
-    """A pipeline name, a comma-separated pass list, or a sequence of pass names."""
+    """A pipeline name, a comma-separated list of pass names, or a sequence of pass names."""
     if isinstance(passes, str):
         if passes in PIPELINES:
             return list(PIPELINES[passes])
@@ -91,28 +103,16 @@ def resolve(passes: str | Sequence[str]) -> list[str]:
 
 
 def optimize(graph: Graph, passes: str | Sequence[str] = "O3", verify: bool = True) -> PassReport:
-    """Run passes in place, verifying the graph after each by default."""
+    """Run ``passes`` on ``graph`` in place (verifying after each one unless told not to)."""
     report = PassReport(nodes_before=len(graph.nodes))
     for name in resolve(passes):
-        t0 = time.perf_counter()
+        began = time.perf_counter()
         changes = PASSES[name](graph)
         if verify:
             graph.verify()
-        report.records.append(PassRecord(name, changes, len(graph.nodes), round(time.perf_counter() - t0, 4)))
+        report.records.append(PassRecord(name, changes, len(graph.nodes), round(time.perf_counter() - began, 4)))
     return report
 
 
-__all__ = [
-    "PASSES",
-    "PIPELINES",
-    "PassReport",
-    "eliminate_common_subexpressions",
-    "eliminate_dead_code",
-    "fold_constants",
-    "fuse",
-    "fuse_elementwise",
-    "optimize",
-    "resolve",
-    "simplify",
-    "to_nhwc",
-]
+__all__ = ["PASSES", "PIPELINES", "PassReport", "eliminate_common_subexpressions", "eliminate_dead_code",
+           "fold_constants", "fuse", "fuse_elementwise", "optimize", "resolve", "simplify", "to_nhwc"]

@@ -74,6 +74,13 @@ def main() -> None:
         "resnet50_b1": lambda: builders.resnet50(1),
         "mobilenet_v2_b1": lambda: builders.mobilenet_v2(1),
         "bert_base_b1": lambda: builders.bert_base(1),
+        "tiny_transformer_separate_qkv": lambda: builders.transformer(separate_qkv=True),
+        "tiny_transformer_erf": lambda: builders.transformer(gelu="erf", causal=False),
+        "bert_2l_b2_separate_qkv": lambda: builders.bert_base(2, layers=2, separate_qkv=True),
+        "gpt2_2l_b1": lambda: builders.gpt2(1, layers=2),
+        "mobilenet_v2_b2": lambda: builders.mobilenet_v2(2),
+        "resnet50_b2": lambda: builders.resnet50(2),
+        "bottleneck_b3": lambda: builders.bottleneck(3),
     }
     fixture = {}
     for name, make in cases.items():
