@@ -49,6 +49,6 @@ def test_cli_compile_onnx_file(tmp_path, capsys, hip_cache):
             "--cache-dir", str(hip_cache), "-o", str(tmp_path / "saved"), "--json"]
     assert cli_main(argv) == 0
     payload = json.loads(capsys.readouterr().out)
-    assert payload["backend"] == "hip" and payload["max_abs_diff_vs_O0"] <= 1e-4
+    assert payload["backend"] == "hip" and payload["max_abs_diff_vs_interpreter"] <= 1e-4
     assert payload["outputs"]["y"].startswith("float32[4, 16, 32]")
     assert (tmp_path / "saved" / "model.json").exists() and payload["latency_ms_min"] > 0

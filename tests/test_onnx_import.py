@@ -413,28 +413,52 @@ def test_malformed_files(tmp_path):
 # -- command line -----------------------------------------------------------------------------
 
 
-def test_cli_inspect_dims_shapes_and_export(tmp_path, capsys):
+def test_cli_compile_binds_dims_and_shapes(tmp_path, capsys):
+    """``mgc compile`` imports the file with its symbolic dimensions bound and reports import
+    errors with exit status 2; without a GPU the build stops at loading, loudly."""
     path = str(GOLDEN / "mlp_dynamic_batch.onnx")
-    assert cli_main(["inspect", path]) == 2
+    assert cli_main(["compile", path]) == 2
     assert "dynamic dimension 'batch'" in capsys.readouterr().err
-    assert cli_main(["inspect", path, "--dim", "batch=6", "--json"]) == 0
-    summary = json.loads(capsys.readouterr().out)
-    assert summary["inputs"] == {"x": "float32[6x16]"}
-    assert cli_main(["inspect", path, "--shape", "x=2x16", "--json"]) == 0
-    assert json.loads(capsys.readouterr().out)["outputs"] == {"y": "float32[2x4]"}
-    assert cli_main(["inspect", path, "--dim", "batch"]) == 2
+    assert cli_main(["compile", path, "--dim", "batch"]) == 2
     assert "--dim expects NAME=INT" in capsys.readouterr().err
-    assert cli_main(["inspect", path, "--shape", "x=2by16"]) == 2
+    assert cli_main(["compile", path, "--shape", "x=2by16"]) == 2
     assert "--shape expects" in capsys.readouterr().err
-    out = tmp_path / "cnn.onnx"
-    assert cli_main(["export", "tiny-cnn", "-o", str(out)]) == 0
-    capsys.readouterr()
-    assert cli_main(["optimize", str(out), "--json"]) == 0
-    assert json.loads(capsys.readouterr().out)["pipeline"] == "O3"
-    assert cli_main(["plan", str(out)]) == 0
-    assert "arena by strategy" in capsys.readouterr().out
-    assert cli_main(["inspect", "no-such-model"]) == 2
+    assert cli_main(["compile", "no-such-model"]) == 2
     assert "neither a file nor a bundled sample" in capsys.readouterr().err
+    assert cli_main(["compile", path, "--dim", "batch=6", "--backend", "c", "--cache-dir", str(tmp_path)]) == 2
+    assert "not part of this build" in capsys.readouterr().err
+    assert cli_main(["compile", path, "--shape", "x=2x16", "--check", "--cache-dir", str(tmp_path)]) == 2
+    assert "no HIP device" in capsys.readouterr().err
+    from ml_graph_compiler.cli import load_model
+
+    assert load_model(path, dims=["batch=6"]).inputs[0].type == TensorType("float32", (6, 16))
+    assert load_model(path, shapes=["x=2x16"]).outputs[0].type == TensorType("float32", (2, 4))
+    # the bundled samples go to ONNX and back unchanged
+    out = tmp_path / "cnn.onnx"
+    save_onnx(builders.tiny_cnn(), out)
+    back = load_model(str(out))
+    from ml_graph_compiler.cli import random_inputs
+    from ml_graph_compiler.evaluate import evaluate_graph
+
+    counts = {k: v for k, v in back.op_counts().items() if k != "Identity"}  # output renames
+    assert counts == builders.tiny_cnn().op_counts()
+    feeds = random_inputs(back, 1)
+    for k, v in evaluate_graph(builders.tiny_cnn(), feeds).items():
+        np.testing.assert_array_equal(evaluate_graph(back, feeds)[k], v)
+
+
+def test_interpreter_check_matches_the_oracle():
+    """``compile --check``'s CPU baseline (the operator table run node by node) agrees with the
+    independent oracle."""
+    from ml_graph_compiler.cli import random_inputs
+    from ml_graph_compiler.evaluate import evaluate_graph
+
+    for make in (builders.tiny_cnn, builders.tiny_bert, builders.mlp):
+        g = make()
+        feeds = random_inputs(g, 3)
+        got, want = evaluate_graph(g, feeds), oracle.run_graph(make(), feeds)
+        for k in want:
+            np.testing.assert_allclose(got[k], want[k], rtol=2e-5, atol=2e-5)
 
 
 def test_cli_random_token_ids_stay_in_range():
