@@ -149,55 +149,50 @@ def collapse(shape: Sequence[int], stride_sets: list[list[int]]) -> tuple[list[i
 
 @dataclass
 class WeightsBuilder:
-    """Constants in one blob at 256-byte aligned offsets (reference: codegen/c.py:166-219).
+    """The weights blob the model uploads once: every constant the kernels read, each starting
+    at a 256-byte aligned offset (the alignment of the DMA loads), and a constant added twice
+    under the same key stored once. Arrays are referenced, not copied, until the blob is
+    materialized."""
 
-    Chunks reference the original arrays until ``write``; equal keys share one chunk."""
-
-    chunks: list[tuple[int, np.ndarray]] = field(default_factory=list)
-    size: int = 0
-    by_key: dict[Any, int] = field(default_factory=dict)
+    pieces: list[tuple[int, np.ndarray]] = field(default_factory=list)
+    end: int = 0
+    offsets: dict[Any, int] = field(default_factory=dict)
 
     def add(self, array: np.ndarray, key: Any = None) -> int:
-        if key is not None and key in self.by_key:
-            return self.by_key[key]
+        """Byte offset of ``array`` in the blob."""
+        if key is not None and key in self.offsets:
+            return self.offsets[key]
         data = np.ascontiguousarray(array)
-        offset = self.size
-        self.chunks.append((offset, data))
-        self.size = offset + data.nbytes
-        self.size += (-self.size) % ALIGN
+        at = (self.end + ALIGN - 1) // ALIGN * ALIGN
+        self.pieces.append((at, data))
+        self.end = at + data.nbytes
         if key is not None:
-            self.by_key[key] = offset
-        return offset
+            self.offsets[key] = at
+        return at
 
     @property
     def nbytes(self) -> int:
-        return max(self.size, ALIGN)
+        return max((self.end + ALIGN - 1) // ALIGN * ALIGN, ALIGN)
 
     def digest(self) -> str:
-        h = hashlib.blake2b(digest_size=12)
-        for offset, data in self.chunks:
-            h.update(offset.to_bytes(8, "little"))
-            h.update(memoryview(data.reshape(-1).view(np.uint8)))
-        return h.hexdigest()
-
-    def write(self, path: Path) -> None:
-        tmp = path.with_suffix(path.suffix + f".tmp{os.getpid()}")
-        with open(tmp, "wb") as f:
-            pos = 0
-            for offset, data in self.chunks:
-                if offset > pos:
-                    f.write(b"\0" * (offset - pos))
-                f.write(memoryview(data.reshape(-1).view(np.uint8)))
-                pos = offset + data.nbytes
-            if self.nbytes > pos:
-                f.write(b"\0" * (self.nbytes - pos))
-        tmp.replace(path)
+        """Content hash of the blob (names the weights file in the build cache)."""
+        h = hashlib.sha256(str(self.nbytes).encode())
+        for at, data in self.pieces:
+            h.update(np.int64(at).tobytes())
+            h.update(data.reshape(-1).view(np.uint8).data)
+        return h.hexdigest()[:24]
 
     def blob(self) -> np.ndarray:
-        out = np.zeros(self.nbytes, np.uint8)
-        for offset, data in self.chunks:
-            out[offset : offset + data.nbytes] = data.reshape(-1).view(np.uint8)
-        return out
+        image = np.zeros(self.nbytes, np.uint8)
+        for at, data in self.pieces:
+            image[at : at + data.nbytes] = data.reshape(-1).view(np.uint8)
+        return image
+
+    def write(self, path: Path) -> None:
+        """Write the blob to ``path`` atomically (a temporary file renamed into place)."""
+        staging = path.with_suffix(path.suffix + f".tmp{os.getpid()}")
+        self.blob().tofile(staging)
+        staging.replace(path)
 
 
 def pack_b_nk(b: np.ndarray) -> np.ndarray:
