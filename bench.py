@@ -10,11 +10,12 @@ Printed: ONE JSON line with the driver's fields plus
 * ``roofline``: the fp32 MFMA GEMM / implicit-GEMM convolution kernels (all conv and FC nodes):
   algorithmic FLOPs per launch (ops.flops of the node, 2 per MAC) over the kernel's average
   duration, measured with a hipEvent pair around every node in eager replays on the model
-  stream; ``traffic`` is the HBM bytes per GEMM launch from the two rocprofv3 counter runs
-  summarized in profiles/<workload>_b<batch>_gemm_traffic.md (``--pmc-probe`` is the program
-  those runs profile and ``--pmc-summary`` turns their CSVs into that file), or null;
+  stream; ``traffic`` is the HBM bytes per GEMM launch, measured in the run by two rocprofv3
+  counter runs (FETCH_SIZE, WRITE_SIZE) over ``--pmc-probe`` (``traffic_source`` says so, or
+  names the committed summary profiles/<workload>_b<batch>_gemm_traffic.md it fell back to);
 * ``cpu_baseline``: the reference's generated-C + OpenMP backend (its own C kernels, built from
-  the reference sources into oracle/_ref) timed on this host's cores on a bounded sample;
+  the reference sources into oracle/_ref) on this host's cores by the reference's latency
+  method (fresh process per cell, 3 interleaved rounds, bootstrap CI) at the GPU batch;
 * ``b1``: the same model at batch 1 (latency and img/s).
 """
 
@@ -200,21 +201,101 @@ def _is_depthwise(node) -> bool:
     return HipEmitter.depthwise(node)
 
 
-def cpu_baseline(workload: str, seconds_budget: float = 20.0) -> dict | None:
-    """The reference's generated-C backend on this host's cores (bounded sample)."""
+def cpu_baseline(workload: str, gpu_batch: int) -> dict | None:
+    """The reference's generated-C backend on this host's cores, by the reference's latency
+    method (oracle/cpu_bench.py: a fresh process per cell, 3 interleaved rounds, bootstrap 95%
+    CI of the median): the GPU batch on every core (the reported value), batch 1 on every core
+    and on one. Bounded to about a minute of CPU time."""
     try:
-        from oracle import cbackend
+        from oracle import cbackend, cpu_bench
     except Exception as exc:  # pragma: no cover - reported, not fatal
         log(f"cpu baseline unavailable: {exc}")
         return None
+    if workload == "single_gemm":
+        gpu_batch = 1
+    batches = cbackend.BASELINES.get(workload, ())
+    if gpu_batch not in batches:
+        log(f"cpu baseline: no prebuilt reference library for {workload} b{gpu_batch}")
+        return None
+    info = cpu_bench.host()
+    cores = info["nproc"]
+    big = gpu_batch > 1
+    cells = [(workload, gpu_batch, cores, 1 if big else 5, 3 if big else 30)]
+    if big:
+        cells.append((workload, 1, cores, 5, 30))
+    cells.append((workload, 1, 1, 1, 3))
     try:
-        base = cbackend.time_baseline(workload, seconds_budget=seconds_budget)
-        one = cbackend.time_baseline(workload, seconds_budget=seconds_budget / 2, threads=1)
-        base["sample"] += f"; on 1 thread: {one['value']} {one['unit']} ({one['sample'].split('(')[1].split(')')[0]})"
-        return base
+        log(f"cpu baseline: {len(cells)} cells x 3 rounds, fresh process each, on {cores} cores of {info['cpu_model']}")
+        rows = {(r["batch"], r["threads"]): r for r in cpu_bench.measure(cells, rounds=3)}
     except Exception as exc:
         log(f"cpu baseline failed: {exc}")
         return None
+    units = 1 if workload == "single_gemm" else gpu_batch
+    unit = {"single_gemm": "calls/s", "bert_base": "seq/s"}.get(workload, "img/s")
+
+    def rate(batch: int, threads: int) -> str:
+        r = rows[(batch, threads)]
+        lo, hi = r["median_ci95_ms"]
+        n = 1 if workload == "single_gemm" else batch
+        return (f"b{batch} on {threads} thread(s): {1e3 * n / r['median_ms']:.2f} {unit} (median {r['median_ms']:.1f} ms, "
+                f"95% CI {lo:.1f}-{hi:.1f} ms, {r['samples']} runs)")
+
+    head = rows[(gpu_batch, cores)]
+    text = "; ".join(rate(b, t) for (b, t) in rows)
+    return {
+        "value": round(1e3 * units / head["median_ms"], 3),
+        "unit": unit,
+        "cores": cores,
+        "kind": "reference",
+        "sample": (f"{workload}: the reference's generated-C + OpenMP backend (its own mgc_kernels.c, -O3 -fopenmp "
+                   f"-march=x86-64-v3) on '{info['cpu_model']}' (nproc {cores}); a fresh process per cell, 3 interleaved "
+                   f"rounds, bootstrap CI of the median (the reference's benchmarks/latency.py method); {text}"),
+        "median_ci95_ms": head["median_ci95_ms"],
+    }
+
+
+def measure_traffic(workload: str, batch: int, cache: Path) -> tuple[int | None, str]:
+    """HBM bytes per GEMM launch measured now: two rocprofv3 counter runs (FETCH_SIZE, then
+    WRITE_SIZE) over ``--pmc-probe``, each calibrated on the probe's 256 MiB copy. Falls back
+    to the committed summary (labelled as recorded) when a run fails."""
+    import shutil
+    import subprocess
+    import tempfile
+
+    prof = shutil.which("rocprofv3")
+    out = Path(tempfile.mkdtemp(prefix="mgc-pmc-", dir="/tmp"))
+    runs = {}
+    try:
+        if prof is None:
+            raise RuntimeError("rocprofv3 not found")
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            d = out / counter.lower()
+            cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", str(d), "-o", "p", "--",
+                   sys.executable, str(ROOT / "bench.py"), "--pmc-probe", "--workload", workload,
+                   "--batch", str(batch), "--cache", str(cache)]
+            log(f"traffic: rocprofv3 --pmc {counter} over the probe")
+            proc = subprocess.run(cmd, cwd="/tmp", env={**os.environ, "TMPDIR": "/tmp"}, capture_output=True,
+                                  text=True, timeout=180, check=False)
+            runs[counter] = per_dispatch(d, counter)
+            if not runs[counter]:
+                raise RuntimeError(f"no {counter} rows (rc {proc.returncode}): {proc.stderr[-400:]}")
+        bf, bw, _, _ = calibration(runs["FETCH_SIZE"], runs["WRITE_SIZE"])
+
+        def is_gemm(name: str) -> bool:
+            return "gemm_" in name and "reduce" not in name
+
+        gf = [v for name, v in runs["FETCH_SIZE"] if is_gemm(name)]
+        gw = [v for name, v in runs["WRITE_SIZE"] if is_gemm(name)]
+        if not gf or len(gf) != len(gw):
+            raise RuntimeError("GEMM dispatch counts differ between the two runs")
+        return int(round((bf * sum(gf) + bw * sum(gw)) / len(gf))), (
+            "measured in this run: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE over bench.py --pmc-probe, "
+            "each scaled by the counter's reading for a 256 MiB copy")
+    except Exception as exc:
+        log(f"traffic measurement failed ({exc}); using the committed summary")
+        return recorded_traffic(workload, batch), f"recorded: {traffic_file(workload, batch).relative_to(ROOT)}"
+    finally:
+        shutil.rmtree(out, ignore_errors=True)
 
 
 TRAFFIC_KEY = "traffic_bytes_per_launch:"
@@ -537,6 +618,7 @@ def main() -> int:
     p.add_argument("--batch", type=int, default=32)
     p.add_argument("--profile-replays", type=int, default=5)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-traffic", action="store_true", help="report the committed traffic summary instead of measuring")
     p.add_argument("--no-b1", action="store_true")
     p.add_argument("--cache", default=os.environ.get("MGC_BENCH_CACHE", "/tmp/mgc-bench-cache"))
     p.add_argument("--pmc-probe", action="store_true", help="run the counter-run program and exit")
@@ -595,10 +677,13 @@ def main() -> int:
     value = units * args.steps / wall
     log(f"{ms_per_step:.3f} ms/step (events {ev_ms / args.steps:.3f} ms), {value:.1f} units/s")
     roof = gemm_roofline(graph, model, args.profile_replays)
-    roof["traffic"] = recorded_traffic(args.workload, batch)
-    log(f"roofline {roof}")
     total_flops = sum(model.node_flops)
     model.release()
+    if args.no_traffic:
+        roof["traffic"], roof["traffic_source"] = recorded_traffic(args.workload, batch), "recorded (--no-traffic)"
+    else:
+        roof["traffic"], roof["traffic_source"] = measure_traffic(args.workload, batch, cache)
+    log(f"roofline {roof}")
 
     b1 = None
     if args.workload in ("resnet50", "bottleneck", "mobilenet_v2", "bert_base", "gpt2") and not args.no_b1 and batch != 1:
@@ -613,7 +698,7 @@ def main() -> int:
         m1.release()
         log(f"b1 {b1}")
 
-    cpu = None if args.no_cpu_baseline else cpu_baseline(args.workload)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(args.workload, units)
     unit = {"resnet50": "img/s", "bottleneck": "img/s", "mobilenet_v2": "img/s", "bert_base": "seq/s",
             "gpt2": "seq/s", "single_gemm": "calls/s"}[args.workload]
     line = {
