@@ -122,6 +122,16 @@ typedef struct {
     float *workspace;
     long workspace_floats;
     int split_k;
+    /* A concatenated-K GEMM when k1 > 0: columns k >= k1 of A are columns k - k1 of a2, an
+     * NHWC image read as a 1 x 1 convolution (kind MGC_OP_CONV_NHWC, KH = KW = 1, no padding,
+     * strides SH / SW, output OH x OW, cg = C), so one launch computes act([A | A2] B + bias)
+     * with B the (K1 + K2) x N stack of both weight matrices: a residual block's last 1 x 1
+     * convolution together with its projection shortcut. Needs a strided A with unit column
+     * stride (row stride, a2's C and both pointers multiples of 4 floats / 16 bytes), a2's
+     * C = K - k1, k1 a multiple of 32, B packed as [N][K] (rs 1, cs a multiple of 4) and
+     * batch_rank 0; sets the launch error otherwise. k1 = 0 is an ordinary GEMM. */
+    mgc_hip_operand a2;
+    int k1;
 } mgc_hip_gemm_args;
 
 void mgc_hip_gemm(mgc_hip_exec *x, const mgc_hip_gemm_args *g);

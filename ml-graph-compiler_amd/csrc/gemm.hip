@@ -40,7 +40,10 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef unsigned uint4_t __attribute__((ext_vector_type(4)));
 
-enum { AM_VEC = 0, AM_CONV_VEC = 1, AM_GEN = 2 };
+// A operand forms: strided with unit column stride, NHWC image (implicit im2col), generic
+// (register-staged), and a concatenation of a strided matrix (columns < k1) with an NHWC image
+// read as a strided 1 x 1 convolution (columns >= k1).
+enum { AM_VEC = 0, AM_CONV_VEC = 1, AM_GEN = 2, AM_CAT = 3 };
 
 // 16 zero bytes: the load address of every out-of-range operand element.
 __device__ __attribute__((aligned(16))) float g_zero_page[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -75,6 +78,9 @@ struct GemmDev {
     int vec_out;
     FastDiv div_ow, div_ohw, div_cg, div_kw;  // A as NHWC image: OW, OH * OW, cg, KW
     long a_bytes, b_bytes;  // bytes of A and B reachable from a.p / b.p (all batch elements)
+    mgc_hip_operand a2;     // AM_CAT: the image whose 1 x 1 strided window gives columns >= k1
+    int k1;
+    long a2_bytes;
     int nbatch;                       // batch elements  // 16-byte epilogue accesses are aligned (ldc, ldr, pointers)
 };
 
@@ -570,7 +576,7 @@ __global__ void __launch_bounds__(256) gemm_dma_kernel(const GemmDev p) {
     constexpr int SMEM_LOOP = STAGES * STAGE;
     constexpr int SMEM_EPI = BM * (BN + 8);
     constexpr int SMEM = SMEM_LOOP > SMEM_EPI ? SMEM_LOOP : SMEM_EPI;
-    static_assert(AMODE == AM_VEC || AMODE == AM_CONV_VEC, "vector A only");
+    static_assert(AMODE == AM_VEC || AMODE == AM_CONV_VEC || AMODE == AM_CAT, "vector A only");
 
     __shared__ __attribute__((aligned(16))) float smem[SMEM];
 
@@ -614,15 +620,24 @@ __global__ void __launch_bounds__(256) gemm_dma_kernel(const GemmDev p) {
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
         (void *)bbase, (short)0, (int)(p.b_bytes - bo * 4), 0x00020000);
     constexpr unsigned OOB = 0x80000000u;  // past every resource's end (extents are < 2^31 bytes)
+    // AM_CAT: the second source (batch_rank 0, so no batch offset)
+    const __amdgpu_buffer_rsrc_t ra2 = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(AMODE == AM_CAT ? p.a2.p : abase), (short)0, (int)(AMODE == AM_CAT ? p.a2_bytes : 0), 0x00020000);
     unsigned aoff[AI];  // byte offset of the row (AM_VEC) or of its window origin (AM_CONV_VEC)
+    unsigned aoff2[AI];  // AM_CAT: byte offset of the row's pixel in the second source
     int aih[AI], aiw[AI];
-    const int ohw = p.a.OH * p.a.OW;
+    const int ohw = AMODE == AM_CAT ? p.a2.OH * p.a2.OW : p.a.OH * p.a.OW;
 #pragma unroll
     for (int i = 0; i < AI; ++i) {
         const int m = m0 + (i * 4 + wave) * 8 + rsub;
-        aoff[i] = OOB;
+        aoff[i] = aoff2[i] = OOB;
         aih[i] = aiw[i] = -0x40000000;  // fails the window bounds test
         if (m < p.M) {
+            if (AMODE == AM_CAT) {
+                const int n = fdiv(m, p.div_ohw), rr = m - n * ohw;
+                const int oh = fdiv(rr, p.div_ow), ow = rr - oh * p.a2.OW;
+                aoff2[i] = (unsigned)(((n * p.a2.H + oh * p.a2.SH) * p.a2.W + ow * p.a2.SW) * p.a2.C) * 4u;
+            }
             if (AMODE == AM_CONV_VEC) {
                 const int n = fdiv(m, p.div_ohw), rr = m - n * ohw;
                 const int oh = fdiv(rr, p.div_ow), ow = rr - oh * p.a.OW;
@@ -659,6 +674,18 @@ __global__ void __launch_bounds__(256) gemm_dma_kernel(const GemmDev p) {
 #pragma unroll
             for (int i = 0; i < AI; ++i)
                 dma16_buf(ra, kok ? aoff[i] + (unsigned)k * 4u : OOB, sa + (i * 4 + wave) * 8 * BK);
+        } else if constexpr (AMODE == AM_CAT) {
+            // k1 is a multiple of the 32-wide stage, so a whole stage reads one source
+            if (k < p.k1) {
+#pragma unroll
+                for (int i = 0; i < AI; ++i)
+                    dma16_buf(ra, kok ? aoff[i] + (unsigned)k * 4u : OOB, sa + (i * 4 + wave) * 8 * BK);
+            } else {
+                const unsigned k2 = (unsigned)(k - p.k1) * 4u;
+#pragma unroll
+                for (int i = 0; i < AI; ++i)
+                    dma16_buf(ra2, kok ? aoff2[i] + k2 : OOB, sa + (i * 4 + wave) * 8 * BK);
+            }
         } else {
             const int dh = ckh * p.a.DH, dw = ckw * p.a.DW;
             const unsigned koff = (unsigned)((dh * p.a.W + dw) * p.a.C + cc) * 4u;
@@ -761,7 +788,7 @@ __global__ void __launch_bounds__(256) gemm_dma_wsplit_kernel(const GemmDev p) {
     constexpr int LDC = T + 8;
     constexpr int SMEM = 4 * RING;     // 64 KB; the epilogue uses 5 * T * LDC floats of it
     static_assert(5 * T * LDC <= SMEM, "epilogue staging");
-    static_assert(AMODE == AM_VEC || AMODE == AM_CONV_VEC, "vector A only");
+    static_assert(AMODE == AM_VEC || AMODE == AM_CONV_VEC || AMODE == AM_CAT, "vector A only");
 
     __shared__ __attribute__((aligned(16))) float smem[SMEM];
 
@@ -798,15 +825,22 @@ __global__ void __launch_bounds__(256) gemm_dma_wsplit_kernel(const GemmDev p) {
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
         (void *)bbase, (short)0, (int)(p.b_bytes - bo * 4), 0x00020000);
     constexpr unsigned OOB = 0x80000000u;
-    unsigned aoff[4];
+    const __amdgpu_buffer_rsrc_t ra2 = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(AMODE == AM_CAT ? p.a2.p : abase), (short)0, (int)(AMODE == AM_CAT ? p.a2_bytes : 0), 0x00020000);
+    unsigned aoff[4], aoff2[4];
     int aih[4], aiw[4];
-    const int ohw = p.a.OH * p.a.OW;
+    const int ohw = AMODE == AM_CAT ? p.a2.OH * p.a2.OW : p.a.OH * p.a.OW;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int m = m0 + i * 8 + rsub;
-        aoff[i] = OOB;
+        aoff[i] = aoff2[i] = OOB;
         aih[i] = aiw[i] = -0x40000000;
         if (m < p.M) {
+            if (AMODE == AM_CAT) {
+                const int n = fdiv(m, p.div_ohw), rr = m - n * ohw;
+                const int oh = fdiv(rr, p.div_ow), ow = rr - oh * p.a2.OW;
+                aoff2[i] = (unsigned)(((n * p.a2.H + oh * p.a2.SH) * p.a2.W + ow * p.a2.SW) * p.a2.C) * 4u;
+            }
             if (AMODE == AM_CONV_VEC) {
                 const int n = fdiv(m, p.div_ohw), rr = m - n * ohw;
                 const int oh = fdiv(rr, p.div_ow), ow = rr - oh * p.a.OW;
@@ -842,6 +876,15 @@ __global__ void __launch_bounds__(256) gemm_dma_wsplit_kernel(const GemmDev p) {
         if constexpr (AMODE == AM_VEC) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) dma16_buf(ra, kok ? aoff[i] + (unsigned)k * 4u : OOB, sa + i * 8 * BK);
+        } else if constexpr (AMODE == AM_CAT) {
+            if (k < p.k1) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) dma16_buf(ra, kok ? aoff[i] + (unsigned)k * 4u : OOB, sa + i * 8 * BK);
+            } else {
+                const unsigned k2 = (unsigned)(k - p.k1) * 4u;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) dma16_buf(ra2, kok ? aoff2[i] + k2 : OOB, sa + i * 8 * BK);
+            }
         } else {
             const int dh = ckh * p.a.DH, dw = ckw * p.a.DW;
             const unsigned koff = (unsigned)((dh * p.a.W + dw) * p.a.C + cc) * 4u;
@@ -1023,12 +1066,15 @@ static GemmKernel pick_kernel(int am, int bm) {
 
 template <int BM, int BN, int WGM>
 static GemmKernel pick_dma(int am) {
-    return am == AM_VEC ? &gemm_dma_kernel<BM, BN, WGM, 2, AM_VEC>
-                        : &gemm_dma_kernel<BM, BN, WGM, 2, AM_CONV_VEC>;
+    return am == AM_VEC   ? &gemm_dma_kernel<BM, BN, WGM, 2, AM_VEC>
+           : am == AM_CAT ? &gemm_dma_kernel<BM, BN, WGM, 2, AM_CAT>
+                          : &gemm_dma_kernel<BM, BN, WGM, 2, AM_CONV_VEC>;
 }
 
 static GemmKernel pick_wsplit(int am) {
-    return am == AM_VEC ? &gemm_dma_wsplit_kernel<AM_VEC> : &gemm_dma_wsplit_kernel<AM_CONV_VEC>;
+    return am == AM_VEC   ? &gemm_dma_wsplit_kernel<AM_VEC>
+           : am == AM_CAT ? &gemm_dma_wsplit_kernel<AM_CAT>
+                          : &gemm_dma_wsplit_kernel<AM_CONV_VEC>;
 }
 
 struct TileChoice {
@@ -1312,12 +1358,28 @@ static void gemm_launch(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const LnTai
     if (batch <= 0) return;
 
     int am = AM_GEN;
-    if (p.a.kind == MGC_OP_STRIDED && p.a.cs == 1 && p.a.rs % 4 == 0 && p.K % 4 == 0 &&
-        aligned16(p.a.p) && bs_div4(p.a_bs, p.batch_rank))
+    p.a2 = g->a2;
+    p.k1 = g->k1;
+    p.a2_bytes = 0;
+    if (g->k1 > 0) {
+        const mgc_hip_operand &s2 = g->a2;
+        const bool ok = g->batch_rank == 0 && p.a.kind == MGC_OP_STRIDED && p.a.cs == 1 && p.a.rs % 4 == 0 &&
+                        aligned16(p.a.p) && s2.kind == MGC_OP_CONV_NHWC && s2.KH == 1 && s2.KW == 1 &&
+                        s2.PT == 0 && s2.PL == 0 && s2.C % 4 == 0 && s2.cg == s2.C && aligned16(s2.p) &&
+                        s2.OH > 0 && s2.OW > 0 && g->k1 % 32 == 0 && g->k1 < p.K && s2.C == p.K - g->k1;
+        if (!ok) {
+            x->launch_error = (int)hipErrorInvalidValue;
+            set_error("mgc_hip_gemm: concatenated-K operands outside their limits", hipErrorInvalidValue);
+            return;
+        }
+        am = AM_CAT;
+    } else if (p.a.kind == MGC_OP_STRIDED && p.a.cs == 1 && p.a.rs % 4 == 0 && p.K % 4 == 0 &&
+               aligned16(p.a.p) && bs_div4(p.a_bs, p.batch_rank)) {
         am = AM_VEC;
-    else if (p.a.kind == MGC_OP_CONV_NHWC && p.a.cg % 4 == 0 && p.a.C % 4 == 0 &&
-             aligned16(p.a.p) && bs_div4(p.a_bs, p.batch_rank))
+    } else if (p.a.kind == MGC_OP_CONV_NHWC && p.a.cg % 4 == 0 && p.a.C % 4 == 0 &&
+               aligned16(p.a.p) && bs_div4(p.a_bs, p.batch_rank)) {
         am = AM_CONV_VEC;
+    }
     int bm = BD_GEN;
     if (p.b.kind == MGC_OP_STRIDED && p.b.rs == 1 && p.b.cs % 4 == 0 && p.K % 4 == 0 &&
         aligned16(p.b.p) && bs_div4(p.b_bs, p.batch_rank))
@@ -1346,8 +1408,9 @@ static void gemm_launch(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const LnTai
     p.kchunk = (kchunk + 31) / 32 * 32;
     if (p.kchunk == 0) p.kchunk = 32;
     p.ws = g->workspace;
-    p.div_ow = make_fastdiv((unsigned)(p.a.OW > 0 ? p.a.OW : 1));
-    p.div_ohw = make_fastdiv((unsigned)(p.a.OH * p.a.OW > 0 ? p.a.OH * p.a.OW : 1));
+    const mgc_hip_operand &img = am == AM_CAT ? p.a2 : p.a;  // the operand whose rows are pixels
+    p.div_ow = make_fastdiv((unsigned)(img.OW > 0 ? img.OW : 1));
+    p.div_ohw = make_fastdiv((unsigned)(img.OH * img.OW > 0 ? img.OH * img.OW : 1));
     p.div_cg = make_fastdiv((unsigned)(p.a.cg > 0 ? p.a.cg : 1));
     p.div_kw = make_fastdiv((unsigned)(p.a.KW > 0 ? p.a.KW : 1));
 
@@ -1358,6 +1421,10 @@ static void gemm_launch(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const LnTai
         const long ohw = (long)p.a.OH * p.a.OW;
         const long n_img = ohw > 0 ? (p.M + ohw - 1) / ohw : 0;
         a_ext = n_img * p.a.H * p.a.W * p.a.C - (p.a.C - p.a.cg);
+    } else if (am == AM_CAT) {
+        a_ext = (long)(p.M - 1) * p.a.rs + (long)(p.k1 - 1) * p.a.cs + 1;
+        const long ohw = (long)p.a2.OH * p.a2.OW;
+        p.a2_bytes = (p.M + ohw - 1) / ohw * p.a2.H * p.a2.W * p.a2.C * 4;
     } else {
         a_ext = (long)(p.M - 1) * p.a.rs + (long)(p.K - 1) * p.a.cs + 1;
     }
@@ -1374,9 +1441,15 @@ static void gemm_launch(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const LnTai
                   p.ldr >= 0;
     for (int d = 0; d < p.batch_rank; ++d)
         nonneg = nonneg && p.a_bs[d] >= 0 && p.b_bs[d] >= 0 && p.c_bs[d] >= 0 && p.r_bs[d] >= 0;
-    const bool dma_ok = nonneg && (am == AM_VEC || am == AM_CONV_VEC) && bm == BD_NK_VEC && p.K > 0 &&
-                        p.a_bytes > 0 && p.a_bytes < kMaxRes && p.b_bytes > 0 &&
-                        p.b_bytes < kMaxRes;
+    const bool dma_ok = nonneg && (am == AM_VEC || am == AM_CONV_VEC || am == AM_CAT) && bm == BD_NK_VEC &&
+                        p.K > 0 && p.a_bytes > 0 && p.a_bytes < kMaxRes && p.b_bytes > 0 &&
+                        p.b_bytes < kMaxRes && (am != AM_CAT || (p.a2_bytes > 0 && p.a2_bytes < kMaxRes));
+    if (am == AM_CAT && !dma_ok) {  // only the DMA kernels read a second source
+        x->launch_error = (int)hipErrorInvalidValue;
+        set_error("mgc_hip_gemm: concatenated-K GEMM needs a packed [N][K] B and extents below 2 GiB",
+                  hipErrorInvalidValue);
+        return;
+    }
 
     int wsk = dma_ok && !ln && g->split_k <= 0 ? wave_split(p.M, p.N, p.K, batch) : 0;
     if (wsk > 1 && (g->workspace == nullptr || g->workspace_floats < (long)wsk * p.M * p.N)) wsk = 1;

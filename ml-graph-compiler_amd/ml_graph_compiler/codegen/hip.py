@@ -98,6 +98,10 @@ FUSE_ATTENTION = True
 # Run a LayerNormalization that directly follows the FusedGemm producing its input inside that
 # GEMM's split-K reduction (mgc_hip_gemm_layer_norm); tests turn it off to compare.
 FUSE_GEMM_LAYER_NORM = True
+# Compute a residual block's projection shortcut (a 1 x 1 convolution with no activation that
+# only the block's last 1 x 1 convolution reads, as its residual) inside that convolution's GEMM
+# by concatenating the two reductions along K; tests turn it off to compare.
+FUSE_PROJECTION_SHORTCUT = True
 
 MAX_RANK = 6
 MAX_LEAVES = 16
@@ -195,6 +199,55 @@ class WeightsBuilder:
         staging.replace(path)
 
 
+def _pointwise_nhwc(node: Node) -> bool:
+    """A float32 NHWC convolution with a constant 1 x 1 kernel, no padding and one group."""
+    if node.op not in ("Conv", "FusedConv") or ops.conv_layout(node) != "NHWC":
+        return False
+    w, xt = node.input(1), node.input(0).tensor_type
+    if w.data is None or xt.dtype != "float32" or w.tensor_type.shape[:2] != (1, 1):
+        return False
+    if int(node.attrs.get("group", 1)) != 1:
+        return False
+    g = ops.window_geometry(node, xt.shape[1:3], (1, 1))
+    return all(p == 0 for p in g.pads) and all(v is None or v.data is not None for v in node.inputs[2:3])
+
+
+def find_projection_shortcuts(graph: Graph) -> dict[int, Node]:
+    """id(c3) -> ds for every residual block whose projection shortcut ds can run inside the
+    GEMM of the block's last convolution c3 (a ResNet downsample block).
+
+    c3: pointwise NHWC FusedConv, stride 1, whose residual input is ds's output and whose
+    input channels K1 are a multiple of 32 (a whole number of 32-wide K stages before the
+    second source starts). ds: pointwise NHWC convolution with no activation and no residual,
+    any stride, input channels a multiple of 4, whose output only c3 reads (as its residual) and
+    which the schedule puts before c3; its input must be a tensor (not a constant)."""
+    order = {id(n): i for i, n in enumerate(graph.nodes)}
+    outputs = {id(v) for v in graph.outputs}
+    found: dict[int, Node] = {}
+    for c3 in graph.nodes:
+        if c3.op != "FusedConv" or not _pointwise_nhwc(c3):
+            continue
+        r = c3.optional_input(3)
+        ds = r.producer if r is not None else None
+        if ds is None or not _pointwise_nhwc(ds) or id(r) in outputs or r.users != [c3]:
+            continue
+        if sum(v is r for v in c3.inputs) != 1 or order[id(ds)] > order[id(c3)]:
+            continue
+        if ds.op == "FusedConv" and (ds.attrs.get("activation", "none") != "none" or ds.optional_input(3) is not None):
+            continue
+        xt, at = ds.input(0).tensor_type, c3.input(0).tensor_type
+        g3 = ops.window_geometry(c3, at.shape[1:3], (1, 1))
+        gd = ops.window_geometry(ds, xt.shape[1:3], (1, 1))
+        if g3.strides != (1, 1) or tuple(gd.out_hw) != tuple(at.shape[1:3]) or xt.shape[0] != at.shape[0]:
+            continue
+        if ds.input(0).data is not None or at.shape[3] % 32 or xt.shape[3] % 4:
+            continue
+        if ds.input(1).tensor_type.shape[3] != c3.input(1).tensor_type.shape[3]:
+            continue
+        found[id(c3)] = ds
+    return found
+
+
 def pack_b_nk(b: np.ndarray) -> np.ndarray:
     """A constant K x N right-hand side stored as its transpose [N][K] (k contiguous), the
     layout the MFMA GEMM reads with 16-byte k-quad loads."""
@@ -247,8 +300,15 @@ class HipEmitter:
         self.graph = graph
         self.profile = profile
         self._gemm_ws = gemm_workspace
+        # id(last 1 x 1 conv) -> its projection shortcut, and the shortcuts' ids. The shortcut's
+        # input is then read at the last conv's step, which the plan must keep it alive for.
+        self._shortcut: dict[int, Node] = find_projection_shortcuts(graph) if FUSE_PROJECTION_SHORTCUT else {}
+        self._shortcut_skip = {id(ds) for ds in self._shortcut.values()}
+        order = {id(n): i for i, n in enumerate(graph.nodes)}
+        keep = {id(ds.input(0)): order[id(c3)] for c3 in graph.nodes
+                if (ds := self._shortcut.get(id(c3))) is not None}
         self.plan = plan_memory(graph, strategy=strategy, alignment=ALIGN, inplace=inplace,
-                                workspace=self._workspace_bytes)
+                                workspace=self._workspace_bytes, extra_reads=keep)
         self.weights = WeightsBuilder()
         self.body: list[str] = []
         self.kernels: dict[str, int] = {}
@@ -274,7 +334,7 @@ class HipEmitter:
                     out_bytes = max(out_bytes, m.out.tensor_type.nbytes)
                 if m.qkv_gemms:
                     qkv_bytes = max(qkv_bytes, 3 * m.out.tensor_type.nbytes)
-        excluded = set(self._attn_skip) | set(self._attn_emit)
+        excluded = set(self._attn_skip) | set(self._attn_emit) | set(self._shortcut) | self._shortcut_skip
         self._folds = plan_folds(graph, self.plan, self._workspace_bytes, excluded) if FOLD_TRANSPOSES else FoldPlan()
         self._scratch_qkv_off = self._scratch_off
         self._scratch_out_off = self._scratch_off + (qkv_bytes + ALIGN - 1) // ALIGN * ALIGN
@@ -383,7 +443,12 @@ class HipEmitter:
         shape = self._gemm_shape(node)
         if shape is None:
             return 0
-        return 4 * int(self._gemm_ws(*shape))
+        need = 4 * int(self._gemm_ws(*shape))
+        ds = self._shortcut.get(id(node))
+        if ds is not None:  # the GEMM over both reductions
+            m, n, k, batch = shape
+            need = max(need, 4 * int(self._gemm_ws(m, n, k + ds.input(0).tensor_type.shape[3], batch)))
+        return need
 
     # -- pointers ------------------------------------------------------------------------------
     def _root(self, value: Value) -> Value:
@@ -446,6 +511,10 @@ class HipEmitter:
             return
         if id(node) in self._s2d_skip:
             self.emit("/* read in NCHW by the space-to-depth copy of the convolution it feeds */")
+            self.count("folded")
+            return
+        if id(node) in self._shortcut_skip:
+            self.emit("/* projection shortcut: computed in the GEMM of the convolution that adds it */")
             self.count("folded")
             return
         if id(node) in self._ln_skip:
@@ -854,9 +923,10 @@ class HipEmitter:
                    bias: str = "NULL", bias_mode: int = 0, res: str = "NULL", ldr: int = 0,
                    beta: float = 1.0, act: str = "none", lo: float = 0.0, hi: float = 6.0,
                    workspace: str = "NULL", workspace_floats: int = 0,
-                   layer_norm: tuple[str, str, str, str] | None = None) -> None:
+                   layer_norm: tuple[str, str, str, str] | None = None, extra: Sequence[str] = ()) -> None:
         """One mgc_hip_gemm call; ``layer_norm`` = (scale, bias, eps, out) makes it an
-        mgc_hip_gemm_layer_norm call whose split-K reduction also normalizes the rows."""
+        mgc_hip_gemm_layer_norm call whose split-K reduction also normalizes the rows; ``extra``
+        are further field assignments (the concatenated-K operand)."""
         if len(batch) > MAX_BATCH_RANK:
             raise CodegenError(f"GEMM with {len(batch)} batch dimensions is not supported")
         parts = ["mgc_hip_gemm_args g; memset(&g, 0, sizeof g);", f"g.M = {m}; g.N = {n}; g.K = {k};"]
@@ -869,6 +939,7 @@ class HipEmitter:
             for d, (dim, abs_, bbs, cbs, rbs) in enumerate(batch):
                 parts.append(f"g.batch_dims[{d}] = {dim}; g.a_bs[{d}] = {abs_}L; g.b_bs[{d}] = {bbs}L; g.c_bs[{d}] = {cbs}L; g.r_bs[{d}] = {rbs}L;")
         parts.append(f"g.workspace = {workspace}; g.workspace_floats = {workspace_floats}L;")
+        parts += extra
         if layer_norm is not None:
             scale, lbias, eps, out = layer_norm
             parts.append(f"mgc_hip_gemm_layer_norm(x, &g, {scale}, {lbias}, {eps}, {out});")
@@ -1125,6 +1196,9 @@ class HipEmitter:
         if id(node) in self._s2d:
             self._conv_space_to_depth(node, bias, res, act, lo, hi)
             return
+        if id(node) in self._shortcut:
+            self._conv_with_shortcut(node, self._shortcut[id(node)])
+            return
         kg = kout // group
         geo = (f"g.{{f}}.H = {h}; g.{{f}}.W = {wd}; g.{{f}}.C = {c}; g.{{f}}.KH = {kh}; g.{{f}}.KW = {kw}; "
                f"g.{{f}}.SH = {g.strides[0]}; g.{{f}}.SW = {g.strides[1]}; g.{{f}}.DH = {g.dilations[0]}; "
@@ -1160,6 +1234,49 @@ class HipEmitter:
                     batch=batch, bias=gbias, bias_mode=2 if bias != "NULL" else 0,
                     res=f"({res} + {gi * kg * plane})" if res != "NULL" else "NULL", ldr=plane, act=act, lo=lo, hi=hi,
                 )
+
+    def _conv_with_shortcut(self, node: Node, ds: Node) -> None:
+        """act(a W3 + x_s Wd + b3 + bd) as one GEMM over K = K1 + C2: a is the pointwise
+        convolution's NHWC input (K1 channels), x_s the shortcut's input x sampled at its
+        stride (C2 channels), B the two weight matrices stacked along K and the bias their sum.
+        The shortcut's output is never written. When a or x is a caller buffer the generated
+        code checks its 16-byte alignment and otherwise runs the two convolutions apart."""
+        a, xv = node.input(0), ds.input(0)
+        nb, oh, ow, k1 = a.tensor_type.shape
+        _, h2, w2, c2 = xv.tensor_type.shape
+        w3, wd = node.input(1).data, ds.input(1).data
+        n = w3.shape[3]
+        stacked = np.concatenate([w3.reshape(k1, n), wd.reshape(c2, n)], axis=0).astype(np.float32)
+        bspec = self._packed_b(stacked, ("shortcut", id(node.input(1)), id(ds.input(1))))
+        biases = [v.data for v in (node.optional_input(2), ds.optional_input(2)) if v is not None]
+        bias = "NULL"
+        if biases:  # summed in double, rounded once
+            total = sum(np.asarray(b, np.float64).reshape(n) for b in biases)
+            bias = f"(const float *)(W + {self.weights.add(total.astype(np.float32), key=('shortcut_bias', id(node)))})"
+        sh, sw = ops.window_geometry(ds, (h2, w2), (1, 1)).strides
+        act, lo, hi = self._act(node)
+        ws, ws_floats = self._workspace(node)
+        a2 = (f"g.a2.kind = MGC_OP_CONV_NHWC; g.a2.p = {self.fptr(xv)}; g.a2.H = {h2}; g.a2.W = {w2}; "
+              f"g.a2.C = {c2}; g.a2.KH = 1; g.a2.KW = 1; g.a2.SH = {sh}; g.a2.SW = {sw}; g.a2.DH = 1; "
+              f"g.a2.DW = 1; g.a2.PT = 0; g.a2.PL = 0; g.a2.OH = {oh}; g.a2.OW = {ow}; g.a2.cg = {c2}; "
+              f"g.k1 = {k1};")
+        external = [v for v in (a, xv) if self.plan.location(v).kind == "input"]
+        if external:
+            cond = " && ".join(f"(((uintptr_t){self.ptr(v)} & 15) == 0)" for v in external)
+            self.emit(f"if ({cond}) {{")
+        self._gemm_call(nb * oh * ow, n, k1 + c2, self._strided("a", self.fptr(a), k1, 1), bspec,
+                        self.fptr(node.output), n, bias=bias, bias_mode=1 if bias != "NULL" else 0,
+                        act=act, lo=lo, hi=hi, workspace=ws, workspace_floats=ws_floats, extra=[a2])
+        self.count("gemm_shortcut")
+        if external:
+            self.emit("} else {")
+            saved = self._shortcut.pop(id(node))
+            try:
+                self.op_FusedConv(ds)
+                self.op_FusedConv(node)
+            finally:
+                self._shortcut[id(node)] = saved
+            self.emit("}")
 
     # -- space-to-depth convolution -------------------------------------------------------------
     @staticmethod
@@ -1312,6 +1429,7 @@ class HipEmitter:
         head = [
             "/* Generated by ml-graph-compiler (hip backend, gfx950). Host code only: every node is",
             " * one launcher call into libmgc_hip.so with constant offsets. */",
+            "#include <stdint.h>",
             "#include <string.h>",
             "#include <math.h>",
             '#include "mgc_hip.h"',

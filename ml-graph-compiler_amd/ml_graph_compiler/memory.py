@@ -24,7 +24,7 @@ tests/golden/reference_plans.json. The rules that fix them:
 
 from __future__ import annotations
 
-from collections.abc import Callable
+from collections.abc import Callable, Mapping
 from dataclasses import dataclass, field
 from itertools import accumulate
 from typing import Literal
@@ -186,8 +186,13 @@ def _peak_concurrent(blocks: list[Buffer], steps: int) -> int:
 
 
 def plan_memory(graph: Graph, strategy: Strategy = "greedy_by_size", alignment: int = 64,
-                inplace: bool = True, workspace: WorkspaceFn | None = None) -> MemoryPlan:
-    """Assign every non-constant value of a scheduled graph a location."""
+                inplace: bool = True, workspace: WorkspaceFn | None = None,
+                extra_reads: Mapping[int, int] | None = None) -> MemoryPlan:
+    """Assign every non-constant value of a scheduled graph a location.
+
+    ``extra_reads`` maps id(value) to a step at which a code generator reads that value besides
+    the graph's own readers (a node fused into a later one reads its inputs there): the value
+    then stays alive, and unwritten, through that step."""
     if strategy not in STRATEGIES:
         raise GraphError(f"unknown strategy {strategy!r}; known: {STRATEGIES}")
     steps = len(graph.nodes)
@@ -199,6 +204,8 @@ def plan_memory(graph: Graph, strategy: Strategy = "greedy_by_size", alignment: 
                 last_read[id(v)] = step
     for v in graph.outputs:
         last_read[id(v)] = steps
+    for key, step in (extra_reads or {}).items():
+        last_read[key] = max(last_read.get(key, -1), step)
     output_ids = {id(v) for v in graph.outputs}
 
     slots = _Slots()

@@ -82,6 +82,7 @@ def test_kernel_mix_matches_reference(name, kernels, arena, monkeypatch):
     from ml_graph_compiler.codegen import hip as hip_codegen
 
     make = builders.SAMPLES.get(name) or builders.CONFIGS[name]
+    monkeypatch.setattr(hip_codegen, "FUSE_PROJECTION_SHORTCUT", False)
     monkeypatch.setattr(hip_codegen, "SPACE_TO_DEPTH", False)
     gen = generate_hip(o3(make()))
     assert gen.kernels == kernels
@@ -95,6 +96,32 @@ def test_kernel_mix_matches_reference(name, kernels, arena, monkeypatch):
     assert s2d.plan.arena_bytes == gen.plan.arena_bytes
     assert gen.weights.nbytes % 256 == 0 and len(gen.weights.digest()) == 24
     assert "mgc_forward" in gen.source and "int mgc_run(" in gen.source
+
+
+def test_projection_shortcuts_join_their_block_gemm():
+    """ResNet-50's four downsample blocks each lose their shortcut GEMM; the shortcut input
+    stays alive (its arena block clear of everything placed) until the fused GEMM reads it."""
+    from ml_graph_compiler.codegen.hip import find_projection_shortcuts
+
+    g = o3(builders.resnet50())
+    pairs = find_projection_shortcuts(g)
+    assert len(pairs) == 4
+    gen = generate_hip(g, gemm_workspace=native.gemm_workspace_floats)
+    assert gen.kernels["gemm_shortcut"] == 4 and gen.kernels["gemm"] == 50
+    assert gen.source.count("g.k1 = ") == 4
+    order = {id(n): i for i, n in enumerate(g.nodes)}
+    by_value = {id(v): b for b in gen.plan.buffers for v in b.values}
+    for c3 in g.nodes:
+        ds = pairs.get(id(c3))
+        if ds is None:
+            continue
+        x = by_value[id(ds.input(0))]
+        assert x.end >= order[id(c3)]
+        for b in gen.plan.buffers:
+            if b is x or not (b.start <= order[id(c3)] <= b.end):
+                continue
+            assert b.offset + b.size <= x.offset or x.offset + x.size <= b.offset
+    assert not find_projection_shortcuts(o3(builders.bottleneck()))  # identity shortcuts only
 
 
 def test_every_sample_and_config_generates_and_builds(hip_cache):

@@ -52,6 +52,7 @@ class GemmArgs(ctypes.Structure):
         ("a_bs", ctypes.c_long * 4), ("b_bs", ctypes.c_long * 4), ("c_bs", ctypes.c_long * 4), ("r_bs", ctypes.c_long * 4),
         ("workspace", ctypes.c_void_p), ("workspace_floats", ctypes.c_long),
         ("split_k", ctypes.c_int),
+        ("a2", Operand), ("k1", ctypes.c_int),
     ]
 
 
