@@ -81,7 +81,7 @@ struct GemmDev {
     mgc_hip_operand a2;     // AM_CAT: the image whose 1 x 1 strided window gives columns >= k1
     int k1;
     long a2_bytes;
-    int nbatch;                       // batch elements  // 16-byte epilogue accesses are aligned (ldc, ldr, pointers)
+    int nbatch;   // batch elements
 };
 
 __device__ __forceinline__ void batch_offsets(const GemmDev &p, int bz, long &ao, long &bo,
@@ -956,6 +956,246 @@ __global__ void __launch_bounds__(256) gemm_dma_wsplit_kernel(const GemmDev p) {
     gemm_lds_to_global<T, T>(p, Cs, m0, n0, ks, co, ro);
 }
 
+// vmcnt wait for a count known only at run time (0 <= n < 8 stages of PER loads each).
+template <int PER>
+__device__ __forceinline__ void wait_stages(int n) {
+    switch (n) {
+    case 0: wait_vmcnt<0>(); break;
+    case 1: wait_vmcnt<PER>(); break;
+    case 2: wait_vmcnt<2 * PER>(); break;
+    case 3: wait_vmcnt<3 * PER>(); break;
+    case 4: wait_vmcnt<4 * PER>(); break;
+    case 5: wait_vmcnt<5 * PER>(); break;
+    case 6: wait_vmcnt<6 * PER>(); break;
+    default: wait_vmcnt<7 * PER>(); break;
+    }
+}
+
+// GEMM / implicit-GEMM convolution on 16 x 16 output tiles whose K range is dealt out to the
+// workgroup's WAVES waves (wave w takes the 32-wide K stages w, w + WAVES, ...), each with a
+// STAGES-deep DMA ring of its own, on v_mfma_f32_16x16x4f32 (the 32 x 32 x 2 form's rate per
+// SIMD). For batch-1 layers whose 32 x 32 tiles are too few for the CUs even with their K dealt
+// to four waves: a 14 x 14 image with 256 output channels has 56 tiles of 32 x 32 and 208 of
+// 16 x 16, so the latter needs no K split over workgroups and no reduction launch. A stage is
+// a quarter of a 32 x 32 stage's MFMA work; with eight waves two share each SIMD, so one
+// multiplies while the other waits for its loads.
+// Operand forms as gemm_dma_wsplit_kernel; row r of a 16-row block keeps k-chunk q at LDS
+// position q ^ (r & 7).
+//
+// The k order inside a stage is permuted: lane group g = lane / 16 reads chunks 2g and 2g + 1
+// (k = 8g .. 8g + 7) of its row and MFMA j takes element j of those eight, so instruction j
+// multiplies A[:, 8g + j] by B[8g + j, :] over the four groups; A and B use the same
+// permutation, and the eight instructions cover the stage's 32 k once. Register r of the
+// 16 x 16 accumulator holds row 4 (lane / 16) + r, column lane % 16.
+//
+// The epilogue's bias and residual chunks are requested before the main loop, so their latency
+// overlaps the K loop instead of following it.
+template <int AMODE, int STAGES, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES) gemm_dma_wsplit16_kernel(const GemmDev p) {
+    constexpr int BK = 32, T = 16;
+    constexpr int STAGE = 2 * T * BK;  // one wave's A and B blocks of one stage (floats)
+    constexpr int RING = STAGES * STAGE;
+    constexpr int LDC = T + 4;
+    constexpr int SMEM = WAVES * RING;
+    constexpr int PER = 4;  // DMA loads per lane per stage (two A, two B)
+    static_assert(WAVES * T * LDC <= SMEM, "epilogue staging");
+    static_assert(STAGES >= 2 && STAGES <= 8, "stages");
+    static_assert(AMODE == AM_VEC || AMODE == AM_CONV_VEC || AMODE == AM_CAT, "vector A only");
+
+    __shared__ __attribute__((aligned(16))) float smem[SMEM];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    const int nb = gridDim.x;
+    const int full = nb & ~7;
+    int lin = blockIdx.x;
+    if (lin < full) {  // consecutive tiles (which share A rows) on one XCD
+        const int per = full >> 3;
+        lin = (lin & 7) * per + (lin >> 3);
+    }
+    const int tm = lin / p.tiles_n;
+    const int tn = lin - tm * p.tiles_n;
+    const int m0 = tm * T, n0 = tn * T;
+
+    const int bz = blockIdx.z / p.split;
+    const int ks = blockIdx.z - bz * p.split;
+    long ao, bo, co, ro;
+    batch_offsets(p, bz, ao, bo, co, ro);
+
+    // ---- epilogue operands first (thread t < 64: row t / 4, columns 4 (t % 4) .. + 3) ------
+    const bool split_out = p.split > 1;
+    const int er = tid >> 2, ec = (tid & 3) * 4;
+    const int erow = m0 + er, ecol = n0 + ec;
+    const bool eok = tid < 64 && erow < p.M && ecol < p.N;
+    const bool efull = eok && ecol + 4 <= p.N && (split_out ? (p.N % 4 == 0) : p.vec_out != 0);
+    const f4 zero4 = {0.f, 0.f, 0.f, 0.f};
+    f4 ebias = zero4, eres = zero4;
+    if (efull && !split_out) {
+        if (p.bias && p.bias_mode == 1) ebias = ldg4(p.bias + ecol);
+        if (p.res) eres = ldg4(p.res + ro + (long)erow * p.ldr + ecol);
+    }
+
+    const float *abase = p.a.p + ao;
+    const float *bbase = p.b.p + bo;
+    const int kbeg = ks * p.kchunk;
+    const int kend = min(p.K, kbeg + p.kchunk);
+    const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+    const int nkw = nk > wave ? (nk - 1 - wave) / WAVES + 1 : 0;  // this wave's stages
+
+    const int rsub = lane >> 3;
+    const int q4 = ((lane & 7) ^ rsub) * 4;  // this lane's k offset within a stage
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)abase, (short)0, (int)(p.a_bytes - ao * 4), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)bbase, (short)0, (int)(p.b_bytes - bo * 4), 0x00020000);
+    const __amdgpu_buffer_rsrc_t ra2 = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(AMODE == AM_CAT ? p.a2.p : abase), (short)0, (int)(AMODE == AM_CAT ? p.a2_bytes : 0), 0x00020000);
+    constexpr unsigned OOB = 0x80000000u;
+    unsigned aoff[2], aoff2[2], boff[2];
+    int aih[2], aiw[2];
+    const int ohw = AMODE == AM_CAT ? p.a2.OH * p.a2.OW : p.a.OH * p.a.OW;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int m = m0 + i * 8 + rsub;
+        aoff[i] = aoff2[i] = OOB;
+        aih[i] = aiw[i] = -0x40000000;
+        if (m < p.M) {
+            if (AMODE == AM_CAT) {
+                const int n = fdiv(m, p.div_ohw), rr = m - n * ohw;
+                const int oh = fdiv(rr, p.div_ow), ow = rr - oh * p.a2.OW;
+                aoff2[i] = (unsigned)(((n * p.a2.H + oh * p.a2.SH) * p.a2.W + ow * p.a2.SW) * p.a2.C) * 4u;
+            }
+            if (AMODE == AM_CONV_VEC) {
+                const int n = fdiv(m, p.div_ohw), rr = m - n * ohw;
+                const int oh = fdiv(rr, p.div_ow), ow = rr - oh * p.a.OW;
+                aih[i] = oh * p.a.SH - p.a.PT;
+                aiw[i] = ow * p.a.SW - p.a.PL;
+                aoff[i] = (unsigned)(((n * p.a.H + aih[i]) * p.a.W + aiw[i]) * p.a.C) * 4u;
+            } else {
+                aoff[i] = (unsigned)m * (unsigned)p.a.rs * 4u;
+            }
+        }
+        const int n = n0 + i * 8 + rsub;
+        boff[i] = n < p.N ? (unsigned)n * (unsigned)p.b.cs * 4u : OOB;
+    }
+    int knext = kbeg + wave * BK + q4;
+    int cc = 0, ckw = 0, ckh = 0;
+    if (AMODE == AM_CONV_VEC) {
+        const int t = fdiv(knext, p.div_cg);
+        cc = knext - t * p.a.cg;
+        ckh = fdiv(t, p.div_kw);
+        ckw = t - ckh * p.a.KW;
+    }
+    float *const ring = smem + wave * RING;
+
+    auto issue = [&](int buf) __attribute__((always_inline)) {
+        const int k = knext;
+        const bool kok = k < kend;
+        float *sa = ring + buf * STAGE;
+        float *sb = sa + T * BK;
+        if constexpr (AMODE == AM_VEC) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) dma16_buf(ra, kok ? aoff[i] + (unsigned)k * 4u : OOB, sa + i * 8 * BK);
+        } else if constexpr (AMODE == AM_CAT) {
+            // k1 is a multiple of 32, so a whole stage reads one source
+            if (k < p.k1) {
+#pragma unroll
+                for (int i = 0; i < 2; ++i) dma16_buf(ra, kok ? aoff[i] + (unsigned)k * 4u : OOB, sa + i * 8 * BK);
+            } else {
+                const unsigned k2 = (unsigned)(k - p.k1) * 4u;
+#pragma unroll
+                for (int i = 0; i < 2; ++i) dma16_buf(ra2, kok ? aoff2[i] + k2 : OOB, sa + i * 8 * BK);
+            }
+        } else {
+            const int dh = ckh * p.a.DH, dw = ckw * p.a.DW;
+            const unsigned koff = (unsigned)((dh * p.a.W + dw) * p.a.C + cc) * 4u;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const bool ok = kok && (unsigned)(aih[i] + dh) < (unsigned)p.a.H &&
+                                (unsigned)(aiw[i] + dw) < (unsigned)p.a.W;
+                dma16_buf(ra, ok ? aoff[i] + koff : OOB, sa + i * 8 * BK);
+            }
+            cc += WAVES * BK;
+            while (cc >= p.a.cg) {
+                cc -= p.a.cg;
+                if (++ckw == p.a.KW) {
+                    ckw = 0;
+                    ++ckh;
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) dma16_buf(rb, kok ? boff[i] + (unsigned)k * 4u : OOB, sb + i * 8 * BK);
+        knext = k + WAVES * BK;
+    };
+
+    f4 acc = zero4;
+    const int li = lane & 15;
+    const int lg = lane >> 4;
+    const int sw = li & 7;
+    const int pa = li * BK + (((2 * lg) ^ sw) << 2);      // chunk 2g of row li
+    const int pb = li * BK + (((2 * lg + 1) ^ sw) << 2);  // chunk 2g + 1
+
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s)
+        if (s < nkw) issue(s);
+    for (int kt = 0; kt < nkw; ++kt) {
+        // stage kt has landed once at most the later stages' loads are outstanding; this wave's
+        // reads of the buffer the next issue overwrites (stage kt - 1) are complete
+        wait_stages<PER>(min(nkw - 1 - kt, STAGES - 2));
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (kt + STAGES - 1 < nkw) issue((kt + STAGES - 1) % STAGES);
+        const float *as = ring + (kt % STAGES) * STAGE;
+        const float *bs = as + T * BK;
+        const f4 a0 = *reinterpret_cast<const f4 *>(&as[pa]);
+        const f4 a1 = *reinterpret_cast<const f4 *>(&as[pb]);
+        const f4 b0 = *reinterpret_cast<const f4 *>(&bs[pa]);
+        const f4 b1 = *reinterpret_cast<const f4 *>(&bs[pb]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[e], b0[e], acc, 0, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a1[e], b1[e], acc, 0, 0, 0);
+    }
+    __syncthreads();  // every wave is done with its ring (the slots below overlap the rings)
+    float *const slot = smem + wave * (T * LDC);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) slot[(4 * lg + r) * LDC + li] = acc[r];
+    __syncthreads();
+    if (!eok) return;
+    const int o = er * LDC + ec;
+    f4 v = *reinterpret_cast<const f4 *>(&smem[o]);
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) v += *reinterpret_cast<const f4 *>(&smem[w * T * LDC + o]);
+    const int ncol = min(4, p.N - ecol);
+    if (split_out) {
+        float *dst = p.ws + (long)ks * p.M * p.N + (long)erow * p.N + ecol;
+        if (efull) {
+            *reinterpret_cast<f4 *>(dst) = v;
+        } else {
+            for (int e = 0; e < ncol; ++e) dst[e] = v[e];
+        }
+        return;
+    }
+    if (!efull) {  // scalar bias and residual reads
+        for (int e = 0; e < ncol; ++e) {
+            if (p.bias && p.bias_mode == 1) ebias[e] = ldg(p.bias + ecol + e);
+            if (p.res) eres[e] = ldg(p.res + ro + (long)erow * p.ldr + ecol + e);
+        }
+    }
+    v = v * p.alpha + ebias;
+    if (p.bias && p.bias_mode == 2) v += ldg(p.bias + erow);
+    if (p.res) v += p.beta * eres;
+    v = act4(v, p.act, p.lo, p.hi);
+    float *dst = p.c + co + (long)erow * p.ldc + ecol;
+    if (efull) {
+        *reinterpret_cast<f4 *>(dst) = v;
+    } else {
+        for (int e = 0; e < ncol; ++e) dst[e] = v[e];
+    }
+}
+
 // Sum the split-K partials and apply the epilogue (one batch element).
 __global__ void gemm_splitk_reduce(const GemmDev p) {
     const long total = (long)p.M * p.N;
@@ -1071,6 +1311,23 @@ static GemmKernel pick_dma(int am) {
                           : &gemm_dma_kernel<BM, BN, WGM, 2, AM_CONV_VEC>;
 }
 
+// 16 x 16 wave-split launches: eight waves with three-stage rings for K of 1024 and more (two
+// waves per SIMD, one computing while the other waits for its loads), four waves with
+// two-stage rings below. Measured against each other (same table as use_tile16): eight waves
+// 5.9 / 7.3 / 6.7 us on 196 x 256 x 1024 / 49 x 512 x 2048 / 1 x 1000 x 2048 against 6.2 /
+// 8.2 / 7.9 with four waves and four stages; four waves 5.6 us on 784 x 128 x 512 against 7.1
+// with eight; rings of 6 and 8 stages were slower throughout.
+static int wsplit16_waves(int K) { return K >= 1024 ? 8 : 4; }
+
+template <int STAGES, int WAVES>
+static GemmKernel pick16(int am) {
+    return am == AM_VEC   ? &gemm_dma_wsplit16_kernel<AM_VEC, STAGES, WAVES>
+           : am == AM_CAT ? &gemm_dma_wsplit16_kernel<AM_CAT, STAGES, WAVES>
+                          : &gemm_dma_wsplit16_kernel<AM_CONV_VEC, STAGES, WAVES>;
+}
+
+static GemmKernel pick_wsplit16(int am, int K) { return wsplit16_waves(K) == 8 ? pick16<3, 8>(am) : pick16<2, 4>(am); }
+
 static GemmKernel pick_wsplit(int am) {
     return am == AM_VEC   ? &gemm_dma_wsplit_kernel<AM_VEC>
            : am == AM_CAT ? &gemm_dma_wsplit_kernel<AM_CAT>
@@ -1162,6 +1419,20 @@ static int wave_split(int M, int N, int K, int batch) {
         }
     }
     return best;
+}
+
+// 16 x 16 tiles instead of the 32 x 32 wave-split launch: when there are at most two of them
+// per CU (512) and K is at most 2560. Graph replays of 16 independent GEMMs per shape at batch 1
+// on MI355X, us per GEMM, 32 x 32 wave split (with its K split and reduction where it takes
+// one) against 16 x 16: 784 x 128 x 512 6.8 / 5.6, 196 x 256 x 1024 9.1 / 5.9, 196 x 512 x 1024
+// 9.3 / 7.4, 49 x 2048 x 512 6.9 / 6.2, 49 x 512 x 2048 9.9 / 7.3, 1 x 1000 x 2048 9.0 / 6.7,
+// 128 x 768 x 768 8.1 / 6.9; 3 x 3 convolutions 28 x 28 x 128 11.5 / 8.1, 14 x 14 x 256
+// 12.7 / 8.9. Where the rule says no: 128 x 2304 x 768 (1152 tiles) 12.0 / 14.4,
+// 128 x 3072 x 768 12.3 / 16.8, 196 x 1024 x 256 6.0 / 7.5, 56 x 56 x 64 3 x 3 8.0 / 7.9,
+// deep K: 128 x 768 x 3072 14.7 / 15.5, 7 x 7 x 512 3 x 3 (K 4608) 12.9 / 13.0.
+static bool use_tile16(int M, int N, int K) {
+    const long tiles16 = (long)((M + 15) / 16) * ((N + 15) / 16);
+    return tiles16 <= 2 * kCUs && K <= 2560;
 }
 
 // The same choice for a GEMM whose split-K reduction ends in a LayerNorm (the split is
@@ -1454,27 +1725,31 @@ static void gemm_launch(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const LnTai
     int wsk = dma_ok && !ln && g->split_k <= 0 ? wave_split(p.M, p.N, p.K, batch) : 0;
     if (wsk > 1 && (g->workspace == nullptr || g->workspace_floats < (long)wsk * p.M * p.N)) wsk = 1;
     if (dma_ok && ln && batch == 1 && p.split >= 2) wsk = wave_split_ln(p.M, p.N, p.K, p.split);
+    const bool w16 = wsk > 0 && !ln && batch == 1 && use_tile16(p.M, p.N, p.K);
+    if (w16) wsk = 1;
     const bool wsplit = wsk > 0;
     if (wsplit) {
         p.split = wsk;
         p.kchunk = ((p.K + wsk - 1) / wsk + 31) / 32 * 32;
     }
     const bool narrow = dma_ok && !wsplit && narrow_tiles(p.N, p.split);
-    t.bm = wsplit ? 32 : narrow ? 128 : 64;
-    t.bn = wsplit || narrow ? 32 : 64;
+    t.bm = w16 ? 16 : wsplit ? 32 : narrow ? 128 : 64;
+    t.bn = w16 ? 16 : wsplit || narrow ? 32 : 64;
     p.tiles_m = (p.M + t.bm - 1) / t.bm;
     p.tiles_n = (p.N + t.bn - 1) / t.bn;
-    const GemmKernel kern = wsplit   ? pick_wsplit(am)
+    const GemmKernel kern = w16      ? pick_wsplit16(am, p.K)
+                            : wsplit ? pick_wsplit(am)
                             : narrow ? pick_dma<128, 32, 4>(am)
                             : dma_ok ? pick_dma<64, 64, 2>(am)
                                      : pick_kernel<64, 64, 2>(am, bm);
+    const int threads = w16 ? 64 * wsplit16_waves(p.K) : 256;
     const dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)(batch * p.split));
     if (ln && p.split < 2) {  // the workspace did not allow the split the reduction needs
         x->launch_error = (int)hipErrorInvalidValue;
         set_error("mgc_hip_gemm_layer_norm: no K split", hipErrorInvalidValue);
         return;
     }
-    MGC_LAUNCH(x, kern, grid, dim3(256), 0, p);
+    MGC_LAUNCH(x, kern, grid, dim3(threads), 0, p);
     if (ln) {
         // a wavefront per row; one-wave workgroups when there are few rows, to spread them over CUs
         const int rows_per_block = p.M >= 1024 ? 4 : 1;
