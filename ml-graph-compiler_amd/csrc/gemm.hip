@@ -771,8 +771,9 @@ __global__ void __launch_bounds__(256) gemm_dma_kernel(const GemmDev p) {
 
 // GEMM / implicit-GEMM convolution on 32 x 32 output tiles whose K range is dealt out to the
 // workgroup's four waves (wave w takes the 32-wide K stages w, w + 4, ...), each with its own
-// two-stage DMA ring in LDS; the four partial tiles are summed through LDS in wave order before
-// the shared epilogue. For GEMMs whose 64 x 64 tiles are too few to occupy the CUs (small M at
+// two-stage DMA ring in LDS; the four partial tiles are summed through LDS in wave order, each
+// thread adding the 16-byte chunk whose bias and residual it requested when the kernel started
+// (their latency overlaps the K loop). For GEMMs whose 64 x 64 tiles are too few to occupy the CUs (small M at
 // batch 1), where the alternative is a K split over workgroups and a second kernel that adds
 // the partials: this kernel spreads the same work over four times as many tiles and finishes
 // in one launch. The waves synchronise only around the epilogue; in the main loop each wave
@@ -786,8 +787,8 @@ __global__ void __launch_bounds__(256) gemm_dma_wsplit_kernel(const GemmDev p) {
     constexpr int STAGE = 2 * T * BK;  // one wave's A and B blocks of one stage (floats)
     constexpr int RING = 2 * STAGE;    // two stages per wave
     constexpr int LDC = T + 8;
-    constexpr int SMEM = 4 * RING;     // 64 KB; the epilogue uses 5 * T * LDC floats of it
-    static_assert(5 * T * LDC <= SMEM, "epilogue staging");
+    constexpr int SMEM = 4 * RING;     // 64 KB; the epilogue uses 4 * T * LDC floats of it
+    static_assert(4 * T * LDC <= SMEM, "epilogue staging");
     static_assert(AMODE == AM_VEC || AMODE == AM_CONV_VEC || AMODE == AM_CAT, "vector A only");
 
     __shared__ __attribute__((aligned(16))) float smem[SMEM];
@@ -811,6 +812,20 @@ __global__ void __launch_bounds__(256) gemm_dma_wsplit_kernel(const GemmDev p) {
     const int ks = blockIdx.z - bz * p.split;
     long ao, bo, co, ro;
     batch_offsets(p, bz, ao, bo, co, ro);
+
+    // epilogue operands first: thread t owns row t / 8, columns 4 (t % 8) .. + 3
+    const bool split_out = p.split > 1;
+    const int er = tid >> 3, ec = (tid & 7) * 4;
+    const int erow = m0 + er, ecol = n0 + ec;
+    const bool eok = erow < p.M && ecol < p.N;
+    const bool efull = eok && ecol + 4 <= p.N && (split_out ? (p.N % 4 == 0) : p.vec_out != 0);
+    const f4 zero4 = {0.f, 0.f, 0.f, 0.f};
+    f4 ebias = zero4, eres = zero4;
+    if (efull && !split_out) {
+        if (p.bias && p.bias_mode == 1) ebias = ldg4(p.bias + ecol);
+        if (p.res) eres = ldg4(p.res + ro + (long)erow * p.ldr + ecol);
+    }
+
     const float *abase = p.a.p + ao;
     const float *bbase = p.b.p + bo;
     const int kbeg = ks * p.kchunk;
@@ -942,18 +957,38 @@ __global__ void __launch_bounds__(256) gemm_dma_wsplit_kernel(const GemmDev p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) slot[((r >> 2) * 8 + lh * 4 + (r & 3)) * LDC + li] = acc[r];
     __syncthreads();
-    float *const Cs = smem + 4 * T * LDC;
-    {
-        const int row = tid >> 3, c = (tid & 7) * 4;
-        const int o = row * LDC + c;
-        f4 v = *reinterpret_cast<const f4 *>(&smem[o]);
-        v += *reinterpret_cast<const f4 *>(&smem[T * LDC + o]);
-        v += *reinterpret_cast<const f4 *>(&smem[2 * T * LDC + o]);
-        v += *reinterpret_cast<const f4 *>(&smem[3 * T * LDC + o]);
-        *reinterpret_cast<f4 *>(&Cs[o]) = v;
+    if (!eok) return;
+    const int o = er * LDC + ec;
+    f4 v = *reinterpret_cast<const f4 *>(&smem[o]);
+    v += *reinterpret_cast<const f4 *>(&smem[T * LDC + o]);
+    v += *reinterpret_cast<const f4 *>(&smem[2 * T * LDC + o]);
+    v += *reinterpret_cast<const f4 *>(&smem[3 * T * LDC + o]);
+    const int ncol = min(4, p.N - ecol);
+    if (split_out) {
+        float *dst = p.ws + (long)ks * p.M * p.N + (long)erow * p.N + ecol;
+        if (efull) {
+            *reinterpret_cast<f4 *>(dst) = v;
+        } else {
+            for (int e = 0; e < ncol; ++e) dst[e] = v[e];
+        }
+        return;
     }
-    __syncthreads();
-    gemm_lds_to_global<T, T>(p, Cs, m0, n0, ks, co, ro);
+    if (!efull) {  // scalar bias and residual reads
+        for (int e = 0; e < ncol; ++e) {
+            if (p.bias && p.bias_mode == 1) ebias[e] = ldg(p.bias + ecol + e);
+            if (p.res) eres[e] = ldg(p.res + ro + (long)erow * p.ldr + ecol + e);
+        }
+    }
+    v = v * p.alpha + ebias;
+    if (p.bias && p.bias_mode == 2) v += ldg(p.bias + erow);
+    if (p.res) v += p.beta * eres;
+    v = act4(v, p.act, p.lo, p.hi);
+    float *dst = p.c + co + (long)erow * p.ldc + ecol;
+    if (efull) {
+        *reinterpret_cast<f4 *>(dst) = v;
+    } else {
+        for (int e = 0; e < ncol; ++e) dst[e] = v[e];
+    }
 }
 
 // vmcnt wait for a count known only at run time (0 <= n < 8 stages of PER loads each).
@@ -1430,9 +1465,15 @@ static int wave_split(int M, int N, int K, int batch) {
 // 12.7 / 8.9. Where the rule says no: 128 x 2304 x 768 (1152 tiles) 12.0 / 14.4,
 // 128 x 3072 x 768 12.3 / 16.8, 196 x 1024 x 256 6.0 / 7.5, 56 x 56 x 64 3 x 3 8.0 / 7.9,
 // deep K: 128 x 768 x 3072 14.7 / 15.5, 7 x 7 x 512 3 x 3 (K 4608) 12.9 / 13.0.
-static bool use_tile16(int M, int N, int K) {
+// Deeper K (the 3 x 3 convolutions of a 7 x 7 image, K 4608) splits into chunks of at most 2304
+// when the split tiles still number at most 512 and the workspace allows the split (wsk, the
+// 32 x 32 launch's split, is what it was sized for); returns that split, 1 without, 0 for the
+// 32 x 32 tiles.
+static int use_tile16(int M, int N, int K, int wsk) {
     const long tiles16 = (long)((M + 15) / 16) * ((N + 15) / 16);
-    return tiles16 <= 2 * kCUs && K <= 2560;
+    if (K <= 2560) return tiles16 <= 2 * kCUs ? 1 : 0;
+    const int s = (K + 2303) / 2304;
+    return s <= wsk && tiles16 * s <= 2 * kCUs ? s : 0;
 }
 
 // The same choice for a GEMM whose split-K reduction ends in a LayerNorm (the split is
@@ -1725,8 +1766,9 @@ static void gemm_launch(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const LnTai
     int wsk = dma_ok && !ln && g->split_k <= 0 ? wave_split(p.M, p.N, p.K, batch) : 0;
     if (wsk > 1 && (g->workspace == nullptr || g->workspace_floats < (long)wsk * p.M * p.N)) wsk = 1;
     if (dma_ok && ln && batch == 1 && p.split >= 2) wsk = wave_split_ln(p.M, p.N, p.K, p.split);
-    const bool w16 = wsk > 0 && !ln && batch == 1 && use_tile16(p.M, p.N, p.K);
-    if (w16) wsk = 1;
+    const int s16 = wsk > 0 && !ln && batch == 1 ? use_tile16(p.M, p.N, p.K, wsk) : 0;
+    const bool w16 = s16 > 0;
+    if (w16) wsk = s16;
     const bool wsplit = wsk > 0;
     if (wsplit) {
         p.split = wsk;
@@ -1737,12 +1779,12 @@ static void gemm_launch(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const LnTai
     t.bn = w16 ? 16 : wsplit || narrow ? 32 : 64;
     p.tiles_m = (p.M + t.bm - 1) / t.bm;
     p.tiles_n = (p.N + t.bn - 1) / t.bn;
-    const GemmKernel kern = w16      ? pick_wsplit16(am, p.K)
+    const GemmKernel kern = w16      ? pick_wsplit16(am, p.kchunk)
                             : wsplit ? pick_wsplit(am)
                             : narrow ? pick_dma<128, 32, 4>(am)
                             : dma_ok ? pick_dma<64, 64, 2>(am)
                                      : pick_kernel<64, 64, 2>(am, bm);
-    const int threads = w16 ? 64 * wsplit16_waves(p.K) : 256;
+    const int threads = w16 ? 64 * wsplit16_waves(p.kchunk) : 256;
     const dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)(batch * p.split));
     if (ln && p.split < 2) {  // the workspace did not allow the split the reduction needs
         x->launch_error = (int)hipErrorInvalidValue;

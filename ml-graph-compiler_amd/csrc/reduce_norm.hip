@@ -604,14 +604,12 @@ __global__ void __launch_bounds__(256) depthwise3x3_nhwc_lds(const DwGeo g, int 
     const int oh0 = th * T, ow0 = tw * T;
     const int ih0 = oh0 * S - g.PT, iw0 = ow0 * S - g.PL;
     const float4 *img = reinterpret_cast<const float4 *>(in) + (long)n * g.H * g.W * C4;
-    const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (int e = threadIdx.x; e < IT * IT * CQ; e += 256) {
         const int q = e % CQ, pix = e / CQ;
         const int r = pix / IT, col = pix - r * IT;
         const int ih = ih0 + r, iw = iw0 + col, c4 = c4base + q;
-        float4 v = zero;
-        if (ih >= 0 && ih < g.H && iw >= 0 && iw < g.W && c4 < C4) v = img[((long)ih * g.W + iw) * C4 + c4];
-        tile[e] = v;
+        const bool inside = ih >= 0 && ih < g.H && iw >= 0 && iw < g.W && c4 < C4;
+        tile[e] = inside ? img[((long)ih * g.W + iw) * C4 + c4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
     __syncthreads();
     const int q = threadIdx.x % CQ, c4 = c4base + q;
@@ -620,7 +618,7 @@ __global__ void __launch_bounds__(256) depthwise3x3_nhwc_lds(const DwGeo g, int 
     float4 wv[9];
 #pragma unroll
     for (int t = 0; t < 9; ++t) wv[t] = w4[t * C4 + c4];
-    const float4 bv = bias ? reinterpret_cast<const float4 *>(bias)[c4] : zero;
+    const float4 bv = bias ? reinterpret_cast<const float4 *>(bias)[c4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
         const int p = threadIdx.x / CQ + 32 * k;
