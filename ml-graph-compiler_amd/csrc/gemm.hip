@@ -1231,6 +1231,124 @@ __global__ void __launch_bounds__(64 * WAVES) gemm_dma_wsplit16_kernel(const Gem
     }
 }
 
+// GEMMs with short K (K <= 2 * KH, KH 8 or 16, K % 4 == 0) over many rows: the expand and
+// project 1 x 1 convolutions of MobileNet-style blocks at large batch, which move tens of MB
+// per launch for a few FLOP per byte and so are HBM-bound. The tiled kernels spend most of such
+// a launch on per-workgroup latency (load, multiply, stage through LDS, store, one tile per
+// workgroup). Here each wave streams 32-row tiles on its own: A goes straight from memory into
+// registers (a tile's rows are contiguous, 32 x K floats), the next tile's A is requested before
+// this tile's MFMAs (two register sets used in turn), the wave's column group of B (NB blocks of
+// 32 columns) stays in registers for all its tiles, and the epilogue writes from the
+// accumulators (no LDS, no barriers). Lane (li, h) = (lane % 32, lane / 32) holds k = KH h ..
+// KH h + KH - 1 of row li (A) and of column li (B), and MFMA j multiplies A[:, KH h + j] by
+// B[KH h + j, :] over both halves, so the KH instructions cover the 2 KH k once; register r of a
+// 32 x 32 accumulator holds row 8 (r / 4) + 4 h + r % 4, column li. Every operand goes through
+// a buffer resource: columns of B past N, k past K and rows of A past M load as zeros (so the
+// padding multiplies 0 by 0), and C and residual accesses past M or N are dropped, which keeps
+// the epilogue free of branches. Activation none, relu or clip, as one clamp to [lo, hi]
+// (lo = -inf, hi = +inf for none). Waves are dealt to column groups, wave w of a group taking
+// M-tiles w, w + waves_per_group, ...
+template <int KH, int NB>
+__global__ void __launch_bounds__(256) gemm_stream_kernel(const GemmDev p, int groups, int waves_per_group,
+                                                          float lo, float hi, long c_bytes, long r_bytes) {
+    const int lane = threadIdx.x & 63, li = lane & 31, h = lane >> 5;
+    const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (gw >= groups * waves_per_group) return;
+    const int grp = gw % groups;
+    const int tiles_m = (p.M + 31) / 32;
+    const int n0 = grp * NB * 32;
+    const int kh0 = KH * h;  // this lane's first k
+    constexpr int Q = KH / 4;
+    constexpr unsigned OOB = 0x80000000u;
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void *)p.a.p, (short)0, (int)p.a_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void *)p.b.p, (short)0, (int)p.b_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc((void *)p.c, (short)0, (int)c_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc((void *)(p.res ? p.res : p.c), (short)0,
+                                                                        (int)(p.res ? r_bytes : 0), 0x00020000);
+    const bool has_res = p.res != nullptr;
+    const float alpha = p.alpha, beta = p.beta;
+    bool kok[Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) kok[q] = kh0 + 4 * q < p.K;
+
+    f4 b[NB][Q];
+    float bias[NB];
+    unsigned cofs[NB], rofs[NB];  // byte offsets of this lane's column in C / R (row 0), or OOB
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        const int n = n0 + nb * 32 + li;
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+            const unsigned off = n < p.N && kok[q] ? ((unsigned)n * (unsigned)p.b.cs + kh0 + 4 * q) * 4u : OOB;
+            b[nb][q] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 0));
+        }
+        bias[nb] = p.bias && n < p.N ? ldg(p.bias + n) : 0.0f;
+        cofs[nb] = n < p.N ? (unsigned)n * 4u : OOB;
+        rofs[nb] = n < p.N ? (unsigned)n * 4u : OOB;
+    }
+    const unsigned ldc4 = (unsigned)p.ldc * 4u, ldr4 = (unsigned)p.ldr * 4u;
+
+    auto load_a = [&](f4 (&a)[Q], int tm) __attribute__((always_inline)) {
+        const int row = tm * 32 + li;
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+            const unsigned off = row < p.M && kok[q] ? ((unsigned)row * (unsigned)p.a.rs + kh0 + 4 * q) * 4u : OOB;
+            a[q] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0));
+        }
+    };
+    auto tile = [&](const f4 (&a)[Q], int tm) __attribute__((always_inline)) {
+        floatx16 acc[NB];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[nb][r] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < KH; ++j)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+                acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[j >> 2][j & 3], b[nb][j >> 2][j & 3], acc[nb], 0, 0, 0);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            unsigned rowofs[16];
+            float res[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = tm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                rowofs[r] = row < p.M ? (unsigned)row : OOB;
+                res[r] = 0.0f;
+            }
+            if (has_res) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const unsigned off = rowofs[r] == OOB || rofs[nb] == OOB ? OOB : rowofs[r] * ldr4 + rofs[nb];
+                    res[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, off, 0, 0));
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float v = acc[nb][r] * alpha + bias[nb] + beta * res[r];
+                v = fminf(fmaxf(v, lo), hi);
+                const unsigned off = rowofs[r] == OOB || cofs[nb] == OOB ? OOB : rowofs[r] * ldc4 + cofs[nb];
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, v), rc, off, 0, 0);
+            }
+        }
+    };
+
+    f4 a0[Q], a1[Q];
+    int tm = gw / groups;
+    if (tm < tiles_m) load_a(a0, tm);
+    while (tm < tiles_m) {
+        const int t1 = tm + waves_per_group;
+        if (t1 < tiles_m) load_a(a1, t1);
+        tile(a0, tm);
+        if (t1 >= tiles_m) break;
+        const int t2 = t1 + waves_per_group;
+        if (t2 < tiles_m) load_a(a0, t2);
+        tile(a1, t1);
+        tm = t2;
+    }
+}
+
 // Sum the split-K partials and apply the epilogue (one batch element).
 __global__ void gemm_splitk_reduce(const GemmDev p) {
     const long total = (long)p.M * p.N;
@@ -1326,6 +1444,7 @@ static bool bs_div4(const long *bs, int rank) {
 }
 
 typedef void (*GemmKernel)(const GemmDev);
+typedef void (*GemmKernelStream)(const GemmDev, int, int, float, float, long, long);
 
 template <int BM, int BN, int WGM>
 static GemmKernel pick_kernel(int am, int bm) {
@@ -1474,6 +1593,48 @@ static int use_tile16(int M, int N, int K, int wsk) {
     if (K <= 2560) return tiles16 <= 2 * kCUs ? 1 : 0;
     const int s = (K + 2303) / 2304;
     return s <= wsk && tiles16 * s <= 2 * kCUs ? s : 0;
+}
+
+// The streaming kernel for short K over many rows (K <= 32, K % 4 == 0, at least 4096 rows,
+// at most 768 columns).
+static bool use_stream(int M, int N, int K) { return K <= 32 && K % 4 == 0 && M >= 4096 && N <= 24 * 32; }
+static bool stream_act(int act) { return act == MGC_ACT_NONE || act == MGC_ACT_RELU || act == MGC_ACT_CLIP; }
+
+template <int KH>
+static GemmKernelStream pick_stream(int nb) {
+    return nb == 1 ? &gemm_stream_kernel<KH, 1> : nb == 2 ? &gemm_stream_kernel<KH, 2> : &gemm_stream_kernel<KH, 3>;
+}
+
+// Column groups of at most three 32-column blocks (the B registers of one group), as even as
+// the block count allows: wider groups (five and six blocks, one wave per SIMD) were slower
+// than the tiled kernel on MobileNetV2's 24 -> 144 and 32 -> 192 layers at batch 32 (27.0 /
+// 13.2 us against 23.8 / 11.5), three blocks faster (16 -> 96: 32.1 against 49.5); as many waves as the kernel's registers let the CUs hold at once
+// (each wave loops over its tiles, so a second round of waves would only start late).
+static void stream_launch(mgc_hip_exec *x, const GemmDev &p) {
+    const int blocks = (p.N + 31) / 32;
+    const int groups = (blocks + 2) / 3;
+    const int nb = (blocks + groups - 1) / groups;
+    const int tiles_m = (p.M + 31) / 32;
+    const GemmKernelStream kern = p.K <= 16 ? pick_stream<8>(nb) : pick_stream<16>(nb);
+    static int resident[2][4];  // workgroups per CU, by (KH, NB); 0 = not asked yet
+    int &per_cu = resident[p.K <= 16 ? 0 : 1][nb];
+    if (per_cu == 0) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void *>(kern), 256, 0) !=
+                hipSuccess || n < 1)
+            n = 1;
+        per_cu = n;
+    }
+    const int waves = per_cu * 4 * kCUs;
+    int per_group = waves / groups;
+    if (per_group > tiles_m) per_group = tiles_m;
+    if (per_group < 1) per_group = 1;
+    const int wgs = (groups * per_group + 3) / 4;
+    const float lo = p.act == MGC_ACT_CLIP ? p.lo : p.act == MGC_ACT_RELU ? 0.0f : -INFINITY;
+    const float hi = p.act == MGC_ACT_CLIP ? p.hi : INFINITY;
+    const long c_bytes = ((long)(p.M - 1) * p.ldc + p.N) * 4;
+    const long r_bytes = p.res ? ((long)(p.M - 1) * p.ldr + p.N) * 4 : 0;
+    MGC_LAUNCH(x, kern, dim3((unsigned)wgs), dim3(256), 0, p, groups, per_group, lo, hi, c_bytes, r_bytes);
 }
 
 // The same choice for a GEMM whose split-K reduction ends in a LayerNorm (the split is
@@ -1756,6 +1917,12 @@ static void gemm_launch(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const LnTai
     const bool dma_ok = nonneg && (am == AM_VEC || am == AM_CONV_VEC || am == AM_CAT) && bm == BD_NK_VEC &&
                         p.K > 0 && p.a_bytes > 0 && p.a_bytes < kMaxRes && p.b_bytes > 0 &&
                         p.b_bytes < kMaxRes && (am != AM_CAT || (p.a2_bytes > 0 && p.a2_bytes < kMaxRes));
+    if (dma_ok && am == AM_VEC && !ln && g->split_k <= 0 && batch == 1 && use_stream(p.M, p.N, p.K) &&
+        p.bias_mode != 2 && stream_act(p.act) && p.ldc >= p.N && (long)p.M * p.ldc * 4 < kMaxRes &&
+        (!p.res || (long)p.M * p.ldr * 4 < kMaxRes)) {
+        stream_launch(x, p);
+        return;
+    }
     if (am == AM_CAT && !dma_ok) {  // only the DMA kernels read a second source
         x->launch_error = (int)hipErrorInvalidValue;
         set_error("mgc_hip_gemm: concatenated-K GEMM needs a packed [N][K] B and extents below 2 GiB",
