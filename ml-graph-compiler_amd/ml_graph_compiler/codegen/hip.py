@@ -1498,12 +1498,17 @@ class HipEmitter:
 
     def _node_flops(self) -> list[int]:
         """FLOPs per node, with the nodes a fused attention call absorbs (among them a QKV
-        projection GEMM) counted at the node that emits the call, whose launches do that work."""
+        projection GEMM) counted at the node that emits the call, and a projection shortcut at
+        the convolution whose GEMM computes it: the launches of that node do the work."""
         index = {id(n): i for i, n in enumerate(self.graph.nodes)}
         flops = [ops.flops(n) for n in self.graph.nodes]
         for nid, m in self._attn_skip.items():
             i = index[nid]
             flops[index[id(m.emit_at)]] += flops[i]
+            flops[i] = 0
+        for c3_id, ds in self._shortcut.items():
+            i = index[id(ds)]
+            flops[index[c3_id]] += flops[i]
             flops[i] = 0
         return flops
 

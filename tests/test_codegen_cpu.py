@@ -109,6 +109,10 @@ def test_projection_shortcuts_join_their_block_gemm():
     gen = generate_hip(g, gemm_workspace=native.gemm_workspace_floats)
     assert gen.kernels["gemm_shortcut"] == 4 and gen.kernels["gemm"] == 50
     assert gen.source.count("g.k1 = ") == 4
+    # the shortcut's FLOPs are timed with the GEMM that computes them
+    from ml_graph_compiler import ops
+    assert sum(gen.node_flops) == sum(ops.flops(n) for n in g.nodes)
+    assert all(gen.node_flops[i] == 0 for i, n in enumerate(g.nodes) if id(n) in {id(d) for d in pairs.values()})
     order = {id(n): i for i, n in enumerate(g.nodes)}
     by_value = {id(v): b for b in gen.plan.buffers for v in b.values}
     for c3 in g.nodes:
