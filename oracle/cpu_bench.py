@@ -35,15 +35,21 @@ def bootstrap_median_ci(samples: np.ndarray, n: int = 2000, seed: int = 0) -> tu
 
 
 def host() -> dict:
-    """nproc, the CPU model (lscpu) and the threads the OpenMP runtime would use."""
-    model = "unknown"
+    """nproc and the CPU model as lscpu reports it: the model name plus family / model /
+    stepping, sockets and threads per core (a virtualized host may name only the vendor line)."""
+    fields = {}
     try:
         out = subprocess.run(["lscpu"], capture_output=True, text=True, check=False).stdout
         for line in out.splitlines():
-            if line.startswith("Model name:"):
-                model = line.split(":", 1)[1].strip()
+            key, _, value = line.partition(":")
+            fields[key.strip()] = value.strip()
     except OSError:
         pass
+    model = fields.get("Model name", "unknown")
+    detail = [f"{k.lower()} {fields[k]}" for k in ("CPU family", "Model", "Stepping", "Socket(s)",
+                                                   "Core(s) per socket", "Thread(s) per core") if fields.get(k)]
+    if detail:
+        model += " (" + ", ".join(detail) + ")"
     try:
         nproc = int(subprocess.run(["nproc"], capture_output=True, text=True, check=False).stdout.strip())
     except (OSError, ValueError):
