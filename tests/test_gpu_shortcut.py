@@ -6,9 +6,11 @@ convolution of the block input x to the output of the block's last 1 x 1 convolu
 hip backend runs both as one GEMM with K = K1 + C2: columns below K1 read c3's input, the
 others read x at the shortcut's stride. Each case builds such a block, compiles it at O3,
 asserts how many blocks were fused and compares with the oracle on the unoptimized graph; the
-shapes reach the 64 x 64 and 128 x 32 DMA tiles, the wave-split kernel and a K split. The
-same blocks compiled with the fusion off give the reference's two-GEMM form; both must agree
-with the oracle to the same bound.
+shapes reach the 64 x 64 and 128 x 32 DMA tiles and the 32 x 32 and 16 x 16 wave-split
+kernels. The same blocks compiled with the fusion off give the reference's two-GEMM form; both
+must agree with the oracle to the same bound. When the two GEMM inputs are caller buffers the
+generated code checks their 16-byte alignment at run time and runs the two GEMMs apart if
+either is misaligned; both branches are run.
 """
 
 from __future__ import annotations
@@ -147,6 +149,38 @@ def test_shortcut_over_caller_buffers(hip_cache, monkeypatch):
     try:
         assert model.report.kernels.get("gemm_shortcut") == 1, model.report.kernels
         got = model.run(feeds)["y"]
+    finally:
+        model.release()
+    np.testing.assert_allclose(got, expected, rtol=RTOL, atol=ATOL)
+
+
+def test_shortcut_over_misaligned_caller_buffers(hip_cache, monkeypatch):
+    """Caller buffers 4 bytes off a 16-byte boundary: the generated code sees the misalignment at
+    run time and runs the shortcut and the last convolution as two GEMMs instead."""
+    import torch
+
+    print("[gpu] shortcut over misaligned caller buffers", flush=True)
+    monkeypatch.setattr(hip_codegen, "FUSE_PROJECTION_SHORTCUT", True)
+    g, feeds = _nhwc_block(1, 14, 64, 64, 256, 2, seed=13)
+    expected = oracle.run_graph(g, feeds)["y"]
+    model = compile_hip(g, hip_cache, "O0")
+    try:
+        assert model.report.kernels.get("gemm_shortcut") == 1, model.report.kernels
+        dev = torch.device("cuda:0")
+        keep = []
+        ptrs = []
+        for name, _ in model.inputs:
+            host = torch.from_numpy(np.ascontiguousarray(feeds[name]).reshape(-1))
+            buf = torch.zeros(host.numel() + 1, dtype=torch.float32, device=dev)
+            view = buf[1:]  # 4 bytes past the allocation's start
+            view.copy_(host)
+            assert view.data_ptr() % 16 == 4
+            keep.append(buf)
+            ptrs.append(view.data_ptr())
+        out = torch.empty(expected.size, dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+        model.run_device(ptrs, [out.data_ptr()])
+        got = out.cpu().numpy().reshape(expected.shape)
     finally:
         model.release()
     np.testing.assert_allclose(got, expected, rtol=RTOL, atol=ATOL)
