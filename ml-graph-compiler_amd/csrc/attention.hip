@@ -54,16 +54,24 @@ struct AttnDev {
     float fill;
 };
 
-__global__ void __launch_bounds__(256) attention_kernel(const AttnDev p) {
+template <int G>
+__global__ void __launch_bounds__(256 * G) attention_kernel(const AttnDev p) {
     __shared__ __attribute__((aligned(16))) float Qs[ATT_BQ * ATT_P];
-    __shared__ __attribute__((aligned(16))) float Ks[ATT_BK * ATT_P];
-    __shared__ __attribute__((aligned(16))) float Vt[ATT_DMAX * ATT_P];  // [d][key]
-    __shared__ __attribute__((aligned(16))) float Ps[ATT_BQ * ATT_P];    // scores, then exp terms
-    __shared__ float rowscale[ATT_BQ];  // exp(m_old - m_new) of the block; 1 / l at the end
+    __shared__ __attribute__((aligned(16))) float Ks_all[G][ATT_BK * ATT_P];
+    __shared__ __attribute__((aligned(16))) float Vt_all[G][ATT_DMAX * ATT_P];  // [d][key]
+    __shared__ __attribute__((aligned(16))) float Ps_all[G][ATT_BQ * ATT_P];    // scores, then exp terms
+    __shared__ float rowscale_all[G][ATT_BQ];  // exp(m_old - m_new) of the block; 1 / l at the end
+    __shared__ float mstate[G][2][ATT_BQ];     // G > 1: each group's final m and l per row
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int grp = G > 1 ? tid >> 8 : 0;  // key group: takes key blocks grp, grp + G, ...
+    const int gt = tid & 255;              // thread within its group
+    float *const Ks = Ks_all[grp];
+    float *const Vt = Vt_all[grp];
+    float *const Ps = Ps_all[grp];
+    float *const rowscale = rowscale_all[grp];
+    const int lane = gt & 63;
+    const int wave = gt >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int li = lane & 31, lh = lane >> 5;
     const int qblocks = (p.S + ATT_BQ - 1) / ATT_BQ;
@@ -84,7 +92,7 @@ __global__ void __launch_bounds__(256) attention_kernel(const AttnDev p) {
     const float NEG_INF = -__builtin_huge_valf();
     const f4 zero4 = {0.f, 0.f, 0.f, 0.f};
     // softmax role: four neighbouring threads share a row
-    const int srow = tid >> 2, part = tid & 3;
+    const int srow = gt >> 2, part = gt & 3;
     float m_run = NEG_INF, l_run = 0.f;
 
     // Tiles of 64 rows x 16 float quads are moved as 4 quads per thread. Q and K: thread t takes
@@ -99,7 +107,7 @@ __global__ void __launch_bounds__(256) attention_kernel(const AttnDev p) {
     auto load_kv = [&](int k0) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < QUADS; ++i) {
-            const int e = tid + 256 * i;
+            const int e = gt + 256 * i;
             const int r = e >> 4, c4 = e & 15;
             kst[i] = zero4;
             if (k0 + r < p.Skv && c4 < D4) kst[i] = *reinterpret_cast<const f4 *>(kbase + (long)(k0 + r) * p.k_s + c4 * 4);
@@ -111,7 +119,7 @@ __global__ void __launch_bounds__(256) attention_kernel(const AttnDev p) {
     auto store_kv = [&]() __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < QUADS; ++i) {
-            const int e = tid + 256 * i;
+            const int e = gt + 256 * i;
             *reinterpret_cast<f4 *>(&Ks[(e >> 4) * ATT_P + (e & 15) * 4]) = kst[i];
 #pragma unroll
             for (int j = 0; j < 4; ++j) Vt[((e >> 6) * 4 + j) * ATT_P + (e & 63)] = vst[i][j];
@@ -121,18 +129,22 @@ __global__ void __launch_bounds__(256) attention_kernel(const AttnDev p) {
     // 1. Q rows (rows past S and columns past D are zero), requested with the first key block
     {
         f4 qst[QUADS];
+        if (grp == 0) {
 #pragma unroll
-        for (int i = 0; i < QUADS; ++i) {
-            const int e = tid + 256 * i;
-            const int r = e >> 4, c4 = e & 15;
-            qst[i] = zero4;
-            if (q0 + r < p.S && c4 < D4) qst[i] = *reinterpret_cast<const f4 *>(qbase + (long)(q0 + r) * p.q_s + c4 * 4);
+            for (int i = 0; i < QUADS; ++i) {
+                const int e = gt + 256 * i;
+                const int r = e >> 4, c4 = e & 15;
+                qst[i] = zero4;
+                if (q0 + r < p.S && c4 < D4) qst[i] = *reinterpret_cast<const f4 *>(qbase + (long)(q0 + r) * p.q_s + c4 * 4);
+            }
         }
-        load_kv(0);
+        if (grp < kblocks) load_kv(grp * ATT_BK);
+        if (grp == 0) {
 #pragma unroll
-        for (int i = 0; i < QUADS; ++i) {
-            const int e = tid + 256 * i;
-            *reinterpret_cast<f4 *>(&Qs[(e >> 4) * ATT_P + (e & 15) * 4]) = qst[i];
+            for (int i = 0; i < QUADS; ++i) {
+                const int e = gt + 256 * i;
+                *reinterpret_cast<f4 *>(&Qs[(e >> 4) * ATT_P + (e & 15) * 4]) = qst[i];
+            }
         }
     }
 
@@ -140,60 +152,71 @@ __global__ void __launch_bounds__(256) attention_kernel(const AttnDev p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) oacc[r] = 0.f;
 
-    for (int kb = 0; kb < kblocks; ++kb) {
+    // Each iteration every group takes its own key block (none when past the keys); barriers are
+    // workgroup-wide, so a group without a block still meets them.
+    const int iters = (kblocks + G - 1) / G;
+    for (int it = 0; it < iters; ++it) {
+        const int kb = it * G + grp;
         const int k0 = kb * ATT_BK;
-        if (causal && k0 > q_last) {
-            // every key from here on is masked in every row of the block
-            const bool zero_terms = q0 + srow > q_last || fill == NEG_INF || fill <= m_run - ATT_SKIP_MARGIN;
-            if (__syncthreads_and(zero_terms)) break;
+        bool active = kb < kblocks;
+        if (G == 1) {
+            if (causal && k0 > q_last) {
+                // every key from here on is masked in every row of the block
+                const bool zero_terms = q0 + srow > q_last || fill == NEG_INF || fill <= m_run - ATT_SKIP_MARGIN;
+                if (__syncthreads_and(zero_terms)) break;
+            }
+        } else if (active && causal && k0 > q_last && fill == NEG_INF) {
+            active = false;  // every term of this block is exactly zero
         }
         __syncthreads();  // Ks, Vt, Ps and rowscale free; Qs visible
         // 2. K block [key][d], V block transposed [d][key], from the registers loaded one block
         // ahead; then the next block's loads go out
-        store_kv();
-        if (kb + 1 < kblocks) load_kv(k0 + ATT_BK);
+        if (kb < kblocks) store_kv();
+        if (kb + G < kblocks) load_kv(k0 + G * ATT_BK);
         __syncthreads();
         floatx16 acc;
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[r] = 0.f;
-        for (int c = 0; c < dchunks; ++c) {
-            f4 af[4], bf[4];
+        if (active) {
+            for (int c = 0; c < dchunks; ++c) {
+                f4 af[4], bf[4];
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                af[s] = *reinterpret_cast<const f4 *>(&Qs[(wm * 32 + li) * ATT_P + c * 32 + lh * 16 + 4 * s]);
-                bf[s] = *reinterpret_cast<const f4 *>(&Ks[(wn * 32 + li) * ATT_P + c * 32 + lh * 16 + 4 * s]);
+                for (int s = 0; s < 4; ++s) {
+                    af[s] = *reinterpret_cast<const f4 *>(&Qs[(wm * 32 + li) * ATT_P + c * 32 + lh * 16 + 4 * s]);
+                    bf[s] = *reinterpret_cast<const f4 *>(&Ks[(wn * 32 + li) * ATT_P + c * 32 + lh * 16 + 4 * s]);
+                }
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[s][e], bf[s][e], acc, 0, 0, 0);
             }
+            // register r of lane (li, lh): query row 8 (r / 4) + 4 lh + r % 4, key column li
+            const int key = k0 + wn * 32 + li;
 #pragma unroll
-            for (int s = 0; s < 4; ++s)
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[s][e], bf[s][e], acc, 0, 0, 0);
-        }
-        // register r of lane (li, lh): query row 8 (r / 4) + 4 lh + r % 4, key column li
-        const int key = k0 + wn * 32 + li;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int row = wm * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
-            const int q = q0 + row;
-            float t;
-            if (key >= p.Skv) {
-                t = NEG_INF;
-            } else if (q >= p.S) {
-                t = 0.f;
-            } else {
-                t = scale_div ? acc[r] / scale : acc[r] * scale;
-                if (bias) t += bias[(long)q * p.bias_s + (long)key * p.bias_j];
-                bool keep = true;
-                if (causal) keep = key <= q;
-                else if (mask) keep = (mask[(long)q * p.mask_s + (long)key * p.mask_j] != 0) == keep_set;
-                if (!keep) t = fill;
+            for (int r = 0; r < 16; ++r) {
+                const int row = wm * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
+                const int q = q0 + row;
+                float t;
+                if (key >= p.Skv) {
+                    t = NEG_INF;
+                } else if (q >= p.S) {
+                    t = 0.f;
+                } else {
+                    t = scale_div ? acc[r] / scale : acc[r] * scale;
+                    if (bias) t += bias[(long)q * p.bias_s + (long)key * p.bias_j];
+                    bool keep = true;
+                    if (causal) keep = key <= q;
+                    else if (mask) keep = (mask[(long)q * p.mask_s + (long)key * p.mask_j] != 0) == keep_set;
+                    if (!keep) t = fill;
+                }
+                Ps[row * ATT_P + wn * 32 + li] = t;
             }
-            Ps[row * ATT_P + wn * 32 + li] = t;
         }
         __syncthreads();
 
         // 3. running softmax over the block's 64 scores of each row (16 per thread)
-        {
+        if (active) {
             float *prow = &Ps[srow * ATT_P + part * 16];
             f4 x[4];
 #pragma unroll
@@ -227,7 +250,7 @@ __global__ void __launch_bounds__(256) attention_kernel(const AttnDev p) {
         __syncthreads();
 
         // 4. O = alpha O + P V for this block (V^T in LDS: [d][key])
-        if (wn * 32 < D) {
+        if (active && wn * 32 < D) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) oacc[r] *= rowscale[wm * 32 + (r >> 2) * 8 + lh * 4 + (r & 3)];
 #pragma unroll
@@ -247,12 +270,52 @@ __global__ void __launch_bounds__(256) attention_kernel(const AttnDev p) {
         }
     }
     __syncthreads();  // every wave is past its last read of rowscale
-    if (part == 0) rowscale[srow] = 1.0f / l_run;
+    const int d = wn * 32 + li;
+    if (G == 1) {
+        if (part == 0) rowscale[srow] = 1.0f / l_run;
+    } else {
+        // The groups' partial states combine as m = max(m_g), l = sum_g l_g exp(m_g - m),
+        // O = sum_g O_g exp(m_g - m) / l. Groups past the first leave m, l and O (in their Ps
+        // tile) in LDS; the first group scales and adds.
+        if (part == 0) {
+            mstate[grp][0][srow] = m_run;
+            mstate[grp][1][srow] = l_run;
+        }
+        if (grp > 0 && d < D) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) Ps[(wm * 32 + (r >> 2) * 8 + lh * 4 + (r & 3)) * ATT_P + d] = oacc[r];
+        }
+        __syncthreads();
+        if (grp == 0 && part == 0) {
+            float m = NEG_INF;
+#pragma unroll
+            for (int g2 = 0; g2 < G; ++g2) m = fmaxf(m, mstate[g2][0][srow]);
+            float l = 0.f;
+#pragma unroll
+            for (int g2 = 0; g2 < G; ++g2) {
+                const float mg = mstate[g2][0][srow];
+                const float w = mg == NEG_INF ? 0.f : expf(mg - m);
+                mstate[g2][0][srow] = w;  // the group's weight
+                l += mstate[g2][1][srow] * w;
+            }
+            rowscale[srow] = 1.0f / l;
+        }
+        __syncthreads();
+        if (grp == 0 && d < D) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = wm * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
+                float v = oacc[r] * mstate[0][0][row];
+#pragma unroll
+                for (int g2 = 1; g2 < G; ++g2) v += Ps_all[g2][row * ATT_P + d] * mstate[g2][0][row];
+                oacc[r] = v;
+            }
+        }
+    }
     __syncthreads();
 
     // 5. O rows: register r of lane (li, lh) is query 8 (r / 4) + 4 lh + r % 4, column d = li
-    const int d = wn * 32 + li;
-    if (d < D) {
+    if (grp == 0 && d < D) {
         float *obase = p.o + b * p.o_b + h * p.o_h + d;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -321,5 +384,12 @@ extern "C" void mgc_hip_attention(mgc_hip_exec *x, const mgc_hip_attention_args 
     p.mask_keep = a->mask_keep;
     p.causal = a->causal;
     p.fill = a->fill;
-    MGC_LAUNCH(x, attention_kernel, dim3((unsigned)blocks), dim3(256), 0, p);
+    // Fewer (batch, head, 64-query) blocks than CUs and at least two key blocks: two groups of
+    // four waves per workgroup take alternate key blocks and combine at the end (one workgroup
+    // per CU then: the groups' tiles take 122 KB of LDS).
+    const int kblocks = (a->Skv + ATT_BK - 1) / ATT_BK;
+    if (blocks < 256 && kblocks >= 2)
+        MGC_LAUNCH(x, attention_kernel<2>, dim3((unsigned)blocks), dim3(512), 0, p);
+    else
+        MGC_LAUNCH(x, attention_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, p);
 }

@@ -7,7 +7,10 @@ blocks and end mid-block, long sequences (the keys stream through a running soft
 dim below 64, separate Q/K/V tensors and a fused QKV projection. The score ops cover what the
 matcher accepts: Mul or Div by a scalar, an additive bias (constant or computed at run time,
 broadcast over heads or queries), and a Where mask in both polarities (constant causal with a
-finite or -inf fill, an arbitrary constant mask, a mask fed as an input).
+finite or -inf fill, an arbitrary constant mask, a mask fed as an input). With fewer than 256
+(batch, head, query block) workgroups the kernel splits each workgroup's key blocks between two
+groups of waves and merges their softmax states at the end (odd key-block counts leave the second
+group idle in the last step); the many-head cases (512 and more workgroups) run one group.
 """
 
 from __future__ import annotations
@@ -172,6 +175,8 @@ def test_causal_and_biased_many_heads(hip_cache):
     g, feeds = attention_graph(2, 32, 520, 520, 64, True, mask="causal", fill=-np.inf)
     _check(g, feeds, hip_cache)
     g, feeds = attention_graph(2, 32, 520, 520, 64, True, bias="input")
+    _check(g, feeds, hip_cache)
+    g, feeds = attention_graph(2, 32, 520, 520, 64, True, mask="causal")  # finite fill past the diagonal
     _check(g, feeds, hip_cache)
 
 
