@@ -174,6 +174,29 @@ long mgc_hip_gemm_layer_norm_workspace(int M, int N, int K);
 /* 1 when mgc_hip_gemm_layer_norm takes an M x N output. */
 int mgc_hip_gemm_layer_norm_supported(int M, int N);
 
+/* A depthwise 3 x 3 convolution and the 1 x 1 convolution that reads its output, as one
+ * launch: the GEMM of g (C = act(alpha A B + bias + beta R), batch_rank 0, B packed [N][K])
+ * whose A operand is computed on the fly as the depthwise output
+ *   A[m][k] = act_d(bias_d[k] + sum_{i,j < 3} x[n][oh SH - PT + i][ow SW - PL + j][k] w[(3 i + j) C + k])
+ * for output pixel m = (n OH + oh) OW + ow of the NHWC batch x [n][H][W][C] (taps outside the
+ * image are zero), so the depthwise output is never stored; g->a is not read and g->K = C.
+ * Replaces mgc_depthwise_nhwc followed by mgc_gemm of the pointwise convolution
+ * (src/ml_graph_compiler/codegen/runtime/mgc_kernels.c:455-473 and :370-396, which the
+ * reference's C backend emits as two calls, codegen/c.py:1126-1135 and :1140-1167). Needs
+ * SH = SW in {1, 2}, C % 4 == 0, 16-byte aligned x, w, bias and B, B's column stride a multiple
+ * of 4, bias_mode 1 (or no bias), M a whole number of OH x OW images and x below 2 GiB; sets the
+ * launch error otherwise. */
+typedef struct {
+    const float *x;     /* NHWC input [N][H][W][C] */
+    const float *w;     /* [3][3][C], channel fastest */
+    const float *bias;  /* [C] or NULL */
+    int H, W, C, SH, SW, PT, PL, OH, OW;
+    int act;            /* MGC_ACT_* applied to the depthwise output */
+    float lo, hi;
+} mgc_hip_dw_args;
+
+void mgc_hip_gemm_dw(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const mgc_hip_dw_args *dw);
+
 /* ---------------------------------------------------------------------------------------- */
 /* memory-bound kernels                                                                      */
 /* ---------------------------------------------------------------------------------------- */

@@ -1349,6 +1349,285 @@ __global__ void __launch_bounds__(256) gemm_stream_kernel(const GemmDev p, int g
     }
 }
 
+// A depthwise 3 x 3 convolution computed inside the GEMM of the 1 x 1 convolution that reads it
+// (mgc_hip_gemm_dw): A[m][k] = act_d(bd[k] + sum_{i,j} X[n, oh SH - PT + i, ow SW - PL + j, k]
+// wd[(3 i + j) C + k]) for output pixel m = (n, oh, ow) and channel k, evaluated while the A tile
+// is staged, so the depthwise output never goes to memory. The taps are summed in the order of
+// the standalone depthwise kernel (bias first, then row by row), so A holds exactly the values
+// that kernel would store.
+struct DwDev {
+    const float *x, *w, *bias;
+    int H, W, C, PT, PL, OH, OW;
+    int act;
+    float lo, hi;
+    int tiles_h, tiles_w;  // 8 x 8 output-pixel tiles per image
+    long x_bytes;          // bytes of x reachable from d.x
+};
+
+// One workgroup (256 threads) computes an 8 x 8 block of output pixels of one image (64 GEMM
+// rows) times BN output channels; K runs over the depthwise channels in stages of 32.
+//  * Per stage the input patch the 64 depthwise windows cover ((7 S + 3)^2 pixels x 32 channels)
+//    travels to LDS by DMA (buffer_load ... lds, 16 bytes per lane, zeros outside the image and
+//    past C), each element once; the depthwise weights, bias and the B quads of the stage come
+//    into registers one stage ahead. With PBUF 2 the patch is double-buffered (its DMA for the
+//    next stage runs under this stage's depthwise and MFMA work); with PBUF 1 the next patch is
+//    requested after the depthwise pass (less LDS, more workgroups per CU).
+//  * Thread t computes channel quad t & 7 of tile rows t >> 3 and (t >> 3) + 32 (row r is pixel
+//    (r >> 3, r & 7) of the block) from the patch into the A tile. BN 64: 2 x 2 waves of 32 x 32
+//    MFMA blocks; BN 32: waves w and w + 2 share the 32 x 32 block of rows 32 w, taking k 0-15
+//    and 16-31 of each stage, and sum their halves through LDS at the end.
+//  * The epilogue maps tile rows back to pixels (rows outside the image are not stored).
+template <int BN, int S, int PBUF>
+__global__ void __launch_bounds__(256) gemm_dw_kernel(const GemmDev p, const DwDev d) {
+    constexpr int BM = 64;
+    constexpr int BK = 32;
+    constexpr int LDK = BK + 4;
+    constexpr int PWID = 7 * S + 3;                    // patch rows and columns
+    constexpr int PQUADS = PWID * PWID * 8;             // 16-byte quads of one patch
+    constexpr int PINS = (PQUADS + 63) / 64;            // DMA instructions per patch
+    constexpr int PIW = (PINS + 3) / 4;                 // per wave
+    constexpr int PFLOATS = PINS * 64 * 4;              // one patch buffer, whole instructions
+    constexpr int BV = BN / 32;
+    constexpr int LDC = BN + 8;
+    constexpr int SMEM_LOOP = PBUF * PFLOATS + BM * LDK + BN * LDK;
+    constexpr int SMEM_EPI = BM * LDC + (BN == 32 ? 2 * 1024 : 0);
+    constexpr int SMEM = SMEM_LOOP > SMEM_EPI ? SMEM_LOOP : SMEM_EPI;
+    static_assert(BN == 32 || BN == 64, "tile");
+    static_assert(S == 1 || S == 2, "stride");
+    static_assert(PBUF == 1 || PBUF == 2, "patch buffers");
+
+    __shared__ __attribute__((aligned(16))) float smem[SMEM];
+    float *const Ps = smem;                          // [PBUF][PFLOATS] patches [pixel][32]
+    float *const As = smem + PBUF * PFLOATS;         // [BM][LDK]
+    float *const Bs = As + BM * LDK;                 // [BN][LDK]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = BN == 64 ? wave >> 1 : wave & 1;
+    const int wn = BN == 64 ? wave & 1 : 0;
+    const int khalf = BN == 64 ? 0 : wave >> 1;
+
+    // tile order: XCD-aware, output-channel tiles of one pixel block adjacent (they read the
+    // same patches)
+    const int nb = gridDim.x;
+    const int full = nb & ~7;
+    int lin = blockIdx.x;
+    if (lin < full) {
+        const int per = full >> 3;
+        lin = (lin & 7) * per + (lin >> 3);
+    }
+    const int tm = lin / p.tiles_n;
+    const int tn = lin - tm * p.tiles_n;
+    const int n0 = tn * BN;
+    const int per_img = d.tiles_h * d.tiles_w;
+    const int img = tm / per_img;
+    const int tr = tm - img * per_img;
+    const int th = tr / d.tiles_w;
+    const int oh0 = th * 8, ow0 = (tr - th * d.tiles_w) * 8;
+
+    const int N = p.N, K = p.K;
+    const int H = d.H, W = d.W, C = d.C;
+    const int nk = (K + BK - 1) / BK;
+    const int q = tid & 7;
+    const int kq = q * 4;
+    const int ih0 = oh0 * S - d.PT, iw0 = ow0 * S - d.PL;
+
+    // DMA lanes: quad e = 64 i + lane of the patch is pixel e >> 3 (row-major over the patch),
+    // channel quad e & 7; its byte offset without the stage's k (OOB outside the image)
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void *)d.x, (short)0, (int)d.x_bytes, 0x00020000);
+    constexpr unsigned OOB = 0x80000000u;
+    // (all byte offsets fit in 31 bits: the launcher checks the extents)
+    const unsigned img_off = (unsigned)img * (unsigned)(H * W);
+    unsigned poff[PIW];
+#pragma unroll
+    for (int j = 0; j < PIW; ++j) {
+        const int e = (j * 4 + wave) * 64 + lane;
+        const int pp = e >> 3;
+        const int pr = pp / PWID, pc = pp - (pp / PWID) * PWID;
+        const int ih = ih0 + pr, iw = iw0 + pc;
+        poff[j] = e < PQUADS && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W
+                      ? ((img_off + (unsigned)(ih * W + iw)) * (unsigned)C + (unsigned)kq) * 4u
+                      : OOB;
+    }
+    auto issue_patch = [&](int kt, int buf) __attribute__((always_inline)) {
+        const int k0 = kt * BK;
+        const bool kok = k0 + kq < K;  // lane & 7 == tid & 7: the DMA lane's channel quad is kq
+        float *dst = Ps + buf * PFLOATS;
+#pragma unroll
+        for (int j = 0; j < PIW; ++j) {
+            const int i = j * 4 + wave;
+            if (i < PINS) dma16_buf(rx, kok && poff[j] != OOB ? poff[j] + (unsigned)k0 * 4u : OOB, dst + i * 256);
+        }
+    };
+
+    // depthwise weights [9][C], bias [C] and B through buffer resources: out-of-range quads
+    // (k >= K, n >= N, no bias) read as zeros; tap t's weights sit t C floats further (a scalar
+    // offset, so the nine loads share one address)
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void *)d.w, (short)0, 9 * C * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rbias =
+        __builtin_amdgcn_make_buffer_rsrc((void *)(d.bias ? d.bias : d.w), (short)0, d.bias ? C * 4 : 0, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rbm = __builtin_amdgcn_make_buffer_rsrc((void *)p.b.p, (short)0, (int)p.b_bytes, 0x00020000);
+    unsigned boff[BV];
+#pragma unroll
+    for (int r = 0; r < BV; ++r) {
+        const int n = n0 + (tid >> 3) + 32 * r;
+        boff[r] = n < N ? ((unsigned)n * (unsigned)p.b.cs + (unsigned)kq) * 4u : OOB;
+    }
+    f4 wq[9], bq, breg[BV];
+    auto load_regs = [&](int kt) __attribute__((always_inline)) {
+        const int k0 = kt * BK;
+        const bool kok = k0 + kq < K;
+        const unsigned voff = kok ? (unsigned)(k0 + kq) * 4u : OOB;
+#pragma unroll
+        for (int t = 0; t < 9; ++t)
+            wq[t] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rw, voff, t * C * 4, 0));
+        bq = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rbias, voff, 0, 0));
+#pragma unroll
+        for (int r = 0; r < BV; ++r)
+            breg[r] = __builtin_bit_cast(
+                f4, __builtin_amdgcn_raw_buffer_load_b128(rbm, kok && boff[r] != OOB ? boff[r] + (unsigned)k0 * 4u : OOB, 0, 0));
+    };
+    // depthwise outputs of this thread's two tile rows from patch buffer buf, into the A tile;
+    // the stage's B quads into the B tile
+    auto stage_tiles = [&](int buf) __attribute__((always_inline)) {
+        const float *ps = Ps + buf * PFLOATS;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int row = (tid >> 3) + 32 * h;
+            const int r = row >> 3, c = row & 7;
+            f4 v = bq;
+#pragma unroll
+            for (int i = 0; i < 3; ++i)
+#pragma unroll
+                for (int j = 0; j < 3; ++j) {
+                    const f4 xv = *reinterpret_cast<const f4 *>(&ps[((r * S + i) * PWID + c * S + j) * 32 + kq]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = fmaf(xv[e], wq[i * 3 + j][e], v[e]);
+                }
+            *reinterpret_cast<f4 *>(&As[row * LDK + kq]) = act4(v, d.act, d.lo, d.hi);
+        }
+#pragma unroll
+        for (int r = 0; r < BV; ++r) *reinterpret_cast<f4 *>(&Bs[((tid >> 3) + 32 * r) * LDK + kq]) = breg[r];
+    };
+
+    floatx16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    const int li = lane & 31;
+    const int lh = lane >> 5;
+
+    if (nk > 0) {
+        issue_patch(0, 0);
+        load_regs(0);
+    }
+    for (int kt = 0; kt < nk; ++kt) {
+        const int buf = PBUF == 2 ? (kt & 1) : 0;
+        wait_vmcnt<0>();
+        barrier_lds();  // the stage's patch is in LDS; the A and B tiles are free
+        if (PBUF == 2 && kt + 1 < nk) issue_patch(kt + 1, buf ^ 1);
+        stage_tiles(buf);
+        if (kt + 1 < nk) load_regs(kt + 1);
+        barrier_lds();  // A and B tiles complete; the patch is free
+        if (PBUF == 1 && kt + 1 < nk) issue_patch(kt + 1, 0);
+        if constexpr (BN == 64) {
+            f4 af[4], bf[4];
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2) {
+                af[s2] = *reinterpret_cast<const f4 *>(&As[(wm * 32 + li) * LDK + lh * 16 + 4 * s2]);
+                bf[s2] = *reinterpret_cast<const f4 *>(&Bs[(wn * 32 + li) * LDK + lh * 16 + 4 * s2]);
+            }
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[s2][e], bf[s2][e], acc, 0, 0, 0);
+        } else {
+            f4 af[2], bf[2];
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) {
+                af[s2] = *reinterpret_cast<const f4 *>(&As[(wm * 32 + li) * LDK + khalf * 16 + lh * 8 + 4 * s2]);
+                bf[s2] = *reinterpret_cast<const f4 *>(&Bs[li * LDK + khalf * 16 + lh * 8 + 4 * s2]);
+            }
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[s2][e], bf[s2][e], acc, 0, 0, 0);
+        }
+    }
+    __syncthreads();
+
+    // accumulators -> LDS tile [row][BN] (register r of lane (li, lh): row 8 (r / 4) + 4 lh + r % 4
+    // of the wave's 32-row block, column li of its 32-column block)
+    float *const Cs = smem;
+    if constexpr (BN == 64) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) Cs[(wm * 32 + (r >> 2) * 8 + lh * 4 + (r & 3)) * LDC + wn * 32 + li] = acc[r];
+    } else {
+        float *const part = smem + BM * LDC;  // the k 16-31 halves of both row blocks
+        if (khalf == 1) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) part[wm * 1024 + r * 64 + lane] = acc[r];
+        }
+        __syncthreads();
+        if (khalf == 0) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                Cs[(wm * 32 + (r >> 2) * 8 + lh * 4 + (r & 3)) * LDC + li] = acc[r] + part[wm * 1024 + r * 64 + lane];
+        }
+    }
+    __syncthreads();
+
+    // LDS tile -> epilogue -> memory: thread t owns 16-byte column chunk t % (BN / 4) and the
+    // tile rows t / (BN / 4) + RSTEP i
+    constexpr int C4 = BN / 4;
+    constexpr int RSTEP = 256 / C4;
+    constexpr int ITERS = BM / RSTEP;
+    const float alpha = p.alpha, beta = p.beta, lo = p.lo, hi = p.hi;
+    const int act = p.act, OH = d.OH, OW = d.OW;
+    const int cl = (tid % C4) * 4;
+    const int col = n0 + cl;
+    const int r0 = tid / C4;
+    if (col >= N) return;
+    const int ncol = min(4, N - col);
+    const bool full4 = p.vec_out && ncol == 4;
+    f4 cbias = {0.f, 0.f, 0.f, 0.f};
+    if (p.bias) {
+        if (full4) {
+            cbias = ldg4(p.bias + col);
+        } else {
+            for (int e = 0; e < ncol; ++e) cbias[e] = ldg(p.bias + col + e);
+        }
+    }
+    float *const cbase = p.c;
+    const float *const rbase = p.res;
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+        const int rl = r0 + RSTEP * it;
+        const int oh = oh0 + (rl >> 3), ow = ow0 + (rl & 7);
+        if (oh >= OH || ow >= OW) continue;
+        const long m = ((long)img * OH + oh) * OW + ow;
+        f4 v = *reinterpret_cast<const f4 *>(&Cs[rl * LDC + cl]);
+        v = v * alpha + cbias;
+        if (rbase) {
+            const float *src = rbase + m * p.ldr + col;
+            if (full4) {
+                v += beta * ldg4(src);
+            } else {
+                for (int e = 0; e < ncol; ++e) v[e] += beta * ldg(src + e);
+            }
+        }
+        v = act4(v, act, lo, hi);
+        float *dst = cbase + m * p.ldc + col;
+        if (full4) {
+            *reinterpret_cast<f4 *>(dst) = v;
+        } else {
+            for (int e = 0; e < ncol; ++e) dst[e] = v[e];
+        }
+    }
+}
+
 // Sum the split-K partials and apply the epilogue (one batch element).
 __global__ void gemm_splitk_reduce(const GemmDev p) {
     const long total = (long)p.M * p.N;
@@ -1797,6 +2076,72 @@ extern "C" void mgc_hip_gemm_layer_norm(mgc_hip_exec *x, const mgc_hip_gemm_args
     a.split_k = split;
     const LnTail tail{ln_scale, ln_bias, eps, ln_out};
     gemm_launch(x, &a, &tail);
+}
+
+extern "C" void mgc_hip_gemm_dw(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const mgc_hip_dw_args *dw) {
+    if (g->M <= 0 || g->N <= 0) return;
+    const long ohw = (long)dw->OH * dw->OW;
+    const long n_img = ohw > 0 ? g->M / ohw : 0;
+    const long x_bytes = n_img * dw->H * dw->W * (long)dw->C * 4;
+    const long b_bytes = ((long)(g->N - 1) * g->b.cs + g->K) * 4;
+    const bool ok = g->batch_rank == 0 && g->k1 == 0 && g->K == dw->C && dw->C > 0 && dw->C % 4 == 0 &&
+                    dw->H > 0 && dw->W > 0 && dw->SH == dw->SW && (dw->SH == 1 || dw->SH == 2) && ohw > 0 &&
+                    g->M % ohw == 0 && x_bytes < 0x7fffffffL && b_bytes < 0x7fffffffL &&
+                    9L * dw->C * 4 < 0x7fffffffL && (!g->bias || g->bias_mode == 1) &&
+                    g->b.kind == MGC_OP_STRIDED && g->b.rs == 1 && g->b.cs >= g->K && g->b.cs % 4 == 0 &&
+                    aligned16(g->b.p) && aligned16(dw->x) && aligned16(dw->w) && aligned16(dw->bias);
+    if (!ok) {
+        x->launch_error = (int)hipErrorInvalidValue;
+        set_error("mgc_hip_gemm_dw: shape, layout or alignment outside its limits", hipErrorInvalidValue);
+        return;
+    }
+    GemmDev p{};
+    p.M = g->M;
+    p.N = g->N;
+    p.K = g->K;
+    p.b = g->b;
+    p.c = g->c;
+    p.ldc = g->ldc;
+    p.alpha = g->alpha;
+    p.beta = g->beta;
+    p.bias = g->bias;
+    p.bias_mode = g->bias ? 1 : 0;
+    p.res = g->res;
+    p.ldr = g->ldr;
+    p.act = g->act;
+    p.lo = g->lo;
+    p.hi = g->hi;
+    p.split = 1;
+    p.nbatch = 1;
+    p.b_bytes = b_bytes;
+    p.vec_out = p.ldc % 4 == 0 && aligned16(p.c) && (!p.res || (p.ldr % 4 == 0 && aligned16(p.res))) &&
+                aligned16(p.bias);
+    DwDev d;
+    d.x = dw->x;
+    d.w = dw->w;
+    d.bias = dw->bias;
+    d.H = dw->H;
+    d.W = dw->W;
+    d.C = dw->C;
+    d.PT = dw->PT;
+    d.PL = dw->PL;
+    d.OH = dw->OH;
+    d.OW = dw->OW;
+    d.act = dw->act;
+    d.lo = dw->lo;
+    d.hi = dw->hi;
+    d.tiles_h = (dw->OH + 7) / 8;
+    d.tiles_w = (dw->OW + 7) / 8;
+    d.x_bytes = x_bytes;
+    // 64 x 32 tiles when N fits in 32 columns (MobileNet's narrow projections), else 64 x 64
+    const int bn = p.N <= 32 ? 32 : 64;
+    p.tiles_m = (int)(n_img * d.tiles_h * d.tiles_w);
+    p.tiles_n = (p.N + bn - 1) / bn;
+    typedef void (*DwKernel)(const GemmDev, const DwDev);
+    const bool s2 = dw->SH == 2;
+    const DwKernel kern = bn == 32 ? (s2 ? &gemm_dw_kernel<32, 2, 1> : &gemm_dw_kernel<32, 1, 2>)
+                                   : (s2 ? &gemm_dw_kernel<64, 2, 1> : &gemm_dw_kernel<64, 1, 2>);
+    MGC_LAUNCH(x, kern, dim3((unsigned)(p.tiles_m * p.tiles_n)), dim3(256), 0, p, d);
 }
 
 static void gemm_launch(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const LnTail *ln) {

@@ -102,6 +102,14 @@ FUSE_GEMM_LAYER_NORM = True
 # only the block's last 1 x 1 convolution reads, as its residual) inside that convolution's GEMM
 # by concatenating the two reductions along K; tests turn it off to compare.
 FUSE_PROJECTION_SHORTCUT = True
+# Compute a 3 x 3 depthwise convolution inside the GEMM of the 1 x 1 convolution that alone reads
+# its output (mgc_hip_gemm_dw: the A tiles are the depthwise output, which is never stored), for
+# GEMMs of at least DEPTHWISE_FUSE_MIN_ROWS output pixels (enough 8 x 8 pixel tiles to occupy
+# every CU) or over at most DEPTHWISE_FUSE_SHALLOW_K channels (three K stages or fewer, where
+# the saved launch outweighs the few tiles); tests turn it off to compare.
+FUSE_DEPTHWISE_POINTWISE = True
+DEPTHWISE_FUSE_MIN_ROWS = 16384
+DEPTHWISE_FUSE_SHALLOW_K = 96
 
 MAX_RANK = 6
 MAX_LEAVES = 16
@@ -248,6 +256,52 @@ def find_projection_shortcuts(graph: Graph) -> dict[int, Node]:
     return found
 
 
+def _depthwise3x3_nhwc(node: Node) -> bool:
+    """A float32 NHWC depthwise convolution (one channel per group) with a constant 3 x 3
+    kernel, strides (1, 1) or (2, 2), no dilation, constant bias (or none), no residual and
+    C % 4 == 0."""
+    if node.op not in ("Conv", "FusedConv") or ops.conv_layout(node) != "NHWC":
+        return False
+    w, xt = node.input(1), node.input(0).tensor_type
+    if w.data is None or xt.dtype != "float32" or xt.rank != 4 or not HipEmitter.depthwise(node):
+        return False
+    if w.tensor_type.shape[:2] != (3, 3) or xt.shape[3] % 4 or node.input(0).data is not None:
+        return False
+    g = ops.window_geometry(node, xt.shape[1:3], (3, 3))
+    if tuple(g.dilations) != (1, 1) or tuple(g.strides) not in ((1, 1), (2, 2)):
+        return False
+    b = node.optional_input(2)
+    return (b is None or b.data is not None) and node.optional_input(3) is None
+
+
+def find_depthwise_pointwise(graph: Graph, min_rows: int | None = None) -> dict[int, Node]:
+    """id(pw) -> dw for every 3 x 3 depthwise convolution dw whose output only the pointwise
+    convolution pw reads (MobileNet's depthwise -> projection pair), when pw's GEMM has at least
+    ``min_rows`` rows (default DEPTHWISE_FUSE_MIN_ROWS) or at most DEPTHWISE_FUSE_SHALLOW_K
+    input channels: pw is a stride-1 pointwise NHWC convolution, dw a depthwise 3 x 3
+    convolution (stride 1 or 2, any padding) over a tensor whose channels are a multiple of 4."""
+    if min_rows is None:
+        min_rows = DEPTHWISE_FUSE_MIN_ROWS
+    outputs = {id(v) for v in graph.outputs}
+    found: dict[int, Node] = {}
+    for pw in graph.nodes:
+        if not _pointwise_nhwc(pw):
+            continue
+        d = pw.input(0)
+        dw = d.producer
+        if dw is None or not _depthwise3x3_nhwc(dw) or id(d) in outputs or d.users != [pw]:
+            continue
+        if sum(v is d for v in pw.inputs) != 1:
+            continue
+        at = d.tensor_type
+        if ops.window_geometry(pw, at.shape[1:3], (1, 1)).strides != (1, 1):
+            continue
+        if at.shape[0] * at.shape[1] * at.shape[2] < min_rows and at.shape[3] > DEPTHWISE_FUSE_SHALLOW_K:
+            continue
+        found[id(pw)] = dw
+    return found
+
+
 def pack_b_nk(b: np.ndarray) -> np.ndarray:
     """A constant K x N right-hand side stored as its transpose [N][K] (k contiguous), the
     layout the MFMA GEMM reads with 16-byte k-quad loads."""
@@ -304,9 +358,18 @@ class HipEmitter:
         # input is then read at the last conv's step, which the plan must keep it alive for.
         self._shortcut: dict[int, Node] = find_projection_shortcuts(graph) if FUSE_PROJECTION_SHORTCUT else {}
         self._shortcut_skip = {id(ds) for ds in self._shortcut.values()}
+        # id(pointwise conv) -> the depthwise convolution computed in its GEMM; the depthwise
+        # input is then read at the pointwise step, which the plan must keep it alive for.
+        self._dwpw: dict[int, Node] = find_depthwise_pointwise(graph) if FUSE_DEPTHWISE_POINTWISE else {}
+        for pw_id in [i for i, dw in self._dwpw.items() if id(dw) in self._shortcut or i in self._shortcut]:
+            del self._dwpw[pw_id]
+        self._dwpw_skip = {id(dw) for dw in self._dwpw.values()}
         order = {id(n): i for i, n in enumerate(graph.nodes)}
         keep = {id(ds.input(0)): order[id(c3)] for c3 in graph.nodes
                 if (ds := self._shortcut.get(id(c3))) is not None}
+        for pw in graph.nodes:
+            if (dw := self._dwpw.get(id(pw))) is not None:
+                keep[id(dw.input(0))] = max(keep.get(id(dw.input(0)), 0), order[id(pw)])
         self.plan = plan_memory(graph, strategy=strategy, alignment=ALIGN, inplace=inplace,
                                 workspace=self._workspace_bytes, extra_reads=keep)
         self.weights = WeightsBuilder()
@@ -334,7 +397,8 @@ class HipEmitter:
                     out_bytes = max(out_bytes, m.out.tensor_type.nbytes)
                 if m.qkv_gemms:
                     qkv_bytes = max(qkv_bytes, 3 * m.out.tensor_type.nbytes)
-        excluded = set(self._attn_skip) | set(self._attn_emit) | set(self._shortcut) | self._shortcut_skip
+        excluded = (set(self._attn_skip) | set(self._attn_emit) | set(self._shortcut) | self._shortcut_skip
+                    | set(self._dwpw) | self._dwpw_skip)
         self._folds = plan_folds(graph, self.plan, self._workspace_bytes, excluded) if FOLD_TRANSPOSES else FoldPlan()
         self._scratch_qkv_off = self._scratch_off
         self._scratch_out_off = self._scratch_off + (qkv_bytes + ALIGN - 1) // ALIGN * ALIGN
@@ -515,6 +579,10 @@ class HipEmitter:
             return
         if id(node) in self._shortcut_skip:
             self.emit("/* projection shortcut: computed in the GEMM of the convolution that adds it */")
+            self.count("folded")
+            return
+        if id(node) in self._dwpw_skip:
+            self.emit("/* depthwise convolution: computed in the GEMM of the pointwise convolution that reads it */")
             self.count("folded")
             return
         if id(node) in self._ln_skip:
@@ -923,10 +991,12 @@ class HipEmitter:
                    bias: str = "NULL", bias_mode: int = 0, res: str = "NULL", ldr: int = 0,
                    beta: float = 1.0, act: str = "none", lo: float = 0.0, hi: float = 6.0,
                    workspace: str = "NULL", workspace_floats: int = 0,
-                   layer_norm: tuple[str, str, str, str] | None = None, extra: Sequence[str] = ()) -> None:
+                   layer_norm: tuple[str, str, str, str] | None = None, extra: Sequence[str] = (),
+                   depthwise: str | None = None) -> None:
         """One mgc_hip_gemm call; ``layer_norm`` = (scale, bias, eps, out) makes it an
         mgc_hip_gemm_layer_norm call whose split-K reduction also normalizes the rows; ``extra``
-        are further field assignments (the concatenated-K operand)."""
+        are further field assignments (the concatenated-K operand); ``depthwise`` declares and
+        fills an mgc_hip_dw_args ``d`` and makes it an mgc_hip_gemm_dw call."""
         if len(batch) > MAX_BATCH_RANK:
             raise CodegenError(f"GEMM with {len(batch)} batch dimensions is not supported")
         parts = ["mgc_hip_gemm_args g; memset(&g, 0, sizeof g);", f"g.M = {m}; g.N = {n}; g.K = {k};"]
@@ -943,6 +1013,8 @@ class HipEmitter:
         if layer_norm is not None:
             scale, lbias, eps, out = layer_norm
             parts.append(f"mgc_hip_gemm_layer_norm(x, &g, {scale}, {lbias}, {eps}, {out});")
+        elif depthwise is not None:
+            parts += [depthwise, "mgc_hip_gemm_dw(x, &g, &d);"]
         else:
             parts.append("mgc_hip_gemm(x, &g);")
         self.emit("{ " + " ".join(parts) + " }")
@@ -1199,6 +1271,9 @@ class HipEmitter:
         if id(node) in self._shortcut:
             self._conv_with_shortcut(node, self._shortcut[id(node)])
             return
+        if id(node) in self._dwpw:
+            self._conv_with_depthwise(node, self._dwpw[id(node)])
+            return
         kg = kout // group
         geo = (f"g.{{f}}.H = {h}; g.{{f}}.W = {wd}; g.{{f}}.C = {c}; g.{{f}}.KH = {kh}; g.{{f}}.KW = {kw}; "
                f"g.{{f}}.SH = {g.strides[0]}; g.{{f}}.SW = {g.strides[1]}; g.{{f}}.DH = {g.dilations[0]}; "
@@ -1239,8 +1314,9 @@ class HipEmitter:
         """act(a W3 + x_s Wd + b3 + bd) as one GEMM over K = K1 + C2: a is the pointwise
         convolution's NHWC input (K1 channels), x_s the shortcut's input x sampled at its
         stride (C2 channels), B the two weight matrices stacked along K and the bias their sum.
-        The shortcut's output is never written. When a or x is a caller buffer the generated
-        code checks its 16-byte alignment and otherwise runs the two convolutions apart."""
+        The shortcut's output is never written. When a or x is a caller buffer (a graph input or
+        output) the generated code checks its 16-byte alignment and otherwise runs the two
+        convolutions apart."""
         a, xv = node.input(0), ds.input(0)
         nb, oh, ow, k1 = a.tensor_type.shape
         _, h2, w2, c2 = xv.tensor_type.shape
@@ -1260,7 +1336,7 @@ class HipEmitter:
               f"g.a2.C = {c2}; g.a2.KH = 1; g.a2.KW = 1; g.a2.SH = {sh}; g.a2.SW = {sw}; g.a2.DH = 1; "
               f"g.a2.DW = 1; g.a2.PT = 0; g.a2.PL = 0; g.a2.OH = {oh}; g.a2.OW = {ow}; g.a2.cg = {c2}; "
               f"g.k1 = {k1};")
-        external = [v for v in (a, xv) if self.plan.location(v).kind == "input"]
+        external = [v for v in (a, xv) if self.plan.location(v).kind in ("input", "output")]
         if external:
             cond = " && ".join(f"(((uintptr_t){self.ptr(v)} & 15) == 0)" for v in external)
             self.emit(f"if ({cond}) {{")
@@ -1276,6 +1352,47 @@ class HipEmitter:
                 self.op_FusedConv(node)
             finally:
                 self._shortcut[id(node)] = saved
+            self.emit("}")
+
+    def _conv_with_depthwise(self, node: Node, dw: Node) -> None:
+        """pw(act_d(dw(x))) as one GEMM whose A tiles are the depthwise output, computed from x
+        while each tile is staged (mgc_hip_gemm_dw); the depthwise output is never written. When
+        x is a caller buffer (a graph input or output) the generated code checks its 16-byte
+        alignment and otherwise runs the two convolutions apart."""
+        xv = dw.input(0)
+        nb, h, wd, c = xv.tensor_type.shape
+        g = ops.window_geometry(dw, (h, wd), (3, 3))
+        oh, ow = g.out_hw
+        wdw = np.ascontiguousarray(dw.input(1).data.reshape(9, c), np.float32)
+        dwoff = self.weights.add(wdw, key=("dw", id(dw.input(1))))
+        dbias_v = dw.optional_input(2)
+        dbias = self._vector_ptr(dbias_v, c, "Conv bias") if dbias_v is not None else "NULL"
+        dact, dlo, dhi = self._act(dw) if dw.op == "FusedConv" else ("none", 0.0, 6.0)
+        n = node.input(1).tensor_type.shape[3]
+        bspec = self._packed_b(node.input(1).data.reshape(c, n), ("conv", id(node.input(1)), 0))
+        bias_v, res_v = node.optional_input(2), node.optional_input(3)
+        bias = self._vector_ptr(bias_v, n, "Conv bias") if bias_v is not None else "NULL"
+        res = self.fptr(res_v) if res_v is not None else "NULL"
+        act, lo, hi = self._act(node) if node.op == "FusedConv" else ("none", 0.0, 6.0)
+        dws = (f"mgc_hip_dw_args d; memset(&d, 0, sizeof d); d.x = {self.fptr(xv)}; "
+               f"d.w = (const float *)(W + {dwoff}); d.bias = {dbias}; d.H = {h}; d.W = {wd}; d.C = {c}; "
+               f"d.SH = {g.strides[0]}; d.SW = {g.strides[1]}; d.PT = {g.pads[0]}; d.PL = {g.pads[1]}; "
+               f"d.OH = {oh}; d.OW = {ow}; d.act = {ACT_CODES[dact]}; d.lo = {_f(dlo)}; d.hi = {_f(dhi)};")
+        external = self.plan.location(xv).kind in ("input", "output")
+        if external:
+            self.emit(f"if ((((uintptr_t){self.ptr(xv)}) & 15) == 0) {{")
+        self._gemm_call(nb * oh * ow, n, c, [], bspec, self.fptr(node.output), n, bias=bias,
+                        bias_mode=1 if bias != "NULL" else 0, res=res, ldr=n, act=act, lo=lo, hi=hi,
+                        depthwise=dws)
+        self.count("gemm_depthwise")
+        if external:
+            self.emit("} else {")
+            saved = self._dwpw.pop(id(node))
+            try:
+                self.op_FusedConv(dw)
+                self.op_FusedConv(node)
+            finally:
+                self._dwpw[id(node)] = saved
             self.emit("}")
 
     # -- space-to-depth convolution -------------------------------------------------------------
@@ -1498,8 +1615,9 @@ class HipEmitter:
 
     def _node_flops(self) -> list[int]:
         """FLOPs per node, with the nodes a fused attention call absorbs (among them a QKV
-        projection GEMM) counted at the node that emits the call, and a projection shortcut at
-        the convolution whose GEMM computes it: the launches of that node do the work."""
+        projection GEMM) counted at the node that emits the call, and a projection shortcut or a
+        depthwise convolution at the convolution whose GEMM computes it: the launches of that
+        node do the work."""
         index = {id(n): i for i, n in enumerate(self.graph.nodes)}
         flops = [ops.flops(n) for n in self.graph.nodes]
         for nid, m in self._attn_skip.items():
@@ -1509,6 +1627,10 @@ class HipEmitter:
         for c3_id, ds in self._shortcut.items():
             i = index[id(ds)]
             flops[index[c3_id]] += flops[i]
+            flops[i] = 0
+        for pw_id, dw in self._dwpw.items():
+            i = index[id(dw)]
+            flops[index[pw_id]] += flops[i]
             flops[i] = 0
         return flops
 

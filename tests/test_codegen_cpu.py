@@ -83,6 +83,7 @@ def test_kernel_mix_matches_reference(name, kernels, arena, monkeypatch):
 
     make = builders.SAMPLES.get(name) or builders.CONFIGS[name]
     monkeypatch.setattr(hip_codegen, "FUSE_PROJECTION_SHORTCUT", False)
+    monkeypatch.setattr(hip_codegen, "FUSE_DEPTHWISE_POINTWISE", False)
     monkeypatch.setattr(hip_codegen, "SPACE_TO_DEPTH", False)
     gen = generate_hip(o3(make()))
     assert gen.kernels == kernels
@@ -126,6 +127,42 @@ def test_projection_shortcuts_join_their_block_gemm():
                 continue
             assert b.offset + b.size <= x.offset or x.offset + x.size <= b.offset
     assert not find_projection_shortcuts(o3(builders.bottleneck()))  # identity shortcuts only
+
+
+def test_depthwise_pointwise_pairs_join_one_gemm():
+    """MobileNetV2 at batch 32: the six depthwise -> projection pairs whose GEMMs have at least
+    DEPTHWISE_FUSE_MIN_ROWS rows (the 112 x 112, 56 x 56 and 28 x 28 outputs) each run as one
+    mgc_hip_gemm_dw call; the depthwise input stays alive (its arena block clear of everything
+    placed) until that call reads it, and the depthwise FLOPs are counted at the call's node. At
+    batch 1 only the two shallow pairs (32 and 96 channels) are fused."""
+    from ml_graph_compiler import ops
+    from ml_graph_compiler.codegen.hip import find_depthwise_pointwise
+
+    g = o3(builders.mobilenet_v2(batch=32))
+    pairs = find_depthwise_pointwise(g)
+    assert len(pairs) == 6
+    assert all(dw.output.tensor_type.shape[1] in (112, 56, 28) for dw in pairs.values())
+    assert len(find_depthwise_pointwise(g, min_rows=0)) == 17
+    gen = generate_hip(g, gemm_workspace=native.gemm_workspace_floats)
+    assert gen.kernels["gemm_depthwise"] == 6 and gen.kernels["depthwise"] == 11 and gen.kernels["gemm"] == 36
+    assert gen.source.count("mgc_hip_gemm_dw(x, &g, &d);") == 6
+    assert sum(gen.node_flops) == sum(ops.flops(n) for n in g.nodes)
+    skipped = {id(d) for d in pairs.values()}
+    assert all(gen.node_flops[i] == 0 for i, n in enumerate(g.nodes) if id(n) in skipped)
+    order = {id(n): i for i, n in enumerate(g.nodes)}
+    by_value = {id(v): b for b in gen.plan.buffers for v in b.values}
+    for pw in g.nodes:
+        dw = pairs.get(id(pw))
+        if dw is None:
+            continue
+        x = by_value[id(dw.input(0))]
+        assert x.end >= order[id(pw)]
+        for b in gen.plan.buffers:
+            if b is x or not (b.start <= order[id(pw)] <= b.end):
+                continue
+            assert b.offset + b.size <= x.offset or x.offset + x.size <= b.offset
+    shallow = find_depthwise_pointwise(o3(builders.mobilenet_v2(batch=1)))  # 112 x 112 = 12544 rows
+    assert sorted(dw.input(0).tensor_type.shape[3] for dw in shallow.values()) == [32, 96]
 
 
 def test_every_sample_and_config_generates_and_builds(hip_cache):
