@@ -1376,12 +1376,15 @@ struct DwDev {
 //    (r >> 3, r & 7) of the block) from the patch into the A tile. BN 64: 2 x 2 waves of 32 x 32
 //    MFMA blocks; BN 32: waves w and w + 2 share the 32 x 32 block of rows 32 w, taking k 0-15
 //    and 16-31 of each stage, and sum their halves through LDS at the end.
+//  * The A and B tiles keep 32-float rows with the quads XOR-swizzled (no padding): the stride-1
+//    form then takes 38 KB of LDS for BN 32, so four workgroups fit a CU (the CU's 160 KB hold
+//    four of 40 KB only in the occupancy query, not on the hardware).
 //  * The epilogue maps tile rows back to pixels (rows outside the image are not stored).
 template <int BN, int S, int PBUF>
 __global__ void __launch_bounds__(256) gemm_dw_kernel(const GemmDev p, const DwDev d) {
     constexpr int BM = 64;
     constexpr int BK = 32;
-    constexpr int LDK = BK + 4;
+    constexpr int LDK = BK;  // rows unpadded: quad q of row r sits at position q ^ f(r)
     constexpr int PWID = 7 * S + 3;                    // patch rows and columns
     constexpr int PQUADS = PWID * PWID * 8;             // 16-byte quads of one patch
     constexpr int PINS = (PQUADS + 63) / 64;            // DMA instructions per patch
@@ -1398,8 +1401,12 @@ __global__ void __launch_bounds__(256) gemm_dw_kernel(const GemmDev p, const DwD
 
     __shared__ __attribute__((aligned(16))) float smem[SMEM];
     float *const Ps = smem;                          // [PBUF][PFLOATS] patches [pixel][32]
-    float *const As = smem + PBUF * PFLOATS;         // [BM][LDK]
-    float *const Bs = As + BM * LDK;                 // [BN][LDK]
+    float *const As = smem + PBUF * PFLOATS;         // [BM][32], swizzled
+    float *const Bs = As + BM * LDK;                 // [BN][32], swizzled
+    // f(r) = (r & 7) ^ ((r >> 3) & 1): distinct over any 8 consecutive rows and over the 8 even
+    // (or odd) rows of an aligned 16, so 16-byte reads of one quad from 8 or 16 rows spread over
+    // the banks (the layout of gemm_dma_kernel's stages)
+    auto swz = [](int r) __attribute__((always_inline)) { return (r & 7) ^ ((r >> 3) & 1); };
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1505,10 +1512,13 @@ __global__ void __launch_bounds__(256) gemm_dw_kernel(const GemmDev p, const DwD
 #pragma unroll
                     for (int e = 0; e < 4; ++e) v[e] = fmaf(xv[e], wq[i * 3 + j][e], v[e]);
                 }
-            *reinterpret_cast<f4 *>(&As[row * LDK + kq]) = act4(v, d.act, d.lo, d.hi);
+            *reinterpret_cast<f4 *>(&As[row * LDK + ((q ^ swz(row)) << 2)]) = act4(v, d.act, d.lo, d.hi);
         }
 #pragma unroll
-        for (int r = 0; r < BV; ++r) *reinterpret_cast<f4 *>(&Bs[((tid >> 3) + 32 * r) * LDK + kq]) = breg[r];
+        for (int r = 0; r < BV; ++r) {
+            const int row = (tid >> 3) + 32 * r;
+            *reinterpret_cast<f4 *>(&Bs[row * LDK + ((q ^ swz(row)) << 2)]) = breg[r];
+        }
     };
 
     floatx16 acc;
@@ -1516,6 +1526,7 @@ __global__ void __launch_bounds__(256) gemm_dw_kernel(const GemmDev p, const DwD
     for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
     const int li = lane & 31;
     const int lh = lane >> 5;
+    const int sw = swz(li);  // fragment rows start at multiples of 32
 
     if (nk > 0) {
         issue_patch(0, 0);
@@ -1534,8 +1545,8 @@ __global__ void __launch_bounds__(256) gemm_dw_kernel(const GemmDev p, const DwD
             f4 af[4], bf[4];
 #pragma unroll
             for (int s2 = 0; s2 < 4; ++s2) {
-                af[s2] = *reinterpret_cast<const f4 *>(&As[(wm * 32 + li) * LDK + lh * 16 + 4 * s2]);
-                bf[s2] = *reinterpret_cast<const f4 *>(&Bs[(wn * 32 + li) * LDK + lh * 16 + 4 * s2]);
+                af[s2] = *reinterpret_cast<const f4 *>(&As[(wm * 32 + li) * LDK + (((lh * 4 + s2) ^ sw) << 2)]);
+                bf[s2] = *reinterpret_cast<const f4 *>(&Bs[(wn * 32 + li) * LDK + (((lh * 4 + s2) ^ sw) << 2)]);
             }
 #pragma unroll
             for (int s2 = 0; s2 < 4; ++s2)
@@ -1546,8 +1557,8 @@ __global__ void __launch_bounds__(256) gemm_dw_kernel(const GemmDev p, const DwD
             f4 af[2], bf[2];
 #pragma unroll
             for (int s2 = 0; s2 < 2; ++s2) {
-                af[s2] = *reinterpret_cast<const f4 *>(&As[(wm * 32 + li) * LDK + khalf * 16 + lh * 8 + 4 * s2]);
-                bf[s2] = *reinterpret_cast<const f4 *>(&Bs[li * LDK + khalf * 16 + lh * 8 + 4 * s2]);
+                af[s2] = *reinterpret_cast<const f4 *>(&As[(wm * 32 + li) * LDK + (((khalf * 4 + lh * 2 + s2) ^ sw) << 2)]);
+                bf[s2] = *reinterpret_cast<const f4 *>(&Bs[li * LDK + (((khalf * 4 + lh * 2 + s2) ^ sw) << 2)]);
             }
 #pragma unroll
             for (int s2 = 0; s2 < 2; ++s2)
