@@ -477,8 +477,9 @@ def hbm_summary(fetch_dir: Path, write_dir: Path, trace_dir: Path, workload: str
         rows.append((name, fb, wb, sec))
 
     def bound(name: str) -> str:
-        # the split-K reductions move bytes; the streaming short-K GEMM is HBM-bound by design
-        if "gemm_" in name and "splitk" not in name and "gemm_stream" not in name:
+        # the split-K reductions move bytes; the streaming short-K GEMM and the depthwise GEMM
+        # (a 3 x 3 depthwise pass feeding a narrow projection) are HBM-bound by design
+        if "gemm_" in name and "splitk" not in name and "gemm_stream" not in name and "gemm_dw" not in name:
             return "MFMA"
         return "MFMA/latency" if "attention" in name else "HBM"
 
