@@ -703,6 +703,62 @@ __global__ void space_to_depth_kernel(int C, int H2, int W2, int total, FastDiv 
     }
 }
 
+// The same for C <= 4, W % 4 == 0 and 16-byte aligned input: one thread per pair of
+// neighbouring output pixels (b, i, 2 jp .. 2 jp + 1), whose 2 x 4 input block per channel is two
+// 16-byte reads (neighbouring threads read neighbouring 16 bytes of a row). The pair's 8 C output
+// values are contiguous and so are the 64 pairs of a wave, so the wave stages its 64 x 8 C values
+// in LDS and writes them back as whole contiguous 1 KB rows (lane l writes 16 bytes at 16 l of
+// each), instead of 16-byte pieces 32 C bytes apart.
+template <int C>
+__global__ void __launch_bounds__(256) space_to_depth_vec_kernel(int H2, int W4, int total, FastDiv div_w4,
+                                                                 FastDiv div_h2, const float *in, float *out) {
+    constexpr int PAIR = 8 * C;  // floats per pair of output pixels
+    __shared__ __attribute__((aligned(16))) float stage[4][64 * PAIR];
+    const int H = 2 * H2, W = 4 * W4;
+    const int lane = threadIdx.x & 63;
+    float *const buf = stage[threadIdx.x >> 6];
+    const int step = gridDim.x * blockDim.x;
+    // every lane of a wave runs the same trips (the bound is the wave's first pair)
+    for (int base = blockIdx.x * blockDim.x + (threadIdx.x & ~63); base < total; base += step) {
+        const int idx = base + lane;
+        if (idx < total) {
+            const int t = fdiv(idx, div_w4);
+            const int jp = idx - t * W4;
+            const int b = fdiv(t, div_h2);
+            const int i = t - b * H2;
+            const float *src = in + (long)b * C * H * W + (long)(2 * i) * W + 4 * jp;
+            float4 row[C][2];
+#pragma unroll
+            for (int c = 0; c < C; ++c)
+#pragma unroll
+                for (int dy = 0; dy < 2; ++dy)
+                    row[c][dy] = *reinterpret_cast<const float4 *>(src + (long)c * H * W + dy * W);
+            // output pixel q of the pair holds value (dy * 2 + dx) * C + c = input (c, dy, 2 q + dx)
+            float *v = buf + lane * PAIR;
+#pragma unroll
+            for (int c = 0; c < C; ++c)
+#pragma unroll
+                for (int dy = 0; dy < 2; ++dy) {
+                    v[(dy * 2) * C + c] = row[c][dy].x;
+                    v[(dy * 2 + 1) * C + c] = row[c][dy].y;
+                    v[4 * C + (dy * 2) * C + c] = row[c][dy].z;
+                    v[4 * C + (dy * 2 + 1) * C + c] = row[c][dy].w;
+                }
+        }
+        __builtin_amdgcn_wave_barrier();
+        // the wave's pairs [base, base + n) are out[base * PAIR ...] contiguous
+        const int n = min(64, total - base);
+        const float4 *src4 = reinterpret_cast<const float4 *>(buf);
+        float4 *dst4 = reinterpret_cast<float4 *>(out + (long)base * PAIR);
+#pragma unroll
+        for (int q = 0; q < 2 * C; ++q) {
+            const int e = q * 64 + lane;  // 16-byte chunk of the wave's block
+            if (e < n * 2 * C) dst4[e] = src4[e];
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
 template <typename T>
 __global__ void fill_kernel(T *out, long n, T v) {
     for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < n;
@@ -731,6 +787,43 @@ __global__ void gather_kernel(const unsigned char *src, const void *idx, int idx
                 reinterpret_cast<unsigned *>(d)[w] = reinterpret_cast<const unsigned *>(s)[w];
         } else {
             for (long b = threadIdx.x; b < inner_bytes; b += blockDim.x) d[b] = s[b];
+        }
+    }
+}
+
+// Rows of a multiple of 16 bytes with 16-byte aligned table and output (embedding lookups):
+// one wavefront per (outer, t) row, 16 bytes per lane per access, up to four accesses' loads in
+// flight before their stores; four rows per workgroup. Out-of-range indices set the flag and
+// leave their row unwritten, as gather_kernel does.
+__global__ void __launch_bounds__(256) gather_rows16_kernel(const uint4 *src, const void *idx, int idx_dtype,
+                                                            long outer, long dim, long n, long inner16,
+                                                            uint4 *out, int *flag) {
+    const int lane = threadIdx.x & 63;
+    const long rows = outer * n;
+    const long step = ((long)gridDim.x * 256) >> 6;
+    for (long row = ((long)blockIdx.x * 256 + threadIdx.x) >> 6; row < rows; row += step) {
+        const long o = row / n, t = row - o * n;
+        long k = idx_dtype == MGC_I64 ? static_cast<const long long *>(idx)[t]
+                                      : (long)static_cast<const int *>(idx)[t];
+        if (k < 0) k += dim;
+        if (k < 0 || k >= dim) {
+            if (lane == 0) *flag = 1;
+            continue;
+        }
+        const uint4 *s = src + (o * dim + k) * inner16;
+        uint4 *d = out + row * inner16;
+        // every lane loads (past the row's end it rereads the row's last chunk) so the four
+        // loads are issued together without a branch around each; only the stores are masked
+        for (long w0 = lane; w0 < inner16; w0 += 256) {
+            uint4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const long w = w0 + 64 * u;
+                v[u] = s[w < inner16 ? w : inner16 - 1];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (w0 + 64 * u < inner16) d[w0 + 64 * u] = v[u];
         }
     }
 }
@@ -842,6 +935,18 @@ extern "C" void mgc_hip_space_to_depth(mgc_hip_exec *x, int N, int C, int H, int
         set_error("mgc_hip_space_to_depth: unsupported shape or alignment", hipErrorInvalidValue);
         return;
     }
+    if (C <= 4 && W % 4 == 0 && ((uintptr_t)in & 15) == 0) {
+        const long pairs = total / 2;
+        const dim3 grid(blocks_for(pairs, 256, 16384));
+        const FastDiv dw4 = make_fastdiv((unsigned)(W / 4)), dh2 = make_fastdiv((unsigned)(H / 2));
+        switch (C) {
+        case 1: MGC_LAUNCH(x, space_to_depth_vec_kernel<1>, grid, dim3(256), 0, H / 2, W / 4, (int)pairs, dw4, dh2, in, out); break;
+        case 2: MGC_LAUNCH(x, space_to_depth_vec_kernel<2>, grid, dim3(256), 0, H / 2, W / 4, (int)pairs, dw4, dh2, in, out); break;
+        case 3: MGC_LAUNCH(x, space_to_depth_vec_kernel<3>, grid, dim3(256), 0, H / 2, W / 4, (int)pairs, dw4, dh2, in, out); break;
+        default: MGC_LAUNCH(x, space_to_depth_vec_kernel<4>, grid, dim3(256), 0, H / 2, W / 4, (int)pairs, dw4, dh2, in, out); break;
+        }
+        return;
+    }
     MGC_LAUNCH(x, space_to_depth_kernel, dim3(blocks_for(total, 256, 16384)), dim3(256), 0, C, H / 2,
                W / 2, (int)total, make_fastdiv((unsigned)(W / 2)), make_fastdiv((unsigned)(H / 2)), in, out);
 }
@@ -873,6 +978,11 @@ extern "C" void mgc_hip_gather(mgc_hip_exec *x, const void *src, const void *idx
                                long outer, long dim, long n, long inner_bytes, void *out) {
     long rows = outer * n;
     if (rows <= 0 || inner_bytes <= 0) return;
+    if (inner_bytes % 16 == 0 && (((uintptr_t)src | (uintptr_t)out) & 15) == 0) {
+        MGC_LAUNCH(x, gather_rows16_kernel, dim3(blocks_for(rows * 64, 256, 16384)), dim3(256), 0,
+                   (const uint4 *)src, idx, idx_dtype, outer, dim, n, inner_bytes / 16, (uint4 *)out, x->flag);
+        return;
+    }
     unsigned grid = (unsigned)(rows < 65536 ? rows : 65536);
     MGC_LAUNCH(x, gather_kernel, dim3(grid), dim3(256), 0, (const unsigned char *)src, idx,
                idx_dtype, outer, dim, n, inner_bytes, (unsigned char *)out, x->flag);

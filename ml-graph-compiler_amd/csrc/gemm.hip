@@ -1006,6 +1006,81 @@ __device__ __forceinline__ void wait_stages(int n) {
     }
 }
 
+// Epilogue of the 16 x 16 wave-split kernels: each wave's partial tile (register r of acc holds
+// row 4 (lane / 16) + r, column lane % 16) goes to its LDS slot (smem holds at least
+// WAVES * 16 * 20 floats, free when this is called), and thread t < 64 sums the slots' chunk
+// (row t / 4, columns 4 (t % 4) .. + 3) in wave order, applies alpha, bias, residual and
+// activation (its bias and residual chunks requested by the caller before the K loop) and stores
+// it, or writes the raw sum to the K-split workspace.
+template <int WAVES>
+__device__ __forceinline__ void wsplit16_finish(const GemmDev &p, float *smem, const f4 acc, int tid, int ks,
+                                                long co, long ro, bool split_out, int er, int ec, int erow,
+                                                int ecol, bool eok, bool efull, const f4 &ebias, const f4 &eres) {
+    constexpr int T = 16, LDC = T + 4;
+    // the argument block's fields read once into registers (a reference into the kernel's
+    // argument block kept live across the epilogue makes the compiler copy it to scratch)
+    const int M = p.M, N = p.N, act = p.act, bias_mode = p.bias ? p.bias_mode : 0;
+    const float alpha = p.alpha, beta = p.beta, lo = p.lo, hi = p.hi;
+    const float *const bias = p.bias;
+    const float *const res = p.res;
+    float *const ws = p.ws;
+    float *const c = p.c;
+    const long ldr = p.ldr, ldc = p.ldc;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4;
+    float *const slot = smem + wave * (T * LDC);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) slot[(4 * lg + r) * LDC + li] = acc[r];
+    __syncthreads();
+    if (!eok) return;
+    const int o = er * LDC + ec;
+    f4 v = *reinterpret_cast<const f4 *>(&smem[o]);
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) v += *reinterpret_cast<const f4 *>(&smem[w * T * LDC + o]);
+    const int ncol = min(4, N - ecol);
+    // a partial chunk (the last columns of an N that is not a multiple of 4, or unaligned
+    // rows) goes element by element
+    auto store = [&](float *dst) __attribute__((always_inline)) {
+        if (efull) {
+            *reinterpret_cast<f4 *>(dst) = v;
+        } else {
+            dst[0] = v[0];
+            if (ncol > 1) dst[1] = v[1];
+            if (ncol > 2) dst[2] = v[2];
+            if (ncol > 3) dst[3] = v[3];
+        }
+    };
+    if (split_out) {
+        store(ws + (long)ks * M * N + (long)erow * N + ecol);
+        return;
+    }
+    f4 b = ebias, r = eres;
+    if (!efull) {  // scalar bias and residual reads
+        const f4 zero4 = {0.f, 0.f, 0.f, 0.f};
+        b = zero4;
+        r = zero4;
+        if (bias_mode == 1) {
+            const float *bp = bias + ecol;
+            b[0] = ldg(bp);
+            if (ncol > 1) b[1] = ldg(bp + 1);
+            if (ncol > 2) b[2] = ldg(bp + 2);
+            if (ncol > 3) b[3] = ldg(bp + 3);
+        }
+        if (res) {
+            const float *rp = res + ro + (long)erow * ldr + ecol;
+            r[0] = ldg(rp);
+            if (ncol > 1) r[1] = ldg(rp + 1);
+            if (ncol > 2) r[2] = ldg(rp + 2);
+            if (ncol > 3) r[3] = ldg(rp + 3);
+        }
+    }
+    v = v * alpha + b;
+    if (bias_mode == 2) v += ldg(bias + erow);
+    if (res) v += beta * r;
+    v = act4(v, act, lo, hi);
+    store(c + co + (long)erow * ldc + ecol);
+}
+
 // GEMM / implicit-GEMM convolution on 16 x 16 output tiles whose K range is dealt out to the
 // workgroup's WAVES waves (wave w takes the 32-wide K stages w, w + WAVES, ...), each with a
 // STAGES-deep DMA ring of its own, on v_mfma_f32_16x16x4f32 (the 32 x 32 x 2 form's rate per
@@ -1194,41 +1269,7 @@ __global__ void __launch_bounds__(64 * WAVES) gemm_dma_wsplit16_kernel(const Gem
         for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a1[e], b1[e], acc, 0, 0, 0);
     }
     __syncthreads();  // every wave is done with its ring (the slots below overlap the rings)
-    float *const slot = smem + wave * (T * LDC);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) slot[(4 * lg + r) * LDC + li] = acc[r];
-    __syncthreads();
-    if (!eok) return;
-    const int o = er * LDC + ec;
-    f4 v = *reinterpret_cast<const f4 *>(&smem[o]);
-#pragma unroll
-    for (int w = 1; w < WAVES; ++w) v += *reinterpret_cast<const f4 *>(&smem[w * T * LDC + o]);
-    const int ncol = min(4, p.N - ecol);
-    if (split_out) {
-        float *dst = p.ws + (long)ks * p.M * p.N + (long)erow * p.N + ecol;
-        if (efull) {
-            *reinterpret_cast<f4 *>(dst) = v;
-        } else {
-            for (int e = 0; e < ncol; ++e) dst[e] = v[e];
-        }
-        return;
-    }
-    if (!efull) {  // scalar bias and residual reads
-        for (int e = 0; e < ncol; ++e) {
-            if (p.bias && p.bias_mode == 1) ebias[e] = ldg(p.bias + ecol + e);
-            if (p.res) eres[e] = ldg(p.res + ro + (long)erow * p.ldr + ecol + e);
-        }
-    }
-    v = v * p.alpha + ebias;
-    if (p.bias && p.bias_mode == 2) v += ldg(p.bias + erow);
-    if (p.res) v += p.beta * eres;
-    v = act4(v, p.act, p.lo, p.hi);
-    float *dst = p.c + co + (long)erow * p.ldc + ecol;
-    if (efull) {
-        *reinterpret_cast<f4 *>(dst) = v;
-    } else {
-        for (int e = 0; e < ncol; ++e) dst[e] = v[e];
-    }
+    wsplit16_finish<WAVES>(p, smem, acc, tid, ks, co, ro, split_out, er, ec, erow, ecol, eok, efull, ebias, eres);
 }
 
 // GEMMs with short K (K <= 2 * KH, KH 8 or 16, K % 4 == 0) over many rows: the expand and
@@ -1655,22 +1696,44 @@ __global__ void gemm_splitk_reduce(const GemmDev p) {
     }
 }
 
+// Sum of the K-split partials src[0], src[stride], ..., src[(split - 1) * stride] in split
+// order; the loads of up to four splits go out together, so a reduction waits for one or two
+// memory round trips instead of one per split.
+__device__ __forceinline__ f4 sum_partials(const f4 *src, long stride, int split) {
+    const f4 zero4 = {0.f, 0.f, 0.f, 0.f};
+    f4 v = src[0];
+    for (int s0 = 1; s0 < split; s0 += 4) {
+        f4 part[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) part[u] = s0 + u < split ? src[(long)(s0 + u) * stride] : zero4;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (s0 + u < split) v += part[u];
+    }
+    return v;
+}
+
 // The same for N % 4 == 0 with 16-byte aligned output rows: four columns per thread, 16-byte
-// partial loads and stores (element sums in the same split order as above).
+// partial loads and stores (element sums in the same split order as above). The bias and
+// residual chunks are requested before the partials, so their loads overlap.
 __global__ void gemm_splitk_reduce_vec4(const GemmDev p, FastDiv div_n4) {
     const int N4 = p.N >> 2;
     const int total4 = p.M * N4;
-    const long total = (long)p.M * p.N;
+    const long stride4 = ((long)p.M * p.N) >> 2;
     const f4 *ws4 = reinterpret_cast<const f4 *>(p.ws);
+    const f4 zero4 = {0.f, 0.f, 0.f, 0.f};
+    const int bmode = p.bias ? p.bias_mode : 0;
     for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total4; idx += gridDim.x * blockDim.x) {
         const int row = fdiv(idx, div_n4);
         const int col = (idx - row * N4) * 4;
-        f4 v = ws4[idx];
-        for (int s = 1; s < p.split; ++s) v += ws4[(long)s * (total >> 2) + idx];
+        const f4 bcol = bmode == 1 ? ldg4(p.bias + col) : zero4;
+        const float brow = bmode == 2 ? ldg(p.bias + row) : 0.0f;
+        const f4 rv = p.res ? ldg4(p.res + (long)row * p.ldr + col) : zero4;
+        f4 v = sum_partials(ws4 + idx, stride4, p.split);
         v = v * p.alpha;
-        if (p.bias && p.bias_mode == 2) v += p.bias[row];
-        if (p.bias && p.bias_mode == 1) v += ldg4(p.bias + col);
-        if (p.res) v += p.beta * ldg4(p.res + (long)row * p.ldr + col);
+        if (bmode == 2) v += brow;
+        if (bmode == 1) v += bcol;
+        if (p.res) v += p.beta * rv;
         *reinterpret_cast<f4 *>(p.c + (long)row * p.ldc + col) = act4(v, p.act, p.lo, p.hi);
     }
 }
@@ -1679,7 +1742,9 @@ __global__ void gemm_splitk_reduce_vec4(const GemmDev p, FastDiv div_n4) {
 // N <= 1024): one wavefront per row sums the partials, applies the epilogue exactly as
 // gemm_splitk_reduce_vec4 does, stores the GEMM output when p.c is set (other readers need it)
 // and normalizes the row from registers (layer_norm_row_vec4, as the LayerNorm kernel does), so
-// the row makes no second trip through HBM and the LayerNorm needs no launch of its own.
+// the row makes no second trip through HBM and the LayerNorm needs no launch of its own. Every
+// load the row needs (partials, bias, residual, the LayerNorm's scale and bias) is requested
+// before the first is used.
 __global__ void __launch_bounds__(256) gemm_splitk_layer_norm(const GemmDev p, const float4 *ln_scale,
                                                               const float4 *ln_bias, float eps, float4 *ln_out) {
     const int lane = threadIdx.x & 63;
@@ -1688,23 +1753,41 @@ __global__ void __launch_bounds__(256) gemm_splitk_layer_norm(const GemmDev p, c
     const int N4 = p.N >> 2;
     const long total4 = ((long)p.M * p.N) >> 2;
     const f4 *ws4 = reinterpret_cast<const f4 *>(p.ws) + (long)row * N4;
-    // partials summed in split order, as gemm_splitk_reduce_vec4 does; the loads of one split
-    // for all of the lane's columns go out together
+    const f4 zero4 = {0.f, 0.f, 0.f, 0.f};
+    const int bmode = p.bias ? p.bias_mode : 0;
+    f4 bcol[4], rv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int k = lane + 64 * j;
+        const int col = k * 4;
+        const bool ok = k < N4;
+        bcol[j] = ok && bmode == 1 ? ldg4(p.bias + col) : zero4;
+        rv[j] = ok && p.res ? ldg4(p.res + (long)row * p.ldr + col) : zero4;
+    }
+    const float brow = bmode == 2 ? ldg(p.bias + row) : 0.0f;
+    const LnAffine aff = ln_affine_load(lane, N4, ln_scale, ln_bias);
+    // partials summed in split order, as gemm_splitk_reduce_vec4 does
     f4 acc[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int k = lane + 64 * j;
-        acc[j] = k < N4 ? ws4[k] : f4{0.f, 0.f, 0.f, 0.f};
+        acc[j] = k < N4 ? ws4[k] : zero4;
     }
-    for (int s = 1; s < p.split; ++s) {
-        f4 part[4];
+    for (int s0 = 1; s0 < p.split; s0 += 4) {
+        f4 part[4][4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int k = lane + 64 * j;
-            part[j] = k < N4 ? ws4[(long)s * total4 + k] : f4{0.f, 0.f, 0.f, 0.f};
-        }
+        for (int u = 0; u < 4; ++u)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[j] += part[j];
+            for (int j = 0; j < 4; ++j) {
+                const int k = lane + 64 * j;
+                part[u][j] = s0 + u < p.split && k < N4 ? ws4[(long)(s0 + u) * total4 + k] : zero4;
+            }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (s0 + u < p.split) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[j] += part[u][j];
+            }
     }
     float4 y[4];
 #pragma unroll
@@ -1714,15 +1797,15 @@ __global__ void __launch_bounds__(256) gemm_splitk_layer_norm(const GemmDev p, c
         if (k < N4) {
             const int col = k * 4;
             f4 v = acc[j] * p.alpha;
-            if (p.bias && p.bias_mode == 2) v += p.bias[row];
-            if (p.bias && p.bias_mode == 1) v += ldg4(p.bias + col);
-            if (p.res) v += p.beta * ldg4(p.res + (long)row * p.ldr + col);
+            if (bmode == 2) v += brow;
+            if (bmode == 1) v += bcol[j];
+            if (p.res) v += p.beta * rv[j];
             v = act4(v, p.act, p.lo, p.hi);
             if (p.c) *reinterpret_cast<f4 *>(p.c + (long)row * p.ldc + col) = v;
             y[j] = make_float4(v[0], v[1], v[2], v[3]);
         }
     }
-    layer_norm_row_vec4(y, lane, N4, ln_scale, ln_bias, eps, ln_out + (long)row * N4);
+    layer_norm_row_vec4(y, lane, N4, aff, eps, ln_out + (long)row * N4);
 }
 
 static bool aligned16(const void *ptr) { return ((uintptr_t)ptr & 15) == 0; }

@@ -120,13 +120,36 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// The LayerNorm's per-column scale and bias quads one lane applies (column quad lane + 64 j),
+// read before the row's mean is known so that their latency overlaps the row's own loads and
+// reductions; has_scale / has_bias record whether the operands exist.
+struct LnAffine {
+    float4 s[4], b[4];
+    bool has_scale, has_bias;
+};
+
+__device__ __forceinline__ LnAffine ln_affine_load(int lane, int cols4, const float4 *scale, const float4 *bias) {
+    LnAffine a;
+    a.has_scale = scale != nullptr;
+    a.has_bias = bias != nullptr;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int k = lane + 64 * j;
+        const bool ok = k < cols4;
+        a.s[j] = a.has_scale && ok ? scale[k] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+        a.b[j] = a.has_bias && ok ? bias[k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    return a;
+}
+
 // LayerNorm of one row held by a wavefront as up to four float4 per lane (v[j] is column quad
 // lane + 64 j, zero where that is >= cols4): two-pass mean and variance in float, then
-// (x - mean) / sqrt(var + eps) * scale + bias written to dst (scale, bias may be null). Every
-// lane of the wave must call it. Shared by the LayerNorm kernel and the split-K reduction that
-// ends in a LayerNorm, so both round identically.
-__device__ __forceinline__ void layer_norm_row_vec4(const float4 (&v)[4], int lane, int cols4, const float4 *scale,
-                                                    const float4 *bias, float eps, float4 *dst) {
+// (x - mean) / sqrt(var + eps) * scale + bias written to dst (the scale and bias steps are
+// skipped where the operand is absent). Every lane of the wave must call it. Shared by the
+// LayerNorm kernel and the split-K reduction that ends in a LayerNorm, so both round
+// identically.
+__device__ __forceinline__ void layer_norm_row_vec4(const float4 (&v)[4], int lane, int cols4, const LnAffine &aff,
+                                                    float eps, float4 *dst) {
     const float cols = (float)(cols4 * 4);
     float sum = 0.0f;
 #pragma unroll
@@ -147,19 +170,17 @@ __device__ __forceinline__ void layer_norm_row_vec4(const float4 (&v)[4], int la
         if (k < cols4) {
             float4 y = make_float4((v[j].x - mean) * inv, (v[j].y - mean) * inv, (v[j].z - mean) * inv,
                                    (v[j].w - mean) * inv);
-            if (scale) {
-                const float4 s = scale[k];
-                y.x *= s.x;
-                y.y *= s.y;
-                y.z *= s.z;
-                y.w *= s.w;
+            if (aff.has_scale) {
+                y.x *= aff.s[j].x;
+                y.y *= aff.s[j].y;
+                y.z *= aff.s[j].z;
+                y.w *= aff.s[j].w;
             }
-            if (bias) {
-                const float4 b = bias[k];
-                y.x += b.x;
-                y.y += b.y;
-                y.z += b.z;
-                y.w += b.w;
+            if (aff.has_bias) {
+                y.x += aff.b[j].x;
+                y.y += aff.b[j].y;
+                y.z += aff.b[j].z;
+                y.w += aff.b[j].w;
             }
             dst[k] = y;
         }

@@ -29,40 +29,21 @@ __global__ void reduce_mid_strided(int is_max, long outer, long n, long inner, c
     }
 }
 
-// inner % 4 == 0 (global pooling over NHWC): workgroup (x, o) owns 64 column quads of row
-// block o; its four waves each walk every fourth of the n rows with 16-byte loads, then the
-// four partial results meet in LDS. Many more loads are in flight per CU than with one thread
-// per output walking all n rows.
+// inner % 4 == 0 (global pooling over NHWC): workgroup (x, o) owns CQ column quads of row
+// block o, and its 256 / CQ row parts each walk every (256 / CQ)-th of the n rows with 16-byte
+// loads, four rows' loads in flight at a time, then the parts' results meet in LDS in part
+// order. CQ = 16 (16 parts) for long rows such as a 7 x 7 pooling window, so each thread reads
+// about n / 16 rows in one or two memory round trips and even batch 1 runs many workgroups.
+template <int CQ>
 __global__ void __launch_bounds__(256) reduce_mid_vec4(int is_max, int n, int inner4, const float4 *in,
                                                        float4 *out) {
-    const int lane = threadIdx.x & 63, part = threadIdx.x >> 6;
-    const int col = blockIdx.x * 64 + lane;
+    constexpr int P = 256 / CQ;
+    const int cq = threadIdx.x % CQ, part = threadIdx.x / CQ;
+    const int col = blockIdx.x * CQ + cq;
     const long o = blockIdx.y;
     const float init = is_max ? -INFINITY : 0.0f;
     float4 acc = make_float4(init, init, init, init);
-    if (col < inner4) {
-        const float4 *src = in + o * n * inner4 + col;
-        for (int k = part; k < n; k += 4) {
-            const float4 v = src[(long)k * inner4];
-            if (is_max) {
-                acc.x = v.x > acc.x ? v.x : acc.x;
-                acc.y = v.y > acc.y ? v.y : acc.y;
-                acc.z = v.z > acc.z ? v.z : acc.z;
-                acc.w = v.w > acc.w ? v.w : acc.w;
-            } else {
-                acc.x += v.x;
-                acc.y += v.y;
-                acc.z += v.z;
-                acc.w += v.w;
-            }
-        }
-    }
-    __shared__ float4 partial[4][64];
-    partial[part][lane] = acc;
-    __syncthreads();
-    if (part != 0 || col >= inner4) return;
-    for (int q = 1; q < 4; ++q) {
-        const float4 v = partial[q][lane];
+    auto fold = [&](const float4 v) __attribute__((always_inline)) {
         if (is_max) {
             acc.x = v.x > acc.x ? v.x : acc.x;
             acc.y = v.y > acc.y ? v.y : acc.y;
@@ -74,7 +55,24 @@ __global__ void __launch_bounds__(256) reduce_mid_vec4(int is_max, int n, int in
             acc.z += v.z;
             acc.w += v.w;
         }
+    };
+    if (col < inner4) {
+        const float4 *src = in + o * n * inner4 + col;
+        for (int k0 = part; k0 < n; k0 += 4 * P) {
+            float4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                v[u] = k0 + u * P < n ? src[(long)(k0 + u * P) * inner4] : make_float4(init, init, init, init);
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (k0 + u * P < n) fold(v[u]);
+        }
     }
+    __shared__ float4 partial[P][CQ];
+    partial[part][cq] = acc;
+    __syncthreads();
+    if (part != 0 || col >= inner4) return;
+    for (int q = 1; q < P; ++q) fold(partial[q][cq]);
     if (!is_max) {
         const float s = n > 0 ? 1.0f / (float)n : 0.0f;
         acc.x *= s;
@@ -313,7 +311,8 @@ __global__ void __launch_bounds__(256) layer_norm_rows_vec4(int rows, int cols4,
         const int k = lane + 64 * j;
         v[j] = k < cols4 ? src[k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
-    layer_norm_row_vec4(v, lane, cols4, scale, bias, eps, out + (long)r * cols4);
+    const LnAffine aff = ln_affine_load(lane, cols4, scale, bias);
+    layer_norm_row_vec4(v, lane, cols4, aff, eps, out + (long)r * cols4);
 }
 
 // ---- pooling -----------------------------------------------------------------------------------
@@ -723,8 +722,13 @@ extern "C" void mgc_hip_reduce_mid(mgc_hip_exec *x, int is_max, long outer, long
     } else if (inner % 4 == 0 && outer <= 65535 && n < 0x7fffffffL && inner < 0x7fffffffL &&
                (((uintptr_t)in | (uintptr_t)out) & 15) == 0) {
         const int inner4 = (int)(inner / 4);
-        MGC_LAUNCH(x, reduce_mid_vec4, dim3((unsigned)((inner4 + 63) / 64), (unsigned)outer), dim3(256),
-                   0, is_max, (int)n, inner4, (const float4 *)in, (float4 *)out);
+        if (n >= 32) {
+            MGC_LAUNCH(x, reduce_mid_vec4<16>, dim3((unsigned)((inner4 + 15) / 16), (unsigned)outer), dim3(256),
+                       0, is_max, (int)n, inner4, (const float4 *)in, (float4 *)out);
+        } else {
+            MGC_LAUNCH(x, reduce_mid_vec4<64>, dim3((unsigned)((inner4 + 63) / 64), (unsigned)outer), dim3(256),
+                       0, is_max, (int)n, inner4, (const float4 *)in, (float4 *)out);
+        }
     } else {
         MGC_LAUNCH(x, reduce_mid_strided, dim3(blocks_for(outer * inner, 256, 8192)), dim3(256),
                    0, is_max, outer, n, inner, in, out);

@@ -164,6 +164,7 @@ COPY_OPS = {"Transpose", "Expand", "Tile", "Slice", "Concat", "Pad", "Gather", "
         # negative ids counting from the end (reference ops.py:596-603 wraps them)
         ("f32", (30522, 768), 0, True),
         ("f32", (10, 4), 0, False),
+        ("f32", (6, 1100), 0, False),    # rows of 4400 bytes: more than 256 16-byte chunks
         ("f32", (3, 10, 2), 1, True),
         ("f32", (2, 3, 11), 2, False),
         ("f32", (2, 3, 11), -1, False),
@@ -387,3 +388,14 @@ def test_pooling(op, attrs, opt, hip_cache):
 def test_global_pooling(op, opt, hip_cache):
     g, feeds = op_graph(op, [f32(2, 5, 4, 3)])
     check_hip(g, feeds, hip_cache, opt=opt)
+
+
+# Mean and max over the middle axes of an NHWC-shaped tensor (what global pooling becomes at
+# O3): channels divisible by four take the 16-byte kernel, with 16 column quads and 16 row parts
+# per workgroup for windows of 32 or more pixels (7 x 7, 6 x 6: tails of both the column blocks
+# and the row parts) and 64 column quads and 4 row parts below that.
+@pytest.mark.parametrize("op", ["ReduceMean", "ReduceMax"])
+@pytest.mark.parametrize("shape", [(2, 7, 7, 8), (2, 6, 6, 72), (3, 4, 4, 264), (1, 3, 5, 12)])
+def test_reduce_middle_axes_vec4(op, shape, hip_cache):
+    g, feeds = op_graph(op, [f32(*shape)], attrs={"axes": [1, 2], "keepdims": 1})
+    check_hip(g, feeds, hip_cache, opt="O3")
