@@ -791,40 +791,27 @@ __global__ void gather_kernel(const unsigned char *src, const void *idx, int idx
     }
 }
 
-// Rows of a multiple of 16 bytes with 16-byte aligned table and output (embedding lookups):
-// one wavefront per (outer, t) row, 16 bytes per lane per access, up to four accesses' loads in
-// flight before their stores; four rows per workgroup. Out-of-range indices set the flag and
-// leave their row unwritten, as gather_kernel does.
+// Rows of a multiple of 16 bytes with 16-byte aligned table and output (embedding lookups): one
+// workgroup per (outer, t) row, each thread copying 16-byte chunks t, t + 256, ... of it, so a
+// row of 768 floats is one load and one store per thread spread over three waves. (A wave that
+// carried a whole row in a per-thread array of chunks was five times slower: the compiler kept
+// the array in LDS.) Out-of-range indices set the flag and leave their row unwritten, as
+// gather_kernel does.
 __global__ void __launch_bounds__(256) gather_rows16_kernel(const uint4 *src, const void *idx, int idx_dtype,
                                                             long outer, long dim, long n, long inner16,
                                                             uint4 *out, int *flag) {
-    const int lane = threadIdx.x & 63;
-    const long rows = outer * n;
-    const long step = ((long)gridDim.x * 256) >> 6;
-    for (long row = ((long)blockIdx.x * 256 + threadIdx.x) >> 6; row < rows; row += step) {
+    for (long row = blockIdx.x; row < outer * n; row += gridDim.x) {
         const long o = row / n, t = row - o * n;
         long k = idx_dtype == MGC_I64 ? static_cast<const long long *>(idx)[t]
                                       : (long)static_cast<const int *>(idx)[t];
         if (k < 0) k += dim;
         if (k < 0 || k >= dim) {
-            if (lane == 0) *flag = 1;
+            if (threadIdx.x == 0) *flag = 1;
             continue;
         }
         const uint4 *s = src + (o * dim + k) * inner16;
         uint4 *d = out + row * inner16;
-        // every lane loads (past the row's end it rereads the row's last chunk) so the four
-        // loads are issued together without a branch around each; only the stores are masked
-        for (long w0 = lane; w0 < inner16; w0 += 256) {
-            uint4 v[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const long w = w0 + 64 * u;
-                v[u] = s[w < inner16 ? w : inner16 - 1];
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-                if (w0 + 64 * u < inner16) d[w0 + 64 * u] = v[u];
-        }
+        for (long w = threadIdx.x; w < inner16; w += 256) d[w] = s[w];
     }
 }
 
@@ -979,7 +966,7 @@ extern "C" void mgc_hip_gather(mgc_hip_exec *x, const void *src, const void *idx
     long rows = outer * n;
     if (rows <= 0 || inner_bytes <= 0) return;
     if (inner_bytes % 16 == 0 && (((uintptr_t)src | (uintptr_t)out) & 15) == 0) {
-        MGC_LAUNCH(x, gather_rows16_kernel, dim3(blocks_for(rows * 64, 256, 16384)), dim3(256), 0,
+        MGC_LAUNCH(x, gather_rows16_kernel, dim3((unsigned)(rows < 65536 ? rows : 65536)), dim3(256), 0,
                    (const uint4 *)src, idx, idx_dtype, outer, dim, n, inner_bytes / 16, (uint4 *)out, x->flag);
         return;
     }

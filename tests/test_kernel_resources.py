@@ -80,3 +80,22 @@ def test_gemm_lds_is_the_dma_rings(kernels):
     assert lds(r"gemm_dma_wsplit_kernel") == {65536}
     assert lds(r"gemm_dma_wsplit16_kernelILi\dELi3ELi8E") == {8 * 3 * 4096}
     assert lds(r"gemm_dma_wsplit16_kernelILi\dELi2ELi4E") == {4 * 2 * 4096}
+
+
+# Kernels that declare no shared memory. The compiler may still move a per-thread array into
+# LDS (one slot per thread); on MI355X such a kernel ran five times slower (an embedding gather
+# whose four 16-byte chunks per lane went through LDS: 17 us against 3 us), so LDS here is a
+# regression.
+NO_LDS = ("ew_f32_kernel", "ew_program_kernel", "copy_kernel", "gather_kernel", "gather_rows16_kernel",
+          "fill_kernel", "range_kernel", "layer_norm_rows", "softmax_rows", "softmax_strided",
+          "gemm_splitk_reduce", "gemm_splitk_layer_norm", "gemm_stream_kernel", "pool_nhwc",
+          "depthwise3x3_nhwc_vec4", "depthwise_nhwc", "space_to_depth_kernel", "reduce_generic",
+          "reduce_mid_rows", "reduce_mid_strided", "argmax_kernel")
+
+
+def test_no_lds_where_none_is_declared(kernels):
+    hits = {k: v["group_segment_fixed_size"] for k, v in kernels.items()
+            if any(re.search(r"\d" + n + r"[EI]", k) for n in NO_LDS)}
+    assert len(hits) >= len(NO_LDS), sorted(hits)
+    used = {k: lds for k, lds in hits.items() if lds}
+    assert not used, used
