@@ -326,9 +326,206 @@ __global__ void __launch_bounds__(256 * G) attention_kernel(const AttnDev p) {
     }
 }
 
+// Attention over at most 32 W keys (W <= 4) in one pass, for short sequences (BERT-base's 128
+// keys): one workgroup of W waves per (batch, head, 32 queries), wave w owning keys 32 w ..
+// 32 w + 31. No LDS tiles and no running softmax:
+//  1. every wave requests its operands straight into registers at once: the 32 query rows and
+//     its 32 key rows (16-byte loads: lane (li, lh) takes d = 32 c + 16 lh .. + 15 of row li),
+//     and the V elements its P V products need (below);
+//  2. S^T = K Q^T on v_mfma_f32_32x32x2f32 (keys as rows, queries as columns), so register r of
+//     lane (li, lh) holds the score of key 8 (r / 4) + 4 lh + r % 4 and query li;
+//  3. the scores are scaled, biased and masked as the graph says, each query's maximum is taken
+//     over the lane pair (li, li + 32) and, through LDS, over the waves, and the scores become
+//     exp(t - m);
+//  4. O^T = V^T P^T: the score registers already are the B operand of this product (register r
+//     gives keys 8 (r / 4) + 4 lh + r % 4 of lane half lh, and the A operand takes V at the same
+//     keys), so P never goes through LDS;
+//  5. waves 1 .. W - 1 leave their O^T partials and row sums in LDS; wave 0 adds them in wave
+//     order, divides by the sum and writes each query's D outputs.
+// Terms are exp(t - m) with m the maximum over all keys (fp32 expf, as the streaming kernel),
+// and keys past Skv add nothing.
+template <int W, bool HAS_BIAS, bool HAS_MASK>
+__global__ void __launch_bounds__(64 * W) attention_short_kernel(const AttnDev p, int vec_out) {
+    __shared__ float wmax[W][32];
+    __shared__ float wsum[W][32];
+    __shared__ float opart[W > 1 ? W - 1 : 1][32][64];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int li = lane & 31, lh = lane >> 5;
+    const int qblocks = (p.S + 31) >> 5;
+    const int bh = blockIdx.x / qblocks;
+    const int q0 = (blockIdx.x - bh * qblocks) * 32;
+    const int b = bh / p.H, h = bh - (bh / p.H) * p.H;
+    const float *qbase = p.q + b * p.q_b + h * p.q_h;
+    const float *kbase = p.k + b * p.k_b + h * p.k_h;
+    const float *vbase = p.v + b * p.v_b + h * p.v_h;
+    const float *bias = p.bias ? p.bias + b * p.bias_b + h * p.bias_h : nullptr;
+    const unsigned char *mask = p.mask ? p.mask + b * p.mask_b + h * p.mask_h : nullptr;
+    const int D = p.D;
+    const float NEG_INF = -__builtin_huge_valf();
+    const f4 zero4 = {0.f, 0.f, 0.f, 0.f};
+    const int q = q0 + li;
+    const int k0 = 32 * w;
+
+    // 1. operands: Q and K fragments (two 32-wide d chunks), V at the keys of each score register.
+    // Buffer loads: an element past S, Skv or D gets an offset past the resource's end and reads
+    // as zero, so the loads need no branches and the multiplies wait only for their own.
+    constexpr unsigned OOB = 0x80000000u;
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)qbase, (short)0, (int)(((long)(p.S - 1) * p.q_s + D) * 4), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)kbase, (short)0, (int)(((long)(p.Skv - 1) * p.k_s + D) * 4), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)vbase, (short)0, (int)(((long)(p.Skv - 1) * p.v_s + D) * 4), 0x00020000);
+    f4 qf[2][4], kf[2][4];
+    const bool q_ok = q < p.S, k_ok = k0 + li < p.Skv;
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+            const int d = 32 * c + 16 * lh + 4 * s4;
+            const unsigned oq = q_ok && d < D ? (unsigned)((long)q * p.q_s + d) * 4u : OOB;
+            const unsigned ok = k_ok && d < D ? (unsigned)((long)(k0 + li) * p.k_s + d) * 4u : OOB;
+            qf[c][s4] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rq, oq, 0, 0));
+            kf[c][s4] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rk, ok, 0, 0));
+        }
+    float vf[2][16];
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = k0 + 8 * (r >> 2) + 4 * lh + (r & 3);
+            const int d = 32 * db + li;
+            const unsigned ov = key < p.Skv && d < D ? (unsigned)((long)key * p.v_s + d) * 4u : OOB;
+            vf[db][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rv, ov, 0, 0));
+        }
+
+    // the additive bias and the mask of this lane's 16 scores (when the graph has them: HAS_BIAS,
+    // HAS_MASK), requested with the operands; the addresses are clamped into the tensors and the
+    // elements past S or Skv are not used
+    const int qc = q_ok ? q : p.S - 1;
+    float bv[16];
+    unsigned char mv[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int key = min(k0 + 8 * (r >> 2) + 4 * lh + (r & 3), p.Skv - 1);
+        bv[r] = HAS_BIAS ? bias[(long)qc * p.bias_s + (long)key * p.bias_j] : 0.f;
+        mv[r] = HAS_MASK ? mask[(long)qc * p.mask_s + (long)key * p.mask_j] : 0;
+    }
+    // every load above goes out before the first multiply (the scheduler would otherwise hold
+    // some back to save registers and pay their latency one after another)
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. S^T for this wave's 32 keys
+    floatx16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[c][s4][e], qf[c][s4][e], acc, 0, 0, 0);
+
+    // 3. scores, the query's maximum over all keys, exp terms and this wave's sum
+    const float scale = p.scale, fill = p.fill;
+    const bool scale_div = p.scale_div != 0, causal = p.causal != 0, keep_set = p.mask_keep != 0;
+    float m = NEG_INF;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int key = k0 + 8 * (r >> 2) + 4 * lh + (r & 3);
+        float t;
+        if (key >= p.Skv) {
+            t = NEG_INF;
+        } else if (!q_ok) {
+            t = 0.f;
+        } else {
+            t = scale_div ? acc[r] / scale : acc[r] * scale;
+            if (HAS_BIAS) t += bv[r];
+            bool keep = true;
+            if (causal) keep = key <= q;
+            else if (HAS_MASK) keep = (mv[r] != 0) == keep_set;
+            if (!keep) t = fill;
+        }
+        acc[r] = t;
+        m = fmaxf(m, t);
+    }
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    if (W > 1) {
+        if (lh == 0) wmax[w][li] = m;
+        __syncthreads();
+#pragma unroll
+        for (int w2 = 0; w2 < W; ++w2) m = w2 == 0 ? wmax[0][li] : fmaxf(m, wmax[w2][li]);
+    }
+    float l = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const float pe = acc[r] == NEG_INF ? 0.f : expf(acc[r] - m);
+        acc[r] = pe;
+        l += pe;
+    }
+    l += __shfl_xor(l, 32, 64);
+
+    // 4. O^T = V^T P^T over this wave's keys (the second d block only when D > 32)
+    floatx16 o[2];
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[0][r], acc[r], o[0], 0, 0, 0);
+    if (D > 32) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[1][r], acc[r], o[1], 0, 0, 0);
+    }
+
+    // 5. wave order sum of the partials; register r of o[db] is d = 32 db + 8 (r / 4) + 4 lh + r % 4
+    if (W > 1) {
+        if (w > 0) {
+#pragma unroll
+            for (int db = 0; db < 2; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) opart[w - 1][16 * db + r][lane] = o[db][r];
+            if (lh == 0) wsum[w][li] = l;
+        }
+        __syncthreads();
+        if (w > 0) return;
+#pragma unroll
+        for (int w2 = 1; w2 < W; ++w2) {
+#pragma unroll
+            for (int db = 0; db < 2; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[db][r] += opart[w2 - 1][16 * db + r][lane];
+            l += wsum[w2][li];
+        }
+    }
+    if (!q_ok) return;
+    const float inv = 1.0f / l;
+    float *orow = p.o + b * p.o_b + h * p.o_h + (long)q * p.o_s;
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d = 32 * db + 8 * g + 4 * lh;
+            if (d >= D) continue;
+            const f4 v = {o[db][4 * g] * inv, o[db][4 * g + 1] * inv, o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv};
+            if (vec_out) {
+                *reinterpret_cast<f4 *>(orow + d) = v;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) orow[d + e] = v[e];
+            }
+        }
+}
+
 }  // namespace mgc
 
 using namespace mgc;
+
+typedef void (*AttnShortKernel)(AttnDev, int);
 
 extern "C" int mgc_hip_attention_supported(int S, int Skv, int D) {
     return S >= 1 && Skv >= 1 && D >= 4 && D <= ATT_DMAX && D % 4 == 0;
@@ -371,6 +568,15 @@ extern "C" void mgc_hip_attention(mgc_hip_exec *x, const mgc_hip_attention_args 
     p.o_h = a->o_h;
     p.scale = a->scale;
     p.scale_div = a->scale_div;
+    {
+        // dividing by a power of two equals multiplying by its (exact) reciprocal, bit for bit
+        int ex = 0;
+        const float mant = frexpf(a->scale, &ex);
+        if (a->scale_div && mant == 0.5f && ex > -120 && ex < 120) {
+            p.scale = ldexpf(1.0f, 1 - ex);
+            p.scale_div = 0;
+        }
+    }
     p.bias = a->bias;
     p.bias_b = a->bias_b;
     p.bias_h = a->bias_h;
@@ -384,6 +590,27 @@ extern "C" void mgc_hip_attention(mgc_hip_exec *x, const mgc_hip_attention_args 
     p.mask_keep = a->mask_keep;
     p.causal = a->causal;
     p.fill = a->fill;
+    // At most 128 keys: the one-pass kernel, a wave per 32 keys and a workgroup per 32 queries
+    // (with eight waves its registers would no longer fit two waves per SIMD).
+    if (a->Skv <= 128) {
+        const long qb = (long)a->B * a->H * ((a->S + 31) / 32);
+        const int vec_out = a->o_s % 4 == 0 && a->o_b % 4 == 0 && a->o_h % 4 == 0 && ((uintptr_t)a->o & 15) == 0;
+        const int waves = (a->Skv + 31) / 32;
+        if (qb <= 0x7fffffffL) {
+            const int bm = (p.bias ? 1 : 0) | (p.mask && !p.causal ? 2 : 0);
+            const int sel = (waves <= 1 ? 0 : waves <= 2 ? 1 : 2) * 4 + bm;
+            static const AttnShortKernel table[12] = {
+                &attention_short_kernel<1, false, false>, &attention_short_kernel<1, true, false>,
+                &attention_short_kernel<1, false, true>,  &attention_short_kernel<1, true, true>,
+                &attention_short_kernel<2, false, false>, &attention_short_kernel<2, true, false>,
+                &attention_short_kernel<2, false, true>,  &attention_short_kernel<2, true, true>,
+                &attention_short_kernel<4, false, false>, &attention_short_kernel<4, true, false>,
+                &attention_short_kernel<4, false, true>,  &attention_short_kernel<4, true, true>};
+            const int threads = 64 * (waves <= 1 ? 1 : waves <= 2 ? 2 : 4);
+            MGC_LAUNCH(x, table[sel], dim3((unsigned)qb), dim3(threads), 0, p, vec_out);
+            return;
+        }
+    }
     // Fewer (batch, head, 64-query) blocks than CUs and at least two key blocks: two groups of
     // four waves per workgroup take alternate key blocks and combine at the end (one workgroup
     // per CU then: the groups' tiles take 122 KB of LDS).

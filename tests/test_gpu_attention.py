@@ -131,6 +131,8 @@ def _check(g, feeds, hip_cache, opt="O3", fused=True):
         (1, 2, 3, 5, 4, False),      # tiny: one query block, one partial key block, D = 4
         (2, 2, 256, 256, 32, True),  # D of one MFMA column block
         (1, 2, 16, 300, 16, False),  # keys past the old 256 limit
+        (2, 2, 40, 33, 64, False),   # one-pass kernel: 33 keys (two waves), S != Skv
+        (1, 3, 130, 96, 32, False),  # one-pass kernel: three waves, five query blocks
         (1, 3, 700, 700, 64, True),  # long sequence: 11 query blocks x 11 key blocks
         # many (batch, head) pairs: 576 and 512 workgroups, more than two per CU
         (4, 16, 520, 520, 64, True),
@@ -161,6 +163,27 @@ def test_fused_attention_matches_oracle(B, H, S, Skv, D, fused_qkv, hip_cache):
 def test_masked_and_biased_attention(case, opt, hip_cache):
     g, feeds = attention_graph(2, 3, 150, 150, 64, True, scale=0.125, **case)
     _check(g, feeds, hip_cache, opt)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize(
+    "case",
+    [
+        dict(mask="causal"),
+        dict(mask="causal", fill=-np.inf, keep_true=True),
+        dict(mask="random", keep_true=True),
+        dict(mask="input"),
+        dict(bias="const", divide=True),
+        dict(bias="input", mask="causal", fill=-np.inf),
+    ],
+    ids=lambda c: "-".join(f"{k}={v}" for k, v in c.items()),
+)
+@pytest.mark.parametrize("S, D", [(100, 64), (37, 24)])
+def test_masked_and_biased_short_attention(case, S, D, hip_cache):
+    """At most 128 keys: the one-pass kernel (a wave per 32 keys, the last one partly past the
+    keys; a partial last query block; D below one or two MFMA column blocks)."""
+    g, feeds = attention_graph(2, 3, S, S, D, True, scale=0.125, **case)
+    _check(g, feeds, hip_cache)
 
 
 @pytest.mark.gpu
