@@ -274,6 +274,8 @@ struct EwF32Args {
     int n_leaves, n_instr;
     const float *leaf[EWF_LEAVES];
     int lst[EWF_LEAVES][EWF_RANK];  // element strides
+    int leaf_bytes[EWF_LEAVES];     // bytes reachable from leaf[l] (0 past n_leaves)
+    int leaf_quad[EWF_LEAVES];      // 1: the leaf's innermost stride is 1 (16-byte quads), 0: broadcast
     EwF32Instr ins[EWF_INSTR];
     float *out;
     int ost[EWF_RANK];
@@ -338,19 +340,29 @@ __global__ void __launch_bounds__(256) ew_f32_kernel(const EwF32Args e) {
             }
         }
         float R0[NR], R1[NR], R2[NR], R3[NR];
+        if (VEC) {
+            // one 16-byte buffer load per leaf, all issued before any is used: a broadcast leaf
+            // takes element 0 of it, bytes past a leaf's extent (and every byte of an unused
+            // leaf, whose extent is 0) read as zero
 #pragma unroll
-        for (int l = 0; l < NL; ++l) {
-            float v0 = 0.f, v1 = 0.f, v2 = 0.f, v3 = 0.f;
-            if (l < e.n_leaves) {
-                const float *src = e.leaf[l] + off[l];
-                if (VEC && e.lst[l][e.rank - 1] == 1) {
-                    const float4 v = *reinterpret_cast<const float4 *>(src);
-                    v0 = v.x; v1 = v.y; v2 = v.z; v3 = v.w;
-                } else {
-                    v0 = v1 = v2 = v3 = *src;
-                }
+            for (int l = 0; l < NL; ++l) {
+                const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                    (void *)e.leaf[l], (short)0, e.leaf_bytes[l], 0x00020000);
+                const float4 v = __builtin_bit_cast(
+                    float4, __builtin_amdgcn_raw_buffer_load_b128(rs, (unsigned)off[l] * 4u, 0, 0));
+                const bool quad = e.leaf_quad[l] != 0;
+                R0[l] = v.x;
+                R1[l] = quad ? v.y : v.x;
+                R2[l] = quad ? v.z : v.x;
+                R3[l] = quad ? v.w : v.x;
             }
-            R0[l] = v0; R1[l] = v1; R2[l] = v2; R3[l] = v3;
+        } else {
+#pragma unroll
+            for (int l = 0; l < NL; ++l) {
+                float v0 = 0.f;
+                if (l < e.n_leaves) v0 = e.leaf[l][off[l]];
+                R0[l] = R1[l] = R2[l] = R3[l] = v0;
+            }
         }
 #pragma unroll
         for (int r = NL; r < NR; ++r) R0[r] = R1[r] = R2[r] = R3[r] = 0.f;
@@ -419,6 +431,7 @@ static bool ew_f32_plan(const mgc_hip_ew_args *e, EwF32Args &f, bool &vec, int n
             ext += (e->dims[d] - 1) * e->leaf[l].strides[d];
         }
         if (ext >= (1L << 31)) return false;
+        f.leaf_bytes[l] = ext * 4 < 0x7fffffffL ? (int)(ext * 4) : 0;
     }
     long oext = e->out_base + 1;
     for (int d = 0; d < e->rank; ++d) {
@@ -444,6 +457,7 @@ static bool ew_f32_plan(const mgc_hip_ew_args *e, EwF32Args &f, bool &vec, int n
     vec = e->dims[r] % 4 == 0 && e->out_strides[r] == 1 && e->out_base % 4 == 0 &&
           (((uintptr_t)e->out) & 15) == 0;
     for (int d = 0; d < r && vec; ++d) vec = e->out_strides[d] % 4 == 0;
+    for (int l = 0; l < e->n_leaves && vec; ++l) vec = f.leaf_bytes[l] > 0;  // buffer offsets are 32-bit
     for (int l = 0; l < e->n_leaves && vec; ++l) {
         const long st = e->leaf[l].strides[r];
         if (st == 1) {
@@ -465,6 +479,8 @@ static bool ew_f32_plan(const mgc_hip_ew_args *e, EwF32Args &f, bool &vec, int n
     f.n_instr = e->n_instr;
     for (int l = 0; l < EWF_LEAVES; ++l) {
         f.leaf[l] = l < e->n_leaves ? static_cast<const float *>(e->leaf[l].p) : nullptr;
+        if (l >= e->n_leaves) f.leaf_bytes[l] = 0;
+        f.leaf_quad[l] = l < e->n_leaves && e->leaf[l].strides[r] == 1 ? 1 : 0;
         for (int d = 0; d < EWF_RANK; ++d)
             f.lst[l][d] = (l < e->n_leaves && d < e->rank) ? (int)e->leaf[l].strides[d] : 0;
     }

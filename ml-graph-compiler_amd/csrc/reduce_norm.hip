@@ -368,8 +368,8 @@ __global__ void pool_nhwc(const PoolGeo g, const float *in, float *out) {
 
 // NHWC with C % 4 == 0: one thread per output channel quad, 16-byte loads and stores, 32-bit
 // index arithmetic with host-computed divisors (the element count is below 2^31).
-// K > 0: a K x K window with its taps unrolled, so all K * K loads are requested before the
-// first is combined; K == 0: any window.
+// K > 0: a K x K window whose K * K loads are all requested (addresses clamped into the image)
+// before the first is combined; K == 0: any window.
 template <int K>
 __global__ void pool_nhwc_vec4(const PoolGeo g, FastDiv div_c4, FastDiv div_ow, FastDiv div_oh,
                                int total, const float *in, float *out) {
@@ -385,8 +385,43 @@ __global__ void pool_nhwc_vec4(const PoolGeo g, FastDiv div_c4, FastDiv div_ow, 
         const float *img = in + (long)n * g.H * g.W * g.C + c4 * 4;
         const float init = g.is_max ? -INFINITY : 0.0f;
         float4 acc = make_float4(init, init, init, init);
+        if (K > 0) {
+            // every tap's load first (addresses clamped into the image), then the combine: taps
+            // outside the image are skipped, as below
+            float4 v[K > 0 ? K : 1][K > 0 ? K : 1];
+            bool ok[K > 0 ? K : 1][K > 0 ? K : 1];
 #pragma unroll
-        for (int kh = 0; kh < KH; ++kh) {
+            for (int kh = 0; kh < K; ++kh) {
+                const int ih = oh * g.SH - g.PT + kh * g.DH;
+                const int ihc = min(max(ih, 0), g.H - 1);
+#pragma unroll
+                for (int kw = 0; kw < K; ++kw) {
+                    const int iw = ow * g.SW - g.PL + kw * g.DW;
+                    ok[kh][kw] = (unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W;
+                    v[kh][kw] = *reinterpret_cast<const float4 *>(img + (long)(ihc * g.W + min(max(iw, 0), g.W - 1)) * g.C);
+                }
+            }
+#pragma unroll
+            for (int kh = 0; kh < K; ++kh)
+#pragma unroll
+                for (int kw = 0; kw < K; ++kw) {
+                    if (!ok[kh][kw]) continue;
+                    const float4 x = v[kh][kw];
+                    if (g.is_max) {
+                        acc.x = x.x > acc.x ? x.x : acc.x;
+                        acc.y = x.y > acc.y ? x.y : acc.y;
+                        acc.z = x.z > acc.z ? x.z : acc.z;
+                        acc.w = x.w > acc.w ? x.w : acc.w;
+                    } else {
+                        acc.x += x.x;
+                        acc.y += x.y;
+                        acc.z += x.z;
+                        acc.w += x.w;
+                    }
+                }
+        }
+#pragma unroll
+        for (int kh = 0; kh < (K > 0 ? 0 : KH); ++kh) {
             const int ih = oh * g.SH - g.PT + kh * g.DH;
             if (ih < 0 || ih >= g.H) continue;
 #pragma unroll
@@ -574,6 +609,94 @@ __global__ void __launch_bounds__(256) depthwise3x3_nhwc_vec4(const DwGeo g, Fas
             v.z = apply_act(v.z, g.act, g.lo, g.hi);
             v.w = apply_act(v.w, g.act, g.lo, g.hi);
             *reinterpret_cast<float4 *>(out + o) = v;
+        }
+    }
+}
+
+// Stride-2 form: every input and weight load of a thread is issued before the first FMA
+// (addresses clamped into the image; out-of-image taps are skipped afterwards), so the thread
+// waits for memory once. At stride 1 with four outputs per thread the preloaded rows need
+// enough registers to halve occupancy, and the row-by-row kernel above is faster there.
+template <int SW, int T>
+__global__ void __launch_bounds__(256) depthwise3x3_nhwc_preload(const DwGeo g, FastDiv div_c4, FastDiv div_owb,
+                                                                 FastDiv div_oh, int total, const float *in,
+                                                                 const float *w, const float *bias,
+                                                                 const float *res, float *out) {
+    constexpr int NCOL = (T - 1) * SW + 3;
+    const int C4 = g.C >> 2, OWB = (g.OW + T - 1) / T;
+    for (int idx = xcd_block() * blockDim.x + threadIdx.x; idx < total; idx += gridDim.x * blockDim.x) {
+        const int t = fdiv(idx, div_c4);
+        const int c4 = idx - t * C4;
+        const int t2 = fdiv(t, div_owb);
+        const int owb = t - t2 * OWB;
+        const int n = fdiv(t2, div_oh);
+        const int oh = t2 - n * g.OH;
+        const int c = c4 * 4, ow0 = owb * T, iw0 = ow0 * SW - g.PL;
+        // optional operands load from a valid stand-in address and select their values later
+        // (a select between a load and a constant becomes a load through a stack slot)
+        float4 b = *reinterpret_cast<const float4 *>((bias ? bias : w) + c);
+        if (!bias) b = make_float4(0.f, 0.f, 0.f, 0.f);
+        float4 wv[9];
+#pragma unroll
+        for (int k = 0; k < 9; ++k) wv[k] = *reinterpret_cast<const float4 *>(w + k * g.C + c);
+        const float *img = in + (long)n * g.H * g.W * g.C + c;
+        float4 xs[3][NCOL];
+        bool rok[3], cok[NCOL];
+#pragma unroll
+        for (int q = 0; q < NCOL; ++q) cok[q] = (unsigned)(iw0 + q) < (unsigned)g.W;
+#pragma unroll
+        for (int kh = 0; kh < 3; ++kh) {
+            const int ih = oh * g.SH - g.PT + kh;
+            rok[kh] = (unsigned)ih < (unsigned)g.H;
+            const float *row = img + (long)min(max(ih, 0), g.H - 1) * g.W * g.C;
+#pragma unroll
+            for (int q = 0; q < NCOL; ++q)
+                xs[kh][q] = *reinterpret_cast<const float4 *>(row + (long)min(max(iw0 + q, 0), g.W - 1) * g.C);
+        }
+        float4 acc[T];
+#pragma unroll
+        for (int j = 0; j < T; ++j) acc[j] = b;
+#pragma unroll
+        for (int kh = 0; kh < 3; ++kh) {
+#pragma unroll
+            for (int kw = 0; kw < 3; ++kw) {
+#pragma unroll
+                for (int j = 0; j < T; ++j) {
+                    const int q = j * SW + kw;
+                    // taps outside the image add nothing (the reference skips them)
+                    if (!(rok[kh] && cok[q])) continue;
+                    const float4 xv = xs[kh][q];
+                    const float4 wk = wv[kh * 3 + kw];
+                    acc[j].x = fmaf(xv.x, wk.x, acc[j].x);
+                    acc[j].y = fmaf(xv.y, wk.y, acc[j].y);
+                    acc[j].z = fmaf(xv.z, wk.z, acc[j].z);
+                    acc[j].w = fmaf(xv.w, wk.w, acc[j].w);
+                }
+            }
+        }
+        const long base = ((long)(n * g.OH + oh) * g.OW + ow0) * g.C + c;
+        // the residual quads of the thread's outputs together, then the stores (no early exit,
+        // so the accumulators stay in registers)
+        float4 rv[T];
+#pragma unroll
+        for (int j = 0; j < T; ++j)
+            rv[j] = *reinterpret_cast<const float4 *>(res ? res + base + (long)min(j, g.OW - 1 - ow0) * g.C : in + c);
+#pragma unroll
+        for (int j = 0; j < T; ++j) {
+            if (ow0 + j < g.OW) {
+                float4 v = acc[j];
+                if (res) {
+                    v.x += rv[j].x;
+                    v.y += rv[j].y;
+                    v.z += rv[j].z;
+                    v.w += rv[j].w;
+                }
+                v.x = apply_act(v.x, g.act, g.lo, g.hi);
+                v.y = apply_act(v.y, g.act, g.lo, g.hi);
+                v.z = apply_act(v.z, g.act, g.lo, g.hi);
+                v.w = apply_act(v.w, g.act, g.lo, g.hi);
+                *reinterpret_cast<float4 *>(out + base + (long)j * g.C) = v;
+            }
         }
     }
 }
@@ -882,7 +1005,7 @@ extern "C" void mgc_hip_depthwise(mgc_hip_exec *x, int nhwc, int N, int H, int W
             const int tile = dw3_tile(OW, SW);
             const int owb = (OW + tile - 1) / tile;
             const int quads = (int)((long)N * OH * owb * (C / 4));
-            auto kern = SW == 2 ? depthwise3x3_nhwc_vec4<2, 2>
+            auto kern = SW == 2 ? depthwise3x3_nhwc_preload<2, 2>
                                 : (tile == 4 ? depthwise3x3_nhwc_vec4<1, 4> : depthwise3x3_nhwc_vec4<1, 2>);
             MGC_LAUNCH(x, kern, dim3(blocks_for(quads, 256, 16384)), dim3(256), 0, g,
                        make_fastdiv((unsigned)(C / 4)), make_fastdiv((unsigned)owb), make_fastdiv((unsigned)OH),
