@@ -82,6 +82,7 @@ struct GemmDev {
     int k1;
     long a2_bytes;
     int nbatch;   // batch elements
+    int nfull = 0x7fffffff;  // gemm_dma_kernel: workgroups from this id on compute quarter tiles
 };
 
 __device__ __forceinline__ void batch_offsets(const GemmDev &p, int bz, long &ao, long &bo,
@@ -767,6 +768,291 @@ __global__ void __launch_bounds__(256) gemm_dma_kernel(const GemmDev p) {
     }
     __syncthreads();
     gemm_store_tile<BM, BN, WGM>(p, smem, acc, m0, n0, ks, co, ro);
+}
+
+// Body of gemm_dma_tail_kernel: gemm_dma_kernel's whole 64 x 64 tiles, and (QUARTER) a 64 x 64
+// tile's 32 x 32 quarter computed by all four waves, each over a quarter of K. A ring stage then holds 64 k of the quarter's 32 A rows and 32 B rows
+// (LDS row r < 32: k block 0, r >= 32: k block 1, same 32-float row format and swizzle), the
+// same 16 KB as a 64 x 64 stage; wave w multiplies the 16 k (w & 1) of k block w >> 1. The
+// four partial tiles are summed through LDS in wave order before the common epilogue.
+template <int BM, int BN, int STAGES>
+constexpr int dma_smem_floats() {
+    return STAGES * (BM + BN) * 32 > BM * (BN + 8) ? STAGES * (BM + BN) * 32 : BM * (BN + 8);
+}
+
+template <int BM, int BN, int WGM, int STAGES, int AMODE, bool QUARTER>
+__device__ __forceinline__ void gemm_dma_tile(const GemmDev p, float *smem, const int m0, const int n0) {
+    constexpr int BK = 32;
+    constexpr int KSTEP = QUARTER ? 2 * BK : BK;  // k covered by one ring stage
+    static_assert(!QUARTER || (BM == 64 && BN == 64 && WGM == 2), "quarters of a 64 x 64 tile");
+    constexpr int WGN = 4 / WGM;
+    constexpr int WM = BM / WGM;
+    constexpr int WN = BN / WGN;
+    constexpr int RM = WM / 32;
+    constexpr int RN = WN / 32;
+    static_assert(RM >= 1 && RN >= 1 && WGM * WGN == 4, "bad tile");
+    static_assert(STAGES >= 2 && STAGES <= 4, "stages");
+    constexpr int AI = BM / 32;  // DMA instructions per wave per stage, A block
+    constexpr int BI = BN / 32;  // and B block
+    constexpr int STAGE = (BM + BN) * BK;
+    static_assert(AMODE == AM_VEC || AMODE == AM_CONV_VEC || AMODE == AM_CAT, "vector A only");
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WGN, wn = wave - (wave / WGN) * WGN;
+
+    const int bz = blockIdx.z / p.split;
+    const int ks = blockIdx.z - bz * p.split;
+    long ao, bo, co, ro;
+    batch_offsets(p, bz, ao, bo, co, ro);
+    const float *abase = p.a.p + ao;
+    const float *bbase = p.b.p + bo;
+    const int kbeg = ks * p.kchunk;
+    const int kend = min(p.K, kbeg + p.kchunk);
+    const int nk = kend > kbeg ? (kend - kbeg + KSTEP - 1) / KSTEP : 0;
+
+    // ---- DMA source state: row (i * 4 + wave) * 8 + (lane >> 3) of each block --------------
+    // Row r keeps k-chunk q at position q ^ f(r) with f(r) = (r & 7) ^ ((r >> 3) & 1): distinct
+    // over any 8 consecutive rows and over the 8 even (or odd) rows of any aligned 16, so
+    // 16-byte reads of one chunk from 8 or 16 consecutive rows spread over all banks.
+    const int q4 = ((lane & 7) ^ (lane >> 3) ^ (wave & 1)) * 4;  // this lane's k offset
+    const int rsub = lane >> 3;
+    // Operands are read through buffer resources: a masked lane gets an offset past the end of
+    // the resource and the hardware returns zeros for it, so no zero page, no select after
+    // the load and 32-bit offsets instead of 64-bit addresses.
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)abase, (short)0, (int)(p.a_bytes - ao * 4), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)bbase, (short)0, (int)(p.b_bytes - bo * 4), 0x00020000);
+    constexpr unsigned OOB = 0x80000000u;  // past every resource's end (extents are < 2^31 bytes)
+    // AM_CAT: the second source (batch_rank 0, so no batch offset)
+    const __amdgpu_buffer_rsrc_t ra2 = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(AMODE == AM_CAT ? p.a2.p : abase), (short)0, (int)(AMODE == AM_CAT ? p.a2_bytes : 0), 0x00020000);
+    unsigned aoff[AI];  // byte offset of the row (AM_VEC) or of its window origin (AM_CONV_VEC)
+    unsigned aoff2[AI];  // AM_CAT: byte offset of the row's pixel in the second source
+    int aih[AI], aiw[AI];
+    const int ohw = AMODE == AM_CAT ? p.a2.OH * p.a2.OW : p.a.OH * p.a.OW;
+#pragma unroll
+    for (int i = 0; i < AI; ++i) {
+        // a quarter's DMA instruction i fetches k block i of the wave's eight rows
+        const int m = m0 + (QUARTER ? wave : i * 4 + wave) * 8 + rsub;
+        const unsigned kshift = QUARTER ? (unsigned)i * BK * 4u : 0u;
+        aoff[i] = aoff2[i] = OOB;
+        aih[i] = aiw[i] = -0x40000000;  // fails the window bounds test
+        if (m < p.M) {
+            if (AMODE == AM_CAT) {
+                const int n = fdiv(m, p.div_ohw), rr = m - n * ohw;
+                const int oh = fdiv(rr, p.div_ow), ow = rr - oh * p.a2.OW;
+                aoff2[i] = (unsigned)(((n * p.a2.H + oh * p.a2.SH) * p.a2.W + ow * p.a2.SW) * p.a2.C) * 4u + kshift;
+            }
+            if (AMODE == AM_CONV_VEC) {
+                const int n = fdiv(m, p.div_ohw), rr = m - n * ohw;
+                const int oh = fdiv(rr, p.div_ow), ow = rr - oh * p.a.OW;
+                aih[i] = oh * p.a.SH - p.a.PT;
+                aiw[i] = ow * p.a.SW - p.a.PL;
+                aoff[i] = (unsigned)(((n * p.a.H + aih[i]) * p.a.W + aiw[i]) * p.a.C) * 4u + kshift;
+            } else {
+                aoff[i] = (unsigned)m * (unsigned)p.a.rs * 4u + kshift;
+            }
+        }
+    }
+    unsigned boff[BI];
+#pragma unroll
+    for (int i = 0; i < BI; ++i) {
+        const int n = n0 + (QUARTER ? wave : i * 4 + wave) * 8 + rsub;
+        boff[i] = n < p.N ? (unsigned)n * (unsigned)p.b.cs * 4u + (QUARTER ? (unsigned)i * BK * 4u : 0u) : OOB;
+    }
+    // The lane's next k and, for an image, its (kh, kw, c) split, advanced one stage per issue.
+    int knext = kbeg + q4;
+    int cc = 0, ckw = 0, ckh = 0;
+    if (AMODE == AM_CONV_VEC) {
+        const int t = fdiv(knext, p.div_cg);
+        cc = knext - t * p.a.cg;
+        ckh = fdiv(t, p.div_kw);
+        ckw = t - ckh * p.a.KW;
+    }
+
+    auto issue = [&](int buf) __attribute__((always_inline)) {
+        const int k = knext;
+        // k block 1 of a quarter stage starts 32 k later (its offsets carry the shift); a whole
+        // tile's stage has one k range (written so that it compiles to the plain form)
+        const bool kok0 = k < kend;
+        const bool kok1 = QUARTER ? k + BK < kend : kok0;
+#define KOK(i) ((QUARTER && (i) == 1) ? kok1 : kok0)
+        float *sa = smem + buf * STAGE;
+        float *sb = sa + BM * BK;
+        if constexpr (AMODE == AM_VEC) {
+#pragma unroll
+            for (int i = 0; i < AI; ++i)
+                dma16_buf(ra, KOK(i) ? aoff[i] + (unsigned)k * 4u : OOB, sa + (i * 4 + wave) * 8 * BK);
+        } else if constexpr (AMODE == AM_CAT) {
+            // k1 is a multiple of the stage's k (32, or 64 for a quarter tile), so a whole stage
+            // reads one source
+            if (k < p.k1) {
+#pragma unroll
+                for (int i = 0; i < AI; ++i)
+                    dma16_buf(ra, KOK(i) ? aoff[i] + (unsigned)k * 4u : OOB, sa + (i * 4 + wave) * 8 * BK);
+            } else {
+                const unsigned k2 = (unsigned)(k - p.k1) * 4u;
+#pragma unroll
+                for (int i = 0; i < AI; ++i)
+                    dma16_buf(ra2, KOK(i) ? aoff2[i] + k2 : OOB, sa + (i * 4 + wave) * 8 * BK);
+            }
+        } else {
+            // a quarter stage's second k block is the same window tap 32 channels on (the
+            // channel group is a multiple of 64)
+            const int dh = ckh * p.a.DH, dw = ckw * p.a.DW;
+            const unsigned koff = (unsigned)((dh * p.a.W + dw) * p.a.C + cc) * 4u;
+#pragma unroll
+            for (int i = 0; i < AI; ++i) {
+                const bool ok = KOK(i) && (unsigned)(aih[i] + dh) < (unsigned)p.a.H &&
+                                (unsigned)(aiw[i] + dw) < (unsigned)p.a.W;
+                dma16_buf(ra, ok ? aoff[i] + koff : OOB, sa + (i * 4 + wave) * 8 * BK);
+            }
+            cc += KSTEP;
+            while (cc >= p.a.cg) {
+                cc -= p.a.cg;
+                if (++ckw == p.a.KW) {
+                    ckw = 0;
+                    ++ckh;
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < BI; ++i)
+            dma16_buf(rb, KOK(i) ? boff[i] + (unsigned)k * 4u : OOB, sb + (i * 4 + wave) * 8 * BK);
+        knext = k + KSTEP;
+#undef KOK
+    };
+
+    floatx16 acc[RM][RN];
+#pragma unroll
+    for (int i = 0; i < RM; ++i)
+#pragma unroll
+        for (int j = 0; j < RN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    const int li = lane & 31;
+    const int lh = lane >> 5;
+    const int sw = (li & 7) ^ ((li >> 3) & 1);  // f(row): fragment rows start at multiples of 32
+
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s)
+        if (s < nk) issue(s);
+
+    constexpr int PER_STAGE = AI + BI;
+    for (int kt = 0; kt < nk; ++kt) {
+        // Stage kt has landed once at most the later stages' loads are outstanding.
+        const int ahead = min(nk - 1 - kt, STAGES - 2);
+        if (STAGES >= 4 && ahead >= 2) {
+            wait_vmcnt<(STAGES >= 4 ? 2 : 0) * PER_STAGE>();
+        } else if (STAGES >= 3 && ahead >= 1) {
+            wait_vmcnt<PER_STAGE>();
+        } else {
+            wait_vmcnt<0>();
+        }
+        barrier_lds();
+        if (kt + STAGES - 1 < nk) issue((kt + STAGES - 1) % STAGES);
+        const float *as = smem + (kt % STAGES) * STAGE;
+        const float *bs = as + BM * BK;
+        if constexpr (QUARTER) {
+            // 16 k of k block wave >> 1: chunks (wave & 1) * 4 + lh * 2 + s of rows 32 * kb + li
+            const int rq = ((wave >> 1) * 32 + li) * BK;
+            const int c0 = (wave & 1) * 4 + lh * 2;
+            f4 af[2], bf[2];
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                af[s] = *reinterpret_cast<const f4 *>(&as[rq + (((c0 + s) ^ sw) << 2)]);
+                bf[s] = *reinterpret_cast<const f4 *>(&bs[rq + (((c0 + s) ^ sw) << 2)]);
+            }
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[s][e], bf[s][e], acc[0][0], 0, 0, 0);
+        } else {
+            f4 af[RM][4], bf[RN][4];
+#pragma unroll
+            for (int i = 0; i < RM; ++i)
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+                    af[i][s] = *reinterpret_cast<const f4 *>(
+                        &as[(wm * WM + i * 32 + li) * BK + (((lh * 4 + s) ^ sw) << 2)]);
+#pragma unroll
+            for (int j = 0; j < RN; ++j)
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+                    bf[j][s] = *reinterpret_cast<const f4 *>(
+                        &bs[(wn * WN + j * 32 + li) * BK + (((lh * 4 + s) ^ sw) << 2)]);
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+#pragma unroll
+                    for (int i = 0; i < RM; ++i)
+#pragma unroll
+                        for (int j = 0; j < RN; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s][e], bf[j][s][e],
+                                                                              acc[i][j], 0, 0, 0);
+        }
+    }
+    __syncthreads();
+    if constexpr (QUARTER) {
+        // the four waves' partial quarters (pitch 40 floats, 5 KB apart), summed in wave order
+        // into the first; register r holds row 8 * (r / 4) + 4 * lh + r % 4, column li
+        constexpr int LDQ = 40, PART = 32 * LDQ;
+        float *const cw = smem + wave * PART;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) cw[((r >> 2) * 8 + lh * 4 + (r & 3)) * LDQ + li] = acc[0][0][r];
+        __syncthreads();
+        const int o = (tid >> 3) * LDQ + (tid & 7) * 4;
+        f4 v = *reinterpret_cast<const f4 *>(&smem[o]);
+        v += *reinterpret_cast<const f4 *>(&smem[PART + o]);
+        v += *reinterpret_cast<const f4 *>(&smem[2 * PART + o]);
+        v += *reinterpret_cast<const f4 *>(&smem[3 * PART + o]);
+        *reinterpret_cast<f4 *>(&smem[o]) = v;
+        __syncthreads();
+        gemm_lds_to_global<32, 32>(p, smem, m0, n0, ks, co, ro);
+    } else {
+        gemm_store_tile<BM, BN, WGM>(p, smem, acc, m0, n0, ks, co, ro);
+    }
+}
+
+// The 64 x 64 launch with a quarter-tile tail: workgroups below p.nfull take whole tiles, the
+// rest take quarters of the tiles after them (four workgroups per tile), so a tile count just
+// past a multiple of the CU count does not leave a few CUs running one more whole tile than the
+// others. Within each range consecutive tiles go to one XCD (the hardware deals workgroup ids
+// round-robin to the eight XCDs), which keeps a tile row's A block in one L2. Launches without
+// such a tail run gemm_dma_kernel: its whole tiles compile to a tighter K loop than this
+// kernel's shared body (measured 2-4% faster per launch).
+template <int AMODE>
+__global__ void __launch_bounds__(256) gemm_dma_tail_kernel(const GemmDev p) {
+    constexpr int BM = 64, BN = 64, WGM = 2, STAGES = 2;
+    __shared__ __attribute__((aligned(16))) float smem[dma_smem_floats<BM, BN, STAGES>()];
+    const int nb = gridDim.x;
+    const int nfull = p.nfull < nb ? p.nfull : nb;
+    int lin = blockIdx.x;
+    const bool quarter = lin >= nfull;
+    const int first = quarter ? nfull : 0;
+    const int span = (quarter ? nb - nfull : nfull) & ~7;
+    lin -= first;
+    if (lin < span) {
+        const int per = span >> 3;
+        lin = (lin & 7) * per + (lin >> 3);
+    }
+    if (quarter) {
+        const int t = nfull + (lin >> 2);
+        const int tm = t / p.tiles_n;
+        const int tn = t - tm * p.tiles_n;
+        gemm_dma_tile<BM, BN, WGM, STAGES, AMODE, true>(p, smem, tm * BM + (lin & 1) * 32,
+                                                       tn * BN + ((lin >> 1) & 1) * 32);
+        return;
+    }
+    const int tm = lin / p.tiles_n;
+    const int tn = lin - tm * p.tiles_n;
+    gemm_dma_tile<BM, BN, WGM, STAGES, AMODE, false>(p, smem, tm * BM, tn * BN);
 }
 
 // GEMM / implicit-GEMM convolution on 32 x 32 output tiles whose K range is dealt out to the
@@ -1838,6 +2124,12 @@ static GemmKernel pick_dma(int am) {
                           : &gemm_dma_kernel<BM, BN, WGM, 2, AM_CONV_VEC>;
 }
 
+static GemmKernel pick_dma_tail(int am) {
+    return am == AM_VEC   ? &gemm_dma_tail_kernel<AM_VEC>
+           : am == AM_CAT ? &gemm_dma_tail_kernel<AM_CAT>
+                          : &gemm_dma_tail_kernel<AM_CONV_VEC>;
+}
+
 // 16 x 16 wave-split launches: eight waves with three-stage rings for K of 1024 and more (two
 // waves per SIMD, one computing while the other waits for its loads), four waves with
 // two-stage rings below. Measured against each other (same table as use_tile16): eight waves
@@ -1969,6 +2261,19 @@ static int use_tile16(int M, int N, int K, int wsk) {
     if (K <= 2560) return tiles16 <= 2 * kCUs ? 1 : 0;
     const int s = (K + 2303) / 2304;
     return s <= wsk && tiles16 * s <= 2 * kCUs ? s : 0;
+}
+
+// Quarter tiles for the last tiles of a 64 x 64 launch: with T = q * 256 + r tiles (0 < r <=
+// kQuarterTiles, q >= 1) the busiest CUs would run q + 1 tiles while most run q; the last r
+// tiles are computed as 4 r quarter tiles instead (a quarter's MFMA work is a fourth), so no
+// CU runs more than q tiles and two quarters. The quarter form reads 64 k per ring stage:
+// convolution windows need channel groups of a multiple of 64, a concatenated K a first
+// part of a multiple of 64.
+static const int kQuarterTiles = 64;
+static const int kQuarterMinK = 256;
+
+static bool quarter_tiles_ok(int am, const GemmDev &p) {
+    return am == AM_VEC || (am == AM_CONV_VEC && p.a.cg % 64 == 0) || (am == AM_CAT && p.k1 % 64 == 0);
 }
 
 // The streaming kernel for short K over many rows (K <= 32, K % 4 == 0, at least 4096 rows,
@@ -2388,13 +2693,22 @@ static void gemm_launch(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const LnTai
     t.bn = w16 ? 16 : wsplit || narrow ? 32 : 64;
     p.tiles_m = (p.M + t.bm - 1) / t.bm;
     p.tiles_n = (p.N + t.bn - 1) / t.bn;
-    const GemmKernel kern = w16      ? pick_wsplit16(am, p.kchunk)
+    GemmKernel kern = w16      ? pick_wsplit16(am, p.kchunk)
                             : wsplit ? pick_wsplit(am)
                             : narrow ? pick_dma<128, 32, 4>(am)
                             : dma_ok ? pick_dma<64, 64, 2>(am)
                                      : pick_kernel<64, 64, 2>(am, bm);
     const int threads = w16 ? 64 * wsplit16_waves(p.kchunk) : 256;
-    const dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)(batch * p.split));
+    dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)(batch * p.split));
+    if (dma_ok && !wsplit && !narrow && p.split == 1 && batch == 1 && quarter_tiles_ok(am, p)) {
+        const int tiles = p.tiles_m * p.tiles_n;
+        const int rest = tiles % kCUs;
+        if (tiles >= kCUs && rest > 0 && rest <= kQuarterTiles && p.K >= kQuarterMinK) {
+            p.nfull = tiles - rest;
+            grid.x = (unsigned)(p.nfull + 4 * rest);
+            kern = pick_dma_tail(am);
+        }
+    }
     if (ln && p.split < 2) {  // the workspace did not allow the split the reduction needs
         x->launch_error = (int)hipErrorInvalidValue;
         set_error("mgc_hip_gemm_layer_norm: no K split", hipErrorInvalidValue);

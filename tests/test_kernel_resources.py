@@ -78,6 +78,8 @@ def test_gemm_lds_is_the_dma_rings(kernels):
         return {v["group_segment_fixed_size"] for k, v in kernels.items() if re.search(pattern, k)}
 
     assert lds(r"gemm_dma_wsplit_kernel") == {65536}
+    # 64 x 64 tiles, with and without the quarter-tile tail: a two-stage ring of 2 x 64 x 32 floats
+    assert lds(r"gemm_dma_kernelILi64ELi64E|gemm_dma_tail_kernel") == {32768}
     assert lds(r"gemm_dma_wsplit16_kernelILi\dELi3ELi8E") == {8 * 3 * 4096}
     assert lds(r"gemm_dma_wsplit16_kernelILi\dELi2ELi4E") == {4 * 2 * 4096}
 
