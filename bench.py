@@ -183,7 +183,7 @@ def gemm_roofline(graph, model, replays: int) -> dict:
     achieved = flops / secs / 1e12 if secs > 0 else 0.0
     return {
         "bound": "mfma",
-        "kernel": "gemm_{dma,dma_wsplit,mfma}_kernel (fp32 MFMA implicit-GEMM conv / GEMM family)",
+        "kernel": "gemm_{dma,dma_tail,dma_wsplit,mfma}_kernel (fp32 MFMA implicit-GEMM conv / GEMM family)",
         "achieved": round(achieved, 2),
         "peak": MFMA_FP32_PEAK_TFLOPS,
         "unit": "TFLOP/s",
