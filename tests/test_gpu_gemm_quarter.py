@@ -1,5 +1,6 @@
 """64 x 64 GEMM launches whose tile count is just past a multiple of the 256 CUs: the last r
-tiles (0 < r <= 128) run as 4 r quarter tiles of 32 x 32, the four waves of a quarter's
+tiles (0 < r <= 64, K >= 256, csrc/gemm.hip kQuarterTiles / kQuarterMinK) run as 4 r quarter
+tiles of 32 x 32, the four waves of a quarter's
 workgroup each taking a quarter of K (16 of every 64 k) and the partial quarters summed in LDS
 in wave order (csrc/gemm.hip, gemm_dma_tile with QUARTER). Shapes chosen so that the tail
 applies: ragged M and N (quarters partly or wholly past the matrix edge), K not a multiple of
@@ -21,10 +22,11 @@ pytestmark = pytest.mark.gpu
 @pytest.mark.parametrize(
     "m, n, k, epilogue",
     [
-        (16428, 64, 100, "bias_relu"),  # 257 tiles: one tile in quarters, the last 44 rows
-        (19200, 120, 72, "residual"),   # 600 tiles (88 in quarters), ragged columns, short K
+        (16428, 64, 300, "bias_relu"),  # 257 tiles: one tile in quarters, the last 44 rows
+        (17000, 120, 264, "residual"),  # 532 tiles (20 in quarters), ragged rows and columns,
+                                        # the last 64-k stage holds 8 k
         (5000, 832, 256, "none"),       # 1027 tiles: four full rounds, then 3 tiles in quarters
-        (16640, 50, 64, "bias_relu"),   # 260 tiles, N not a multiple of 4
+        (16640, 50, 256, "bias_relu"),  # 260 tiles, N not a multiple of 4
     ],
 )
 def test_quarter_tail_gemm(m, n, k, epilogue, hip_cache):
