@@ -771,9 +771,9 @@ __global__ void __launch_bounds__(256) gemm_dma_kernel(const GemmDev p) {
 }
 
 // Body of gemm_dma_tail_kernel: gemm_dma_kernel's whole 64 x 64 tiles, and (QUARTER) a 64 x 64
-// tile's 32 x 32 quarter computed by all four waves, each over a quarter of K. A ring stage then holds 64 k of the quarter's 32 A rows and 32 B rows
-// (LDS row r < 32: k block 0, r >= 32: k block 1, same 32-float row format and swizzle), the
-// same 16 KB as a 64 x 64 stage; wave w multiplies the 16 k (w & 1) of k block w >> 1. The
+// tile's 32 x 32 quarter computed by all four waves, each over a quarter of K. A quarter's ring
+// stage holds 64 k of its 32 A rows and 32 B rows (LDS row r < 32: k block 0, r >= 32: k block
+// 1, same 32-float row format and swizzle), the same 16 KB as a 64 x 64 stage; wave w multiplies the 16 k (w & 1) of k block w >> 1. The
 // four partial tiles are summed through LDS in wave order before the common epilogue.
 template <int BM, int BN, int STAGES>
 constexpr int dma_smem_floats() {
@@ -2266,9 +2266,11 @@ static int use_tile16(int M, int N, int K, int wsk) {
 // Quarter tiles for the last tiles of a 64 x 64 launch: with T = q * 256 + r tiles (0 < r <=
 // kQuarterTiles, q >= 1) the busiest CUs would run q + 1 tiles while most run q; the last r
 // tiles are computed as 4 r quarter tiles instead (a quarter's MFMA work is a fourth), so no
-// CU runs more than q tiles and two quarters. The quarter form reads 64 k per ring stage:
-// convolution windows need channel groups of a multiple of 64, a concatenated K a first
-// part of a multiple of 64.
+// CU runs more than q tiles and one quarter. Below K = 256 a quarter's fixed costs (first
+// stage, epilogue) outweigh its share of the work, and with r > 64 CUs would run two or more
+// quarters (MobileNetV2 b32 0.693 -> 0.704 ms with r <= 128 at any K; ResNet-50 b32 the same
+// within 0.3%). The quarter form reads 64 k per ring stage: convolution windows need channel
+// groups of a multiple of 64, a concatenated K a first part of a multiple of 64.
 static const int kQuarterTiles = 64;
 static const int kQuarterMinK = 256;
 
