@@ -2266,13 +2266,13 @@ static int use_tile16(int M, int N, int K, int wsk) {
 // Quarter tiles for the last tiles of a 64 x 64 launch: with T = q * 256 + r tiles (0 < r <=
 // kQuarterTiles, q >= 1) the busiest CUs would run q + 1 tiles while most run q; the last r
 // tiles are computed as 4 r quarter tiles instead (a quarter's MFMA work is a fourth), so no
-// CU runs more than q tiles and one quarter. Below K = 256 a quarter's fixed costs (first
+// CU runs more than q tiles and one quarter. For short K a quarter's fixed costs (first
 // stage, epilogue) outweigh its share of the work, and with r > 64 CUs would run two or more
 // quarters (MobileNetV2 b32 0.693 -> 0.704 ms with r <= 128 at any K; ResNet-50 b32 the same
-// within 0.3%). The quarter form reads 64 k per ring stage: convolution windows need channel
+// within 0.3%; K >= 128 against K >= 256: ResNet-50 b32 2.764 -> 2.759 ms). The quarter form reads 64 k per ring stage: convolution windows need channel
 // groups of a multiple of 64, a concatenated K a first part of a multiple of 64.
 static const int kQuarterTiles = 64;
-static const int kQuarterMinK = 256;
+static const int kQuarterMinK = 128;
 
 static bool quarter_tiles_ok(int am, const GemmDev &p) {
     return am == AM_VEC || (am == AM_CONV_VEC && p.a.cg % 64 == 0) || (am == AM_CAT && p.k1 % 64 == 0);

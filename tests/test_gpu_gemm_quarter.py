@@ -1,5 +1,5 @@
 """64 x 64 GEMM launches whose tile count is just past a multiple of the 256 CUs: the last r
-tiles (0 < r <= 64, K >= 256, csrc/gemm.hip kQuarterTiles / kQuarterMinK) run as 4 r quarter
+tiles (0 < r <= 64, K >= 128, csrc/gemm.hip kQuarterTiles / kQuarterMinK) run as 4 r quarter
 tiles of 32 x 32, the four waves of a quarter's
 workgroup each taking a quarter of K (16 of every 64 k) and the partial quarters summed in LDS
 in wave order (csrc/gemm.hip, gemm_dma_tile with QUARTER). Shapes chosen so that the tail
