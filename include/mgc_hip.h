@@ -146,13 +146,17 @@ long mgc_hip_gemm_workspace(int M, int N, int K, int batch);
 /* mgc_hip_gemm for callers that cannot allocate device memory (code under HIP graph capture,
  * serving loops, harnesses that forbid hipMalloc). No counterpart in the reference: its C
  * backend allocates nothing to begin with. Computes exactly what mgc_hip_gemm computes with a
- * sufficient workspace, but keeps the K-split partials in the library's own per-GPU device
- * array of MGC_HIP_NOALLOC_SCRATCH_FLOATS floats: g->workspace and g->workspace_floats are
- * ignored, and the call allocates nothing. `stream` is a hipStream_t (NULL = the null stream);
- * the call only enqueues work. Returns MGC_OK, MGC_ERR_ARGS (no arguments, or a GEMM whose
- * K split needs more than MGC_HIP_NOALLOC_SCRATCH_FLOATS floats; see mgc_hip_last_error) or
- * MGC_ERR_HIP (launch or runtime failure). Every call on one GPU shares that GPU's array:
- * calls that overlap on one GPU (different streams without ordering) race on it. */
+ * workspace of MGC_HIP_NOALLOC_SCRATCH_FLOATS floats, which it keeps in the library's own
+ * per-GPU device array: g->workspace and g->workspace_floats are ignored, and the call
+ * allocates nothing. A K split the library chooses (split_k 0) whose partials would not fit
+ * is dropped, as mgc_hip_gemm drops it for a small workspace; an explicit split_k that does
+ * not fit is refused. `stream` is a hipStream_t (NULL = the null stream); the call only
+ * enqueues work. Returns MGC_OK, MGC_ERR_ARGS (no arguments, an explicit split_k whose
+ * partials need more than MGC_HIP_NOALLOC_SCRATCH_FLOATS floats, or operands outside a
+ * kernel's limits; see mgc_hip_last_error) or MGC_ERR_HIP (launch or runtime failure). An
+ * error left pending on the calling thread before the call is cleared, not reported. Every
+ * call on one GPU shares that GPU's array: calls that overlap on one GPU (different streams
+ * without ordering) race on it. */
 int mgc_hip_gemm_noalloc(void *stream, const mgc_hip_gemm_args *g);
 
 /* A GEMM (batch_rank 0) whose output rows then go through a LayerNorm: out = LayerNorm(C) with

@@ -1572,12 +1572,13 @@ __global__ void __launch_bounds__(64 * WAVES) gemm_dma_wsplit16_kernel(const Gem
 // 32 x 32 accumulator holds row 8 (r / 4) + 4 h + r % 4, column li. Every operand goes through
 // a buffer resource: columns of B past N, k past K and rows of A past M load as zeros (so the
 // padding multiplies 0 by 0), and C and residual accesses past M or N are dropped, which keeps
-// the epilogue free of branches. Activation none, relu or clip, as one clamp to [lo, hi]
-// (lo = -inf, hi = +inf for none). Waves are dealt to column groups, wave w of a group taking
-// M-tiles w, w + waves_per_group, ...
+// the epilogue free of branches. Activation relu or clip as one clamp to [lo, hi] (lo = 0,
+// hi = +inf for relu: fmaxf maps NaN to 0 as relu's v > 0 ? v : 0 does); none stores v unchanged
+// (clamp = 0, a uniform test), so NaN passes through as in every other epilogue. Waves are dealt
+// to column groups, wave w of a group taking M-tiles w, w + waves_per_group, ...
 template <int KH, int NB>
 __global__ void __launch_bounds__(256) gemm_stream_kernel(const GemmDev p, int groups, int waves_per_group,
-                                                          float lo, float hi, long c_bytes, long r_bytes) {
+                                                          int clamp, float lo, float hi, long c_bytes, long r_bytes) {
     const int lane = threadIdx.x & 63, li = lane & 31, h = lane >> 5;
     const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (gw >= groups * waves_per_group) return;
@@ -1654,7 +1655,7 @@ __global__ void __launch_bounds__(256) gemm_stream_kernel(const GemmDev p, int g
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 float v = acc[nb][r] * alpha + bias[nb] + beta * res[r];
-                v = fminf(fmaxf(v, lo), hi);
+                if (clamp) v = fminf(fmaxf(v, lo), hi);
                 const unsigned off = rowofs[r] == OOB || cofs[nb] == OOB ? OOB : rowofs[r] * ldc4 + cofs[nb];
                 __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, v), rc, off, 0, 0);
             }
@@ -2103,7 +2104,7 @@ static bool bs_div4(const long *bs, int rank) {
 }
 
 typedef void (*GemmKernel)(const GemmDev);
-typedef void (*GemmKernelStream)(const GemmDev, int, int, float, float, long, long);
+typedef void (*GemmKernelStream)(const GemmDev, int, int, int, float, float, long, long);
 
 template <int BM, int BN, int WGM>
 static GemmKernel pick_kernel(int am, int bm) {
@@ -2313,11 +2314,12 @@ static void stream_launch(mgc_hip_exec *x, const GemmDev &p) {
     if (per_group > tiles_m) per_group = tiles_m;
     if (per_group < 1) per_group = 1;
     const int wgs = (groups * per_group + 3) / 4;
-    const float lo = p.act == MGC_ACT_CLIP ? p.lo : p.act == MGC_ACT_RELU ? 0.0f : -INFINITY;
+    const int clamp = p.act == MGC_ACT_CLIP || p.act == MGC_ACT_RELU;
+    const float lo = p.act == MGC_ACT_CLIP ? p.lo : 0.0f;
     const float hi = p.act == MGC_ACT_CLIP ? p.hi : INFINITY;
     const long c_bytes = ((long)(p.M - 1) * p.ldc + p.N) * 4;
     const long r_bytes = p.res ? ((long)(p.M - 1) * p.ldr + p.N) * 4 : 0;
-    MGC_LAUNCH(x, kern, dim3((unsigned)wgs), dim3(256), 0, p, groups, per_group, lo, hi, c_bytes, r_bytes);
+    MGC_LAUNCH(x, kern, dim3((unsigned)wgs), dim3(256), 0, p, groups, per_group, clamp, lo, hi, c_bytes, r_bytes);
 }
 
 // The same choice for a GEMM whose split-K reduction ends in a LayerNorm (the split is
@@ -2418,15 +2420,14 @@ extern "C" int mgc_hip_gemm_noalloc(void *stream, const mgc_hip_gemm_args *g) {
     }
     int batch = 1;
     for (int d = 0; d < g->batch_rank && d < 4; ++d) batch *= g->batch_dims[d];
-    // the partials this call needs: the split mgc_hip_gemm takes when its workspace allows
-    // (the wave-split kernel's own K split never needs more), or the caller's explicit split
+    // A caller's explicit split must fit the scratch. The library's own choice (split_k 0) is
+    // taken as mgc_hip_gemm takes it with a workspace of the scratch's size: a split whose
+    // partials would not fit is dropped (one K pass, no reduction), never refused. (choose_tiles
+    // keeps its partials within 5 * 256 tiles of 64 x 64 floats, 20 MiB, so with this scratch
+    // size that does not happen.)
     long need = 0;
-    if (g->M > 0 && g->N > 0 && g->K > 0 && batch > 0) {
-        if (g->split_k > 1 && batch == 1)
-            need = (long)g->split_k * g->M * g->N;
-        else if (g->split_k <= 0)
-            need = mgc_hip_gemm_workspace(g->M, g->N, g->K, batch);
-    }
+    if (g->M > 0 && g->N > 0 && g->K > 0 && batch > 0 && g->split_k > 1 && batch == 1)
+        need = (long)g->split_k * g->M * g->N;
     if (need > MGC_HIP_NOALLOC_SCRATCH_FLOATS) {
         char msg[200];
         snprintf(msg, sizeof msg,
@@ -2447,8 +2448,13 @@ extern "C" int mgc_hip_gemm_noalloc(void *stream, const mgc_hip_gemm_args *g) {
     a.workspace_floats = MGC_HIP_NOALLOC_SCRATCH_FLOATS;
     mgc_hip_exec x{};
     x.stream = static_cast<hipStream_t>(stream);
+    // an error the caller left pending on this thread is not this call's: the launch check
+    // after each kernel reads hipGetLastError()
+    (void)hipGetLastError();
     gemm_launch(&x, &a, nullptr);
-    return x.launch_error ? MGC_ERR_HIP : MGC_OK;
+    if (!x.launch_error) return MGC_OK;
+    // gemm_launch reports operands outside a kernel's limits as hipErrorInvalidValue
+    return x.launch_error == (int)hipErrorInvalidValue ? MGC_ERR_ARGS : MGC_ERR_HIP;
 }
 
 extern "C" int mgc_hip_gemm_layer_norm_supported(int M, int N) {

@@ -110,6 +110,10 @@ FUSE_PROJECTION_SHORTCUT = True
 FUSE_DEPTHWISE_POINTWISE = True
 DEPTHWISE_FUSE_MIN_ROWS = 16384
 DEPTHWISE_FUSE_SHALLOW_K = 96
+# The fused GEMMs address their image and weight operands through buffer resources with 32-bit
+# byte offsets, and their launchers refuse operands of this many bytes or more (the unfused
+# kernels have a generic path for them): both fusions are only taken below it.
+FUSED_OPERAND_LIMIT = 0x7FFFFFFF
 
 MAX_RANK = 6
 MAX_LEAVES = 16
@@ -220,6 +224,11 @@ def _pointwise_nhwc(node: Node) -> bool:
     return all(p == 0 for p in g.pads) and all(v is None or v.data is not None for v in node.inputs[2:3])
 
 
+def _tensor_bytes(v: Value) -> int:
+    t = v.tensor_type
+    return int(np.prod(t.shape, dtype=np.int64)) * np.dtype(numpy_dtype(t.dtype)).itemsize
+
+
 def find_projection_shortcuts(graph: Graph) -> dict[int, Node]:
     """id(c3) -> ds for every residual block whose projection shortcut ds can run inside the
     GEMM of the block's last convolution c3 (a ResNet downsample block).
@@ -228,7 +237,9 @@ def find_projection_shortcuts(graph: Graph) -> dict[int, Node]:
     input channels K1 are a multiple of 32 (a whole number of 32-wide K stages before the
     second source starts). ds: pointwise NHWC convolution with no activation and no residual,
     any stride, input channels a multiple of 4, whose output only c3 reads (as its residual) and
-    which the schedule puts before c3; its input must be a tensor (not a constant)."""
+    which the schedule puts before c3; its input must be a tensor (not a constant). The fused
+    launch reads c3's input, ds's input and the stacked [N][K1 + K2] weights each below
+    FUSED_OPERAND_LIMIT bytes."""
     order = {id(n): i for i, n in enumerate(graph.nodes)}
     outputs = {id(v) for v in graph.outputs}
     found: dict[int, Node] = {}
@@ -251,6 +262,9 @@ def find_projection_shortcuts(graph: Graph) -> dict[int, Node]:
         if ds.input(0).data is not None or at.shape[3] % 32 or xt.shape[3] % 4:
             continue
         if ds.input(1).tensor_type.shape[3] != c3.input(1).tensor_type.shape[3]:
+            continue
+        stacked = 4 * (at.shape[3] + xt.shape[3]) * c3.input(1).tensor_type.shape[3]
+        if max(_tensor_bytes(c3.input(0)), _tensor_bytes(ds.input(0)), stacked) >= FUSED_OPERAND_LIMIT:
             continue
         found[id(c3)] = ds
     return found
@@ -279,7 +293,8 @@ def find_depthwise_pointwise(graph: Graph, min_rows: int | None = None) -> dict[
     convolution pw reads (MobileNet's depthwise -> projection pair), when pw's GEMM has at least
     ``min_rows`` rows (default DEPTHWISE_FUSE_MIN_ROWS) or at most DEPTHWISE_FUSE_SHALLOW_K
     input channels: pw is a stride-1 pointwise NHWC convolution, dw a depthwise 3 x 3
-    convolution (stride 1 or 2, any padding) over a tensor whose channels are a multiple of 4."""
+    convolution (stride 1 or 2, any padding) over a tensor whose channels are a multiple of 4,
+    with the depthwise input and pw's weights each below FUSED_OPERAND_LIMIT bytes."""
     if min_rows is None:
         min_rows = DEPTHWISE_FUSE_MIN_ROWS
     outputs = {id(v) for v in graph.outputs}
@@ -297,6 +312,8 @@ def find_depthwise_pointwise(graph: Graph, min_rows: int | None = None) -> dict[
         if ops.window_geometry(pw, at.shape[1:3], (1, 1)).strides != (1, 1):
             continue
         if at.shape[0] * at.shape[1] * at.shape[2] < min_rows and at.shape[3] > DEPTHWISE_FUSE_SHALLOW_K:
+            continue
+        if max(_tensor_bytes(dw.input(0)), _tensor_bytes(pw.input(1))) >= FUSED_OPERAND_LIMIT:
             continue
         found[id(pw)] = dw
     return found

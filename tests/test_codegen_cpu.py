@@ -165,6 +165,31 @@ def test_depthwise_pointwise_pairs_join_one_gemm():
     assert sorted(dw.input(0).tensor_type.shape[3] for dw in shallow.values()) == [32, 96]
 
 
+def test_fusions_stay_below_the_fused_kernels_operand_limit(monkeypatch):
+    """The fused projection-shortcut and depthwise GEMMs address their operands with 32-bit byte
+    offsets and refuse operands of 2 GiB or more at launch, so the emitter must not choose them
+    there: ResNet-50 at batch 700 (stage 2's shortcut input [700, 56, 56, 256] is 2.25 GB) and
+    MobileNetV2 at batch 450 (the 112 x 112 x 96 depthwise input is 2.17 GB) compile with those
+    pairs left to the unfused kernels, and every launch the source counts stays below the limit."""
+    from ml_graph_compiler.codegen import hip as emitter
+
+    limit = emitter.FUSED_OPERAND_LIMIT
+    nbytes = emitter._tensor_bytes
+    for make, find, kind in ((lambda: builders.resnet50(batch=700), emitter.find_projection_shortcuts, "gemm_shortcut"),
+                             (lambda: builders.mobilenet_v2(batch=450), emitter.find_depthwise_pointwise, "gemm_depthwise")):
+        g = o3(make())
+        pairs = find(g)
+        with monkeypatch.context() as m:
+            m.setattr(emitter, "FUSED_OPERAND_LIMIT", 1 << 62)
+            unlimited = find(g)
+        dropped = [n for n in g.nodes if id(n) in unlimited and id(n) not in pairs]
+        assert len(dropped) == 1, kind
+        big = unlimited[id(dropped[0])].input(0)
+        assert nbytes(big) >= limit > max(nbytes(p.input(0)) for p in pairs.values())
+        gen = generate_hip(g, gemm_workspace=native.gemm_workspace_floats)
+        assert gen.kernels[kind] == len(pairs) == len(unlimited) - 1
+
+
 def test_every_sample_and_config_generates_and_builds(hip_cache):
     for name, make in list(builders.SAMPLES.items()) + [("single_gemm", builders.single_gemm), ("bottleneck", builders.bottleneck)]:
         for level in ("O0", "O3"):

@@ -31,6 +31,8 @@ pytestmark = pytest.mark.gpu
         (8192, 20, 768, "bias"),         # 24 blocks, four groups
         (6000, 32, 16, "residual"),      # project layer with its residual
         (4096, 28, 33, "residual"),      # N = 33: a second block with one live column
+        (4096, 16, 96, "none_nan"),      # a NaN input element: its row stays NaN (no clamp)
+        (4096, 24, 40, "residual_nan"),  # NaN in the residual passes through
     ],
 )
 def test_stream_gemm(m, k, n, epilogue, hip_cache):
@@ -50,13 +52,21 @@ def test_stream_gemm(m, k, n, epilogue, hip_cache):
         lo = g.constant(np.asarray(0.0, np.float32), "lo")
         hi = g.constant(np.asarray(6.0, np.float32), "hi")
         y = g.add_node("Clip", [y, lo, hi], 1, {}, name="clip").output
-    elif epilogue == "residual":
+    elif epilogue.startswith("residual"):
         r = g.add_input("r", TensorType("float32", (m, n)))
         feeds["r"] = rng.standard_normal((m, n)).astype(np.float32)
         y = g.add_node("Add", [y, r], 1, {}, name="res").output
+    if epilogue == "none_nan":
+        feeds["x"][5, 3] = np.nan
+    elif epilogue == "residual_nan":
+        feeds["r"][7, 11] = np.nan
     g.add_output(y, "y")
     infer_shapes(g)
-    check_hip(g, feeds, hip_cache, opt="O3", rtol=2e-5, atol=2e-5)
+    got = check_hip(g, feeds, hip_cache, opt="O3", rtol=2e-5, atol=2e-5)["y"]
+    if epilogue == "none_nan":
+        assert np.isnan(got[5]).all() and np.isfinite(np.delete(got, 5, axis=0)).all()
+    elif epilogue == "residual_nan":
+        assert np.isnan(got[7, 11]) and np.isnan(got).sum() == 1
 
 
 @pytest.mark.parametrize("n, cin, cout, hw, residual", [(2, 16, 96, 56, False), (1, 24, 144, 64, False),

@@ -6,7 +6,9 @@ model (the emitter's call, with the planner's workspace); the new one is called 
 device buffers this test allocates for the operands (the caller still owns inputs and outputs).
 Two calls in a row on the same GPU, the second with a smaller input, must each match the
 compiled model bit for bit (same kernels, same K split) and the oracle within the single-GEMM
-tolerance (1e-4 max-abs). A GEMM whose K split needs more than the scratch holds is rejected.
+tolerance (1e-4 max-abs). An explicit K split that needs more than the scratch holds, and
+operands outside a kernel's limits, are rejected as argument errors; an error left pending on the
+thread before a call does not fail it.
 """
 
 from __future__ import annotations
@@ -108,7 +110,7 @@ def _graph(m: int, n: int, k: int, seed: int):
 
 
 def _noalloc(lib, hip: Hip, m: int, n: int, k: int, x: np.ndarray, w: np.ndarray, bias: np.ndarray,
-             split_k: int = 0) -> tuple[int, np.ndarray | None]:
+             split_k: int = 0, k1: int = 0) -> tuple[int, np.ndarray | None]:
     args = GemmArgs()
     args.M, args.N, args.K = m, n, k
     args.a = Operand(kind=MGC_OP_STRIDED, p=hip.upload(x), rs=k, cs=1)
@@ -120,6 +122,7 @@ def _noalloc(lib, hip: Hip, m: int, n: int, k: int, x: np.ndarray, w: np.ndarray
     args.bias, args.bias_mode = hip.upload(bias), 1
     args.act, args.lo, args.hi = MGC_ACT_RELU, 0.0, 6.0
     args.split_k = split_k
+    args.k1 = k1
     code = lib.mgc_hip_gemm_noalloc(None, ctypes.byref(args))
     return code, (hip.download(c, (m, n)) if code == MGC_OK else None)
 
@@ -162,5 +165,19 @@ def test_noalloc_gemm_matches_mgc_hip_gemm(hip_cache):
                            np.zeros(n, np.float32), split_k=2)
         assert code == MGC_ERR_ARGS
         assert b"more than" in lib.mgc_hip_last_error()
+        # operands outside a kernel's limits are argument errors too: a concatenated-K second
+        # source that is not an NHWC image
+        code, _ = _noalloc(lib, hip, 64, 64, 64, np.zeros((64, 64), np.float32), np.zeros((64, 64), np.float32),
+                           np.zeros(64, np.float32), k1=32)
+        assert code == MGC_ERR_ARGS, lib.mgc_hip_last_error()
+        assert b"concatenated-K" in lib.mgc_hip_last_error()
+        # an error the caller left pending on the thread (a failed hipSetDevice) is not reported
+        # by the next call, which succeeds
+        assert hip.lib.hipSetDevice(1 << 20) != 0
+        m, n, k = 64, 768, 3072
+        g, w, bias, feeds = _graph(m, n, k, 2)
+        code, got = _noalloc(lib, hip, m, n, k, feeds["x"], w, bias)
+        assert code == MGC_OK, lib.mgc_hip_last_error()
+        assert float(np.max(np.abs(got.astype(np.float64) - oracle.run_graph(g, feeds)["y"]))) <= 1e-4
     finally:
         hip.free()
