@@ -78,6 +78,17 @@ enum {
 /* Opaque execution context: stream, error flag and profiling state of one model. */
 typedef struct mgc_hip_exec mgc_hip_exec;
 
+/* An execution context for calling the kernel entry points below directly, without a compiled
+ * model (tests, custom launchers): their kernels go to `stream` (a hipStream_t; NULL = the null
+ * stream). Allocates the context and its device error flag; NULL on failure (see
+ * mgc_hip_last_error). No counterpart in the reference: its C kernels take no context. */
+mgc_hip_exec *mgc_hip_exec_create(void *stream);
+/* Status of the calls made with x since the last check, then cleared: MGC_OK, MGC_ERR_ARGS (a
+ * launcher refused its operands), MGC_ERR_HIP (a launch failed) or MGC_ERR_GATHER_INDEX (after
+ * synchronizing the stream: a Gather index was out of range). */
+int mgc_hip_exec_status(mgc_hip_exec *x);
+void mgc_hip_exec_destroy(mgc_hip_exec *x);
+
 /* ---------------------------------------------------------------------------------------- */
 /* GEMM and implicit-GEMM convolution on fp32 MFMA                                            */
 /* ---------------------------------------------------------------------------------------- */
@@ -132,7 +143,29 @@ typedef struct {
      * batch_rank 0; sets the launch error otherwise. k1 = 0 is an ordinary GEMM. */
     mgc_hip_operand a2;
     int k1;
+    /* Kernel family (MGC_GEMM_*): MGC_GEMM_AUTO (0, what the emitter uses) lets the library
+     * choose family and K split from the shape; any other value runs that family with split_k
+     * as its K split (0 or 1: none) and sets the launch error when the operands, split or
+     * workspace are outside what the family accepts. Counterpart of the reference's
+     * mgc_set_blocking (src/ml_graph_compiler/codegen/runtime/mgc_kernels.c:34-70), which its
+     * tests use to force the C kernels' edge paths (tests/test_codegen.py:444-455); here it
+     * lets a test run every family on shapes the library would send elsewhere. */
+    int kernel;
 } mgc_hip_gemm_args;
+
+/* GEMM kernel families for mgc_hip_gemm_args.kernel. */
+enum {
+    MGC_GEMM_AUTO = 0,     /* the library's choice */
+    MGC_GEMM_TILED = 1,    /* 64 x 64 tiles through an LDS DMA ring (gemm_dma_kernel) */
+    MGC_GEMM_QUARTER = 2,  /* the same, the second half of the tiles as 32 x 32 quarter tiles
+                              (gemm_dma_tail_kernel); batch 1, no K split */
+    MGC_GEMM_NARROW = 3,   /* 128 x 32 tiles (four waves along M) */
+    MGC_GEMM_WSPLIT = 4,   /* 32 x 32 tiles, K stages dealt to four waves */
+    MGC_GEMM_WSPLIT16 = 5, /* 16 x 16 tiles, K stages dealt to four or eight waves */
+    MGC_GEMM_STREAM = 6,   /* short-K streaming kernel: row-major A, K <= 32, batch 1, no K split,
+                              activation none / relu / clip */
+    MGC_GEMM_REGISTER = 7  /* register-staged operands: every operand form (gemm_mfma_kernel) */
+};
 
 void mgc_hip_gemm(mgc_hip_exec *x, const mgc_hip_gemm_args *g);
 

@@ -2672,12 +2672,9 @@ static void gemm_launch(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const LnTai
     const bool dma_ok = nonneg && (am == AM_VEC || am == AM_CONV_VEC || am == AM_CAT) && bm == BD_NK_VEC &&
                         p.K > 0 && p.a_bytes > 0 && p.a_bytes < kMaxRes && p.b_bytes > 0 &&
                         p.b_bytes < kMaxRes && (am != AM_CAT || (p.a2_bytes > 0 && p.a2_bytes < kMaxRes));
-    if (dma_ok && am == AM_VEC && !ln && g->split_k <= 0 && batch == 1 && use_stream(p.M, p.N, p.K) &&
-        p.bias_mode != 2 && stream_act(p.act) && p.ldc >= p.N && (long)p.M * p.ldc * 4 < kMaxRes &&
-        (!p.res || (long)p.M * p.ldr * 4 < kMaxRes)) {
-        stream_launch(x, p);
-        return;
-    }
+    const bool stream_ok = dma_ok && am == AM_VEC && !ln && batch == 1 && p.K <= 32 && p.bias_mode != 2 &&
+                           stream_act(p.act) && p.ldc >= p.N && (long)p.M * p.ldc * 4 < kMaxRes &&
+                           (!p.res || (long)p.M * p.ldr * 4 < kMaxRes);
     if (am == AM_CAT && !dma_ok) {  // only the DMA kernels read a second source
         x->launch_error = (int)hipErrorInvalidValue;
         set_error("mgc_hip_gemm: concatenated-K GEMM needs a packed [N][K] B and extents below 2 GiB",
@@ -2685,38 +2682,84 @@ static void gemm_launch(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const LnTai
         return;
     }
 
-    int wsk = dma_ok && !ln && g->split_k <= 0 ? wave_split(p.M, p.N, p.K, batch) : 0;
-    if (wsk > 1 && (g->workspace == nullptr || g->workspace_floats < (long)wsk * p.M * p.N)) wsk = 1;
-    if (dma_ok && ln && batch == 1 && p.split >= 2) wsk = wave_split_ln(p.M, p.N, p.K, p.split);
-    const int s16 = wsk > 0 && !ln && batch == 1 ? use_tile16(p.M, p.N, p.K, wsk) : 0;
-    const bool w16 = s16 > 0;
-    if (w16) wsk = s16;
-    const bool wsplit = wsk > 0;
-    if (wsplit) {
-        p.split = wsk;
-        p.kchunk = ((p.K + wsk - 1) / wsk + 31) / 32 * 32;
-    }
-    const bool narrow = dma_ok && !wsplit && narrow_tiles(p.N, p.split);
-    t.bm = w16 ? 16 : wsplit ? 32 : narrow ? 128 : 64;
-    t.bn = w16 ? 16 : wsplit || narrow ? 32 : 64;
-    p.tiles_m = (p.M + t.bm - 1) / t.bm;
-    p.tiles_n = (p.N + t.bn - 1) / t.bn;
-    GemmKernel kern = w16      ? pick_wsplit16(am, p.kchunk)
-                            : wsplit ? pick_wsplit(am)
-                            : narrow ? pick_dma<128, 32, 4>(am)
-                            : dma_ok ? pick_dma<64, 64, 2>(am)
-                                     : pick_kernel<64, 64, 2>(am, bm);
-    const int threads = w16 ? 64 * wsplit16_waves(p.kchunk) : 256;
-    dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)(batch * p.split));
-    if (dma_ok && !wsplit && !narrow && p.split == 1 && batch == 1 && quarter_tiles_ok(am, p)) {
-        const int tiles = p.tiles_m * p.tiles_n;
-        const int rest = tiles % kCUs;
-        if (tiles >= kCUs && rest > 0 && rest <= kQuarterTiles && p.K >= kQuarterMinK) {
-            p.nfull = tiles - rest;
-            grid.x = (unsigned)(p.nfull + 4 * rest);
-            kern = pick_dma_tail(am);
+    // The kernel family and K split: the library's choice from the shape, or the caller's
+    // (g->kernel, g->split_k), checked against what that family accepts.
+    int fam;
+    if (g->kernel == MGC_GEMM_AUTO || ln) {
+        if (stream_ok && g->split_k <= 0 && use_stream(p.M, p.N, p.K)) {
+            fam = MGC_GEMM_STREAM;
+        } else {
+            int wsk = dma_ok && !ln && g->split_k <= 0 ? wave_split(p.M, p.N, p.K, batch) : 0;
+            if (wsk > 1 && (g->workspace == nullptr || g->workspace_floats < (long)wsk * p.M * p.N)) wsk = 1;
+            if (dma_ok && ln && batch == 1 && p.split >= 2) wsk = wave_split_ln(p.M, p.N, p.K, p.split);
+            const int s16 = wsk > 0 && !ln && batch == 1 ? use_tile16(p.M, p.N, p.K, wsk) : 0;
+            if (s16 > 0) wsk = s16;
+            if (wsk > 0) p.split = wsk;
+            fam = s16 > 0 ? MGC_GEMM_WSPLIT16
+                  : wsk > 0 ? MGC_GEMM_WSPLIT
+                  : dma_ok && narrow_tiles(p.N, p.split) ? MGC_GEMM_NARROW
+                  : dma_ok ? MGC_GEMM_TILED
+                           : MGC_GEMM_REGISTER;
+            if (fam == MGC_GEMM_TILED && p.split == 1 && batch == 1 && quarter_tiles_ok(am, p)) {
+                const int tiles = ((p.M + 63) / 64) * ((p.N + 63) / 64);
+                const int rest = tiles % kCUs;
+                if (tiles >= kCUs && rest > 0 && rest <= kQuarterTiles && p.K >= kQuarterMinK) {
+                    fam = MGC_GEMM_QUARTER;
+                    p.nfull = tiles - rest;
+                }
+            }
+        }
+    } else {
+        fam = g->kernel;
+        const int split = g->split_k > 1 ? g->split_k : 1;
+        const char *why = nullptr;
+        if (fam < MGC_GEMM_TILED || fam > MGC_GEMM_REGISTER)
+            why = "unknown kernel family";
+        else if (split > 1 && (batch != 1 || g->workspace == nullptr || g->workspace_floats < (long)split * p.M * p.N))
+            why = "a K split needs batch 1 and split_k * M * N floats of workspace";
+        else if (fam != MGC_GEMM_REGISTER && fam != MGC_GEMM_STREAM && !dma_ok)
+            why = "the DMA kernels need k-contiguous operands (row-major A or NHWC image with 16-byte rows, "
+                  "packed [N][K] B, K % 4 == 0) below 2 GiB";
+        else if (fam == MGC_GEMM_QUARTER && (split > 1 || batch != 1 || !quarter_tiles_ok(am, p)))
+            why = "quarter tiles need batch 1, no K split and 64-channel convolution groups";
+        else if (fam == MGC_GEMM_STREAM && !(stream_ok && split == 1))
+            why = "the streaming kernel needs a row-major A, K <= 32, batch 1, no K split, a column bias and "
+                  "activation none, relu or clip";
+        else if (fam == MGC_GEMM_REGISTER && am == AM_CAT)
+            why = "a concatenated-K GEMM runs on the DMA kernels only";
+        if (why) {
+            char msg[300];
+            snprintf(msg, sizeof msg, "mgc_hip_gemm: kernel family %d: %s", fam, why);
+            x->launch_error = (int)hipErrorInvalidValue;
+            set_error(msg, hipErrorInvalidValue);
+            return;
+        }
+        p.split = split;
+        if (fam == MGC_GEMM_QUARTER) {
+            // the second half of the tiles (at least one) as quarters
+            const int tiles = ((p.M + 63) / 64) * ((p.N + 63) / 64);
+            p.nfull = tiles / 2;
         }
     }
+    if (fam == MGC_GEMM_STREAM) {
+        stream_launch(x, p);
+        return;
+    }
+    p.kchunk = ((p.K + p.split - 1) / p.split + 31) / 32 * 32;
+    if (p.kchunk == 0) p.kchunk = 32;
+    const int bm_t = fam == MGC_GEMM_WSPLIT16 ? 16 : fam == MGC_GEMM_WSPLIT ? 32 : fam == MGC_GEMM_NARROW ? 128 : 64;
+    const int bn_t = fam == MGC_GEMM_WSPLIT16 ? 16 : fam == MGC_GEMM_WSPLIT || fam == MGC_GEMM_NARROW ? 32 : 64;
+    p.tiles_m = (p.M + bm_t - 1) / bm_t;
+    p.tiles_n = (p.N + bn_t - 1) / bn_t;
+    GemmKernel kern = fam == MGC_GEMM_WSPLIT16 ? pick_wsplit16(am, p.kchunk)
+                      : fam == MGC_GEMM_WSPLIT ? pick_wsplit(am)
+                      : fam == MGC_GEMM_NARROW ? pick_dma<128, 32, 4>(am)
+                      : fam == MGC_GEMM_QUARTER ? pick_dma_tail(am)
+                      : fam == MGC_GEMM_TILED ? pick_dma<64, 64, 2>(am)
+                                              : pick_kernel<64, 64, 2>(am, bm);
+    const int threads = fam == MGC_GEMM_WSPLIT16 ? 64 * wsplit16_waves(p.kchunk) : 256;
+    dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)(batch * p.split));
+    if (fam == MGC_GEMM_QUARTER) grid.x = (unsigned)(p.nfull + 4 * (p.tiles_m * p.tiles_n - p.nfull));
     if (ln && p.split < 2) {  // the workspace did not allow the split the reduction needs
         x->launch_error = (int)hipErrorInvalidValue;
         set_error("mgc_hip_gemm_layer_norm: no K split", hipErrorInvalidValue);

@@ -10,6 +10,7 @@
 #include <string.h>
 
 #include <mutex>
+#include <new>
 #include <string>
 #include <vector>
 
@@ -135,6 +136,42 @@ int mgc_hip_device_count(void) {
         return 0;
     }
     return n;
+}
+
+mgc_hip_exec *mgc_hip_exec_create(void *stream) {
+    mgc_hip_exec *x = new (std::nothrow) mgc_hip_exec();
+    if (!x) return nullptr;
+    x->stream = static_cast<hipStream_t>(stream);
+    hipError_t err = hipMalloc((void **)&x->flag, sizeof(int));
+    if (err == hipSuccess) err = hipMemset(x->flag, 0, sizeof(int));
+    if (err != hipSuccess) {
+        mgc::set_error("mgc_hip_exec_create", err);
+        if (x->flag) hipFree(x->flag);
+        delete x;
+        return nullptr;
+    }
+    return x;
+}
+
+int mgc_hip_exec_status(mgc_hip_exec *x) {
+    if (!x) return MGC_ERR_ARGS;
+    const int launch = x->launch_error;
+    x->launch_error = 0;
+    // launchers report operands outside a kernel's limits as hipErrorInvalidValue
+    if (launch) return launch == (int)hipErrorInvalidValue ? MGC_ERR_ARGS : MGC_ERR_HIP;
+    int host = 0;
+    MGC_CHECK(hipMemcpyAsync(&host, x->flag, sizeof(int), hipMemcpyDeviceToHost, x->stream));
+    MGC_CHECK(hipStreamSynchronize(x->stream));
+    if (!host) return MGC_OK;
+    MGC_CHECK(hipMemsetAsync(x->flag, 0, sizeof(int), x->stream));
+    MGC_CHECK(hipStreamSynchronize(x->stream));
+    return MGC_ERR_GATHER_INDEX;
+}
+
+void mgc_hip_exec_destroy(mgc_hip_exec *x) {
+    if (!x) return;
+    if (x->flag) hipFree(x->flag);
+    delete x;
 }
 
 int mgc_hip_model_init(mgc_hip_model *m, const unsigned char *weights_host, unsigned char **A,

@@ -53,6 +53,32 @@ def test_kernel_library_exports_every_declared_symbol():
     assert handle.mgc_hip_device_count() >= 0
 
 
+def test_ctypes_views_match_the_header_layout(tmp_path):
+    """The ctypes structures the GPU tests pass to the C ABI (tests/capi.py) have the size and
+    field offsets a C compiler gives the header's structs."""
+    import ctypes
+
+    import capi
+
+    checks = [("mgc_hip_gemm_args", capi.GemmArgs), ("mgc_hip_operand", capi.Operand)]
+    lines = ["#include <stddef.h>", "#include <stdio.h>", '#include "mgc_hip.h"', "int main(void) {"]
+    for cname, cls in checks:
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for field, _ in cls._fields_:
+            lines.append(f'printf("{cname} {field} %zu\\n", offsetof({cname}, {field}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")
+    got = {tuple(line.split()[:2]): int(line.split()[2]) for line in out if line.strip()}
+    for cname, cls in checks:
+        assert got[(cname, "size")] == ctypes.sizeof(cls), cname
+        for field, _ in cls._fields_:
+            assert got[(cname, field)] == getattr(cls, field).offset, (cname, field)
+
+
 def test_model_library_exports_the_model_abi(hip_cache):
     gen = generate_hip(o3(builders.mlp()), profile=True)
     built = native.build_model_library(gen.source, cache_dir=hip_cache, name="abi")

@@ -18,6 +18,7 @@ import ctypes
 import numpy as np
 import pytest
 
+from capi import MGC_ERR_ARGS, MGC_OK, MGC_OP_STRIDED, GemmArgs, Hip, Operand, bind
 from ml_graph_compiler.codegen import compile_graph
 from ml_graph_compiler.codegen.build import load_kernel_library
 from ml_graph_compiler.ir import Graph, TensorType
@@ -28,70 +29,8 @@ from oracle import interpreter as oracle
 
 pytestmark = pytest.mark.gpu
 
-MGC_OP_STRIDED, MGC_ACT_RELU = 0, 1
-MGC_OK, MGC_ERR_ARGS = 0, 3
+MGC_ACT_RELU = 1
 SCRATCH_FLOATS = 1 << 23
-
-
-class Operand(ctypes.Structure):
-    _fields_ = [("kind", ctypes.c_int), ("p", ctypes.c_void_p), ("rs", ctypes.c_long), ("cs", ctypes.c_long)] + [
-        (n, ctypes.c_int) for n in ("H", "W", "C", "KH", "KW", "SH", "SW", "DH", "DW", "PT", "PL", "OH", "OW", "cg")
-    ]
-
-
-class GemmArgs(ctypes.Structure):
-    """mgc_hip_gemm_args (include/mgc_hip.h)."""
-
-    _fields_ = [
-        ("M", ctypes.c_int), ("N", ctypes.c_int), ("K", ctypes.c_int),
-        ("a", Operand), ("b", Operand),
-        ("c", ctypes.c_void_p), ("ldc", ctypes.c_long),
-        ("alpha", ctypes.c_float), ("beta", ctypes.c_float),
-        ("bias", ctypes.c_void_p), ("bias_mode", ctypes.c_int),
-        ("res", ctypes.c_void_p), ("ldr", ctypes.c_long),
-        ("act", ctypes.c_int), ("lo", ctypes.c_float), ("hi", ctypes.c_float),
-        ("batch_rank", ctypes.c_int), ("batch_dims", ctypes.c_int * 4),
-        ("a_bs", ctypes.c_long * 4), ("b_bs", ctypes.c_long * 4), ("c_bs", ctypes.c_long * 4), ("r_bs", ctypes.c_long * 4),
-        ("workspace", ctypes.c_void_p), ("workspace_floats", ctypes.c_long),
-        ("split_k", ctypes.c_int),
-        ("a2", Operand), ("k1", ctypes.c_int),
-    ]
-
-
-class Hip:
-    """The few HIP runtime calls the test needs for its own operand buffers."""
-
-    def __init__(self) -> None:
-        self.lib = ctypes.CDLL("libamdhip64.so.7", mode=ctypes.RTLD_GLOBAL)  # the runtime libmgc_hip.so links
-        self.lib.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
-        self.lib.hipFree.argtypes = [ctypes.c_void_p]
-        self.lib.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
-        self.buffers: list[ctypes.c_void_p] = []
-
-    def check(self, code: int, what: str) -> None:
-        assert code == 0, f"{what} failed with {code}"
-
-    def upload(self, array: np.ndarray) -> int:
-        array = np.ascontiguousarray(array)
-        ptr = ctypes.c_void_p()
-        self.check(self.lib.hipMalloc(ctypes.byref(ptr), max(array.nbytes, 4)), "hipMalloc")
-        self.buffers.append(ptr)
-        self.check(self.lib.hipMemcpy(ptr, array.ctypes.data, array.nbytes, 1), "hipMemcpy H2D")
-        return ptr.value
-
-    def empty(self, nbytes: int) -> int:
-        return self.upload(np.full(nbytes // 4, np.nan, np.float32))
-
-    def download(self, ptr: int, shape, dtype=np.float32) -> np.ndarray:
-        out = np.empty(shape, dtype)
-        self.check(self.lib.hipDeviceSynchronize(), "hipDeviceSynchronize")
-        self.check(self.lib.hipMemcpy(out.ctypes.data, ctypes.c_void_p(ptr), out.nbytes, 2), "hipMemcpy D2H")
-        return out
-
-    def free(self) -> None:
-        for ptr in self.buffers:
-            self.lib.hipFree(ptr)
-        self.buffers.clear()
 
 
 def _graph(m: int, n: int, k: int, seed: int):
@@ -129,11 +68,7 @@ def _noalloc(lib, hip: Hip, m: int, n: int, k: int, x: np.ndarray, w: np.ndarray
 
 def test_noalloc_gemm_matches_mgc_hip_gemm(hip_cache):
     lib = load_kernel_library()
-    lib.mgc_hip_gemm_noalloc.restype = ctypes.c_int
-    lib.mgc_hip_gemm_noalloc.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
-    lib.mgc_hip_gemm_workspace.restype = ctypes.c_long
-    lib.mgc_hip_gemm_workspace.argtypes = [ctypes.c_int] * 4
-    lib.mgc_hip_last_error.restype = ctypes.c_char_p
+    bind(lib)
     hip = Hip()
     try:
         # two calls in a row, the second smaller; both shapes split K (the scratch holds
