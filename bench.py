@@ -231,7 +231,7 @@ def cpu_baseline(workload: str, gpu_batch: int) -> dict | None:
         log(f"cpu baseline failed: {exc}")
         return None
     units = 1 if workload == "single_gemm" else gpu_batch
-    unit = {"single_gemm": "calls/s", "bert_base": "seq/s"}.get(workload, "img/s")
+    unit = {"single_gemm": "calls/s", "bert_base": "seq/s", "gpt2": "seq/s"}.get(workload, "img/s")
 
     def rate(batch: int, threads: int) -> str:
         r = rows[(batch, threads)]

@@ -62,7 +62,7 @@ EXPR = {"Add": "({0} + {1})", "Sub": "({0} - {1})", "Mul": "({0} * {1})", "Div":
 # workload -> the batches a library is prebuilt for: batch 1 and the GPU batch of each BASELINE
 # config (the single GEMM is one call of 128 rows)
 BASELINES = {"resnet50": (1, 32), "bottleneck": (1, 32), "mobilenet_v2": (1, 32), "bert_base": (1, 16),
-             "single_gemm": (1,)}
+             "gpt2": (1, 8), "single_gemm": (1,)}
 
 
 class CBackendError(Exception):
@@ -249,6 +249,8 @@ class CEmitter:
                 e = f"fminf(fmaxf({a[0]}, {lo}), {hi})"
             elif op == "Gelu":
                 e = f"{'mgc_gelu_tanhf' if attrs.get('approximate') == 'tanh' else 'mgc_gelu_erff'}({a[0]})"
+            elif op == "Where":  # a bool condition leaf (uint8_t), float branches (c.py:419-420)
+                e = f"({a[0]} ? {a[1]} : {a[2]})"
             elif op in EXPR:
                 e = EXPR[op].format(*a)
             else:
@@ -576,6 +578,22 @@ def load_baseline(workload: str, batch: int = 1) -> tuple[CModel, Graph, dict]:
     return CModel(lib, g, blob), g, meta
 
 
+def load_baseline_with_weights(workload: str, batch: int, graph: Graph) -> CModel:
+    """The prebuilt library of ``workload`` at ``batch`` run with the constants of ``graph``: the
+    same builder graph with other constant values (for example calibrated BatchNorm
+    statistics), optimized and scheduled. The C generated for ``graph`` must equal the
+    baseline's (the library depends only on shapes, the weights blob holds every constant), so
+    only the blob differs; raises CBackendError otherwise."""
+    lib = baseline_path(workload, batch)
+    if not lib.exists():
+        raise CBackendError(f"{lib.name} is not built: run __graft_entry__.build() where /root/reference exists")
+    base = CEmitter(_baseline_graph(workload, batch)).generate()
+    em = CEmitter(graph)
+    if em.generate() != base:
+        raise CBackendError("the graph's generated C differs from the prebuilt baseline's")
+    return CModel(lib, graph, em.blob.bytes())
+
+
 def _cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -596,7 +614,7 @@ def time_baseline(workload: str, seconds_budget: float = 20.0, threads: int | No
         model.lib.mgc_set_num_threads(int(threads))
     model.lib.mgc_get_max_threads.restype = ctypes.c_int
     n_threads = int(model.lib.mgc_get_max_threads())
-    feeds = random_feeds(g, 0, int_high=30522 if workload == "bert_base" else 100)
+    feeds = random_feeds(g, 0, int_high=30522 if workload in ("bert_base", "gpt2") else 100)
     model.run(feeds)
     times = []
     t_end = time.perf_counter() + seconds_budget
@@ -606,7 +624,7 @@ def time_baseline(workload: str, seconds_budget: float = 20.0, threads: int | No
         times.append(time.perf_counter() - t0)
     med = float(np.median(times))
     units = 1 if workload == "single_gemm" else meta["batch"]
-    unit = {"single_gemm": "calls/s", "bert_base": "seq/s"}.get(workload, "img/s")
+    unit = {"single_gemm": "calls/s", "bert_base": "seq/s", "gpt2": "seq/s"}.get(workload, "img/s")
     return {
         "value": round(units / med, 3),
         "unit": unit,

@@ -63,7 +63,7 @@ def worker(workload: str, batch: int, threads: int, warmup: int, repeat: int) ->
 
     model, graph, meta = cbackend.load_baseline(workload, batch)
     model.lib.mgc_set_num_threads(int(threads))
-    feeds = random_feeds(graph, 0, int_high=30522 if workload == "bert_base" else 100)
+    feeds = random_feeds(graph, 0, int_high=30522 if workload in ("bert_base", "gpt2") else 100)
     for _ in range(warmup):
         model.run(feeds)
     times = []

@@ -132,3 +132,39 @@ def same_numerics(make, passes: str, rtol: float = 1e-5, atol: float = 1e-5) -> 
         assert got[name].shape == value.shape
         np.testing.assert_allclose(got[name], value, rtol=rtol, atol=atol, err_msg=name)
     return graph
+
+
+def batch_norm_statistics(graph: Graph, feeds: dict[str, np.ndarray]) -> list[tuple[np.ndarray, np.ndarray]]:
+    """Calibrate the running statistics of every BatchNormalization of ``graph`` on ``feeds``:
+    run the oracle node by node and, at each BatchNormalization, replace its mean and variance
+    with the batch mean and (biased) variance of its input over every axis but the channel axis
+    before evaluating it, so its output has the drawn scale and shift per channel and the
+    network's activations stay O(1) at any depth. Returns the (mean, var) pairs in node order;
+    ``graph`` is left calibrated."""
+    env = dict((id(v), a) for v, a in zip(graph.inputs, (oracle.check_feeds(graph, feeds)[v.name] for v in graph.inputs)))
+    stats = []
+
+    def get(v):
+        return None if v is None else (v.data if v.data is not None else env[id(v)])
+
+    for node in graph.nodes:
+        if node.op == "BatchNormalization":
+            x = get(node.input(0)).astype(np.float64)
+            axes = (0,) + tuple(range(2, x.ndim))
+            node.input(3).data = x.mean(axis=axes).astype(np.float32)
+            node.input(4).data = x.var(axis=axes).astype(np.float32)
+            stats.append((node.input(3).data, node.input(4).data))
+        for v, a in zip(node.outputs, oracle.run_node(node, [get(v) for v in node.inputs])):
+            env[id(v)] = a
+    return stats
+
+
+def with_batch_norm_statistics(graph: Graph, stats: list[tuple[np.ndarray, np.ndarray]]) -> Graph:
+    """``graph`` with the BatchNormalization statistics ``stats`` (from batch_norm_statistics on
+    a graph of the same builder and seed, any batch) set in node order."""
+    bns = [n for n in graph.nodes if n.op == "BatchNormalization"]
+    assert len(bns) == len(stats)
+    for node, (mean, var) in zip(bns, stats):
+        assert node.input(3).data.shape == mean.shape
+        node.input(3).data, node.input(4).data = mean, var
+    return graph

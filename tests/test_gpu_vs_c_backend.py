@@ -4,7 +4,8 @@ The C side is the reference's mgc_kernels.c driven by its emitter's lowering (or
 prebuilt per workload and batch into oracle/_ref (the libraries bench.py times as its CPU
 baseline); it runs on the host of the GPU box. Both compile the same O3 graph (same seeded
 weights) at batch 1 and at the GPU batch of each BASELINE config, and every element of the batch
-is compared. Bounds: 1e-4 max-abs for the CNNs, 5e-4 for BERT; for
+is compared. Bounds: 1e-4 max-abs for the CNNs, 5e-4 for BERT and GPT-2 (the north-star
+tolerances for transformers; GPT-2's logits must also agree on the arg-max of every position); for
 ResNet-50, whose random-weight logits reach ~4e4, 2e-6 of max|logit| (both backends sit ~5e-7
 from the float64 oracle there). Logits must have the same arg-max in every row.
 
@@ -30,7 +31,9 @@ CASES = {
     "mobilenet_v2": ("logits", 1e-4, False),
     "resnet50": ("logits", 2e-6, True),   # relative to max|logit|
     "bert_base": ("hidden", 5e-4, False),
+    "gpt2": ("logits", 5e-4, False),
 }
+VOCAB = {"bert_base": 30522, "gpt2": 50257}
 PAIRS = [(wl, b) for wl in sorted(CASES) for b in cbackend.BASELINES[wl]]
 
 
@@ -40,7 +43,7 @@ def test_hip_matches_reference_c_backend(workload, batch, hip_cache):
     cmodel, graph, meta = cbackend.load_baseline(workload, batch)
     assert meta["batch"] == batch
     out, tol, relative = CASES[workload]
-    feeds = oracle.random_feeds(graph, 9, int_high=30522 if workload == "bert_base" else 100)
+    feeds = oracle.random_feeds(graph, 9, int_high=VOCAB.get(workload, 100))
     want = cmodel.run(feeds)[out].astype(np.float64)
     build = builders.single_gemm() if workload == "single_gemm" else builders.CONFIGS[workload](batch=batch)
     model = compile_hip(build, hip_cache)

@@ -194,3 +194,31 @@ def test_oracle_agrees_with_reference_c_kernels(name, tmp_path):
     for k, v in expected.items():
         err = float(np.max(np.abs(got[k].astype(np.float64) - v)))
         assert err <= 1e-4 * max(1.0, float(np.max(np.abs(v)))), (k, err)
+
+
+def test_batch_norm_calibration_renormalizes_resnet50():
+    """The calibration the full-depth parity test uses: after batch_norm_statistics on one
+    image, every BatchNormalization of ResNet-50 maps its calibration input to per-channel mean
+    beta and standard deviation |gamma| (closed form of BN with the batch's own statistics),
+    and the logits of fresh images are O(1) instead of ~4e4."""
+    from helpers import batch_norm_statistics, with_batch_norm_statistics
+
+    g = builders.resnet50(1)
+    feeds = oracle.random_feeds(g, 11)
+    stats = batch_norm_statistics(g, feeds)
+    assert len(stats) == 53
+    env = dict(zip((id(v) for v in g.inputs), (feeds[v.name] for v in g.inputs)))
+    for node in g.nodes:
+        xs = [None if v is None else (v.data if v.data is not None else env[id(v)]) for v in node.inputs]
+        out = oracle.run_node(node, xs)[0]
+        env[id(node.output)] = out
+        if node.op == "BatchNormalization":
+            y = out.astype(np.float64)
+            gamma, beta = xs[1].astype(np.float64), xs[2].astype(np.float64)
+            eps = float(node.attrs.get("epsilon", 1e-5))
+            var = xs[4].astype(np.float64)
+            np.testing.assert_allclose(y.mean(axis=(0, 2, 3)), beta, atol=1e-4)
+            np.testing.assert_allclose(y.std(axis=(0, 2, 3)), np.abs(gamma) * np.sqrt(var / (var + eps)), rtol=1e-3)
+    fresh = with_batch_norm_statistics(builders.resnet50(1), stats)
+    logits = oracle.run_graph(fresh, oracle.random_feeds(fresh, 3))["logits"]
+    assert 0.1 < np.abs(logits).max() < 50.0
