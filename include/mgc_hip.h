@@ -234,6 +234,35 @@ typedef struct {
 
 void mgc_hip_gemm_dw(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const mgc_hip_dw_args *dw);
 
+/* A whole inverted-residual block (the MobileNetV2 pattern with expansion > 1) as one launch:
+ * the projection GEMM of g (C = act(alpha A B + bias + beta R), batch_rank 0, B packed [N][K],
+ * K = Cexp) whose A operand is computed on the fly as
+ *   A[m][k] = act_d(bd[k] + sum_{i,j < 3} E[n][oh SH - PT + i][ow SW - PL + j][k] wd[(3 i + j) Cexp + k])
+ *   E[n][y][z][k] = act_e(be[k] + sum_c x[n][y][z][c] we[k Cin + c])  (zero outside the image)
+ * for output pixel m = (n OH + oh) OW + ow of the NHWC batch x [n][H][W][Cin]: the expanded
+ * tensor and the depthwise output never go to memory; g->a is not read. Replaces mgc_gemm,
+ * mgc_depthwise_nhwc and mgc_gemm of the block's three convolutions
+ * (src/ml_graph_compiler/codegen/runtime/mgc_kernels.c:370-396, 455-473, which the reference's
+ * C backend emits as three calls, codegen/c.py:1102-1226). Needs the shapes
+ * mgc_hip_mbconv_supported accepts (Cin 16, 24 or 32; Cexp % 4 == 0 and Cexp <= 256; N <= 32;
+ * SH = SW in {1, 2}), act_e and act_d relu or clip, 16-byte aligned x, we, be, wd, bd and B, B's
+ * column stride a multiple of 4,
+ * bias_mode 1 (or no bias), M a whole number of OH x OW images and x below 2 GiB; sets the
+ * launch error otherwise. */
+typedef struct {
+    const float *x;     /* block input NHWC [N][H][W][Cin] */
+    const float *we;    /* expansion weights packed [Cexp][Cin] */
+    const float *be;    /* expansion bias [Cexp] or NULL */
+    const float *wd;    /* depthwise weights [3][3][Cexp], channel fastest */
+    const float *bd;    /* depthwise bias [Cexp] or NULL */
+    int H, W, Cin, Cexp, SH, SW, PT, PL, OH, OW;
+    int act_e, act_d;   /* MGC_ACT_* after the expansion and after the depthwise convolution */
+    float lo_e, hi_e, lo_d, hi_d;
+} mgc_hip_mbconv_args;
+
+int mgc_hip_mbconv_supported(int Cin, int Cexp, int Cout, int stride);
+void mgc_hip_mbconv(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const mgc_hip_mbconv_args *mb);
+
 /* ---------------------------------------------------------------------------------------- */
 /* memory-bound kernels                                                                      */
 /* ---------------------------------------------------------------------------------------- */

@@ -1967,6 +1967,305 @@ __global__ void __launch_bounds__(256) gemm_dw_kernel(const GemmDev p, const DwD
     }
 }
 
+// A whole inverted-residual block (MobileNetV2 with expansion t > 1) as one launch
+// (mgc_hip_mbconv): the 1 x 1 expansion of the block input x, its activation, the 3 x 3
+// depthwise convolution and its activation are evaluated while the projection GEMM's A operand
+// is formed, so neither the expanded tensor (t times the input's channels) nor the depthwise
+// output ever goes to memory; the projection's bias, residual and activation are the GEMM's
+// epilogue. The reference's C backend runs the three convolutions as three calls with both
+// intermediates in its arena (mgc_gemm, mgc_depthwise_nhwc, mgc_gemm: codegen/c.py:1102-1226,
+// mgc_kernels.c:370-396, 455-473).
+struct MbDev {
+    const float *x;   // block input NHWC [n][H][W][Cin]
+    const float *we;  // expansion weights packed [Cexp][Cin]
+    const float *be;  // expansion bias [Cexp] or null
+    const float *wd;  // depthwise weights [9][Cexp]
+    const float *bd;  // depthwise bias [Cexp] or null
+    int H, W, Cexp, PT, PL, OH, OW;
+    float lo_e, hi_e, lo_d, hi_d;  // both activations as clamps: relu [0, inf), clip [lo, hi]
+    int tiles_h, tiles_w;  // 8 x 8 output-pixel tiles per image
+    long x_bytes;          // bytes of x reachable from d.x
+};
+
+constexpr int kMbMaxCexp = 256;
+
+// One workgroup (256 threads, four waves) computes an 8 x 8 block of output pixels of one image
+// times all N <= 32 projection channels; K runs over the Cexp expanded channels in stages of 32.
+//  * The input patch the block's depthwise windows cover ((7 S + 3)^2 pixels x Cin channels) is
+//    read once per tile straight into registers as the expansion's B operand: patch pixel block
+//    rb (32 pixels) belongs to wave rb % 4, lane (li, h) holding pixel 32 rb + li, input channels
+//    h Cin / 2 .. (h + 1) Cin / 2 (the k order the 32 x 32 x 2 MFMA sums over is permuted the
+//    same way on both operands).
+//  * Per stage each wave multiplies the stage's 32 expansion-weight rows (A) by its pixel blocks
+//    (Cin / 2 MFMAs per block), so lane (li, h) ends with pixel li's channels 8 a + 4 h .. + 3
+//    (a < 4) of the stage: four quads it biases, clamps (relu or clip as one clamp: fmaxf maps
+//    NaN to the lower bound as relu's v > 0 ? v : 0 does), zeroes when the pixel lies outside the
+//    image (the depthwise convolution pads the expanded tensor with zeros) and writes to LDS as
+//    16-byte stores ([pixel][32] floats, quads XOR-permuted by the pixel so the depthwise reads
+//    of eight neighbouring pixels hit different banks). Stride 1 double-buffers the patch (one
+//    barrier per stage), stride 2 does not (two barriers; 37 KB per patch).
+//  * Lane (li, h) of wave (wm, kh) then computes the depthwise outputs of tile pixel 32 wm + li
+//    for the eight stage channels 16 kh + 8 h .. + 7 (nine taps of two 16-byte LDS reads, the
+//    depthwise weights and bias of every stage held in LDS for the whole tile) and feeds them
+//    straight into the projection MFMAs as their A operand: those are exactly the eight k the
+//    lane supplies for rows 32 wm .. 32 wm + 31, with the projection weights B[li][k] in
+//    registers (loaded a stage ahead). Biases and depthwise weights sit in LDS for the tile. Waves kh = 0 and 1 sum the two k halves through LDS at
+//    the end; the epilogue is the GEMM's.
+template <int S, int KH2>
+__global__ void __launch_bounds__(256) mbconv_kernel(const GemmDev p, const MbDev d) {
+    constexpr int CIN = 2 * KH2;
+    constexpr int Q = KH2 / 4;                         // 16-byte quads per lane and row block
+    constexpr int PW = 7 * S + 3;                      // patch rows and columns
+    constexpr int P = PW * PW;                         // patch pixels
+    constexpr int RB = (P + 31) / 32;                  // 32-pixel row blocks of the patch
+    constexpr int RBW = (RB + 3) / 4;                  // row blocks per wave (at most)
+    constexpr int EBUF = S == 1 ? 2 : 1;
+    constexpr int EFLOATS = P * 32;
+    constexpr int LDC = 40;
+    constexpr int SMEM_LOOP = EBUF * EFLOATS;
+    constexpr int SMEM_EPI = 64 * LDC + 2 * 1024;
+    constexpr int SMEM_E = SMEM_LOOP > SMEM_EPI ? SMEM_LOOP : SMEM_EPI;
+    constexpr int WDF = 11 * kMbMaxCexp;               // depthwise weights [9][256], their bias, expansion bias
+    static_assert(S == 1 || S == 2, "stride");
+    static_assert(KH2 % 4 == 0, "Cin a multiple of 8");
+    __shared__ __attribute__((aligned(16))) float smem[SMEM_E + WDF];
+    float *const Wd = smem + SMEM_E;
+    // pixel-dependent quad permutation: distinct over 8 consecutive pixels and over 8 pixels at
+    // stride 2
+    auto fsw = [](int r) __attribute__((always_inline)) { return ((r >> 1) ^ r) & 7; };
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, li = lane & 31, lh = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave & 1, kh = wave >> 1;
+
+    // tile order: XCD-aware (consecutive tiles of an image share input rows in one L2)
+    const int nb = gridDim.x;
+    const int full = nb & ~7;
+    int lin = blockIdx.x;
+    if (lin < full) {
+        const int per = full >> 3;
+        lin = (lin & 7) * per + (lin >> 3);
+    }
+    const int per_img = d.tiles_h * d.tiles_w;
+    const int img = lin / per_img;
+    const int tr = lin - img * per_img;
+    const int th = tr / d.tiles_w;
+    const int oh0 = th * 8, ow0 = (tr - th * d.tiles_w) * 8;
+    const int ih0 = oh0 * S - d.PT, iw0 = ow0 * S - d.PL;
+    const int H = d.H, W = d.W, Cexp = d.Cexp, N = p.N;
+    const int nk = (Cexp + 31) / 32;
+    constexpr unsigned OOB = 0x80000000u;
+
+    // the expansion's B operand for this wave's patch pixel blocks, and which of the lane's
+    // pixels lie inside the image
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void *)d.x, (short)0, (int)d.x_bytes, 0x00020000);
+    f4 xa[RBW][Q];
+    unsigned inside = 0;  // bit j: the lane's pixel of row block j is a patch pixel inside the image
+#pragma unroll
+    for (int j = 0; j < RBW; ++j) {
+        const int rb = wave + 4 * j;
+        const int pa = rb * 32 + li;
+        const int pr = pa / PW, pc = pa - (pa / PW) * PW;
+        const int ih = ih0 + pr, iw = iw0 + pc;
+        const bool ok = rb < RB && pa < P && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
+        const unsigned base = ((((unsigned)img * (unsigned)H + (unsigned)ih) * (unsigned)W + (unsigned)iw) * CIN +
+                               (unsigned)(lh * KH2)) * 4u;
+#pragma unroll
+        for (int q = 0; q < Q; ++q)
+            xa[j][q] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? base + 16u * q : OOB, 0, 0));
+        inside |= (ok ? 1u : 0u) << j;
+    }
+
+    // per-stage operands: expansion weight column kt 32 + li (the lane's k half) and its bias;
+    // projection weights B[li][kt 32 + 16 kh + 8 lh .. + 7]
+    const __amdgpu_buffer_rsrc_t rwe = __builtin_amdgcn_make_buffer_rsrc((void *)d.we, (short)0, Cexp * CIN * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rpb = __builtin_amdgcn_make_buffer_rsrc((void *)p.b.p, (short)0, (int)p.b_bytes, 0x00020000);
+    auto load_we = [&](int kt, f4 (&w)[Q]) __attribute__((always_inline)) {
+        const int c = kt * 32 + li;
+        const bool ok = c < Cexp;
+#pragma unroll
+        for (int q = 0; q < Q; ++q)
+            w[q] = __builtin_bit_cast(
+                f4, __builtin_amdgcn_raw_buffer_load_b128(rwe, ok ? ((unsigned)c * CIN + lh * KH2 + 4 * q) * 4u : OOB, 0, 0));
+    };
+    auto load_pb = [&](int kt, f4 (&b)[2]) __attribute__((always_inline)) {
+        const int k0 = kt * 32 + kh * 16 + lh * 8;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int k = k0 + 4 * h;
+            const bool ok = li < N && k < p.K;
+            b[h] = __builtin_bit_cast(
+                f4, __builtin_amdgcn_raw_buffer_load_b128(rpb, ok ? ((unsigned)li * (unsigned)p.b.cs + k) * 4u : OOB, 0, 0));
+        }
+    };
+
+    f4 we[Q], pb[2];
+    load_we(0, we);
+    load_pb(0, pb);
+    // depthwise weights, depthwise bias and expansion bias of every channel into LDS (zeros
+    // past Cexp)
+    for (int e = tid; e < WDF / 4; e += 256) {
+        const int t = e / (kMbMaxCexp / 4), c = (e - t * (kMbMaxCexp / 4)) * 4;
+        f4 v = {0.f, 0.f, 0.f, 0.f};
+        if (c < Cexp) {
+            if (t < 9)
+                v = ldg4(d.wd + t * Cexp + c);
+            else if (t == 9 && d.bd)
+                v = ldg4(d.bd + c);
+            else if (t == 10 && d.be)
+                v = ldg4(d.be + c);
+        }
+        *reinterpret_cast<f4 *>(&Wd[t * kMbMaxCexp + c]) = v;
+    }
+    // patch pixels outside the image (or past the patch) are zero in every stage: written once
+    // into each patch buffer here, never by the stage loop
+#pragma unroll
+    for (int j = 0; j < RBW; ++j) {
+        const int pix = (wave + 4 * j) * 32 + li;
+        if (wave + 4 * j < RB && pix < P && !((inside >> j) & 1u)) {
+#pragma unroll
+            for (int b = 0; b < EBUF; ++b)
+#pragma unroll
+                for (int a = 0; a < 4; ++a)
+                    *reinterpret_cast<f4 *>(&smem[b * EFLOATS + pix * 32 + 16 * lh + 4 * a]) = f4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    barrier_lds();  // the biases and depthwise weights are in LDS before the first expansion reads them
+    floatx16 pacc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) pacc[r] = 0.0f;
+    const int px = wm * 32 + li;                 // this lane's tile pixel for the depthwise pass
+    const int ppr = px >> 3, ppc = px & 7;
+    const int ch = kh * 16 + lh * 8;             // its eight channels within a stage
+    const float lo_e = d.lo_e, hi_e = d.hi_e, lo_d = d.lo_d, hi_d = d.hi_d;
+
+    for (int kt = 0; kt < nk; ++kt) {
+        float *const E = smem + (EBUF == 2 ? (kt & 1) * EFLOATS : 0);
+        if (EBUF == 1 && kt > 0) barrier_lds();  // every wave's depthwise reads of E are done
+        // expansion of this wave's patch row blocks into E
+#pragma unroll
+        for (int j = 0; j < RBW; ++j) {
+            const int rb = wave + 4 * j;
+            if (rb < RB) {
+                // the accumulators start from the bias of the lane's channels 8 a + 4 lh + e
+                floatx16 acc;
+#pragma unroll
+                for (int a = 0; a < 4; ++a) {
+                    const f4 bq = *reinterpret_cast<const f4 *>(&Wd[10 * kMbMaxCexp + kt * 32 + 8 * a + 4 * lh]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[4 * a + e] = bq[e];
+                }
+#pragma unroll
+                for (int i = 0; i < KH2; ++i)
+                    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(we[i >> 2][i & 3], xa[j][i >> 2][i & 3], acc, 0, 0, 0);
+                const int pix = rb * 32 + li;
+                if ((inside >> j) & 1u) {  // in the image (so also in the patch)
+                    const int sw = fsw(pix);
+#pragma unroll
+                    for (int a = 0; a < 4; ++a) {
+                        f4 v;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v[e] = fminf(fmaxf(acc[4 * a + e], lo_e), hi_e);
+                        *reinterpret_cast<f4 *>(&E[pix * 32 + (((2 * a + lh) ^ sw) << 2)]) = v;
+                    }
+                }
+            }
+        }
+        if (kt + 1 < nk) load_we(kt + 1, we);
+        barrier_lds();  // E complete
+        // depthwise outputs of pixel px, channels kt 32 + ch .. + 7: the projection's A operand
+        const int cg = kt * 32 + ch;
+        f4 a0 = *reinterpret_cast<const f4 *>(&Wd[9 * kMbMaxCexp + cg]);
+        f4 a1 = *reinterpret_cast<const f4 *>(&Wd[9 * kMbMaxCexp + cg + 4]);
+#pragma unroll 1
+        for (int i = 0; i < 3; ++i)
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+                const int prow = (ppr * S + i) * PW + ppc * S + j;
+                const int sw = fsw(prow);
+                const f4 e0 = *reinterpret_cast<const f4 *>(&E[prow * 32 + (((ch >> 2) ^ sw) << 2)]);
+                const f4 e1 = *reinterpret_cast<const f4 *>(&E[prow * 32 + ((((ch >> 2) + 1) ^ sw) << 2)]);
+                const f4 w0 = *reinterpret_cast<const f4 *>(&Wd[(i * 3 + j) * kMbMaxCexp + cg]);
+                const f4 w1 = *reinterpret_cast<const f4 *>(&Wd[(i * 3 + j) * kMbMaxCexp + cg + 4]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    a0[e] = fmaf(e0[e], w0[e], a0[e]);
+                    a1[e] = fmaf(e1[e], w1[e], a1[e]);
+                }
+            }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            a0[e] = fminf(fmaxf(a0[e], lo_d), hi_d);
+            a1[e] = fminf(fmaxf(a1[e], lo_d), hi_d);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pacc = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[e], pb[0][e], pacc, 0, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pacc = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[e], pb[1][e], pacc, 0, 0, 0);
+        if (kt + 1 < nk) load_pb(kt + 1, pb);
+    }
+    __syncthreads();
+
+    // the two k halves -> LDS tile [64][LDC] (register r of lane (li, lh): row 8 (r / 4) + 4 lh
+    // + r % 4 of the wave's 32-row block, column li)
+    float *const Cs = smem;
+    float *const part = smem + 64 * LDC;
+    if (kh == 1) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) part[wm * 1024 + r * 64 + lane] = pacc[r];
+    }
+    __syncthreads();
+    if (kh == 0) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            Cs[(wm * 32 + (r >> 2) * 8 + lh * 4 + (r & 3)) * LDC + li] = pacc[r] + part[wm * 1024 + r * 64 + lane];
+    }
+    __syncthreads();
+
+    // LDS tile -> epilogue -> memory: thread t owns 16-byte column chunk t % 8 and tile rows
+    // t / 8 and t / 8 + 32
+    const float alpha = p.alpha, beta = p.beta, lo = p.lo, hi = p.hi;
+    const int act = p.act, OH = d.OH, OW = d.OW;
+    const int cl = (tid & 7) * 4;
+    const int r0 = tid >> 3;
+    if (cl >= N) return;
+    const int ncol = min(4, N - cl);
+    const bool full4 = p.vec_out && ncol == 4;
+    f4 cbias = {0.f, 0.f, 0.f, 0.f};
+    if (p.bias) {
+        if (full4) {
+            cbias = ldg4(p.bias + cl);
+        } else {
+            for (int e = 0; e < ncol; ++e) cbias[e] = ldg(p.bias + cl + e);
+        }
+    }
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+        const int rl = r0 + 32 * it;
+        const int oh = oh0 + (rl >> 3), ow = ow0 + (rl & 7);
+        if (oh >= OH || ow >= OW) continue;
+        const long m = ((long)img * OH + oh) * OW + ow;
+        f4 v = *reinterpret_cast<const f4 *>(&Cs[rl * LDC + cl]);
+        v = v * alpha + cbias;
+        if (p.res) {
+            const float *src = p.res + m * p.ldr + cl;
+            if (full4) {
+                v += beta * ldg4(src);
+            } else {
+                for (int e = 0; e < ncol; ++e) v[e] += beta * ldg(src + e);
+            }
+        }
+        v = act4(v, act, lo, hi);
+        float *dst = p.c + m * p.ldc + cl;
+        if (full4) {
+            *reinterpret_cast<f4 *>(dst) = v;
+        } else {
+            for (int e = 0; e < ncol; ++e) dst[e] = v[e];
+        }
+    }
+}
+
 // Sum the split-K partials and apply the epilogue (one batch element).
 __global__ void gemm_splitk_reduce(const GemmDev p) {
     const long total = (long)p.M * p.N;
@@ -2552,6 +2851,80 @@ extern "C" void mgc_hip_gemm_dw(mgc_hip_exec *x, const mgc_hip_gemm_args *g, con
     const DwKernel kern = bn == 32 ? (s2 ? &gemm_dw_kernel<32, 2, 1> : &gemm_dw_kernel<32, 1, 2>)
                                    : (s2 ? &gemm_dw_kernel<64, 2, 1> : &gemm_dw_kernel<64, 1, 2>);
     MGC_LAUNCH(x, kern, dim3((unsigned)(p.tiles_m * p.tiles_n)), dim3(256), 0, p, d);
+}
+
+extern "C" int mgc_hip_mbconv_supported(int Cin, int Cexp, int Cout, int stride) {
+    return (Cin == 16 || Cin == 24 || Cin == 32) && Cexp > 0 && Cexp % 4 == 0 && Cexp <= kMbMaxCexp && Cout >= 1 &&
+           Cout <= 32 && (stride == 1 || stride == 2);
+}
+
+extern "C" void mgc_hip_mbconv(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const mgc_hip_mbconv_args *mb) {
+    if (g->M <= 0 || g->N <= 0) return;
+    const long ohw = (long)mb->OH * mb->OW;
+    const long n_img = ohw > 0 ? g->M / ohw : 0;
+    const long x_bytes = n_img * mb->H * mb->W * (long)mb->Cin * 4;
+    const long b_bytes = ((long)(g->N - 1) * g->b.cs + g->K) * 4;
+    const bool acts = (mb->act_e == MGC_ACT_RELU || mb->act_e == MGC_ACT_CLIP) &&
+                      (mb->act_d == MGC_ACT_RELU || mb->act_d == MGC_ACT_CLIP);
+    const bool ok = mgc_hip_mbconv_supported(mb->Cin, mb->Cexp, g->N, mb->SH) && mb->SH == mb->SW && acts &&
+                    g->batch_rank == 0 && g->k1 == 0 && g->K == mb->Cexp && mb->H > 0 && mb->W > 0 && ohw > 0 &&
+                    g->M % ohw == 0 && x_bytes < 0x7fffffffL && b_bytes < 0x7fffffffL &&
+                    (!g->bias || g->bias_mode == 1) && g->b.kind == MGC_OP_STRIDED && g->b.rs == 1 &&
+                    g->b.cs >= g->K && g->b.cs % 4 == 0 && aligned16(g->b.p) && aligned16(mb->x) &&
+                    aligned16(mb->we) && aligned16(mb->be) && aligned16(mb->wd) && aligned16(mb->bd);
+    if (!ok) {
+        x->launch_error = (int)hipErrorInvalidValue;
+        set_error("mgc_hip_mbconv: shape, layout or alignment outside its limits", hipErrorInvalidValue);
+        return;
+    }
+    GemmDev p{};
+    p.M = g->M;
+    p.N = g->N;
+    p.K = g->K;
+    p.b = g->b;
+    p.c = g->c;
+    p.ldc = g->ldc;
+    p.alpha = g->alpha;
+    p.beta = g->beta;
+    p.bias = g->bias;
+    p.bias_mode = g->bias ? 1 : 0;
+    p.res = g->res;
+    p.ldr = g->ldr;
+    p.act = g->act;
+    p.lo = g->lo;
+    p.hi = g->hi;
+    p.split = 1;
+    p.nbatch = 1;
+    p.b_bytes = b_bytes;
+    p.vec_out = p.ldc % 4 == 0 && aligned16(p.c) && (!p.res || (p.ldr % 4 == 0 && aligned16(p.res))) &&
+                aligned16(p.bias);
+    MbDev d;
+    d.x = mb->x;
+    d.we = mb->we;
+    d.be = mb->be;
+    d.wd = mb->wd;
+    d.bd = mb->bd;
+    d.H = mb->H;
+    d.W = mb->W;
+    d.Cexp = mb->Cexp;
+    d.PT = mb->PT;
+    d.PL = mb->PL;
+    d.OH = mb->OH;
+    d.OW = mb->OW;
+    d.lo_e = mb->act_e == MGC_ACT_CLIP ? mb->lo_e : 0.0f;
+    d.hi_e = mb->act_e == MGC_ACT_CLIP ? mb->hi_e : INFINITY;
+    d.lo_d = mb->act_d == MGC_ACT_CLIP ? mb->lo_d : 0.0f;
+    d.hi_d = mb->act_d == MGC_ACT_CLIP ? mb->hi_d : INFINITY;
+    d.tiles_h = (mb->OH + 7) / 8;
+    d.tiles_w = (mb->OW + 7) / 8;
+    d.x_bytes = x_bytes;
+    const long tiles = n_img * d.tiles_h * d.tiles_w;
+    typedef void (*MbKernel)(const GemmDev, const MbDev);
+    const bool s2 = mb->SH == 2;
+    const MbKernel kern = mb->Cin == 16   ? (s2 ? &mbconv_kernel<2, 8> : &mbconv_kernel<1, 8>)
+                          : mb->Cin == 24 ? (s2 ? &mbconv_kernel<2, 12> : &mbconv_kernel<1, 12>)
+                                          : (s2 ? &mbconv_kernel<2, 16> : &mbconv_kernel<1, 16>);
+    MGC_LAUNCH(x, kern, dim3((unsigned)tiles), dim3(256), 0, p, d);
 }
 
 static void gemm_launch(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const LnTail *ln) {

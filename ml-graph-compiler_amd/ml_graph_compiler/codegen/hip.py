@@ -110,6 +110,16 @@ FUSE_PROJECTION_SHORTCUT = True
 FUSE_DEPTHWISE_POINTWISE = True
 DEPTHWISE_FUSE_MIN_ROWS = 16384
 DEPTHWISE_FUSE_SHALLOW_K = 96
+# Run a whole inverted-residual block (1 x 1 expansion with relu / clip -> 3 x 3 depthwise with
+# relu / clip -> 1 x 1 projection, MobileNetV2's t > 1 blocks) as one mgc_hip_mbconv launch,
+# for blocks of at least MBCONV_MIN_ROWS output pixels (the kernel's 8 x 8-pixel tiles then
+# number at least 256, one per CU); tests turn it off to compare.
+FUSE_INVERTED_RESIDUAL = True
+MBCONV_MIN_ROWS = 16384
+# mgc_hip_mbconv_supported: input channels, expanded channels, output channels
+MBCONV_CIN = (16, 24, 32)
+MBCONV_MAX_CEXP = 256
+MBCONV_MAX_COUT = 32
 # The fused GEMMs address their image and weight operands through buffer resources with 32-bit
 # byte offsets, and their launchers refuse operands of this many bytes or more (the unfused
 # kernels have a generic path for them): both fusions are only taken below it.
@@ -319,6 +329,51 @@ def find_depthwise_pointwise(graph: Graph, min_rows: int | None = None) -> dict[
     return found
 
 
+def find_inverted_residuals(graph: Graph, min_rows: int | None = None) -> dict[int, tuple[Node, Node]]:
+    """id(pw) -> (ex, dw) for every inverted-residual block that mgc_hip_mbconv can run as one
+    launch: ex a pointwise NHWC FusedConv (stride 1, relu or clip, no residual) whose output only
+    dw reads, dw a 3 x 3 depthwise FusedConv (stride 1 or 2, relu or clip) whose output only pw
+    reads, pw a stride-1 pointwise NHWC convolution (any bias, residual and activation), with
+    the kernel's channel limits (input 16, 24 or 32 channels, at most MBCONV_MAX_CEXP expanded
+    and MBCONV_MAX_COUT output channels), at least ``min_rows`` output pixels (default
+    MBCONV_MIN_ROWS) and the block input below FUSED_OPERAND_LIMIT bytes."""
+    if min_rows is None:
+        min_rows = MBCONV_MIN_ROWS
+    outputs = {id(v) for v in graph.outputs}
+
+    def clamp_act(node: Node) -> bool:
+        return node.op == "FusedConv" and node.attrs.get("activation", "none") in ("relu", "clip")
+
+    found: dict[int, tuple[Node, Node]] = {}
+    for pw in graph.nodes:
+        if not _pointwise_nhwc(pw):
+            continue
+        d = pw.input(0)
+        dw = d.producer
+        if dw is None or not _depthwise3x3_nhwc(dw) or not clamp_act(dw) or id(d) in outputs or d.users != [pw]:
+            continue
+        if sum(v is d for v in pw.inputs) != 1:
+            continue
+        e = dw.input(0)
+        ex = e.producer
+        if ex is None or not _pointwise_nhwc(ex) or not clamp_act(ex) or ex.optional_input(3) is not None:
+            continue
+        if id(e) in outputs or e.users != [dw] or ex.input(0).data is not None:
+            continue
+        xt, et, dt = ex.input(0).tensor_type, e.tensor_type, d.tensor_type
+        if ops.window_geometry(ex, xt.shape[1:3], (1, 1)).strides != (1, 1):
+            continue
+        if ops.window_geometry(pw, dt.shape[1:3], (1, 1)).strides != (1, 1):
+            continue
+        cin, cexp, cout = xt.shape[3], et.shape[3], pw.input(1).tensor_type.shape[3]
+        if cin not in MBCONV_CIN or cexp % 4 or cexp > MBCONV_MAX_CEXP or cout > MBCONV_MAX_COUT:
+            continue
+        if dt.shape[0] * dt.shape[1] * dt.shape[2] < min_rows or _tensor_bytes(ex.input(0)) >= FUSED_OPERAND_LIMIT:
+            continue
+        found[id(pw)] = (ex, dw)
+    return found
+
+
 def pack_b_nk(b: np.ndarray) -> np.ndarray:
     """A constant K x N right-hand side stored as its transpose [N][K] (k contiguous), the
     layout the MFMA GEMM reads with 16-byte k-quad loads."""
@@ -377,8 +432,16 @@ class HipEmitter:
         self._shortcut_skip = {id(ds) for ds in self._shortcut.values()}
         # id(pointwise conv) -> the depthwise convolution computed in its GEMM; the depthwise
         # input is then read at the pointwise step, which the plan must keep it alive for.
+        # id(projection conv) -> (expansion, depthwise) of an inverted-residual block run as one
+        # launch; the block input is then read at the projection's step.
+        self._mb: dict[int, tuple[Node, Node]] = find_inverted_residuals(graph) if FUSE_INVERTED_RESIDUAL else {}
+        taken = set(self._shortcut) | self._shortcut_skip
+        for pw_id in [i for i, (ex, dw) in self._mb.items() if {i, id(ex), id(dw)} & taken]:
+            del self._mb[pw_id]
+        self._mb_skip = {id(n) for pair in self._mb.values() for n in pair}
         self._dwpw: dict[int, Node] = find_depthwise_pointwise(graph) if FUSE_DEPTHWISE_POINTWISE else {}
-        for pw_id in [i for i, dw in self._dwpw.items() if id(dw) in self._shortcut or i in self._shortcut]:
+        taken |= set(self._mb) | self._mb_skip
+        for pw_id in [i for i, dw in self._dwpw.items() if id(dw) in taken or i in taken]:
             del self._dwpw[pw_id]
         self._dwpw_skip = {id(dw) for dw in self._dwpw.values()}
         order = {id(n): i for i, n in enumerate(graph.nodes)}
@@ -387,6 +450,9 @@ class HipEmitter:
         for pw in graph.nodes:
             if (dw := self._dwpw.get(id(pw))) is not None:
                 keep[id(dw.input(0))] = max(keep.get(id(dw.input(0)), 0), order[id(pw)])
+            if (pair := self._mb.get(id(pw))) is not None:
+                xin = pair[0].input(0)
+                keep[id(xin)] = max(keep.get(id(xin), 0), order[id(pw)])
         self.plan = plan_memory(graph, strategy=strategy, alignment=ALIGN, inplace=inplace,
                                 workspace=self._workspace_bytes, extra_reads=keep)
         self.weights = WeightsBuilder()
@@ -415,7 +481,7 @@ class HipEmitter:
                 if m.qkv_gemms:
                     qkv_bytes = max(qkv_bytes, 3 * m.out.tensor_type.nbytes)
         excluded = (set(self._attn_skip) | set(self._attn_emit) | set(self._shortcut) | self._shortcut_skip
-                    | set(self._dwpw) | self._dwpw_skip)
+                    | set(self._dwpw) | self._dwpw_skip | set(self._mb) | self._mb_skip)
         self._folds = plan_folds(graph, self.plan, self._workspace_bytes, excluded) if FOLD_TRANSPOSES else FoldPlan()
         self._scratch_qkv_off = self._scratch_off
         self._scratch_out_off = self._scratch_off + (qkv_bytes + ALIGN - 1) // ALIGN * ALIGN
@@ -600,6 +666,10 @@ class HipEmitter:
             return
         if id(node) in self._dwpw_skip:
             self.emit("/* depthwise convolution: computed in the GEMM of the pointwise convolution that reads it */")
+            self.count("folded")
+            return
+        if id(node) in self._mb_skip:
+            self.emit("/* inverted-residual block: computed in the launch of its projection convolution */")
             self.count("folded")
             return
         if id(node) in self._ln_skip:
@@ -1009,9 +1079,10 @@ class HipEmitter:
                    beta: float = 1.0, act: str = "none", lo: float = 0.0, hi: float = 6.0,
                    workspace: str = "NULL", workspace_floats: int = 0,
                    layer_norm: tuple[str, str, str, str] | None = None, extra: Sequence[str] = (),
-                   depthwise: str | None = None) -> None:
+                   depthwise: str | None = None, mbconv: str | None = None) -> None:
         """One mgc_hip_gemm call; ``layer_norm`` = (scale, bias, eps, out) makes it an
-        mgc_hip_gemm_layer_norm call whose split-K reduction also normalizes the rows; ``extra``
+        mgc_hip_gemm_layer_norm call whose split-K reduction also normalizes the rows; ``mbconv``
+        declares and fills an mgc_hip_mbconv_args ``mb`` and makes it an mgc_hip_mbconv call; ``extra``
         are further field assignments (the concatenated-K operand); ``depthwise`` declares and
         fills an mgc_hip_dw_args ``d`` and makes it an mgc_hip_gemm_dw call."""
         if len(batch) > MAX_BATCH_RANK:
@@ -1032,6 +1103,8 @@ class HipEmitter:
             parts.append(f"mgc_hip_gemm_layer_norm(x, &g, {scale}, {lbias}, {eps}, {out});")
         elif depthwise is not None:
             parts += [depthwise, "mgc_hip_gemm_dw(x, &g, &d);"]
+        elif mbconv is not None:
+            parts += [mbconv, "mgc_hip_mbconv(x, &g, &mb);"]
         else:
             parts.append("mgc_hip_gemm(x, &g);")
         self.emit("{ " + " ".join(parts) + " }")
@@ -1291,6 +1364,9 @@ class HipEmitter:
         if id(node) in self._dwpw:
             self._conv_with_depthwise(node, self._dwpw[id(node)])
             return
+        if id(node) in self._mb:
+            self._inverted_residual(node, *self._mb[id(node)])
+            return
         kg = kout // group
         geo = (f"g.{{f}}.H = {h}; g.{{f}}.W = {wd}; g.{{f}}.C = {c}; g.{{f}}.KH = {kh}; g.{{f}}.KW = {kw}; "
                f"g.{{f}}.SH = {g.strides[0]}; g.{{f}}.SW = {g.strides[1]}; g.{{f}}.DH = {g.dilations[0]}; "
@@ -1410,6 +1486,59 @@ class HipEmitter:
                 self.op_FusedConv(node)
             finally:
                 self._dwpw[id(node)] = saved
+            self.emit("}")
+
+    def _inverted_residual(self, node: Node, ex: Node, dw: Node) -> None:
+        """pw(act_d(dw(act_e(ex(x))))) as one mgc_hip_mbconv launch: the projection GEMM whose
+        A operand is the depthwise output of the expansion of x, both evaluated per tile; neither
+        intermediate is written. When x is a caller buffer (a graph input or output) the
+        generated code checks its 16-byte alignment and otherwise runs the three convolutions
+        apart."""
+        xv = ex.input(0)
+        nb, h, wd, cin = xv.tensor_type.shape
+        cexp = ex.input(1).tensor_type.shape[3]
+        g = ops.window_geometry(dw, (h, wd), (3, 3))
+        oh, ow = g.out_hw
+        we = self._packed_b(ex.input(1).data.reshape(cin, cexp), ("conv", id(ex.input(1)), 0))[0]
+        we_ptr = we.split("g.b.p = ")[1].split(";")[0]
+        ebias_v = ex.optional_input(2)
+        ebias = self._vector_ptr(ebias_v, cexp, "Conv bias") if ebias_v is not None else "NULL"
+        wdw = np.ascontiguousarray(dw.input(1).data.reshape(9, cexp), np.float32)
+        dwoff = self.weights.add(wdw, key=("dw", id(dw.input(1))))
+        dbias_v = dw.optional_input(2)
+        dbias = self._vector_ptr(dbias_v, cexp, "Conv bias") if dbias_v is not None else "NULL"
+        eact, elo, ehi = self._act(ex)
+        dact, dlo, dhi = self._act(dw)
+        n = node.input(1).tensor_type.shape[3]
+        bspec = self._packed_b(node.input(1).data.reshape(cexp, n), ("conv", id(node.input(1)), 0))
+        bias_v, res_v = node.optional_input(2), node.optional_input(3)
+        bias = self._vector_ptr(bias_v, n, "Conv bias") if bias_v is not None else "NULL"
+        res = self.fptr(res_v) if res_v is not None else "NULL"
+        act, lo, hi = self._act(node) if node.op == "FusedConv" else ("none", 0.0, 6.0)
+        mbs = (f"mgc_hip_mbconv_args mb; memset(&mb, 0, sizeof mb); mb.x = {self.fptr(xv)}; "
+               f"mb.we = (const float *){we_ptr}; mb.be = {ebias}; mb.wd = (const float *)(W + {dwoff}); "
+               f"mb.bd = {dbias}; mb.H = {h}; mb.W = {wd}; mb.Cin = {cin}; mb.Cexp = {cexp}; "
+               f"mb.SH = {g.strides[0]}; mb.SW = {g.strides[1]}; mb.PT = {g.pads[0]}; mb.PL = {g.pads[1]}; "
+               f"mb.OH = {oh}; mb.OW = {ow}; mb.act_e = {ACT_CODES[eact]}; mb.lo_e = {_f(elo)}; "
+               f"mb.hi_e = {_f(ehi)}; mb.act_d = {ACT_CODES[dact]}; mb.lo_d = {_f(dlo)}; mb.hi_d = {_f(dhi)};")
+        external = self.plan.location(xv).kind in ("input", "output")
+        if external:
+            self.emit(f"if ((((uintptr_t){self.ptr(xv)}) & 15) == 0) {{")
+        self._gemm_call(nb * oh * ow, n, cexp, [], bspec, self.fptr(node.output), n, bias=bias,
+                        bias_mode=1 if bias != "NULL" else 0, res=res, ldr=n, act=act, lo=lo, hi=hi, mbconv=mbs)
+        self.count("gemm_mbconv")
+        if external:
+            self.emit("} else {")
+            saved = self._mb.pop(id(node))
+            skipped = {id(ex), id(dw)}
+            self._mb_skip -= skipped
+            try:
+                self.op_FusedConv(ex)
+                self.op_FusedConv(dw)
+                self.op_FusedConv(node)
+            finally:
+                self._mb[id(node)] = saved
+                self._mb_skip |= skipped
             self.emit("}")
 
     # -- space-to-depth convolution -------------------------------------------------------------
@@ -1649,6 +1778,11 @@ class HipEmitter:
             i = index[id(dw)]
             flops[index[pw_id]] += flops[i]
             flops[i] = 0
+        for pw_id, pair in self._mb.items():
+            for n in pair:
+                i = index[id(n)]
+                flops[index[pw_id]] += flops[i]
+                flops[i] = 0
         return flops
 
 

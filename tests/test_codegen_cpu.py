@@ -155,15 +155,17 @@ def test_projection_shortcuts_join_their_block_gemm():
     assert not find_projection_shortcuts(o3(builders.bottleneck()))  # identity shortcuts only
 
 
-def test_depthwise_pointwise_pairs_join_one_gemm():
+def test_depthwise_pointwise_pairs_join_one_gemm(monkeypatch):
     """MobileNetV2 at batch 32: the six depthwise -> projection pairs whose GEMMs have at least
     DEPTHWISE_FUSE_MIN_ROWS rows (the 112 x 112, 56 x 56 and 28 x 28 outputs) each run as one
     mgc_hip_gemm_dw call; the depthwise input stays alive (its arena block clear of everything
     placed) until that call reads it, and the depthwise FLOPs are counted at the call's node. At
     batch 1 only the two shallow pairs (32 and 96 channels) are fused."""
     from ml_graph_compiler import ops
+    from ml_graph_compiler.codegen import hip as emitter
     from ml_graph_compiler.codegen.hip import find_depthwise_pointwise
 
+    monkeypatch.setattr(emitter, "FUSE_INVERTED_RESIDUAL", False)  # whole blocks: the next test
     g = o3(builders.mobilenet_v2(batch=32))
     pairs = find_depthwise_pointwise(g)
     assert len(pairs) == 6
@@ -191,6 +193,42 @@ def test_depthwise_pointwise_pairs_join_one_gemm():
     assert sorted(dw.input(0).tensor_type.shape[3] for dw in shallow.values()) == [32, 96]
 
 
+def test_inverted_residual_blocks_run_as_one_launch():
+    """MobileNetV2 at batch 32: the five expanded blocks whose outputs have at least
+    MBCONV_MIN_ROWS pixels (56 x 56 and 28 x 28, both strides, 16 / 24 / 32 input channels) each
+    run as one mgc_hip_mbconv call; the first block (no expansion) keeps the fused depthwise
+    GEMM. The block input stays alive (its arena block clear of everything placed) until the
+    call reads it, and the expansion and depthwise FLOPs are counted at the call's node. At
+    batch 1 no block has enough output pixels."""
+    from ml_graph_compiler import ops
+    from ml_graph_compiler.codegen.hip import find_inverted_residuals
+
+    g = o3(builders.mobilenet_v2(batch=32))
+    blocks = find_inverted_residuals(g)
+    shapes = sorted((ex.input(0).tensor_type.shape[1:], dw.output.tensor_type.shape[1:]) for ex, dw in blocks.values())
+    assert shapes == [((28, 28, 32), (28, 28, 192))] * 2 + [((56, 56, 24), (28, 28, 144)), ((56, 56, 24), (56, 56, 144)),
+                                                            ((112, 112, 16), (56, 56, 96))]
+    gen = generate_hip(g, gemm_workspace=native.gemm_workspace_floats)
+    assert gen.kernels["gemm_mbconv"] == 5 and gen.kernels["gemm_depthwise"] == 1 and gen.kernels["depthwise"] == 11
+    assert gen.source.count("mgc_hip_mbconv(x, &g, &mb);") == 5
+    assert sum(gen.node_flops) == sum(ops.flops(n) for n in g.nodes)
+    skipped = {id(n) for pair in blocks.values() for n in pair}
+    assert all(gen.node_flops[i] == 0 for i, n in enumerate(g.nodes) if id(n) in skipped)
+    order = {id(n): i for i, n in enumerate(g.nodes)}
+    by_value = {id(v): b for b in gen.plan.buffers for v in b.values}
+    for pw in g.nodes:
+        pair = blocks.get(id(pw))
+        if pair is None:
+            continue
+        x = by_value[id(pair[0].input(0))]
+        assert x.end >= order[id(pw)]
+        for b in gen.plan.buffers:
+            if b is x or not (b.start <= order[id(pw)] <= b.end):
+                continue
+            assert b.offset + b.size <= x.offset or x.offset + x.size <= b.offset
+    assert not find_inverted_residuals(o3(builders.mobilenet_v2(batch=1)))
+
+
 def test_fusions_stay_below_the_fused_kernels_operand_limit(monkeypatch):
     """The fused projection-shortcut and depthwise GEMMs address their operands with 32-bit byte
     offsets and refuse operands of 2 GiB or more at launch, so the emitter must not choose them
@@ -201,6 +239,7 @@ def test_fusions_stay_below_the_fused_kernels_operand_limit(monkeypatch):
 
     limit = emitter.FUSED_OPERAND_LIMIT
     nbytes = emitter._tensor_bytes
+    monkeypatch.setattr(emitter, "FUSE_INVERTED_RESIDUAL", False)  # (its own limit: the next test)
     for make, find, kind in ((lambda: builders.resnet50(batch=700), emitter.find_projection_shortcuts, "gemm_shortcut"),
                              (lambda: builders.mobilenet_v2(batch=450), emitter.find_depthwise_pointwise, "gemm_depthwise")):
         g = o3(make())
