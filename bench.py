@@ -478,7 +478,12 @@ def hbm_summary(fetch_dir: Path, write_dir: Path, trace_dir: Path, workload: str
 
     def bound(name: str) -> str:
         # the split-K reductions move bytes; the streaming short-K GEMM and the depthwise GEMM
-        # (a 3 x 3 depthwise pass feeding a narrow projection) are HBM-bound by design
+        # (a 3 x 3 depthwise pass feeding a narrow projection) are HBM-bound by design. A whole
+        # inverted-residual block (mbconv_kernel) does 53-57 algorithmic FLOP per byte it moves
+        # (expansion, depthwise and projection per output pixel against its input, output and
+        # residual), above the 19.7 FLOP/B ridge: MFMA-bound.
+        if "mbconv" in name:
+            return "MFMA"
         if "gemm_" in name and "splitk" not in name and "gemm_stream" not in name and "gemm_dw" not in name:
             return "MFMA"
         return "MFMA/latency" if "attention" in name else "HBM"

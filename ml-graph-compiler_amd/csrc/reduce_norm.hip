@@ -613,10 +613,10 @@ __global__ void __launch_bounds__(256) depthwise3x3_nhwc_vec4(const DwGeo g, Fas
     }
 }
 
-// Stride-2 form: every input and weight load of a thread is issued before the first FMA
-// (addresses clamped into the image; out-of-image taps are skipped afterwards), so the thread
-// waits for memory once. At stride 1 with four outputs per thread the preloaded rows need
-// enough registers to halve occupancy, and the row-by-row kernel above is faster there.
+// Preloading form (stride 2, and stride 1 on wide rows): every input and weight load of a
+// thread is issued before the first FMA (addresses clamped into the image; out-of-image taps
+// are skipped afterwards), so the thread waits for memory once. Two outputs per thread: with
+// four, the preloaded rows need enough registers to halve occupancy.
 template <int SW, int T>
 __global__ void __launch_bounds__(256) depthwise3x3_nhwc_preload(const DwGeo g, FastDiv div_c4, FastDiv div_owb,
                                                                  FastDiv div_oh, int total, const float *in,
@@ -967,11 +967,13 @@ extern "C" void mgc_hip_pool(mgc_hip_exec *x, int nhwc, int is_max, int N, int H
     }
 }
 
-// Output pixels per thread of the 3x3 depthwise kernel: four on wide stride-1 rows, else two
-// (four would leave too few threads and waste a partial tile on every narrow row; at stride 2
-// four outputs share fewer of their nine columns). Chosen by timing MobileNetV2's 17 depthwise
-// layers at batch 32 with each choice.
-static int dw3_tile(int OW, int SW) { return SW == 1 && OW >= 28 ? 4 : 2; }
+// The stride-1 3x3 depthwise form: on wide rows (OW >= 28) the preloading kernel with two
+// outputs per thread (every input, weight and residual load issued before the first FMA), on
+// narrow rows the row-by-row column kernel. MobileNetV2's stride-1 layers at batch 32, eager
+// hipEvent timing of 50 launches, against the row-by-row kernel with four outputs per thread:
+// 56 x 56 x 144 16.9 vs 28.1 us (85% of 8 TB/s), 28 x 28 x 192 8.2 vs 12.2 us; the preloading
+// kernel on the 14 x 14 and 7 x 7 layers was 0-8% slower than the two-output column kernel.
+static bool dw3_preload_s1(int OW) { return OW >= 28; }
 
 // The LDS-tiled 3x3 kernel (equal strides) for launches of at most 2^18 output quads: there a
 // workgroup's three loads per thread, all issued before the first is used, beat the per-thread
@@ -1002,11 +1004,10 @@ extern "C" void mgc_hip_depthwise(mgc_hip_exec *x, int nhwc, int N, int H, int W
             MGC_LAUNCH(x, kern, dim3((unsigned)blocks), dim3(256), 0, g, tiles_w, tiles_h, cgroups, in, w, bias,
                        res, out);
         } else if (vec && k3) {
-            const int tile = dw3_tile(OW, SW);
-            const int owb = (OW + tile - 1) / tile;
+            const int owb = (OW + 1) / 2;
             const int quads = (int)((long)N * OH * owb * (C / 4));
             auto kern = SW == 2 ? depthwise3x3_nhwc_preload<2, 2>
-                                : (tile == 4 ? depthwise3x3_nhwc_vec4<1, 4> : depthwise3x3_nhwc_vec4<1, 2>);
+                                : (dw3_preload_s1(OW) ? depthwise3x3_nhwc_preload<1, 2> : depthwise3x3_nhwc_vec4<1, 2>);
             MGC_LAUNCH(x, kern, dim3(blocks_for(quads, 256, 16384)), dim3(256), 0, g,
                        make_fastdiv((unsigned)(C / 4)), make_fastdiv((unsigned)owb), make_fastdiv((unsigned)OH),
                        quads, in, w, bias, res, out);
