@@ -9,10 +9,12 @@ stream synchronizations (wall clock, cross-checked with hipEvents on the model s
 Printed: ONE JSON line with the driver's fields plus
 * ``roofline``: the fp32 MFMA GEMM / implicit-GEMM convolution kernels (all conv and FC nodes):
   algorithmic FLOPs per launch (ops.flops of the node, 2 per MAC) over the kernel's average
-  duration, measured with a hipEvent pair around every node in eager replays on the model
-  stream; ``traffic`` is the HBM bytes per GEMM launch, measured in the run by two rocprofv3
-  counter runs (FETCH_SIZE, WRITE_SIZE) over ``--pmc-probe`` (``traffic_source`` says so, or
-  names the committed summary profiles/<workload>_b<batch>_gemm_traffic.md it fell back to);
+  duration in graph replays, measured in the run by a rocprofv3 --kernel-trace child over
+  ``--trace-probe`` (``duration_source`` says so; ``event_avg_launch_us`` is the eager
+  per-node hipEvent figure, and ``--no-trace`` falls back to it); ``traffic`` is the HBM bytes
+  per GEMM launch, measured in the run by two rocprofv3 counter runs (FETCH_SIZE, WRITE_SIZE)
+  over ``--pmc-probe`` (``traffic_source`` says so, or names the committed summary
+  profiles/<workload>_b<batch>_gemm_traffic.md it fell back to);
 * ``cpu_baseline``: the reference's generated-C + OpenMP backend (its own C kernels, built from
   the reference sources into oracle/_ref) on this host's cores by the reference's latency
   method (fresh process per cell, 3 interleaved rounds, bootstrap CI) at the GPU batch;
@@ -233,12 +235,15 @@ def cpu_baseline(workload: str, gpu_batch: int) -> dict | None:
     units = 1 if workload == "single_gemm" else gpu_batch
     unit = {"single_gemm": "calls/s", "bert_base": "seq/s", "gpt2": "seq/s"}.get(workload, "img/s")
 
+    plan = {(b, t): (w, rep) for _, b, t, w, rep in cells}
+
     def rate(batch: int, threads: int) -> str:
         r = rows[(batch, threads)]
         lo, hi = r["median_ci95_ms"]
         n = 1 if workload == "single_gemm" else batch
+        warm, rep = plan[(batch, threads)]
         return (f"b{batch} on {threads} thread(s): {1e3 * n / r['median_ms']:.2f} {unit} (median {r['median_ms']:.1f} ms, "
-                f"95% CI {lo:.1f}-{hi:.1f} ms, {r['samples']} runs)")
+                f"95% CI {lo:.1f}-{hi:.1f} ms, {r['samples']} runs: warmup {warm} and repeat {rep} per round)")
 
     head = rows[(gpu_batch, cores)]
     text = "; ".join(rate(b, t) for (b, t) in rows)
@@ -249,7 +254,9 @@ def cpu_baseline(workload: str, gpu_batch: int) -> dict | None:
         "kind": "reference",
         "sample": (f"{workload}: the reference's generated-C + OpenMP backend (its own mgc_kernels.c, -O3 -fopenmp "
                    f"-march=x86-64-v3) on '{info['cpu_model']}' (nproc {cores}); a fresh process per cell, 3 interleaved "
-                   f"rounds, bootstrap CI of the median (the reference's benchmarks/latency.py method); {text}"),
+                   f"rounds, bootstrap CI of the median (the reference's benchmarks/latency.py method; its warmup 5 / "
+                   f"repeat 30 are cut for the GPU-batch cell and the one-thread cell to keep the run within minutes); "
+                   f"{text}"),
         "median_ci95_ms": head["median_ci95_ms"],
     }
 
@@ -281,11 +288,8 @@ def measure_traffic(workload: str, batch: int, cache: Path) -> tuple[int | None,
                 raise RuntimeError(f"no {counter} rows (rc {proc.returncode}): {proc.stderr[-400:]}")
         bf, bw, _, _ = calibration(runs["FETCH_SIZE"], runs["WRITE_SIZE"])
 
-        def is_gemm(name: str) -> bool:
-            return "gemm_" in name and "reduce" not in name
-
-        gf = [v for name, v in runs["FETCH_SIZE"] if is_gemm(name)]
-        gw = [v for name, v in runs["WRITE_SIZE"] if is_gemm(name)]
+        gf = [v for name, v in runs["FETCH_SIZE"] if _is_gemm_kernel(name)]
+        gw = [v for name, v in runs["WRITE_SIZE"] if _is_gemm_kernel(name)]
         if not gf or len(gf) != len(gw):
             raise RuntimeError("GEMM dispatch counts differ between the two runs")
         return int(round((bf * sum(gf) + bw * sum(gw)) / len(gf))), (
@@ -343,6 +347,66 @@ def pmc_probe(workload: str, batch: int, cache: Path) -> None:
     log("pmc probe done: calibration copy, then one eager forward")
 
 
+TRACE_REPLAYS = 20
+
+
+def trace_probe(workload: str, batch: int, cache: Path) -> None:
+    """The program the kernel-trace run profiles: TRACE_REPLAYS graph replays of the workload on
+    resident inputs after a warmup, the conditions of the timed region."""
+    graph, model = compile_workload(workload, batch, cache)
+    model.upload(feeds_for(graph))
+    model.launch(3)
+    model.sync()
+    model.launch(TRACE_REPLAYS)
+    model.sync()
+    model.release()
+    log(f"trace probe done: {TRACE_REPLAYS} graph replays")
+
+
+def _is_gemm_kernel(name: str) -> bool:
+    """The GEMM family: every GEMM / implicit-GEMM kernel (the whole-block mbconv kernel is the
+    projection GEMM with its producers fused), not the split-K reductions."""
+    return ("gemm_" in name or "mbconv_kernel" in name) and "splitk" not in name
+
+
+def traced_gemm_launch(workload: str, batch: int, cache: Path) -> dict | None:
+    """Average duration of the GEMM-family kernels (and per GEMM node with its split-K
+    reduction) over TRACE_REPLAYS graph replays, from a rocprofv3 --kernel-trace child run of
+    --trace-probe: the duration roofline.achieved divides by."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+
+    prof = shutil.which("rocprofv3")
+    if prof is None:
+        log("kernel trace: rocprofv3 not found")
+        return None
+    out = Path(tempfile.mkdtemp(prefix="mgc-trace-", dir="/tmp"))
+    try:
+        cmd = [prof, "--kernel-trace", "--output-format", "csv", "-d", str(out), "-o", "p", "--",
+               sys.executable, str(ROOT / "bench.py"), "--trace-probe", "--workload", workload,
+               "--batch", str(batch), "--cache", str(cache)]
+        log("kernel trace: rocprofv3 --kernel-trace over the graph-replay probe")
+        proc = subprocess.run(cmd, cwd="/tmp", env={**os.environ, "TMPDIR": "/tmp"}, capture_output=True,
+                              text=True, timeout=300, check=False)
+        rows = []
+        for f in sorted(out.rglob("*kernel_trace.csv")):
+            for r in csv.DictReader(open(f)):
+                rows.append((r["Kernel_Name"], (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3))
+        gemm = [us for name, us in rows if _is_gemm_kernel(name)]
+        red = [us for name, us in rows if "splitk" in name]
+        if not gemm:
+            raise RuntimeError(f"no GEMM dispatches traced (rc {proc.returncode}): {proc.stderr[-300:]}")
+        return {"launches": len(gemm), "avg_us": sum(gemm) / len(gemm),
+                "avg_us_with_reductions": (sum(gemm) + sum(red)) / len(gemm), "reductions": len(red)}
+    except Exception as exc:
+        log(f"kernel trace failed: {exc}")
+        return None
+    finally:
+        shutil.rmtree(out, ignore_errors=True)
+
+
 def per_dispatch(d: Path, counter: str) -> list[tuple[str, float]]:
     """(kernel name, counter value) of every dispatch of a rocprofv3 --pmc run, in dispatch order."""
     import csv
@@ -373,11 +437,8 @@ def pmc_summary(fetch_dir: Path, write_dir: Path, workload: str, batch: int) -> 
     bf, bw, cal_f, cal_w = calibration(fetch, write)
     kf, kw = bf / 1024.0, bw / 1024.0
 
-    def is_gemm(name: str) -> bool:
-        return "gemm_" in name and "reduce" not in name
-
-    gf = [v for name, v in fetch if is_gemm(name)]
-    gw = [v for name, v in write if is_gemm(name)]
+    gf = [v for name, v in fetch if _is_gemm_kernel(name)]
+    gw = [v for name, v in write if _is_gemm_kernel(name)]
     n = len(gf)
     fetch_b = kf * 1024.0 * sum(gf) / n
     write_b = kw * 1024.0 * sum(gw) / n
@@ -641,6 +702,9 @@ def main() -> int:
     p.add_argument("--no-b1", action="store_true")
     p.add_argument("--cache", default=os.environ.get("MGC_BENCH_CACHE", "/tmp/mgc-bench-cache"))
     p.add_argument("--pmc-probe", action="store_true", help="run the counter-run program and exit")
+    p.add_argument("--trace-probe", action="store_true", help="run the kernel-trace program (graph replays) and exit")
+    p.add_argument("--no-trace", action="store_true",
+                   help="time the GEMM launches with eager hipEvents instead of a rocprofv3 kernel trace")
     p.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                    help="summarize the FETCH_SIZE / WRITE_SIZE runs into profiles/ and exit")
     p.add_argument("--hbm-summary", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "TRACE_DIR"),
@@ -681,6 +745,9 @@ def main() -> int:
     if args.pmc_probe:
         pmc_probe(args.workload, batch, cache)
         return 0
+    if args.trace_probe:
+        trace_probe(args.workload, batch, cache)
+        return 0
 
     log(f"compiling {args.workload} b{batch} (O3, hip)")
     graph, model = compile_workload(args.workload, batch, cache)
@@ -698,6 +765,20 @@ def main() -> int:
     roof = gemm_roofline(graph, model, args.profile_replays)
     total_flops = sum(model.node_flops)
     model.release()
+    traced = None if args.no_trace else traced_gemm_launch(args.workload, batch, cache)
+    if traced is not None:
+        # the kernel's own duration in graph replays, from the kernel trace; the eager per-node
+        # hipEvent figure (event overhead included) is kept beside it
+        flops = roof["flops_per_launch"]
+        roof["event_avg_launch_us"] = roof["avg_launch_us"]
+        roof["avg_launch_us"] = round(traced["avg_us"], 2)
+        roof["achieved"] = round(flops / traced["avg_us"] / 1e6, 2)
+        roof["frac"] = round(roof["achieved"] / MFMA_FP32_PEAK_TFLOPS, 4)
+        roof["achieved_with_reductions"] = round(flops / traced["avg_us_with_reductions"] / 1e6, 2)
+        roof["duration_source"] = (f"rocprofv3 --kernel-trace over {TRACE_REPLAYS} graph replays "
+                                   f"({traced['launches']} GEMM dispatches, {traced['reductions']} split-K reductions)")
+    else:
+        roof["duration_source"] = "eager per-node hipEvent pairs on the model stream"
     if args.no_traffic:
         roof["traffic"], roof["traffic_source"] = recorded_traffic(args.workload, batch), "recorded (--no-traffic)"
     else:

@@ -75,8 +75,11 @@ __global__ void __launch_bounds__(256 * G) attention_kernel(const AttnDev p) {
     const int wm = wave >> 1, wn = wave & 1;
     const int li = lane & 31, lh = lane >> 5;
     const int qblocks = (p.S + ATT_BQ - 1) / ATT_BQ;
-    const int bh = blockIdx.x / qblocks;
-    const int q0 = (blockIdx.x - bh * qblocks) * ATT_BQ;
+    // XCD order: the query blocks of one (batch, head) run on one XCD, so its K and V come
+    // into that XCD's L2 once instead of once per query block
+    const int blk = xcd_block();
+    const int bh = blk / qblocks;
+    const int q0 = (blk - bh * qblocks) * ATT_BQ;
     const int b = bh / p.H, h = bh - (bh / p.H) * p.H;
     const float *qbase = p.q + b * p.q_b + h * p.q_h;
     const float *kbase = p.k + b * p.k_b + h * p.k_h;
@@ -355,8 +358,11 @@ __global__ void __launch_bounds__(64 * W) attention_short_kernel(const AttnDev p
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int li = lane & 31, lh = lane >> 5;
     const int qblocks = (p.S + 31) >> 5;
-    const int bh = blockIdx.x / qblocks;
-    const int q0 = (blockIdx.x - bh * qblocks) * 32;
+    // XCD order: the query blocks of one (batch, head) run on one XCD, so its K and V come
+    // into that XCD's L2 once instead of once per query block
+    const int blk = xcd_block();
+    const int bh = blk / qblocks;
+    const int q0 = (blk - bh * qblocks) * 32;
     const int b = bh / p.H, h = bh - (bh / p.H) * p.H;
     const float *qbase = p.q + b * p.q_b + h * p.q_h;
     const float *kbase = p.k + b * p.k_b + h * p.k_h;
