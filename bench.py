@@ -602,6 +602,76 @@ MI355X_SIMDS = 256 * 4
 MFMA_COUNTERS = "SQ_INSTS_VALU_MFMA_MOPS_F32 SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CU_CYCLES GRBM_GUI_ACTIVE"
 
 
+def kernel_summary(trace_dir: Path, workload: str, batch: int) -> str:
+    """Per-kernel durations of graph replays: a rocprofv3 --kernel-trace run of --trace-probe
+    (3 warmup + TRACE_REPLAYS replays, nothing else on the GPU apart from the upload copies),
+    averaged per forward, with the GEMM family's algorithmic TFLOP/s (node FLOPs from the
+    compiled graph, a fused projection shortcut or depthwise convolution counted at the launch
+    that computes it)."""
+    import csv
+
+    from ml_graph_compiler.codegen import build as native
+    from ml_graph_compiler.codegen.hip import generate_hip
+
+    rows = []
+    for f in sorted(trace_dir.rglob("*kernel_trace.csv")):
+        for r in csv.DictReader(open(f)):
+            if r["Kernel_Name"].startswith("__amd_rocclr"):
+                continue
+            rows.append((int(r["Dispatch_Id"]), _short_kernel(r["Kernel_Name"]),
+                         (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-9))
+    rows.sort()
+    forwards = 3 + TRACE_REPLAYS
+    fam: dict[str, list] = {}
+    for _, name, sec in rows:
+        a = fam.setdefault(name, [0, 0.0])
+        a[0] += 1
+        a[1] += sec
+    total = sum(sec for _, _, sec in rows) / forwards
+    g = build_graph(workload, batch)
+    from ml_graph_compiler.passes import optimize
+    from ml_graph_compiler.schedule import schedule
+
+    optimize(g, "O3")
+    schedule(g)
+    gen = generate_hip(g, gemm_workspace=native.gemm_workspace_floats,
+                       gemm_ln_workspace=native.gemm_layer_norm_workspace_floats)
+    gemm_flops = sum(f for f, n in zip(gen.node_flops, g.nodes)
+                     if n.op in ("FusedConv", "Conv", "FusedGemm", "Gemm", "MatMul") and not _is_depthwise(n))
+    gemm_sec = sum(sec for _, name, sec in rows if _is_gemm_kernel(name)) / forwards
+    gemm_n = sum(1 for _, name, _ in rows if _is_gemm_kernel(name)) / forwards
+    label = "128 rows" if workload == "single_gemm" else f"batch {batch}"
+    out = [
+        f"# Kernels of one forward in graph replays: {workload} ({label}, hip backend, -O3)",
+        "",
+        "Commands (repo root, on the MI355X box):",
+        "",
+        "```",
+        "cd /tmp && export TMPDIR=/tmp",
+        f"rocprofv3 --kernel-trace --output-format csv -d $GRAFT_REPO_ROOT/gpurun_out/kt_{workload}_b{batch} -o p -- "
+        f"python3 $GRAFT_REPO_ROOT/bench.py --trace-probe --workload {workload} --batch {batch}",
+        f"python3 bench.py --kernel-summary gpurun_out/kt_{workload}_b{batch} --workload {workload} --batch {batch}",
+        "```",
+        "",
+        f"The probe replays the captured forward {forwards} times (3 warmup + {TRACE_REPLAYS}) on resident inputs; "
+        f"durations are the kernel trace's end - start of each dispatch, averaged per forward. Kernel time per "
+        f"forward: {total * 1e6:.1f} us in {len(rows) / forwards:.0f} launches.",
+        "",
+        "| kernel | launches per forward | avg us | us per forward | % of forward |",
+        "|---|---:|---:|---:|---:|",
+    ]
+    for name, (cnt, sec) in sorted(fam.items(), key=lambda kv: -kv[1][1]):
+        out.append(f"| `{name}` | {cnt / forwards:g} | {sec / cnt * 1e6:.2f} | {sec / forwards * 1e6:.1f} | "
+                   f"{100 * sec / forwards / total:.1f} |")
+    if gemm_n:
+        tf = gemm_flops / gemm_sec / 1e12
+        out += ["", f"GEMM family (every GEMM / implicit-GEMM kernel, split-K reductions apart): {gemm_n:g} launches "
+                    f"per forward, {gemm_sec / gemm_n * 1e6:.2f} us average, {gemm_flops / 1e9:.2f} GFLOP algorithmic "
+                    f"per forward -> {tf:.1f} TFLOP/s = {100 * tf / MFMA_FP32_PEAK_TFLOPS:.1f}% of the "
+                    f"{MFMA_FP32_PEAK_TFLOPS} TFLOP/s fp32 MFMA peak.", ""]
+    return "\n".join(out)
+
+
 def mfma_summary(pmc_dir: Path, trace_dir: Path, workload: str, batch: int) -> str:
     """MFMA work and utilisation of every matrix-core dispatch of one eager forward: one counter
     run over --pmc-probe (MFMA_COUNTERS) and the kernel-trace run of the same program for
@@ -713,11 +783,20 @@ def main() -> int:
     p.add_argument("--mfma-summary", nargs=2, metavar=("PMC_DIR", "TRACE_DIR"),
                    help="per-kernel MFMA FLOP, TFLOP/s and busy cycles from a counter run and a "
                         "kernel trace of --pmc-probe, written to profiles/ and printed")
+    p.add_argument("--kernel-summary", metavar="TRACE_DIR",
+                   help="per-kernel durations of graph replays from a kernel trace of --trace-probe, written "
+                        "to profiles/ and printed")
     p.add_argument("--membench", action="store_true",
                    help="achieved HBM bandwidth of every memory-bound kernel family at large sizes; prints a table")
     args = p.parse_args()
     if args.membench:
         print(membench(Path(args.cache)))
+        return 0
+    if args.kernel_summary:
+        batch = 128 if args.workload == "single_gemm" else args.batch
+        text = kernel_summary(Path(args.kernel_summary), args.workload, batch)
+        (ROOT / "profiles" / f"{args.workload}_b{batch}_kernels.md").write_text(text)
+        print(text)
         return 0
     if args.mfma_summary:
         batch = 128 if args.workload == "single_gemm" else args.batch
