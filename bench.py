@@ -636,8 +636,7 @@ def kernel_summary(trace_dir: Path, workload: str, batch: int) -> str:
     schedule(g)
     gen = generate_hip(g, gemm_workspace=native.gemm_workspace_floats,
                        gemm_ln_workspace=native.gemm_layer_norm_workspace_floats)
-    gemm_flops = sum(f for f, n in zip(gen.node_flops, g.nodes)
-                     if n.op in ("FusedConv", "Conv", "FusedGemm", "Gemm", "MatMul") and not _is_depthwise(n))
+    gemm_flops = gen.gemm_flops
     gemm_sec = sum(sec for _, name, sec in rows if _is_gemm_kernel(name)) / forwards
     gemm_n = sum(1 for _, name, _ in rows if _is_gemm_kernel(name)) / forwards
     label = "128 rows" if workload == "single_gemm" else f"batch {batch}"

@@ -391,6 +391,10 @@ class GeneratedModel:
     lines: int
     kernels: dict[str, int]
     node_flops: list[int]
+    # algorithmic FLOPs of the GEMM-family launches (every mgc_hip_gemm / _gemm_dw / _mbconv /
+    # _gemm_layer_norm call: 2 M N K per batch element, plus the depthwise and expansion work a
+    # fused call computes); attention products run in the attention kernel and are not counted
+    gemm_flops: int = 0
 
 
 class HipEmitter:
@@ -458,6 +462,7 @@ class HipEmitter:
         self.weights = WeightsBuilder()
         self.body: list[str] = []
         self.kernels: dict[str, int] = {}
+        self._gemm_flops = 0
         # Constants the emitter creates itself (unfused BatchNorm scale/shift). Weights chunks are
         # keyed by id(value), so these must outlive the emission or a later temporary could reuse
         # an id and alias an earlier chunk.
@@ -1079,7 +1084,7 @@ class HipEmitter:
                    beta: float = 1.0, act: str = "none", lo: float = 0.0, hi: float = 6.0,
                    workspace: str = "NULL", workspace_floats: int = 0,
                    layer_norm: tuple[str, str, str, str] | None = None, extra: Sequence[str] = (),
-                   depthwise: str | None = None, mbconv: str | None = None) -> None:
+                   depthwise: str | None = None, mbconv: str | None = None, extra_flops: int = 0) -> None:
         """One mgc_hip_gemm call; ``layer_norm`` = (scale, bias, eps, out) makes it an
         mgc_hip_gemm_layer_norm call whose split-K reduction also normalizes the rows; ``mbconv``
         declares and fills an mgc_hip_mbconv_args ``mb`` and makes it an mgc_hip_mbconv call; ``extra``
@@ -1109,6 +1114,7 @@ class HipEmitter:
             parts.append("mgc_hip_gemm(x, &g);")
         self.emit("{ " + " ".join(parts) + " }")
         self.count("gemm")
+        self._gemm_flops += 2 * m * n * k * math.prod(d for d, *_ in batch) + extra_flops
         if layer_norm is not None:
             self.count("gemm_layer_norm")
 
@@ -1439,11 +1445,13 @@ class HipEmitter:
         self.count("gemm_shortcut")
         if external:
             self.emit("} else {")
+            counted = self._gemm_flops  # the fallback's launches run instead of the fused one
             saved = self._shortcut.pop(id(node))
             try:
                 self.op_FusedConv(ds)
                 self.op_FusedConv(node)
             finally:
+                self._gemm_flops = counted
                 self._shortcut[id(node)] = saved
             self.emit("}")
 
@@ -1476,15 +1484,17 @@ class HipEmitter:
             self.emit(f"if ((((uintptr_t){self.ptr(xv)}) & 15) == 0) {{")
         self._gemm_call(nb * oh * ow, n, c, [], bspec, self.fptr(node.output), n, bias=bias,
                         bias_mode=1 if bias != "NULL" else 0, res=res, ldr=n, act=act, lo=lo, hi=hi,
-                        depthwise=dws)
+                        depthwise=dws, extra_flops=ops.flops(dw))
         self.count("gemm_depthwise")
         if external:
             self.emit("} else {")
+            counted = self._gemm_flops  # the fallback's launches run instead of the fused one
             saved = self._dwpw.pop(id(node))
             try:
                 self.op_FusedConv(dw)
                 self.op_FusedConv(node)
             finally:
+                self._gemm_flops = counted
                 self._dwpw[id(node)] = saved
             self.emit("}")
 
@@ -1525,18 +1535,21 @@ class HipEmitter:
         if external:
             self.emit(f"if ((((uintptr_t){self.ptr(xv)}) & 15) == 0) {{")
         self._gemm_call(nb * oh * ow, n, cexp, [], bspec, self.fptr(node.output), n, bias=bias,
-                        bias_mode=1 if bias != "NULL" else 0, res=res, ldr=n, act=act, lo=lo, hi=hi, mbconv=mbs)
+                        bias_mode=1 if bias != "NULL" else 0, res=res, ldr=n, act=act, lo=lo, hi=hi, mbconv=mbs,
+                        extra_flops=ops.flops(ex) + ops.flops(dw))
         self.count("gemm_mbconv")
         if external:
             self.emit("} else {")
             saved = self._mb.pop(id(node))
             skipped = {id(ex), id(dw)}
             self._mb_skip -= skipped
+            counted = self._gemm_flops  # the fallback's launches run instead of the fused one
             try:
                 self.op_FusedConv(ex)
                 self.op_FusedConv(dw)
                 self.op_FusedConv(node)
             finally:
+                self._gemm_flops = counted
                 self._mb[id(node)] = saved
                 self._mb_skip |= skipped
             self.emit("}")
@@ -1629,9 +1642,11 @@ class HipEmitter:
                f"g.a.SW = 1; g.a.DH = 1; g.a.DW = 1; g.a.PT = {s2['P']}; g.a.PL = {s2['Q']}; "
                f"g.a.OH = {oh}; g.a.OW = {ow}; g.a.cg = {c4};")
         aspec = [f"g.a.kind = MGC_OP_CONV_NHWC; g.a.p = (const float *){dst}; " + geo]
+        # algorithmic work is the original convolution's (the zero taps of the rearranged kernel
+        # are padding the matrix cores execute)
         self._gemm_call(nb * oh * ow, kout, kdim, aspec, bspec, self.ptr(node.output), kout,
                         bias=bias, bias_mode=1 if bias != "NULL" else 0, res=res, ldr=kout,
-                        act=act, lo=lo, hi=hi)
+                        act=act, lo=lo, hi=hi, extra_flops=ops.flops(node) - 2 * nb * oh * ow * kout * kdim)
 
     def _pool(self, node: Node, is_max: int) -> None:
         xv = node.input(0)
@@ -1757,6 +1772,7 @@ class HipEmitter:
             lines=source.count("\n"),
             kernels=dict(sorted(self.kernels.items())),
             node_flops=self._node_flops(),
+            gemm_flops=self._gemm_flops,
         )
 
     def _node_flops(self) -> list[int]:

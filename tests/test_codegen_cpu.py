@@ -362,3 +362,20 @@ def test_reference_vector_cases_the_backend_rejects():
                 generate_hip(g)
         else:
             generate_hip(g)
+
+
+def test_gemm_family_flops_are_the_algorithmic_work():
+    """The emitter's count of the GEMM-family launches' algorithmic FLOPs (what the profiles'
+    TFLOP/s divide): ResNet-50 is 8,178,368,512 per image (the 53 convolutions and the FC, with
+    the space-to-depth stem counted as the original 7 x 7 convolution and the projection
+    shortcuts at the launches that compute them); BERT-base is everything but the attention
+    products (4 B H S^2 D per layer, which the attention kernel computes)."""
+    from ml_graph_compiler import ops
+
+    gen = generate_hip(o3(builders.resnet50(batch=2)), gemm_workspace=native.gemm_workspace_floats)
+    assert gen.gemm_flops == 2 * 8_178_368_512
+    g = o3(builders.bert_base(batch=1, layers=2))
+    gen = generate_hip(g, gemm_workspace=native.gemm_workspace_floats,
+                       gemm_ln_workspace=native.gemm_layer_norm_workspace_floats)
+    contractions = sum(ops.flops(n) for n in g.nodes if n.op in ("FusedGemm", "MatMul", "Gemm"))
+    assert gen.gemm_flops == contractions - 2 * 4 * 12 * 128 * 128 * 64
