@@ -647,7 +647,7 @@ def kernel_summary(trace_dir: Path, workload: str, batch: int) -> str:
         "",
         "```",
         "cd /tmp && export TMPDIR=/tmp",
-        f"rocprofv3 --kernel-trace --output-format csv -d $GRAFT_REPO_ROOT/gpurun_out/kt_{workload}_b{batch} -o p -- "
+        f"rocprofv3 --kernel-trace --stats --output-format csv -d $GRAFT_REPO_ROOT/gpurun_out/kt_{workload}_b{batch} -o p -- "
         f"python3 $GRAFT_REPO_ROOT/bench.py --trace-probe --workload {workload} --batch {batch}",
         f"python3 bench.py --kernel-summary gpurun_out/kt_{workload}_b{batch} --workload {workload} --batch {batch}",
         "```",
@@ -667,7 +667,16 @@ def kernel_summary(trace_dir: Path, workload: str, batch: int) -> str:
         out += ["", f"GEMM family (every GEMM / implicit-GEMM kernel, split-K reductions apart): {gemm_n:g} launches "
                     f"per forward, {gemm_sec / gemm_n * 1e6:.2f} us average, {gemm_flops / 1e9:.2f} GFLOP algorithmic "
                     f"per forward -> {tf:.1f} TFLOP/s = {100 * tf / MFMA_FP32_PEAK_TFLOPS:.1f}% of the "
-                    f"{MFMA_FP32_PEAK_TFLOPS} TFLOP/s fp32 MFMA peak.", ""]
+                    f"{MFMA_FP32_PEAK_TFLOPS} TFLOP/s fp32 MFMA peak."]
+        stats = []
+        for f in sorted(trace_dir.rglob("*kernel_stats.csv")):
+            stats += [(r["Name"], int(r["Calls"]), float(r["TotalDurationNs"])) for r in csv.DictReader(open(f))]
+        calls = sum(c for name, c, _ in stats if _is_gemm_kernel(name))
+        if calls:
+            ns = sum(t for name, _, t in stats if _is_gemm_kernel(name))
+            out += ["", f"rocprofv3 --stats of the same run (kernel_stats.csv): GEMM family {calls} calls, "
+                        f"{ns / calls / 1e3:.2f} us average (all {forwards} forwards)."]
+        out.append("")
     return "\n".join(out)
 
 
