@@ -263,6 +263,35 @@ typedef struct {
 int mgc_hip_mbconv_supported(int Cin, int Cexp, int Cout, int stride);
 void mgc_hip_mbconv(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const mgc_hip_mbconv_args *mb);
 
+/* The expansion and depthwise convolutions of an inverted-residual block as one launch, with
+ * the expanded tensor never in memory:
+ *   out[n][oh][ow][k] = act_d(bd[k] + sum_{i,j < 3} E[n][oh SH - PT + i][ow SW - PL + j][k] wd[(3 i + j) Cexp + k])
+ *   E[n][y][z][k] = act_e(be[k] + sum_c x[n][y][z][c] we[k Cin + c])  (zero outside the image)
+ * for the NHWC batch x [N][H][W][Cin] and out [N][OH][OW][Cexp]. Replaces mgc_gemm and
+ * mgc_depthwise_nhwc of the block's first two convolutions
+ * (src/ml_graph_compiler/codegen/runtime/mgc_kernels.c:370-396, 455-473, which the reference's
+ * C backend emits as two calls, codegen/c.py:1102-1226). One workgroup per image and 32
+ * expanded channels, so it suits small images at large batch (MobileNetV2's 14 x 14 and 7 x 7
+ * blocks at batch 32). Needs the shapes mgc_hip_expand_dw_supported accepts (Cin 64 or 96 with
+ * H W <= 256, or 160 with H W <= 64; Cexp % 32 == 0; SH = SW in {1, 2}; the depthwise window
+ * ((OH - 1) SH + 3) x ((OW - 1) SW + 3) at most 256 pixels, 128 for Cin 160), PT and PL in
+ * 0..2, act_e and act_d relu or clip, 16-byte aligned x, we, be, wd, bd and out, and x below
+ * 2 GiB; sets the launch error otherwise. */
+typedef struct {
+    const float *x;     /* block input NHWC [N][H][W][Cin] */
+    const float *we;    /* expansion weights packed [Cexp][Cin] */
+    const float *be;    /* expansion bias [Cexp] or NULL */
+    const float *wd;    /* depthwise weights [3][3][Cexp], channel fastest */
+    const float *bd;    /* depthwise bias [Cexp] or NULL */
+    float *out;         /* depthwise output NHWC [N][OH][OW][Cexp] */
+    int N, H, W, Cin, Cexp, SH, SW, PT, PL, OH, OW;
+    int act_e, act_d;   /* MGC_ACT_* after the expansion and after the depthwise convolution */
+    float lo_e, hi_e, lo_d, hi_d;
+} mgc_hip_expand_dw_args;
+
+int mgc_hip_expand_dw_supported(int H, int W, int Cin, int Cexp, int stride, int OH, int OW);
+void mgc_hip_expand_dw(mgc_hip_exec *x, const mgc_hip_expand_dw_args *a);
+
 /* ---------------------------------------------------------------------------------------- */
 /* memory-bound kernels                                                                      */
 /* ---------------------------------------------------------------------------------------- */

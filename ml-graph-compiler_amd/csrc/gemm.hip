@@ -2266,6 +2266,189 @@ __global__ void __launch_bounds__(256) mbconv_kernel(const GemmDev p, const MbDe
     }
 }
 
+// The 1 x 1 expansion of an inverted-residual block together with the 3 x 3 depthwise
+// convolution that alone reads it (mgc_hip_expand_dw), for images whose depthwise window (the
+// image plus the padding its outputs reach) fits LDS: a workgroup computes one image times 32
+// expanded channels, so the expanded tensor never goes to memory and the depthwise windows need
+// nothing from other workgroups; the depthwise output is stored for the projection GEMM. The
+// reference's C backend runs the two convolutions as two calls with the expanded tensor in its
+// arena (mgc_gemm, mgc_depthwise_nhwc: codegen/c.py:1102-1226, mgc_kernels.c:370-396, 455-473).
+struct XdDev {
+    const float *x;   // block input NHWC [n][H][W][CIN]
+    const float *we;  // expansion weights packed [Cexp][CIN]
+    const float *be;  // expansion bias [Cexp] or null
+    const float *wd;  // depthwise weights [9][Cexp]
+    const float *bd;  // depthwise bias [Cexp] or null
+    float *out;       // depthwise output NHWC [n][OH][OW][Cexp]
+    int H, W, Cexp, PT, PL, OH, OW;
+    int HP, WP;       // window rows and columns: (OH - 1) S + 3, (OW - 1) S + 3
+    int slices;       // Cexp / 32
+    float lo_e, hi_e, lo_d, hi_d;  // both activations as clamps: relu [0, inf), clip [lo, hi]
+    long x_bytes;
+};
+
+// One workgroup (four waves) per (image, 32-channel slice), in XCD-aware order so the slices of
+// an image share its input in one L2.
+//  * Expansion on v_mfma_f32_16x16x4f32 with channels as rows and pixels as columns: 16-pixel
+//    row block rb of the image (row-major pixels) belongs to wave rb % 4. For 16-channel chunk c
+//    lane (li, g) = (lane % 16, lane / 16) supplies we[channel 16 cb + li][16 c + 4 g + s] and
+//    x[pixel 16 rb + li][16 c + 4 g + s] as the s-th MFMA's operands (both permute k alike), so
+//    register r of channel block cb's accumulator is channel 16 cb + 4 g + r of pixel
+//    16 rb + li: a 16-byte quad, biased, clamped and written to LDS as E[window pixel][quad],
+//    the quads XOR-permuted by the pixel so neighbouring pixels' reads spread over the banks.
+//  * Every global load is requested when the kernel starts: the slice's weights and biases,
+//    which the workgroup reads once into LDS (expansion-weight quads XOR-permuted by the row),
+//    then the input quads of a wave's first two row blocks (later ones as earlier ones finish),
+//    so filling LDS waits for the weights only. Weights held per lane instead (no LDS copy, no
+//    barrier before the expansion) made every wave fetch the whole slice's weights and was
+//    slower.
+//  * Window pixels outside the image are zero (written once, never by the expansion).
+//  * Depthwise: thread t computes channel quad t % 8 of output pixels t / 8, t / 8 + 32, ...:
+//    the bias plus the nine taps in row-major order from LDS, clamped, stored as 16 bytes;
+//    eight threads cover a pixel's 128 contiguous output bytes.
+template <int S, int CIN, int RBW, int EPX>
+__global__ void __launch_bounds__(256) gemm_expand_dw_kernel(const XdDev d) {
+    constexpr int Q = CIN / 16;     // 16-channel chunks of a pixel
+    constexpr int KQ = CIN / 4;     // 16-byte quads of a weight row
+    constexpr int WEF = 32 * CIN;   // the slice's expansion weights (floats)
+    constexpr int SETS = RBW < 2 ? RBW : 2;
+    static_assert(CIN % 32 == 0, "weight quads permuted in groups of eight");
+    __shared__ __attribute__((aligned(16))) float smem[EPX * 32 + WEF + 11 * 32];
+    float *const E = smem;
+    float *const WE = smem + EPX * 32;
+    float *const WD = WE + WEF;      // [9][32] depthwise weights, [32] depthwise bias, [32] expansion bias
+    auto fsw = [](int r) __attribute__((always_inline)) { return ((r >> 1) ^ r) & 7; };
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, li = lane & 15, g = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lin = xcd_block();
+    const int img = lin / d.slices;
+    const int c0 = (lin - img * d.slices) * 32;
+    const int H = d.H, W = d.W, P = H * W, Cexp = d.Cexp, HP = d.HP, WP = d.WP;
+    const int rbn = (P + 15) / 16;
+    constexpr unsigned OOB = 0x80000000u;
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void *)d.x, (short)0, (int)d.x_bytes, 0x00020000);
+
+    // the slice's depthwise weights and biases (threads < 88), its expansion weights (CIN / 32
+    // quads per thread), then the input quads of row blocks wave + 4 j (j < SETS)
+    f4 wdv = {0.f, 0.f, 0.f, 0.f};
+    if (tid < 88) {
+        const int t = tid >> 3, q4 = (tid & 7) * 4;
+        if (t < 9)
+            wdv = ldg4(d.wd + (long)t * Cexp + c0 + q4);
+        else if (t == 9 && d.bd)
+            wdv = ldg4(d.bd + c0 + q4);
+        else if (t == 10 && d.be)
+            wdv = ldg4(d.be + c0 + q4);
+    }
+    constexpr int WEQ = WEF / 4 / 256;  // expansion-weight quads per thread
+    static_assert(WEQ * 256 * 4 == WEF, "weights spread evenly over the threads");
+    f4 wev[WEQ];
+#pragma unroll
+    for (int i = 0; i < WEQ; ++i) {
+        const int e = tid + 256 * i;
+        const int r = e / KQ, kq = e - r * KQ;
+        wev[i] = ldg4(d.we + (long)(c0 + r) * CIN + 4 * kq);
+    }
+    f4 xv[SETS][Q];
+    auto load_x = [&](int j, f4 (&v)[Q]) __attribute__((always_inline)) {
+        const int rb = wave + 4 * j;
+        const int pix = 16 * rb + li;
+        const bool ok = rb < rbn && pix < P;
+        const unsigned base = ((unsigned)(img * P + pix) * CIN + 4u * g) * 4u;
+#pragma unroll
+        for (int c = 0; c < Q; ++c)
+            v[c] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? base + 64u * c : OOB, 0, 0));
+    };
+#pragma unroll
+    for (int j = 0; j < SETS; ++j) load_x(j, xv[j]);
+
+    // window pixels outside the image to zero; the weights into LDS (expansion-weight row r at
+    // quad position kq ^ (r & 7))
+    for (int e = tid; e < HP * WP * 8; e += 256) {
+        const int lp = e >> 3;
+        const int py = lp / WP, px = lp - (lp / WP) * WP;
+        const int ih = py - d.PT, iw = px - d.PL;
+        if ((unsigned)ih >= (unsigned)H || (unsigned)iw >= (unsigned)W)
+            *reinterpret_cast<f4 *>(&E[lp * 32 + (e & 7) * 4]) = f4{0.f, 0.f, 0.f, 0.f};
+    }
+    if (tid < 88) *reinterpret_cast<f4 *>(&WD[(tid >> 3) * 32 + (tid & 7) * 4]) = wdv;
+#pragma unroll
+    for (int i = 0; i < WEQ; ++i) {
+        const int e = tid + 256 * i;
+        const int r = e / KQ, kq = e - r * KQ;
+        *reinterpret_cast<f4 *>(&WE[r * CIN + ((kq ^ (r & 7)) << 2)]) = wev[i];
+    }
+    barrier_lds();
+
+    // expansion of this wave's row blocks into the window
+    const float lo_e = d.lo_e, hi_e = d.hi_e;
+    const f4 be0 = *reinterpret_cast<const f4 *>(&WD[320 + 4 * g]);
+    const f4 be1 = *reinterpret_cast<const f4 *>(&WD[320 + 16 + 4 * g]);
+    const int wrow0 = li * CIN, wrow1 = (16 + li) * CIN, wsw = li & 7;
+#pragma unroll
+    for (int j = 0; j < RBW; ++j) {
+        const int rb = wave + 4 * j;
+        if (rb >= rbn) break;
+        f4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < Q; ++c) {
+            const int kq = 4 * c + g;
+            const f4 w0 = *reinterpret_cast<const f4 *>(&WE[wrow0 + ((kq ^ wsw) << 2)]);
+            const f4 w1 = *reinterpret_cast<const f4 *>(&WE[wrow1 + ((kq ^ wsw) << 2)]);
+            const f4 xq = xv[j % SETS][c];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(w0[s], xq[s], acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(w1[s], xq[s], acc1, 0, 0, 0);
+            }
+        }
+        if (j + SETS < RBW) load_x(j + SETS, xv[j % SETS]);
+        const int pix = 16 * rb + li;
+        const int ih = pix / W, iw = pix - (pix / W) * W;
+        const int py = ih + d.PT, px = iw + d.PL;
+        if (pix < P && py < HP && px < WP) {
+            const int lp = py * WP + px, sw = fsw(lp);
+            f4 v0, v1;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v0[e] = fminf(fmaxf(acc0[e] + be0[e], lo_e), hi_e);
+                v1[e] = fminf(fmaxf(acc1[e] + be1[e], lo_e), hi_e);
+            }
+            *reinterpret_cast<f4 *>(&E[lp * 32 + ((g ^ sw) << 2)]) = v0;
+            *reinterpret_cast<f4 *>(&E[lp * 32 + (((4 + g) ^ sw) << 2)]) = v1;
+        }
+    }
+    barrier_lds();
+
+    // depthwise outputs: channel quad q of pixels tid / 8 + 32 i
+    const int q = tid & 7;
+    f4 wt[9];
+#pragma unroll
+    for (int t = 0; t < 9; ++t) wt[t] = *reinterpret_cast<const f4 *>(&WD[t * 32 + 4 * q]);
+    const f4 bd = *reinterpret_cast<const f4 *>(&WD[288 + 4 * q]);
+    const float lo_d = d.lo_d, hi_d = d.hi_d;
+    const int OH = d.OH, OW = d.OW, OP = OH * OW;
+    float *const obase = d.out + (long)img * OP * Cexp + c0 + 4 * q;
+    for (int op = tid >> 3; op < OP; op += 32) {
+        const int oh = op / OW, ow = op - (op / OW) * OW;
+        f4 a = bd;
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+                const int lp = (oh * S + i) * WP + ow * S + j;
+                const f4 e = *reinterpret_cast<const f4 *>(&E[lp * 32 + ((q ^ fsw(lp)) << 2)]);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) a[k] = fmaf(e[k], wt[3 * i + j][k], a[k]);
+            }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) a[k] = fminf(fmaxf(a[k], lo_d), hi_d);
+        *reinterpret_cast<f4 *>(obase + (long)op * Cexp) = a;
+    }
+}
+
 // Sum the split-K partials and apply the epilogue (one batch element).
 __global__ void gemm_splitk_reduce(const GemmDev p) {
     const long total = (long)p.M * p.N;
@@ -2925,6 +3108,67 @@ extern "C" void mgc_hip_mbconv(mgc_hip_exec *x, const mgc_hip_gemm_args *g, cons
                           : mb->Cin == 24 ? (s2 ? &mbconv_kernel<2, 12> : &mbconv_kernel<1, 12>)
                                           : (s2 ? &mbconv_kernel<2, 16> : &mbconv_kernel<1, 16>);
     MGC_LAUNCH(x, kern, dim3((unsigned)tiles), dim3(256), 0, p, d);
+}
+
+// Row blocks of 16 image pixels a wave may own and window pixels LDS holds, per input width:
+// 64 and 96 channels up to 256 window pixels (a 14 x 14 image at stride 1 or 2), 160 channels
+// up to 128 (a 7 x 7 image).
+static bool expand_dw_fits(int Cin, int P, int window) {
+    const int rbw = ((P + 15) / 16 + 3) / 4;
+    if (Cin == 64 || Cin == 96) return rbw <= 4 && window <= 256;
+    if (Cin == 160) return rbw <= 1 && window <= 128;
+    return false;
+}
+
+extern "C" int mgc_hip_expand_dw_supported(int H, int W, int Cin, int Cexp, int stride, int OH, int OW) {
+    if (H <= 0 || W <= 0 || OH <= 0 || OW <= 0 || Cexp <= 0 || Cexp % 32 || (stride != 1 && stride != 2)) return 0;
+    const long window = ((long)(OH - 1) * stride + 3) * ((long)(OW - 1) * stride + 3);
+    return (long)H * W <= 256 && window <= 256 && expand_dw_fits(Cin, H * W, (int)window);
+}
+
+extern "C" void mgc_hip_expand_dw(mgc_hip_exec *x, const mgc_hip_expand_dw_args *a) {
+    if (a->N <= 0) return;
+    const long x_bytes = (long)a->N * a->H * a->W * (long)a->Cin * 4;
+    const bool acts = (a->act_e == MGC_ACT_RELU || a->act_e == MGC_ACT_CLIP) &&
+                      (a->act_d == MGC_ACT_RELU || a->act_d == MGC_ACT_CLIP);
+    const bool ok = mgc_hip_expand_dw_supported(a->H, a->W, a->Cin, a->Cexp, a->SH, a->OH, a->OW) && a->SH == a->SW &&
+                    acts && a->PT >= 0 && a->PT <= 2 && a->PL >= 0 && a->PL <= 2 && x_bytes < 0x7fffffffL &&
+                    (long)a->N * (a->Cexp / 32) < 0x7fffffffL && aligned16(a->x) && aligned16(a->we) &&
+                    aligned16(a->be) && aligned16(a->wd) && aligned16(a->bd) && aligned16(a->out) && a->x && a->we &&
+                    a->wd && a->out;
+    if (!ok) {
+        x->launch_error = (int)hipErrorInvalidValue;
+        set_error("mgc_hip_expand_dw: shape, layout or alignment outside its limits", hipErrorInvalidValue);
+        return;
+    }
+    XdDev d;
+    d.x = a->x;
+    d.we = a->we;
+    d.be = a->be;
+    d.wd = a->wd;
+    d.bd = a->bd;
+    d.out = a->out;
+    d.H = a->H;
+    d.W = a->W;
+    d.Cexp = a->Cexp;
+    d.PT = a->PT;
+    d.PL = a->PL;
+    d.OH = a->OH;
+    d.OW = a->OW;
+    d.HP = (a->OH - 1) * a->SH + 3;
+    d.WP = (a->OW - 1) * a->SW + 3;
+    d.slices = a->Cexp / 32;
+    d.lo_e = a->act_e == MGC_ACT_CLIP ? a->lo_e : 0.0f;
+    d.hi_e = a->act_e == MGC_ACT_CLIP ? a->hi_e : INFINITY;
+    d.lo_d = a->act_d == MGC_ACT_CLIP ? a->lo_d : 0.0f;
+    d.hi_d = a->act_d == MGC_ACT_CLIP ? a->hi_d : INFINITY;
+    d.x_bytes = x_bytes;
+    typedef void (*XdKernel)(const XdDev);
+    const bool s2 = a->SH == 2;
+    const XdKernel kern = a->Cin == 64   ? (s2 ? &gemm_expand_dw_kernel<2, 64, 4, 256> : &gemm_expand_dw_kernel<1, 64, 4, 256>)
+                          : a->Cin == 96 ? (s2 ? &gemm_expand_dw_kernel<2, 96, 4, 256> : &gemm_expand_dw_kernel<1, 96, 4, 256>)
+                                         : (s2 ? &gemm_expand_dw_kernel<2, 160, 1, 128> : &gemm_expand_dw_kernel<1, 160, 1, 128>);
+    MGC_LAUNCH(x, kern, dim3((unsigned)((long)a->N * d.slices)), dim3(256), 0, d);
 }
 
 static void gemm_launch(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const LnTail *ln) {

@@ -120,6 +120,14 @@ MBCONV_MIN_ROWS = 16384
 MBCONV_CIN = (16, 24, 32)
 MBCONV_MAX_CEXP = 256
 MBCONV_MAX_COUT = 32
+# Run an inverted-residual block's 1 x 1 expansion (relu / clip) and the 3 x 3 depthwise
+# convolution (relu / clip) that alone reads it as one mgc_hip_expand_dw launch (a workgroup per
+# image and 32 expanded channels; the expanded tensor never goes to memory) when
+# mgc_hip_expand_dw_supported accepts the shape and the images times 32-channel slices number
+# at least EXPAND_DW_MIN_WORKGROUPS (fewer leave CUs idle: batch 1 keeps the two launches);
+# tests turn it off to compare.
+FUSE_EXPAND_DEPTHWISE = True
+EXPAND_DW_MIN_WORKGROUPS = 256
 # The fused GEMMs address their image and weight operands through buffer resources with 32-bit
 # byte offsets, and their launchers refuse operands of this many bytes or more (the unfused
 # kernels have a generic path for them): both fusions are only taken below it.
@@ -374,6 +382,61 @@ def find_inverted_residuals(graph: Graph, min_rows: int | None = None) -> dict[i
     return found
 
 
+def expand_dw_supported(h: int, w: int, cin: int, cexp: int, stride: int, oh: int, ow: int) -> bool:
+    """The shapes mgc_hip_expand_dw_supported accepts: 64 or 96 input channels over at most 256
+    image pixels, or 160 over at most 64; expanded channels a multiple of 32; stride 1 or 2; a
+    depthwise window ((oh - 1) stride + 3) x ((ow - 1) stride + 3) of at most 256 pixels (128
+    for 160 input channels)."""
+    if min(h, w, oh, ow, cexp) <= 0 or cexp % 32 or stride not in (1, 2):
+        return False
+    window = ((oh - 1) * stride + 3) * ((ow - 1) * stride + 3)
+    row_blocks_per_wave = ((h * w + 15) // 16 + 3) // 4
+    if cin in (64, 96):
+        return h * w <= 256 and row_blocks_per_wave <= 4 and window <= 256
+    return cin == 160 and h * w <= 64 and row_blocks_per_wave <= 1 and window <= 128
+
+
+def find_expand_depthwise(graph: Graph, min_workgroups: int | None = None) -> dict[int, Node]:
+    """id(dw) -> ex for every 1 x 1 expansion ex whose output only the 3 x 3 depthwise
+    convolution dw reads, when mgc_hip_expand_dw can run the pair as one launch: ex a pointwise
+    NHWC FusedConv (stride 1, relu or clip, no residual), dw a depthwise FusedConv (relu or
+    clip, stride 1 or 2, padding at most 2), the shape expand_dw_supported accepts, at least
+    ``min_workgroups`` (default EXPAND_DW_MIN_WORKGROUPS) images x 32-channel slices and the
+    block input below FUSED_OPERAND_LIMIT bytes."""
+    if min_workgroups is None:
+        min_workgroups = EXPAND_DW_MIN_WORKGROUPS
+    outputs = {id(v) for v in graph.outputs}
+
+    def clamp_act(node: Node) -> bool:
+        return node.op == "FusedConv" and node.attrs.get("activation", "none") in ("relu", "clip")
+
+    found: dict[int, Node] = {}
+    for dw in graph.nodes:
+        if not _depthwise3x3_nhwc(dw) or not clamp_act(dw):
+            continue
+        e = dw.input(0)
+        ex = e.producer
+        if ex is None or not _pointwise_nhwc(ex) or not clamp_act(ex) or ex.optional_input(3) is not None:
+            continue
+        if id(e) in outputs or e.users != [dw] or ex.input(0).data is not None:
+            continue
+        xt, et = ex.input(0).tensor_type, e.tensor_type
+        if ops.window_geometry(ex, xt.shape[1:3], (1, 1)).strides != (1, 1):
+            continue
+        nb, h, w, cin = xt.shape
+        cexp = et.shape[3]
+        g = ops.window_geometry(dw, (h, w), (3, 3))
+        oh, ow = g.out_hw
+        if g.strides[0] != g.strides[1] or max(g.pads[0], g.pads[1]) > 2:
+            continue
+        if not expand_dw_supported(h, w, cin, cexp, g.strides[0], oh, ow):
+            continue
+        if nb * (cexp // 32) < min_workgroups or _tensor_bytes(ex.input(0)) >= FUSED_OPERAND_LIMIT:
+            continue
+        found[id(dw)] = ex
+    return found
+
+
 def pack_b_nk(b: np.ndarray) -> np.ndarray:
     """A constant K x N right-hand side stored as its transpose [N][K] (k contiguous), the
     layout the MFMA GEMM reads with 16-byte k-quad loads."""
@@ -448,6 +511,13 @@ class HipEmitter:
         for pw_id in [i for i, dw in self._dwpw.items() if id(dw) in taken or i in taken]:
             del self._dwpw[pw_id]
         self._dwpw_skip = {id(dw) for dw in self._dwpw.values()}
+        # id(depthwise conv) -> the expansion computed in its launch (mgc_hip_expand_dw); the
+        # expansion's input is then read at the depthwise step.
+        self._xd: dict[int, Node] = find_expand_depthwise(graph) if FUSE_EXPAND_DEPTHWISE else {}
+        taken |= set(self._dwpw) | self._dwpw_skip
+        for dw_id in [i for i, ex in self._xd.items() if i in taken or id(ex) in taken]:
+            del self._xd[dw_id]
+        self._xd_skip = {id(ex) for ex in self._xd.values()}
         order = {id(n): i for i, n in enumerate(graph.nodes)}
         keep = {id(ds.input(0)): order[id(c3)] for c3 in graph.nodes
                 if (ds := self._shortcut.get(id(c3))) is not None}
@@ -456,6 +526,9 @@ class HipEmitter:
                 keep[id(dw.input(0))] = max(keep.get(id(dw.input(0)), 0), order[id(pw)])
             if (pair := self._mb.get(id(pw))) is not None:
                 xin = pair[0].input(0)
+                keep[id(xin)] = max(keep.get(id(xin), 0), order[id(pw)])
+            if (ex := self._xd.get(id(pw))) is not None:  # pw is the depthwise node here
+                xin = ex.input(0)
                 keep[id(xin)] = max(keep.get(id(xin), 0), order[id(pw)])
         self.plan = plan_memory(graph, strategy=strategy, alignment=ALIGN, inplace=inplace,
                                 workspace=self._workspace_bytes, extra_reads=keep)
@@ -486,7 +559,8 @@ class HipEmitter:
                 if m.qkv_gemms:
                     qkv_bytes = max(qkv_bytes, 3 * m.out.tensor_type.nbytes)
         excluded = (set(self._attn_skip) | set(self._attn_emit) | set(self._shortcut) | self._shortcut_skip
-                    | set(self._dwpw) | self._dwpw_skip | set(self._mb) | self._mb_skip)
+                    | set(self._dwpw) | self._dwpw_skip | set(self._mb) | self._mb_skip | set(self._xd)
+                    | self._xd_skip)
         self._folds = plan_folds(graph, self.plan, self._workspace_bytes, excluded) if FOLD_TRANSPOSES else FoldPlan()
         self._scratch_qkv_off = self._scratch_off
         self._scratch_out_off = self._scratch_off + (qkv_bytes + ALIGN - 1) // ALIGN * ALIGN
@@ -675,6 +749,10 @@ class HipEmitter:
             return
         if id(node) in self._mb_skip:
             self.emit("/* inverted-residual block: computed in the launch of its projection convolution */")
+            self.count("folded")
+            return
+        if id(node) in self._xd_skip:
+            self.emit("/* expansion: computed in the launch of the depthwise convolution that reads it */")
             self.count("folded")
             return
         if id(node) in self._ln_skip:
@@ -1351,6 +1429,9 @@ class HipEmitter:
         if wv.data is None:
             raise CodegenError("convolution weights must be constant for the hip backend")
         out_ptr = self.ptr(node.output)
+        if id(node) in self._xd:
+            self._expand_depthwise(node, self._xd[id(node)])
+            return
         if self.depthwise(node):
             wflat = wv.data.reshape(kh * kw, c) if nhwc else wv.data.reshape(c, kh * kw)
             woff = self.weights.add(np.ascontiguousarray(wflat, np.float32), key=("dw", id(wv)))
@@ -1552,6 +1633,54 @@ class HipEmitter:
                 self._gemm_flops = counted
                 self._mb[id(node)] = saved
                 self._mb_skip |= skipped
+            self.emit("}")
+
+    def _expand_depthwise(self, node: Node, ex: Node) -> None:
+        """act_d(dw(act_e(ex(x)))) as one mgc_hip_expand_dw launch writing the depthwise node's
+        output; the expanded tensor is not written. When x or that output is a caller buffer
+        (a graph input or output) the generated code checks its 16-byte alignment and otherwise
+        runs the two convolutions apart."""
+        xv = ex.input(0)
+        nb, h, wd, cin = xv.tensor_type.shape
+        cexp = ex.input(1).tensor_type.shape[3]
+        g = ops.window_geometry(node, (h, wd), (3, 3))
+        oh, ow = g.out_hw
+        we = self._packed_b(ex.input(1).data.reshape(cin, cexp), ("conv", id(ex.input(1)), 0))[0]
+        we_ptr = we.split("g.b.p = ")[1].split(";")[0]
+        ebias_v = ex.optional_input(2)
+        ebias = self._vector_ptr(ebias_v, cexp, "Conv bias") if ebias_v is not None else "NULL"
+        wdw = np.ascontiguousarray(node.input(1).data.reshape(9, cexp), np.float32)
+        dwoff = self.weights.add(wdw, key=("dw", id(node.input(1))))
+        dbias_v = node.optional_input(2)
+        dbias = self._vector_ptr(dbias_v, cexp, "Conv bias") if dbias_v is not None else "NULL"
+        eact, elo, ehi = self._act(ex)
+        dact, dlo, dhi = self._act(node)
+        args = (f"mgc_hip_expand_dw_args xd; memset(&xd, 0, sizeof xd); xd.x = {self.fptr(xv)}; "
+                f"xd.we = (const float *){we_ptr}; xd.be = {ebias}; xd.wd = (const float *)(W + {dwoff}); "
+                f"xd.bd = {dbias}; xd.out = {self.fptr(node.output)}; xd.N = {nb}; xd.H = {h}; xd.W = {wd}; "
+                f"xd.Cin = {cin}; xd.Cexp = {cexp}; xd.SH = {g.strides[0]}; xd.SW = {g.strides[1]}; "
+                f"xd.PT = {g.pads[0]}; xd.PL = {g.pads[1]}; xd.OH = {oh}; xd.OW = {ow}; "
+                f"xd.act_e = {ACT_CODES[eact]}; xd.lo_e = {_f(elo)}; xd.hi_e = {_f(ehi)}; "
+                f"xd.act_d = {ACT_CODES[dact]}; xd.lo_d = {_f(dlo)}; xd.hi_d = {_f(dhi)};")
+        external = [v for v in (xv, node.output) if self.plan.location(v).kind in ("input", "output")]
+        if external:
+            cond = " && ".join(f"(((uintptr_t){self.ptr(v)} & 15) == 0)" for v in external)
+            self.emit(f"if ({cond}) {{")
+        self.emit("{ " + args + " mgc_hip_expand_dw(x, &xd); }")
+        self.count("expand_depthwise")
+        self._gemm_flops += ops.flops(ex) + ops.flops(node)
+        if external:
+            self.emit("} else {")
+            saved = self._xd.pop(id(node))
+            self._xd_skip.discard(id(ex))
+            counted = self._gemm_flops  # the fallback's launches run instead of the fused one
+            try:
+                self.op_FusedConv(ex)
+                self.op_FusedConv(node)
+            finally:
+                self._gemm_flops = counted
+                self._xd[id(node)] = saved
+                self._xd_skip.add(id(ex))
             self.emit("}")
 
     # -- space-to-depth convolution -------------------------------------------------------------
@@ -1799,6 +1928,10 @@ class HipEmitter:
                 i = index[id(n)]
                 flops[index[pw_id]] += flops[i]
                 flops[i] = 0
+        for dw_id, ex in self._xd.items():
+            i = index[id(ex)]
+            flops[index[dw_id]] += flops[i]
+            flops[i] = 0
         return flops
 
 

@@ -166,6 +166,7 @@ def test_depthwise_pointwise_pairs_join_one_gemm(monkeypatch):
     from ml_graph_compiler.codegen.hip import find_depthwise_pointwise
 
     monkeypatch.setattr(emitter, "FUSE_INVERTED_RESIDUAL", False)  # whole blocks: the next test
+    monkeypatch.setattr(emitter, "FUSE_EXPAND_DEPTHWISE", False)  # expansion + depthwise: below
     g = o3(builders.mobilenet_v2(batch=32))
     pairs = find_depthwise_pointwise(g)
     assert len(pairs) == 6
@@ -193,7 +194,7 @@ def test_depthwise_pointwise_pairs_join_one_gemm(monkeypatch):
     assert sorted(dw.input(0).tensor_type.shape[3] for dw in shallow.values()) == [32, 96]
 
 
-def test_inverted_residual_blocks_run_as_one_launch():
+def test_inverted_residual_blocks_run_as_one_launch(monkeypatch):
     """MobileNetV2 at batch 32: the five expanded blocks whose outputs have at least
     MBCONV_MIN_ROWS pixels (56 x 56 and 28 x 28, both strides, 16 / 24 / 32 input channels) each
     run as one mgc_hip_mbconv call; the first block (no expansion) keeps the fused depthwise
@@ -201,8 +202,10 @@ def test_inverted_residual_blocks_run_as_one_launch():
     call reads it, and the expansion and depthwise FLOPs are counted at the call's node. At
     batch 1 no block has enough output pixels."""
     from ml_graph_compiler import ops
+    from ml_graph_compiler.codegen import hip as emitter
     from ml_graph_compiler.codegen.hip import find_inverted_residuals
 
+    monkeypatch.setattr(emitter, "FUSE_EXPAND_DEPTHWISE", False)  # the smaller blocks: the next test
     g = o3(builders.mobilenet_v2(batch=32))
     blocks = find_inverted_residuals(g)
     shapes = sorted((ex.input(0).tensor_type.shape[1:], dw.output.tensor_type.shape[1:]) for ex, dw in blocks.values())
@@ -227,6 +230,54 @@ def test_inverted_residual_blocks_run_as_one_launch():
                 continue
             assert b.offset + b.size <= x.offset or x.offset + x.size <= b.offset
     assert not find_inverted_residuals(o3(builders.mobilenet_v2(batch=1)))
+
+
+def test_expansion_and_depthwise_run_as_one_launch():
+    """MobileNetV2 at batch 32: the ten expanded blocks on 14 x 14 and 7 x 7 inputs (64, 96 and
+    160 input channels, the 14 -> 7 block at stride 2) run their expansion and depthwise
+    convolution as one mgc_hip_expand_dw call writing the depthwise output (384-960 workgroups
+    of an image and 32 channels each); the projection stays a GEMM. Only the 28 -> 14 block
+    (28 x 28 input: too large a window) keeps its depthwise launch, so with the five whole-block
+    launches and the first block's fused depthwise GEMM one standalone depthwise launch is left
+    of 17. The block input stays alive (its arena block clear of everything placed) until the
+    call reads it, the expansion FLOPs are counted at the call's node, and at batch 1 (12-30
+    workgroups) and batch 8 the pairs stay apart."""
+    from ml_graph_compiler import ops
+    from ml_graph_compiler.codegen.hip import expand_dw_supported, find_expand_depthwise
+
+    g = o3(builders.mobilenet_v2(batch=32))
+    pairs = find_expand_depthwise(g)
+    shapes = sorted((ex.input(0).tensor_type.shape[1:], dw.output.tensor_type.shape[1:]) for dw_id, ex in pairs.items()
+                    for dw in g.nodes if id(dw) == dw_id)
+    assert shapes == ([((7, 7, 160), (7, 7, 960))] * 3 + [((14, 14, 64), (14, 14, 384))] * 4
+                      + [((14, 14, 96), (7, 7, 576))] + [((14, 14, 96), (14, 14, 576))] * 2)
+    gen = generate_hip(g, gemm_workspace=native.gemm_workspace_floats)
+    assert gen.kernels["expand_depthwise"] == 10 and gen.kernels["depthwise"] == 1
+    assert gen.kernels["gemm_mbconv"] == 5 and gen.kernels["gemm_depthwise"] == 1 and gen.kernels["gemm"] == 21
+    assert gen.source.count("mgc_hip_expand_dw(x, &xd);") == 10
+    assert sum(gen.node_flops) == sum(ops.flops(n) for n in g.nodes)
+    skipped = {id(ex) for ex in pairs.values()}
+    assert all(gen.node_flops[i] == 0 for i, n in enumerate(g.nodes) if id(n) in skipped)
+    order = {id(n): i for i, n in enumerate(g.nodes)}
+    by_value = {id(v): b for b in gen.plan.buffers for v in b.values}
+    for dw in g.nodes:
+        ex = pairs.get(id(dw))
+        if ex is None:
+            continue
+        x = by_value[id(ex.input(0))]
+        assert x.end >= order[id(dw)]
+        for b in gen.plan.buffers:
+            if b is x or not (b.start <= order[id(dw)] <= b.end):
+                continue
+            assert b.offset + b.size <= x.offset or x.offset + x.size <= b.offset
+    assert not find_expand_depthwise(o3(builders.mobilenet_v2(batch=1)))
+    assert not find_expand_depthwise(o3(builders.mobilenet_v2(batch=8)))
+    # the kernel's limits: window and row blocks per wave, per input width
+    assert expand_dw_supported(14, 14, 96, 576, 2, 7, 7) and expand_dw_supported(16, 14, 64, 32, 2, 8, 7)
+    assert not expand_dw_supported(28, 28, 32, 192, 2, 14, 14)
+    assert not expand_dw_supported(14, 16, 64, 32, 1, 14, 16)  # window 16 x 18 = 288 pixels
+    assert not expand_dw_supported(14, 14, 160, 960, 1, 14, 14)  # 160 channels: at most 64 pixels
+    assert not expand_dw_supported(7, 7, 160, 944, 1, 7, 7)  # a partial 32-channel slice
 
 
 def test_fusions_stay_below_the_fused_kernels_operand_limit(monkeypatch):
