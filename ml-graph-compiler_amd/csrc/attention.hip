@@ -331,10 +331,12 @@ __global__ void __launch_bounds__(256 * G) attention_kernel(const AttnDev p) {
 
 // Attention over at most 32 W keys (W <= 4) in one pass, for short sequences (BERT-base's 128
 // keys): one workgroup of W waves per (batch, head, 32 queries), wave w owning keys 32 w ..
-// 32 w + 31. No LDS tiles and no running softmax:
-//  1. every wave requests its operands straight into registers at once: the 32 query rows and
-//     its 32 key rows (16-byte loads: lane (li, lh) takes d = 32 c + 16 lh .. + 15 of row li),
-//     and the V elements its P V products need (below);
+// 32 w + 31. No running softmax:
+//  1. every global load goes out at once, all 16 bytes wide: wave w's share of the 32 query rows
+//     (rows w, w + W, ...), its 32 key rows (lane (li, lh) takes d = 32 c + 16 lh .. + 15 of key
+//     row li) and its 32 V rows; the query rows meet in LDS (each read from memory once per
+//     workgroup) and each wave's V rows go to an LDS tile of its own, from which the P V
+//     products read V by column;
 //  2. S^T = K Q^T on v_mfma_f32_32x32x2f32 (keys as rows, queries as columns), so register r of
 //     lane (li, lh) holds the score of key 8 (r / 4) + 4 lh + r % 4 and query li;
 //  3. the scores are scaled, biased and masked as the graph says, each query's maximum is taken
@@ -343,15 +345,18 @@ __global__ void __launch_bounds__(256 * G) attention_kernel(const AttnDev p) {
 //  4. O^T = V^T P^T: the score registers already are the B operand of this product (register r
 //     gives keys 8 (r / 4) + 4 lh + r % 4 of lane half lh, and the A operand takes V at the same
 //     keys), so P never goes through LDS;
-//  5. waves 1 .. W - 1 leave their O^T partials and row sums in LDS; wave 0 adds them in wave
-//     order, divides by the sum and writes each query's D outputs.
+//  5. waves 1 .. W - 1 leave their O^T partials (in their own V tiles) and row sums in LDS;
+//     wave 0 adds them in wave order, divides by the sum and writes each query's D outputs.
 // Terms are exp(t - m) with m the maximum over all keys (fp32 expf, as the streaming kernel),
 // and keys past Skv add nothing.
 template <int W, bool HAS_BIAS, bool HAS_MASK>
 __global__ void __launch_bounds__(64 * W) attention_short_kernel(const AttnDev p, int vec_out) {
+    constexpr int QP = 68;  // query tile pitch: the 16 rows one 16-byte read covers hit different banks
+    constexpr int VP = 72;  // V tile pitch: keys 4 apart (the two lane halves) land 32 banks apart
     __shared__ float wmax[W][32];
     __shared__ float wsum[W][32];
-    __shared__ float opart[W > 1 ? W - 1 : 1][32][64];
+    __shared__ __attribute__((aligned(16))) float qs[32 * QP];
+    __shared__ __attribute__((aligned(16))) float vs[W][32 * VP];  // later: the waves' O^T partials
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -375,9 +380,9 @@ __global__ void __launch_bounds__(64 * W) attention_short_kernel(const AttnDev p
     const int q = q0 + li;
     const int k0 = 32 * w;
 
-    // 1. operands: Q and K fragments (two 32-wide d chunks), V at the keys of each score register.
-    // Buffer loads: an element past S, Skv or D gets an offset past the resource's end and reads
-    // as zero, so the loads need no branches and the multiplies wait only for their own.
+    // 1. operands. Buffer loads: an element past S, Skv or D gets an offset past the resource's
+    // end and reads as zero, so the loads need no branches and the multiplies wait only for their
+    // own.
     constexpr unsigned OOB = 0x80000000u;
     const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
         (void *)qbase, (short)0, (int)(((long)(p.S - 1) * p.q_s + D) * 4), 0x00020000);
@@ -385,28 +390,35 @@ __global__ void __launch_bounds__(64 * W) attention_short_kernel(const AttnDev p
         (void *)kbase, (short)0, (int)(((long)(p.Skv - 1) * p.k_s + D) * 4), 0x00020000);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
         (void *)vbase, (short)0, (int)(((long)(p.Skv - 1) * p.v_s + D) * 4), 0x00020000);
-    f4 qf[2][4], kf[2][4];
+    // this wave's share of the 32 x 16 query quads: quads (w + W j) 64 + lane (row e / 16, d 4 (e % 16))
+    constexpr int QL = 32 * 16 / (64 * W) > 0 ? 32 * 16 / (64 * W) : 1;  // 16-byte quads per lane
+    f4 qv[QL];
+#pragma unroll
+    for (int j = 0; j < QL; ++j) {
+        const int e = (w + W * j) * 64 + lane;  // quad e of the 32 x 16 query quads
+        const int row = e >> 4, d = (e & 15) * 4;
+        const unsigned o = e < 512 && q0 + row < p.S && d < D ? (unsigned)((long)(q0 + row) * p.q_s + d) * 4u : OOB;
+        qv[j] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rq, o, 0, 0));
+    }
+    f4 kf[2][4];
     const bool q_ok = q < p.S, k_ok = k0 + li < p.Skv;
 #pragma unroll
     for (int c = 0; c < 2; ++c)
 #pragma unroll
         for (int s4 = 0; s4 < 4; ++s4) {
             const int d = 32 * c + 16 * lh + 4 * s4;
-            const unsigned oq = q_ok && d < D ? (unsigned)((long)q * p.q_s + d) * 4u : OOB;
             const unsigned ok = k_ok && d < D ? (unsigned)((long)(k0 + li) * p.k_s + d) * 4u : OOB;
-            qf[c][s4] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rq, oq, 0, 0));
             kf[c][s4] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rk, ok, 0, 0));
         }
-    float vf[2][16];
+    // this wave's 32 V rows: quad e = lane + 64 j of the 32 x 16 quads is row e / 16, d 4 (e % 16)
+    f4 vq[8];
 #pragma unroll
-    for (int db = 0; db < 2; ++db)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int key = k0 + 8 * (r >> 2) + 4 * lh + (r & 3);
-            const int d = 32 * db + li;
-            const unsigned ov = key < p.Skv && d < D ? (unsigned)((long)key * p.v_s + d) * 4u : OOB;
-            vf[db][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rv, ov, 0, 0));
-        }
+    for (int j = 0; j < 8; ++j) {
+        const int e = lane + 64 * j;
+        const int key = k0 + (e >> 4), d = (e & 15) * 4;
+        const unsigned o = key < p.Skv && d < D ? (unsigned)((long)key * p.v_s + d) * 4u : OOB;
+        vq[j] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rv, o, 0, 0));
+    }
 
     // the additive bias and the mask of this lane's 16 scores (when the graph has them: HAS_BIAS,
     // HAS_MASK), requested with the operands; the addresses are clamped into the tensors and the
@@ -424,6 +436,20 @@ __global__ void __launch_bounds__(64 * W) attention_short_kernel(const AttnDev p
     // some back to save registers and pay their latency one after another)
     __builtin_amdgcn_sched_barrier(0);
 
+    // the query rows into LDS; once every wave's share is there, each lane takes d = 32 c +
+    // 16 lh .. + 15 of query row li as the B operand
+#pragma unroll
+    for (int j = 0; j < QL; ++j) {
+        const int e = (w + W * j) * 64 + lane;
+        if (e < 512) *reinterpret_cast<f4 *>(&qs[(e >> 4) * QP + (e & 15) * 4]) = qv[j];
+    }
+    __syncthreads();
+    f4 qf[2][4];
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) qf[c][s4] = *reinterpret_cast<const f4 *>(&qs[li * QP + 32 * c + 16 * lh + 4 * s4]);
+
     // 2. S^T for this wave's 32 keys
     floatx16 acc;
 #pragma unroll
@@ -435,6 +461,14 @@ __global__ void __launch_bounds__(64 * W) attention_short_kernel(const AttnDev p
 #pragma unroll
             for (int e = 0; e < 4; ++e)
                 acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[c][s4][e], qf[c][s4][e], acc, 0, 0, 0);
+
+    // this wave's V rows into its tile (read back by this wave only)
+    float *const vt = vs[w];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int e = lane + 64 * j;
+        *reinterpret_cast<f4 *>(&vt[(e >> 4) * VP + (e & 15) * 4]) = vq[j];
+    }
 
     // 3. scores, the query's maximum over all keys, exp terms and this wave's sum
     const float scale = p.scale, fill = p.fill;
@@ -481,20 +515,25 @@ __global__ void __launch_bounds__(64 * W) attention_short_kernel(const AttnDev p
     for (int db = 0; db < 2; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
+    // V at key 8 (r / 4) + 4 lh + r % 4 (tile row) and d = 32 db + li
 #pragma unroll
-    for (int r = 0; r < 16; ++r) o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[0][r], acc[r], o[0], 0, 0, 0);
+    for (int r = 0; r < 16; ++r)
+        o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vt[(8 * (r >> 2) + 4 * lh + (r & 3)) * VP + li], acc[r], o[0], 0, 0, 0);
     if (D > 32) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) o[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[1][r], acc[r], o[1], 0, 0, 0);
+        for (int r = 0; r < 16; ++r)
+            o[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(vt[(8 * (r >> 2) + 4 * lh + (r & 3)) * VP + 32 + li], acc[r], o[1],
+                                                       0, 0, 0);
     }
 
     // 5. wave order sum of the partials; register r of o[db] is d = 32 db + 8 (r / 4) + 4 lh + r % 4
     if (W > 1) {
         if (w > 0) {
+            // into this wave's own V tile, whose last reads (this wave's P V operands) came before
 #pragma unroll
             for (int db = 0; db < 2; ++db)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) opart[w - 1][16 * db + r][lane] = o[db][r];
+                for (int r = 0; r < 16; ++r) vt[(16 * db + r) * 64 + lane] = o[db][r];
             if (lh == 0) wsum[w][li] = l;
         }
         __syncthreads();
@@ -504,7 +543,7 @@ __global__ void __launch_bounds__(64 * W) attention_short_kernel(const AttnDev p
 #pragma unroll
             for (int db = 0; db < 2; ++db)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) o[db][r] += opart[w2 - 1][16 * db + r][lane];
+                for (int r = 0; r < 16; ++r) o[db][r] += vs[w2][(16 * db + r) * 64 + lane];
             l += wsum[w2][li];
         }
     }

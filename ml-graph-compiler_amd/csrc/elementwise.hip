@@ -724,7 +724,10 @@ __global__ void space_to_depth_kernel(int C, int H2, int W2, int total, FastDiv 
 // 16-byte reads (neighbouring threads read neighbouring 16 bytes of a row). The pair's 8 C output
 // values are contiguous and so are the 64 pairs of a wave, so the wave stages its 64 x 8 C values
 // in LDS and writes them back as whole contiguous 1 KB rows (lane l writes 16 bytes at 16 l of
-// each), instead of 16-byte pieces 32 C bytes apart.
+// each), instead of 16-byte pieces 32 C bytes apart. Each wave takes several 64-pair blocks in
+// turn and requests the next block's input before it stages and stores the current one, so its
+// reads of one block overlap its writes of the previous (one read round and one write round per
+// launch otherwise, each waiting for the whole chip's).
 template <int C>
 __global__ void __launch_bounds__(256) space_to_depth_vec_kernel(int H2, int W4, int total, FastDiv div_w4,
                                                                  FastDiv div_h2, const float *in, float *out) {
@@ -734,8 +737,8 @@ __global__ void __launch_bounds__(256) space_to_depth_vec_kernel(int H2, int W4,
     const int lane = threadIdx.x & 63;
     float *const buf = stage[threadIdx.x >> 6];
     const int step = gridDim.x * blockDim.x;
-    // every lane of a wave runs the same trips (the bound is the wave's first pair)
-    for (int base = blockIdx.x * blockDim.x + (threadIdx.x & ~63); base < total; base += step) {
+    // the 2 x 4 input block of every channel of the lane's pair in the wave's block at base
+    auto load = [&](int base, float4 (&row)[C][2]) __attribute__((always_inline)) {
         const int idx = base + lane;
         if (idx < total) {
             const int t = fdiv(idx, div_w4);
@@ -743,22 +746,30 @@ __global__ void __launch_bounds__(256) space_to_depth_vec_kernel(int H2, int W4,
             const int b = fdiv(t, div_h2);
             const int i = t - b * H2;
             const float *src = in + (long)b * C * H * W + (long)(2 * i) * W + 4 * jp;
-            float4 row[C][2];
 #pragma unroll
             for (int c = 0; c < C; ++c)
 #pragma unroll
                 for (int dy = 0; dy < 2; ++dy)
                     row[c][dy] = *reinterpret_cast<const float4 *>(src + (long)c * H * W + dy * W);
-            // output pixel q of the pair holds value (dy * 2 + dx) * C + c = input (c, dy, 2 q + dx)
+        }
+    };
+    // every lane of a wave runs the same trips (the bound is the wave's first pair)
+    int base = blockIdx.x * blockDim.x + (threadIdx.x & ~63);
+    float4 cur[C][2], nxt[C][2];
+    if (base < total) load(base, cur);
+    for (; base < total; base += step) {
+        if (base + step < total) load(base + step, nxt);
+        // output pixel q of the pair holds value (dy * 2 + dx) * C + c = input (c, dy, 2 q + dx)
+        if (base + lane < total) {
             float *v = buf + lane * PAIR;
 #pragma unroll
             for (int c = 0; c < C; ++c)
 #pragma unroll
                 for (int dy = 0; dy < 2; ++dy) {
-                    v[(dy * 2) * C + c] = row[c][dy].x;
-                    v[(dy * 2 + 1) * C + c] = row[c][dy].y;
-                    v[4 * C + (dy * 2) * C + c] = row[c][dy].z;
-                    v[4 * C + (dy * 2 + 1) * C + c] = row[c][dy].w;
+                    v[(dy * 2) * C + c] = cur[c][dy].x;
+                    v[(dy * 2 + 1) * C + c] = cur[c][dy].y;
+                    v[4 * C + (dy * 2) * C + c] = cur[c][dy].z;
+                    v[4 * C + (dy * 2 + 1) * C + c] = cur[c][dy].w;
                 }
         }
         __builtin_amdgcn_wave_barrier();
@@ -772,6 +783,10 @@ __global__ void __launch_bounds__(256) space_to_depth_vec_kernel(int H2, int W4,
             if (e < n * 2 * C) dst4[e] = src4[e];
         }
         __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+            for (int dy = 0; dy < 2; ++dy) cur[c][dy] = nxt[c][dy];
     }
 }
 
@@ -940,7 +955,8 @@ extern "C" void mgc_hip_space_to_depth(mgc_hip_exec *x, int N, int C, int H, int
     }
     if (C <= 4 && W % 4 == 0 && ((uintptr_t)in & 15) == 0) {
         const long pairs = total / 2;
-        const dim3 grid(blocks_for(pairs, 256, 16384));
+        // three 64-pair blocks per wave, so that each wave's reads overlap its previous writes
+        const dim3 grid(blocks_for((pairs + 2) / 3, 256, 16384));
         const FastDiv dw4 = make_fastdiv((unsigned)(W / 4)), dh2 = make_fastdiv((unsigned)(H / 2));
         switch (C) {
         case 1: MGC_LAUNCH(x, space_to_depth_vec_kernel<1>, grid, dim3(256), 0, H / 2, W / 4, (int)pairs, dw4, dh2, in, out); break;
