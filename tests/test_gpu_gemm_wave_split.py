@@ -3,7 +3,7 @@ the library runs them on the wave-split kernel (32 x 32 tiles, the K range dealt
 waves of a workgroup, partial tiles summed in LDS) instead of a K split plus a reduction
 launch (or, for deep K over few rows, with a K split of its own, four times as many waves
 sharing K). Shapes chosen so that the selection applies: K of at least 512, a K split that the
-64 x 64 tiling would take, at most 512 tiles of 32 x 32 (times the split). Ragged M, N and K, a partial last K
+64 x 64 tiling would take, at most 512 tiles of 32 x 32 (times the split; 768 without a split). Ragged M, N and K, a partial last K
 stage, bias / residual / activation epilogues, strided and dilated windows; compared with the
 oracle (rtol 1e-4)."""
 from __future__ import annotations
@@ -26,6 +26,7 @@ pytestmark = pytest.mark.gpu
         (300, 96, 800, "residual"),
         (128, 2304, 768, "bias_relu"),   # 288 tiles: two workgroups per CU
         (196, 1024, 256, "bias_relu"),   # K below the split threshold on 64 too few tiles
+        (6272, 96, 576, "bias_relu"),    # 588 tiles of 32 x 32 (up to three per CU), no K split
         (1, 1000, 2048, "bias_relu"),    # deep K over one row: wave split plus a K split
     ],
 )
