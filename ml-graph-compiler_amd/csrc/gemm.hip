@@ -2759,6 +2759,14 @@ static int use_tile16(int M, int N, int K, int wsk) {
 // groups of a multiple of 64, a concatenated K a first part of a multiple of 64.
 static const int kQuarterTiles = 64;
 static const int kQuarterMinK = 128;
+// A launch of between one and two tiles per CU (256 < T < 512) without a K split runs its first
+// T / 2 tiles whole and the rest as quarters, so the CUs share the second half evenly instead of
+// T - 256 of them running a second whole tile: ResNet-50 b32's five 392-tile 1 x 1 layers (K
+// 1024) 38.1 -> 35.3 us, forward 2.767 -> 2.753 ms. Deep K only: the quarters' fixed costs
+// weigh more where K is short, and launches that split K over workgroups already fill the chip
+// (as half whole tiles and half quarters instead of a split and reduction they were slower:
+// ResNet-50 b32 2.774 -> 2.950 ms).
+static const int kHalfQuarterMinK = 512;
 
 static bool quarter_tiles_ok(int am, const GemmDev &p) {
     return am == AM_VEC || (am == AM_CONV_VEC && p.a.cg % 64 == 0) || (am == AM_CAT && p.k1 % 64 == 0);
@@ -3326,6 +3334,10 @@ static void gemm_launch(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const LnTai
                 if (tiles >= kCUs && rest > 0 && rest <= kQuarterTiles && p.K >= kQuarterMinK) {
                     fam = MGC_GEMM_QUARTER;
                     p.nfull = tiles - rest;
+                } else if (tiles > kCUs && tiles < 2 * kCUs && p.K >= kHalfQuarterMinK) {
+                    // between one and two tiles per CU: half the tiles whole, half as quarters
+                    fam = MGC_GEMM_QUARTER;
+                    p.nfull = tiles / 2;
                 }
             }
         }

@@ -6,7 +6,8 @@ in wave order (csrc/gemm.hip, gemm_dma_tile with QUARTER). Shapes chosen so that
 applies: ragged M and N (quarters partly or wholly past the matrix edge), K not a multiple of
 the 64-k quarter stage, N not a multiple of 4 (scalar stores), convolution windows over 64 and
 128 channels, and a 96-channel window that keeps whole tiles (quarter stages need channel
-groups of a multiple of 64); compared with the oracle."""
+groups of a multiple of 64), and launches of between one and two tiles per CU with K >= 512,
+whose second half of tiles all run as quarters (kHalfQuarterMinK); compared with the oracle."""
 from __future__ import annotations
 
 import numpy as np
@@ -27,6 +28,8 @@ pytestmark = pytest.mark.gpu
                                         # the last 64-k stage holds 8 k
         (5000, 832, 256, "none"),       # 1027 tiles: four full rounds, then 3 tiles in quarters
         (16640, 50, 256, "bias_relu"),  # 260 tiles, N not a multiple of 4
+        (6272, 256, 1024, "bias_relu"), # 392 tiles (1.5 per CU), K >= 512: 196 whole, 784 quarters
+        (7990, 256, 600, "residual"),   # 500 tiles: 250 whole, the last row of quarters past M
     ],
 )
 def test_quarter_tail_gemm(m, n, k, epilogue, hip_cache):
