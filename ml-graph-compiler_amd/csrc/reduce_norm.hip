@@ -973,7 +973,11 @@ extern "C" void mgc_hip_pool(mgc_hip_exec *x, int nhwc, int is_max, int N, int H
 // hipEvent timing of 50 launches, against the row-by-row kernel with four outputs per thread:
 // 56 x 56 x 144 16.9 vs 28.1 us (85% of 8 TB/s), 28 x 28 x 192 8.2 vs 12.2 us; the preloading
 // kernel on the 14 x 14 and 7 x 7 layers was 0-8% slower than the two-output column kernel.
-static bool dw3_preload_s1(int OW) { return OW >= 28; }
+// Large launches whose input does not stay in the caches keep the row-by-row kernel with four
+// outputs per thread (fewer refetches of the shared input columns): 112 x 112 x 144 at batch 32
+// (231 MB of input) 121 us against 198 us with the preloading kernel.
+static bool dw3_preload_s1(int OW, long in_bytes) { return OW >= 28 && in_bytes <= (64L << 20); }
+static int dw3_tile_s1(int OW) { return OW >= 28 ? 4 : 2; }
 
 // The LDS-tiled 3x3 kernel (equal strides) for launches of at most 2^18 output quads: there a
 // workgroup's three loads per thread, all issued before the first is used, beat the per-thread
@@ -1004,10 +1008,14 @@ extern "C" void mgc_hip_depthwise(mgc_hip_exec *x, int nhwc, int N, int H, int W
             MGC_LAUNCH(x, kern, dim3((unsigned)blocks), dim3(256), 0, g, tiles_w, tiles_h, cgroups, in, w, bias,
                        res, out);
         } else if (vec && k3) {
-            const int owb = (OW + 1) / 2;
+            const bool pre = SW == 2 || dw3_preload_s1(OW, (long)N * H * W * C * 4);
+            const int tile = pre ? 2 : dw3_tile_s1(OW);
+            const int owb = (OW + tile - 1) / tile;
             const int quads = (int)((long)N * OH * owb * (C / 4));
             auto kern = SW == 2 ? depthwise3x3_nhwc_preload<2, 2>
-                                : (dw3_preload_s1(OW) ? depthwise3x3_nhwc_preload<1, 2> : depthwise3x3_nhwc_vec4<1, 2>);
+                        : pre   ? depthwise3x3_nhwc_preload<1, 2>
+                        : tile == 4 ? depthwise3x3_nhwc_vec4<1, 4>
+                                    : depthwise3x3_nhwc_vec4<1, 2>;
             MGC_LAUNCH(x, kern, dim3(blocks_for(quads, 256, 16384)), dim3(256), 0, g,
                        make_fastdiv((unsigned)(C / 4)), make_fastdiv((unsigned)owb), make_fastdiv((unsigned)OH),
                        quads, in, w, bias, res, out);

@@ -332,10 +332,12 @@ def test_depthwise_with_residual_and_clip(hip_cache):
     [
         ((1, 32, 30, 30), 1),     # at most 2^18 output quads: the LDS-tiled kernel
         ((1, 48, 61, 61), 2),
-        ((2, 64, 112, 112), 1),   # more: the column kernel, eight outputs per thread
-        ((2, 64, 60, 60), 1),     # ... four outputs per thread (60 is not a multiple of 8)
-        ((2, 64, 240, 240), 2),   # ... stride 2, two outputs per thread
-        ((64, 64, 20, 20), 1),    # ... a narrow image, two outputs per thread
+        ((2, 64, 60, 60), 1),
+        ((2, 64, 112, 112), 1),   # more, wide rows: the preloading kernel, two outputs per thread
+        ((2, 64, 240, 240), 2),   # ... stride 2
+        ((64, 64, 20, 20), 1),    # narrow rows: the column kernel, two outputs per thread
+        ((1, 1024, 130, 130), 1), # wide rows over 64 MB of input: the column kernel, four outputs
+                                  # per thread (130 is not a multiple of four)
     ],
 )
 def test_depthwise_kernels_by_launch_size(x_shape, stride, hip_cache):
