@@ -825,7 +825,9 @@ def main() -> int:
         return 0
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: every GPU box here has one MI355X; "
-                                   "use --gpus 1 (batch sharding across GPUs is described in DESIGN.md)"}))
+                                   "use --gpus 1. Across GPUs the path shards by batch: each GPU replays the same captured "
+                                   "graph on its share of the images or sequences with the weights replicated, and no "
+                                   "device collective is needed"}))
         return 2
     cache = Path(args.cache)
     batch = 128 if args.workload == "single_gemm" else args.batch

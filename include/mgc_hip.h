@@ -162,8 +162,9 @@ enum {
     MGC_GEMM_NARROW = 3,   /* 128 x 32 tiles (four waves along M) */
     MGC_GEMM_WSPLIT = 4,   /* 32 x 32 tiles, K stages dealt to four waves */
     MGC_GEMM_WSPLIT16 = 5, /* 16 x 16 tiles, K stages dealt to four or eight waves */
-    MGC_GEMM_STREAM = 6,   /* short-K streaming kernel: row-major A, K <= 32, batch 1, no K split,
-                              activation none / relu / clip */
+    MGC_GEMM_STREAM = 6,   /* short-K streaming kernel: row-major A with K <= 32, or an NHWC image
+                              of one channel group with K <= 48; batch 1, no K split, a column
+                              bias (or none), activation none / relu / clip */
     MGC_GEMM_REGISTER = 7  /* register-staged operands: every operand form (gemm_mfma_kernel) */
 };
 

@@ -7,7 +7,7 @@ shapes its rule sends it. This test drives mgc_hip_gemm directly through the C A
 tests pin its C kernels' blocking to reach their edge paths (tests/test_codegen.py:444-455)
 and sweep GEMM shapes with a property test (:488-516):
 
-* M, N in {1, 3, 31, 33, 63, 65, 129}; K in {1, 2, 31, 33, 64, 65, 4097} plus the multiples of
+* M, N in {1, 3, 31, 33, 63, 65, 129} (N also 4 and 68); K in {1, 2, 31, 33, 64, 65, 4097} plus the multiples of
   four {4, 8, ..., 32, 36, 68, 4096} that the k-contiguous DMA kernels (and, up to 32, the
   streaming kernel) need;
 * every family: 64 x 64 DMA tiles, quarter tiles, 128 x 32 tiles, 32 x 32 and 16 x 16 wave
@@ -19,7 +19,8 @@ and sweep GEMM shapes with a property test (:488-516):
 Each call's output (the buffer is NaN-filled before the call, so an element the kernel skips
 fails) is compared with float64 numpy plus the oracle's activations at the single-GEMM bound
 (1e-4 absolute + 1e-4 relative). A family the operands do not suit (the DMA kernels need
-K % 4 == 0, the streaming kernel K <= 32 and relu / clip / none with a column bias, quarter
+K % 4 == 0, the streaming kernel K <= 32 (48 over an image) and relu / clip / none with a
+column bias, quarter
 tiles no K split) must refuse the call with MGC_ERR_ARGS, naming the family; the test
 predicts which calls are refused from those documented rules and checks both ways. NHWC
 implicit-GEMM convolutions (3 x 3, strides 1 and 2, ragged images) run through every family
@@ -43,6 +44,7 @@ pytestmark = pytest.mark.gpu
 MN = (1, 3, 31, 33, 63, 65, 129)
 K_ANY = (1, 2, 31, 33, 64, 65, 4097)
 K_VEC = (4, 8, 12, 16, 20, 24, 28, 32, 36, 68, 4096)
+N_VEC = (4, 68)  # column counts the streaming kernel takes (N % 4 == 0)
 SPLIT_FAMILIES = ("tiled", "narrow", "wsplit", "wsplit16", "register")
 FAMILIES = ("tiled", "quarter", "narrow", "wsplit", "wsplit16", "stream", "register")
 LO, HI = -0.5, 0.75
@@ -106,7 +108,7 @@ class Runner:
         return bias[: (n if ep["bias_mode"] == 1 else m)], res
 
 
-def _accepts(family: str, k: int, split: int, ep: dict, conv: bool = False, cg: int = 0) -> bool:
+def _accepts(family: str, k: int, split: int, ep: dict, conv: bool = False, cg: int = 0, n: int = 4) -> bool:
     """Whether the library must run (True) or refuse (False) this forced call, from the
     families' documented limits (include/mgc_hip.h)."""
     dma = k % 4 == 0 and (not conv or cg % 4 == 0)
@@ -117,7 +119,7 @@ def _accepts(family: str, k: int, split: int, ep: dict, conv: bool = False, cg: 
     if family == "quarter":
         return split == 1 and (not conv or cg % 64 == 0)
     if family == "stream":
-        return (not conv and k <= 32 and split == 1 and ep["bias_mode"] != 2
+        return (k <= (48 if conv else 32) and split == 1 and ep["bias_mode"] != 2
                 and ep["act"] in ("none", "relu", "clip"))
     return True
 
@@ -143,7 +145,7 @@ def test_forced_family_on_edge_shapes(family, runner):
     splits = (1, 2, 3) if family in SPLIT_FAMILIES else (1,)
     ran = refused = 0
     worst = 0.0
-    for i, (m, n, k) in enumerate(itertools.product(MN, MN, K_ANY + K_VEC)):
+    for i, (m, n, k) in enumerate(itertools.product(MN, MN + N_VEC, K_ANY + K_VEC)):
         a = rng.standard_normal((m, k)).astype(np.float32)
         b = (rng.standard_normal((k, n)) / np.sqrt(k)).astype(np.float32)
         runner.hip.put(runner.a, a)
@@ -164,7 +166,7 @@ def test_forced_family_on_edge_shapes(family, runner):
             bias, res = runner.epilogue(args, ep, m, n, rng)
             code, got = runner.run(args, m, n)
             what = f"{family} split {split} {m}x{n}x{k} {ep}"
-            if not _accepts(family, k, split, ep):
+            if not _accepts(family, k, split, ep, n=n):
                 assert code == MGC_ERR_ARGS, f"{what}: expected a refusal, got {code}"
                 assert f"kernel family {GEMM_FAMILIES[family]}".encode() in runner.lib.mgc_hip_last_error()
                 refused += 1
@@ -178,6 +180,7 @@ def test_forced_family_on_edge_shapes(family, runner):
 
 CONVS = [  # (images, H, W, C, Kout, stride, pad)
     (1, 7, 9, 4, 5, 1, 1),
+    (2, 9, 8, 4, 40, 2, 1),   # K 36: also the streaming kernel, two 32-column blocks, ragged rows
     (2, 11, 6, 16, 33, 2, 1),
     (1, 9, 9, 64, 65, 1, 1),
     (3, 6, 10, 8, 3, 2, 0),
@@ -185,10 +188,11 @@ CONVS = [  # (images, H, W, C, Kout, stride, pad)
 ]
 
 
-@pytest.mark.parametrize("family", [f for f in FAMILIES if f != "stream"])
+@pytest.mark.parametrize("family", FAMILIES)
 def test_forced_family_on_nhwc_convolutions(family, runner):
     """3 x 3 NHWC convolutions as implicit GEMMs (A read through im2col, B packed [Kout][9 C])
-    through every family that reads an image, against a direct float64 convolution."""
+    through every family, against a direct float64 convolution (the streaming kernel takes the
+    windows of K = 9 C <= 48: the 4-channel cases)."""
     rng = np.random.default_rng(100 + GEMM_FAMILIES[family])
     for j, (nimg, h, w, c, kout, s, pad) in enumerate(CONVS):
         oh, ow = (h + 2 * pad - 3) // s + 1, (w + 2 * pad - 3) // s + 1
@@ -212,7 +216,7 @@ def test_forced_family_on_nhwc_convolutions(family, runner):
             bias, res = runner.epilogue(args, ep, m, kout, rng)
             code, got = runner.run(args, m, kout)
             what = f"{family} split {split} conv {nimg}x{h}x{w}x{c}->{kout} s{s} p{pad} {ep}"
-            if not _accepts(family, k, split, ep, conv=True, cg=c):
+            if not _accepts(family, k, split, ep, conv=True, cg=c, n=kout):
                 assert code == MGC_ERR_ARGS, f"{what}: expected a refusal, got {code}"
                 continue
             assert code == MGC_OK, f"{what}: {runner.lib.mgc_hip_last_error()}"

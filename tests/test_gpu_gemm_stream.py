@@ -2,11 +2,13 @@
 straight into registers, its column group of B held in registers, no LDS).
 
 Selected for a strided A with unit column stride, a constant (packed) B, K <= 32 with K % 4 == 0,
-at least 4096 rows and at most 768 columns: the expand and project 1 x 1 convolutions of
-MobileNet-style blocks at large batch. The cases cover both k layouts (K <= 16: eight k per
-lane half; K <= 32: sixteen), K that leaves part of a lane half unused, one to six 32-column
-blocks per group and several groups, ragged M and N, and the bias / residual / activation
-epilogue; compared with the oracle.
+at least 4096 rows and at most 768 columns: the expand and project 1 x 1 convolutions of MobileNet-style blocks at large batch; and
+over an NHWC image read through its implicit im2col (one channel group, K <= 48, at most 32
+columns): MobileNetV2's stem. The cases cover the k layouts (K <= 16: eight k per lane half;
+K <= 32: sixteen; K <= 48: twenty-four), K that leaves part of a lane half unused, one to six
+32-column blocks per group and several groups, ragged M and N,
+the bias / residual / activation epilogue, and convolution windows with padding and stride;
+compared with the oracle.
 """
 from __future__ import annotations
 
@@ -89,3 +91,30 @@ def test_stream_pointwise_conv(n, cin, cout, hw, residual, hip_cache):
     infer_shapes(g)
     check_hip(g, feeds={"x": rng.standard_normal((n, cin, hw, hw)).astype(np.float32)}, cache=hip_cache,
               opt="O3", rtol=2e-5, atol=2e-5)
+
+
+@pytest.mark.parametrize(
+    "n, h, w, c, kout, k, stride, pad",
+    [
+        (8, 64, 64, 12, 32, 2, 1, 0),   # MobileNetV2's stem form: 2 x 2 over a space-to-depth copy (K 48)
+        (4, 70, 66, 8, 16, 2, 1, 1),    # K 32 with a padded border, ragged rows
+        (5, 61, 63, 4, 24, 3, 2, 1),    # 3 x 3 stride 2 over 4 channels (K 36), ragged rows
+    ],
+)
+def test_stream_convolution(n, h, w, c, kout, k, stride, pad, hip_cache):
+    """NHWC convolutions whose im2col K fits the streaming kernel (>= 4096 output pixels)."""
+    print(f"[gpu] stream conv {n}x{h}x{w}x{c} -> {kout} k{k} s{stride} p{pad}", flush=True)
+    rng = np.random.default_rng(n + h + c + kout)
+    g = Graph("stream_conv")
+    x = g.add_input("x", TensorType("float32", (n, h, w, c)))
+    wt = g.constant((rng.standard_normal((k, k, c, kout)) / np.sqrt(k * k * c)).astype(np.float32), "w")
+    b = g.constant(rng.standard_normal(kout).astype(np.float32), "b")
+    y = g.add_node("FusedConv", [x, wt, b], 1,
+                   {"kernel_shape": [k, k], "pads": [pad] * 4, "strides": [stride, stride], "layout": "NHWC",
+                    "activation": "clip", "clip_min": 0.0, "clip_max": 6.0}, name="conv").output
+    g.add_output(y, "y")
+    infer_shapes(g)
+    oh = (h + 2 * pad - k) // stride + 1
+    ow = (w + 2 * pad - k) // stride + 1
+    assert n * oh * ow >= 4096
+    check_hip(g, {"x": rng.standard_normal((n, h, w, c)).astype(np.float32)}, hip_cache, opt="O0")
