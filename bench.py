@@ -185,7 +185,9 @@ def gemm_roofline(graph, model, replays: int) -> dict:
     achieved = flops / secs / 1e12 if secs > 0 else 0.0
     return {
         "bound": "mfma",
-        "kernel": "gemm_{dma,dma_tail,dma_wsplit,mfma}_kernel (fp32 MFMA implicit-GEMM conv / GEMM family)",
+        "kernel": ("the fp32 MFMA GEMM family: every GEMM / implicit-GEMM convolution kernel (gemm_dma, "
+                   "gemm_dma_tail, gemm_dma_wsplit, gemm_dma_wsplit16, gemm_stream, gemm_mfma, gemm_dw, "
+                   "gemm_expand_dw, mbconv), split-K reductions apart"),
         "achieved": round(achieved, 2),
         "peak": MFMA_FP32_PEAK_TFLOPS,
         "unit": "TFLOP/s",
