@@ -2792,6 +2792,10 @@ static int use_tile16(int M, int N, int K, int wsk) {
 // groups of a multiple of 64, a concatenated K a first part of a multiple of 64.
 static const int kQuarterTiles = 64;
 static const int kQuarterMinK = 128;
+// With K >= 512 a quarter's fixed costs weigh less, and tails of up to 128 tiles run as quarters
+// too: BERT-base b16's 1152-tile Q/K/V projection (K 768), forward 3.434 -> 3.381 ms; GPT-2 and
+// ResNet-50 have no such launch and are unchanged.
+static const int kQuarterTilesDeepK = 128;
 // A launch of between one and two tiles per CU (256 < T < 512) without a K split runs its first
 // T / 2 tiles whole and the rest as quarters, so the CUs share the second half evenly instead of
 // T - 256 of them running a second whole tile: ResNet-50 b32's five 392-tile 1 x 1 layers (K
@@ -3376,7 +3380,8 @@ static void gemm_launch(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const LnTai
             if (fam == MGC_GEMM_TILED && p.split == 1 && batch == 1 && quarter_tiles_ok(am, p)) {
                 const int tiles = ((p.M + 63) / 64) * ((p.N + 63) / 64);
                 const int rest = tiles % kCUs;
-                if (tiles >= kCUs && rest > 0 && rest <= kQuarterTiles && p.K >= kQuarterMinK) {
+                if (tiles >= kCUs && rest > 0 && p.K >= kQuarterMinK &&
+                    (rest <= kQuarterTiles || (rest <= kQuarterTilesDeepK && p.K >= kHalfQuarterMinK))) {
                     fam = MGC_GEMM_QUARTER;
                     p.nfull = tiles - rest;
                 } else if (tiles > kCUs && tiles < 2 * kCUs && p.K >= kHalfQuarterMinK) {

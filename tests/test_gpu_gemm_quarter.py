@@ -1,5 +1,6 @@
 """64 x 64 GEMM launches whose tile count is just past a multiple of the 256 CUs: the last r
-tiles (0 < r <= 64, K >= 128, csrc/gemm.hip kQuarterTiles / kQuarterMinK) run as 4 r quarter
+tiles (0 < r <= 64, K >= 128, or r <= 128 with K >= 512: csrc/gemm.hip kQuarterTiles,
+kQuarterMinK, kQuarterTilesDeepK) run as 4 r quarter
 tiles of 32 x 32, the four waves of a quarter's
 workgroup each taking a quarter of K (16 of every 64 k) and the partial quarters summed in LDS
 in wave order (csrc/gemm.hip, gemm_dma_tile with QUARTER). Shapes chosen so that the tail
@@ -28,6 +29,7 @@ pytestmark = pytest.mark.gpu
                                         # the last 64-k stage holds 8 k
         (5000, 832, 256, "none"),       # 1027 tiles: four full rounds, then 3 tiles in quarters
         (16640, 50, 256, "bias_relu"),  # 260 tiles, N not a multiple of 4
+        (3264, 768, 520, "bias_relu"),  # 612 tiles, K >= 512: a 100-tile tail in quarters
         (6272, 256, 1024, "bias_relu"), # 392 tiles (1.5 per CU), K >= 512: 196 whole, 784 quarters
         (7990, 256, 600, "residual"),   # 500 tiles: 250 whole, the last row of quarters past M
     ],
