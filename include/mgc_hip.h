@@ -264,6 +264,32 @@ typedef struct {
 int mgc_hip_mbconv_supported(int Cin, int Cexp, int Cout, int stride);
 void mgc_hip_mbconv(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const mgc_hip_mbconv_args *mb);
 
+/* The same launch when the block input is itself a convolution's output that never goes to
+ * memory: MobileNetV2's stem (a 3 x 3 convolution of the 3-channel image with its activation)
+ * ahead of the first block (3 x 3 depthwise with its activation, 1 x 1 projection). E above is
+ * then the stem's output,
+ *   E[n][y][z][k] = act_e(be[k] + sum_{i,j < 3, c < 3} img(n, c, y SH - PT + i, z SW - PL + j) we[k 32 + (3 i + j) 3 + c])
+ * with img(n, c, r, s) = st->img[n sn + c sc + r sh + s sw] (zero outside the H x W image), and
+ * zero for (y, z) outside the mb->H x mb->W stem output: an NCHW graph input is read in place,
+ * with no NHWC copy. mb->x is not read; mb->Cin is 32 (the 27 window values, padded), mb->we
+ * [Cexp][32] with columns 27..31 zero, mb->H x mb->W the stem's output size. Replaces the
+ * stem's mgc_gemm over its im2col operand and the block's mgc_depthwise_nhwc and mgc_gemm
+ * (src/ml_graph_compiler/codegen/runtime/mgc_kernels.c:86-133, 370-396, 455-473; three calls
+ * in the reference's C backend, codegen/c.py:1102-1226). Needs the shapes
+ * mgc_hip_mbconv_stem_supported accepts (C = 3, KH = KW = 3; the mbconv limits for Cexp, N and
+ * the depthwise stride), stem strides SH, SW of 1 or 2, non-negative padding and image strides, img 4-byte aligned and the image
+ * below 2 GiB, and otherwise what mgc_hip_mbconv needs; sets the launch error otherwise. */
+typedef struct {
+    const float *img;       /* the stem convolution's input image */
+    int C, H, W;            /* its channels and size */
+    long sn, sc, sh, sw;    /* element strides of image, channel, row and column (NCHW: C H W, H W, W, 1) */
+    int KH, KW, SH, SW, PT, PL; /* the stem's window (3 x 3), strides (1 or 2) and top / left padding */
+} mgc_hip_stem_args;
+
+int mgc_hip_mbconv_stem_supported(int C, int KH, int KW, int Cexp, int Cout, int stride);
+void mgc_hip_mbconv_stem(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const mgc_hip_mbconv_args *mb,
+                         const mgc_hip_stem_args *st);
+
 /* The expansion and depthwise convolutions of an inverted-residual block as one launch, with
  * the expanded tensor never in memory:
  *   out[n][oh][ow][k] = act_d(bd[k] + sum_{i,j < 3} E[n][oh SH - PT + i][ow SW - PL + j][k] wd[(3 i + j) Cexp + k])

@@ -2017,10 +2017,16 @@ struct MbDev {
     int H, W, Cexp, PT, PL, OH, OW;
     float lo_e, hi_e, lo_d, hi_d;  // both activations as clamps: relu [0, inf), clip [lo, hi]
     int tiles_h, tiles_w;  // 8 x 8 output-pixel tiles per image
-    long x_bytes;          // bytes of x reachable from d.x
+    long x_bytes;          // bytes of x reachable from d.x (of img for a stem block)
+    // stem blocks only: the block input is the 3 x 3, 3-channel stem convolution of img, read
+    // through element strides (image, channel, row, column)
+    const float *img;
+    int iH, iW, iSH, iSW, iPT, iPL;
+    unsigned isn, isc, ish, isw;
 };
 
 constexpr int kMbMaxCexp = 256;
+constexpr int kStemC = 3, kStemK = 3;  // the stem convolution a stem block evaluates: 3 x 3 over 3 channels
 
 // One workgroup (256 threads, four waves) computes an 8 x 8 block of output pixels of one image
 // times all N <= 32 projection channels; K runs over the Cexp expanded channels in stages of 32.
@@ -2044,8 +2050,18 @@ constexpr int kMbMaxCexp = 256;
 //    lane supplies for rows 32 wm .. 32 wm + 31, with the projection weights B[li][k] in
 //    registers (loaded a stage ahead). Biases and depthwise weights sit in LDS for the tile. Waves kh = 0 and 1 sum the two k halves through LDS at
 //    the end; the epilogue is the GEMM's.
-template <int S, int KH2>
-__global__ void __launch_bounds__(256) mbconv_kernel(const GemmDev p, const MbDev d) {
+//  * STEM: the block input is itself a convolution's output, never stored: MobileNetV2's stem
+//    (3 x 3 over the 3-channel image, strided, with its activation) ahead of its first block
+//    (depthwise and projection, no expansion). The "expansion" is then the stem: lane (li, h)
+//    gathers window values k = 16 h .. 16 h + 15 (tap k / 3, channel k % 3; k < 27) of its patch
+//    pixel's stem window straight from the image (four-byte loads through element strides, so
+//    an NCHW image is read in place), zeros outside the image and for k >= 27, and the weights
+//    are the stem's, [Cexp][32] with columns 27..31 zero. The rest is the block as above.
+// At least four waves per SIMD: the stride-1 forms fit 128 registers without spilling (four
+// workgroups per CU, as their LDS allows); the compiler leaves the stride-2 forms as they are.
+template <int S, int KH2, bool STEM>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) mbconv_kernel(const GemmDev p, const MbDev d) {
+    static_assert(!STEM || KH2 == 16, "a stem block's window values, 27 padded to 32, are the k operand");
     constexpr int CIN = 2 * KH2;
     constexpr int Q = KH2 / 4;                         // 16-byte quads per lane and row block
     constexpr int PW = 7 * S + 3;                      // patch rows and columns
@@ -2092,9 +2108,34 @@ __global__ void __launch_bounds__(256) mbconv_kernel(const GemmDev p, const MbDe
 
     // the expansion's B operand for this wave's patch pixel blocks, and which of the lane's
     // pixels lie inside the image
-    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void *)d.x, (short)0, (int)d.x_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc((void *)(STEM ? d.img : d.x), (short)0, (int)d.x_bytes, 0x00020000);
     f4 xa[RBW][Q];
     unsigned inside = 0;  // bit j: the lane's pixel of row block j is a patch pixel inside the image
+    // STEM: the image window every stem output of the patch reads, requested here (coalesced:
+    // consecutive threads read consecutive columns of a row of one channel), staged through LDS
+    // after the weights' loads and read from there per lane. Rows and columns RW = 2 PW + 1
+    // cover the patch's windows at stem strides up to 2; zeros outside the image.
+    constexpr int RW = 2 * PW + 1;
+    constexpr int RF = kStemC * RW * RW;
+    constexpr int RPT = STEM ? (RF + 255) / 256 : 1;
+    static_assert(!STEM || RF <= SMEM_E, "the staged window fits the patch buffers");
+    float rv[RPT];
+    if constexpr (STEM) {
+        const int wy0 = ih0 * d.iSH - d.iPT, wx0 = iw0 * d.iSW - d.iPL;  // window origin in the image
+        const unsigned ibase = (unsigned)img * d.isn;
+#pragma unroll
+        for (int u = 0; u < RPT; ++u) {
+            const int e = tid + 256 * u;
+            const int c = e / (RW * RW), rem = e - c * (RW * RW);
+            const int r = rem / RW, col = rem - r * RW;
+            const int y = wy0 + r, x = wx0 + col;
+            const bool in = e < RF && (unsigned)y < (unsigned)d.iH && (unsigned)x < (unsigned)d.iW;
+            const unsigned off =
+                in ? (ibase + (unsigned)c * d.isc + (unsigned)y * d.ish + (unsigned)x * d.isw) * 4u : OOB;
+            rv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, off, 0, 0));
+        }
+    }
 #pragma unroll
     for (int j = 0; j < RBW; ++j) {
         const int rb = wave + 4 * j;
@@ -2102,11 +2143,13 @@ __global__ void __launch_bounds__(256) mbconv_kernel(const GemmDev p, const MbDe
         const int pr = pa / PW, pc = pa - (pa / PW) * PW;
         const int ih = ih0 + pr, iw = iw0 + pc;
         const bool ok = rb < RB && pa < P && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
-        const unsigned base = ((((unsigned)img * (unsigned)H + (unsigned)ih) * (unsigned)W + (unsigned)iw) * CIN +
-                               (unsigned)(lh * KH2)) * 4u;
+        if constexpr (!STEM) {
+            const unsigned base = ((((unsigned)img * (unsigned)H + (unsigned)ih) * (unsigned)W + (unsigned)iw) * CIN +
+                                   (unsigned)(lh * KH2)) * 4u;
 #pragma unroll
-        for (int q = 0; q < Q; ++q)
-            xa[j][q] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? base + 16u * q : OOB, 0, 0));
+            for (int q = 0; q < Q; ++q)
+                xa[j][q] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? base + 16u * q : OOB, 0, 0));
+        }
         inside |= (ok ? 1u : 0u) << j;
     }
 
@@ -2136,10 +2179,11 @@ __global__ void __launch_bounds__(256) mbconv_kernel(const GemmDev p, const MbDe
     f4 we[Q], pb[2];
     load_we(0, we);
     load_pb(0, pb);
-    // depthwise weights, depthwise bias and expansion bias of every channel into LDS (zeros
-    // past Cexp)
-    for (int e = tid; e < WDF / 4; e += 256) {
-        const int t = e / (kMbMaxCexp / 4), c = (e - t * (kMbMaxCexp / 4)) * 4;
+    // depthwise weights, depthwise bias and expansion bias of the channels the stages read into
+    // LDS (zeros past Cexp)
+    const int cq = nk * 8;  // channel quads of the nk stages
+    for (int e = tid; e < 11 * cq; e += 256) {
+        const int t = e / cq, c = (e - t * cq) * 4;
         f4 v = {0.f, 0.f, 0.f, 0.f};
         if (c < Cexp) {
             if (t < 9)
@@ -2150,6 +2194,38 @@ __global__ void __launch_bounds__(256) mbconv_kernel(const GemmDev p, const MbDe
                 v = ldg4(d.be + c);
         }
         *reinterpret_cast<f4 *>(&Wd[t * kMbMaxCexp + c]) = v;
+    }
+    if constexpr (STEM) {
+        // the window into LDS (over the patch buffers, which nothing has written yet), then
+        // lane (li, h)'s window values k = 16 h .. 16 h + 15 of its patch pixels: tap (ty, tx)
+        // and channel c of k are compile-time for either lane half
+#pragma unroll
+        for (int u = 0; u < RPT; ++u) {
+            const int e = tid + 256 * u;
+            if (e < RF) smem[e] = rv[u];
+        }
+        barrier_lds();
+#pragma unroll
+        for (int j = 0; j < RBW; ++j) {
+            const int pa = (wave + 4 * j) * 32 + li;
+            const int pr = pa / PW, pc = pa - (pa / PW) * PW;
+            const bool ok = (inside >> j) & 1u;
+#pragma unroll
+            for (int i = 0; i < KH2; ++i) {
+                constexpr int kTaps = kStemK * kStemK * kStemC;
+                const int k0 = i, k1 = KH2 + i;
+                const int t0 = k0 / kStemC, t1 = k1 / kStemC;
+                const int ty = lh ? t1 / kStemK : t0 / kStemK;
+                const int tx = lh ? t1 % kStemK : t0 % kStemK;
+                const int c = lh ? k1 % kStemC : k0 % kStemC;
+                const bool kin = lh ? k1 < kTaps : k0 < kTaps;
+                // pr, pc < PW and strides <= 2 keep the row and column below RW
+                const int idx = ok && kin ? c * (RW * RW) + (pr * d.iSH + ty) * RW + pc * d.iSW + tx : 0;
+                const float v = smem[idx];
+                xa[j][i >> 2][i & 3] = ok && kin ? v : 0.0f;
+            }
+        }
+        barrier_lds();  // every lane has its window values before the patch buffers are written
     }
     // patch pixels outside the image (or past the patch) are zero in every stage: written once
     // into each patch buffer here, never by the stage loop
@@ -3099,23 +3175,43 @@ extern "C" int mgc_hip_mbconv_supported(int Cin, int Cexp, int Cout, int stride)
            Cout <= 32 && (stride == 1 || stride == 2);
 }
 
-extern "C" void mgc_hip_mbconv(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const mgc_hip_mbconv_args *mb) {
+extern "C" int mgc_hip_mbconv_stem_supported(int C, int KH, int KW, int Cexp, int Cout, int stride) {
+    return C == kStemC && KH == kStemK && KW == kStemK && mgc_hip_mbconv_supported(32, Cexp, Cout, stride);
+}
+
+// mgc_hip_mbconv and mgc_hip_mbconv_stem: st is null for a block whose input is in memory.
+static void mbconv_launch(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const mgc_hip_mbconv_args *mb,
+                          const mgc_hip_stem_args *st) {
     if (g->M <= 0 || g->N <= 0) return;
+    const char *const name = st ? "mgc_hip_mbconv_stem" : "mgc_hip_mbconv";
     const long ohw = (long)mb->OH * mb->OW;
     const long n_img = ohw > 0 ? g->M / ohw : 0;
-    const long x_bytes = n_img * mb->H * mb->W * (long)mb->Cin * 4;
+    long x_bytes = n_img * mb->H * mb->W * (long)mb->Cin * 4;
+    bool input_ok = aligned16(mb->x);
+    if (st) {
+        // bytes from img to the last element the image's strides reach
+        const bool geo = st->C == kStemC && st->KH == kStemK && st->KW == kStemK && st->H > 0 && st->W > 0 &&
+                         st->SH > 0 && st->SW > 0 && st->SH <= 2 && st->SW <= 2 && st->PT >= 0 && st->PL >= 0 && st->sn >= 0 && st->sc >= 0 &&
+                         st->sh >= 0 && st->sw >= 0 && n_img > 0;
+        x_bytes = geo ? ((n_img - 1) * st->sn + (long)(st->C - 1) * st->sc + (long)(st->H - 1) * st->sh +
+                         (long)(st->W - 1) * st->sw + 1) * 4
+                      : -1;
+        input_ok = geo && st->img && ((uintptr_t)st->img & 3) == 0 && mb->Cin == 32;
+    }
     const long b_bytes = ((long)(g->N - 1) * g->b.cs + g->K) * 4;
     const bool acts = (mb->act_e == MGC_ACT_RELU || mb->act_e == MGC_ACT_CLIP) &&
                       (mb->act_d == MGC_ACT_RELU || mb->act_d == MGC_ACT_CLIP);
     const bool ok = mgc_hip_mbconv_supported(mb->Cin, mb->Cexp, g->N, mb->SH) && mb->SH == mb->SW && acts &&
                     g->batch_rank == 0 && g->k1 == 0 && g->K == mb->Cexp && mb->H > 0 && mb->W > 0 && ohw > 0 &&
-                    g->M % ohw == 0 && x_bytes < 0x7fffffffL && b_bytes < 0x7fffffffL &&
+                    g->M % ohw == 0 && x_bytes > 0 && x_bytes < 0x7fffffffL && b_bytes < 0x7fffffffL &&
                     (!g->bias || g->bias_mode == 1) && g->b.kind == MGC_OP_STRIDED && g->b.rs == 1 &&
-                    g->b.cs >= g->K && g->b.cs % 4 == 0 && aligned16(g->b.p) && aligned16(mb->x) &&
+                    g->b.cs >= g->K && g->b.cs % 4 == 0 && aligned16(g->b.p) && input_ok &&
                     aligned16(mb->we) && aligned16(mb->be) && aligned16(mb->wd) && aligned16(mb->bd);
     if (!ok) {
         x->launch_error = (int)hipErrorInvalidValue;
-        set_error("mgc_hip_mbconv: shape, layout or alignment outside its limits", hipErrorInvalidValue);
+        char msg[128];
+        snprintf(msg, sizeof msg, "%s: shape, layout or alignment outside its limits", name);
+        set_error(msg, hipErrorInvalidValue);
         return;
     }
     GemmDev p{};
@@ -3159,13 +3255,44 @@ extern "C" void mgc_hip_mbconv(mgc_hip_exec *x, const mgc_hip_gemm_args *g, cons
     d.tiles_h = (mb->OH + 7) / 8;
     d.tiles_w = (mb->OW + 7) / 8;
     d.x_bytes = x_bytes;
+    d.img = nullptr;
+    d.iH = d.iW = d.iSH = d.iSW = d.iPT = d.iPL = 0;
+    d.isn = d.isc = d.ish = d.isw = 0;
+    if (st) {
+        d.img = st->img;
+        d.iH = st->H;
+        d.iW = st->W;
+        d.iSH = st->SH;
+        d.iSW = st->SW;
+        d.iPT = st->PT;
+        d.iPL = st->PL;
+        d.isn = (unsigned)st->sn;
+        d.isc = (unsigned)st->sc;
+        d.ish = (unsigned)st->sh;
+        d.isw = (unsigned)st->sw;
+    }
     const long tiles = n_img * d.tiles_h * d.tiles_w;
     typedef void (*MbKernel)(const GemmDev, const MbDev);
     const bool s2 = mb->SH == 2;
-    const MbKernel kern = mb->Cin == 16   ? (s2 ? &mbconv_kernel<2, 8> : &mbconv_kernel<1, 8>)
-                          : mb->Cin == 24 ? (s2 ? &mbconv_kernel<2, 12> : &mbconv_kernel<1, 12>)
-                                          : (s2 ? &mbconv_kernel<2, 16> : &mbconv_kernel<1, 16>);
+    const MbKernel kern = st               ? (s2 ? &mbconv_kernel<2, 16, true> : &mbconv_kernel<1, 16, true>)
+                          : mb->Cin == 16 ? (s2 ? &mbconv_kernel<2, 8, false> : &mbconv_kernel<1, 8, false>)
+                          : mb->Cin == 24 ? (s2 ? &mbconv_kernel<2, 12, false> : &mbconv_kernel<1, 12, false>)
+                                          : (s2 ? &mbconv_kernel<2, 16, false> : &mbconv_kernel<1, 16, false>);
     MGC_LAUNCH(x, kern, dim3((unsigned)tiles), dim3(256), 0, p, d);
+}
+
+extern "C" void mgc_hip_mbconv(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const mgc_hip_mbconv_args *mb) {
+    mbconv_launch(x, g, mb, nullptr);
+}
+
+extern "C" void mgc_hip_mbconv_stem(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const mgc_hip_mbconv_args *mb,
+                                    const mgc_hip_stem_args *st) {
+    if (!st) {
+        x->launch_error = (int)hipErrorInvalidValue;
+        set_error("mgc_hip_mbconv_stem: no stem arguments", hipErrorInvalidValue);
+        return;
+    }
+    mbconv_launch(x, g, mb, st);
 }
 
 // Row blocks of 16 image pixels a wave may own and window pixels LDS holds, per input width:

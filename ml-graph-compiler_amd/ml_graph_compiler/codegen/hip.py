@@ -120,6 +120,11 @@ MBCONV_MIN_ROWS = 16384
 MBCONV_CIN = (16, 24, 32)
 MBCONV_MAX_CEXP = 256
 MBCONV_MAX_COUT = 32
+# The same launch with a 3 x 3 convolution of a 3-channel image (with relu / clip) in place of
+# the expansion (mgc_hip_mbconv_stem: MobileNetV2's stem and first block), at any size: the
+# stem's output, the depthwise output and the stem's NHWC input copy are never written.
+FUSE_STEM_BLOCK = True
+MBCONV_STEM_MIN_ROWS = 0
 # Run an inverted-residual block's 1 x 1 expansion (relu / clip) and the 3 x 3 depthwise
 # convolution (relu / clip) that alone reads it as one mgc_hip_expand_dw launch (a workgroup per
 # image and 32 expanded channels; the expanded tensor never goes to memory) when
@@ -242,6 +247,26 @@ def _pointwise_nhwc(node: Node) -> bool:
     return all(p == 0 for p in g.pads) and all(v is None or v.data is not None for v in node.inputs[2:3])
 
 
+def _stem_conv_nhwc(node: Node) -> bool:
+    """A float32 NHWC convolution mgc_hip_mbconv_stem evaluates in place of an expansion: a
+    constant 3 x 3 kernel over 3 input channels, one group, strides 1 or 2, no dilation,
+    constant bias (or none), no residual, relu or clip."""
+    if node.op != "FusedConv" or ops.conv_layout(node) != "NHWC":
+        return False
+    if node.attrs.get("activation", "none") not in ("relu", "clip"):
+        return False
+    w, xt = node.input(1), node.input(0).tensor_type
+    if w.data is None or xt.dtype != "float32" or xt.rank != 4 or w.tensor_type.shape[:3] != (3, 3, 3):
+        return False
+    if int(node.attrs.get("group", 1)) != 1 or node.input(0).data is not None:
+        return False
+    g = ops.window_geometry(node, xt.shape[1:3], (3, 3))
+    if tuple(g.dilations) != (1, 1) or max(g.strides) > 2:
+        return False
+    b = node.optional_input(2)
+    return (b is None or b.data is not None) and node.optional_input(3) is None
+
+
 def _tensor_bytes(v: Value) -> int:
     t = v.tensor_type
     return int(np.prod(t.shape, dtype=np.int64)) * np.dtype(numpy_dtype(t.dtype)).itemsize
@@ -344,7 +369,10 @@ def find_inverted_residuals(graph: Graph, min_rows: int | None = None) -> dict[i
     reads, pw a stride-1 pointwise NHWC convolution (any bias, residual and activation), with
     the kernel's channel limits (input 16, 24 or 32 channels, at most MBCONV_MAX_CEXP expanded
     and MBCONV_MAX_COUT output channels), at least ``min_rows`` output pixels (default
-    MBCONV_MIN_ROWS) and the block input below FUSED_OPERAND_LIMIT bytes."""
+    MBCONV_MIN_ROWS) and the block input below FUSED_OPERAND_LIMIT bytes. With FUSE_STEM_BLOCK,
+    ex may instead be a stem convolution (``_stem_conv_nhwc``: 3 x 3 over a 3-channel image,
+    stride 1 or 2, any padding) ahead of a block without expansion, which mgc_hip_mbconv_stem runs as
+    one launch at MBCONV_STEM_MIN_ROWS output pixels or more."""
     if min_rows is None:
         min_rows = MBCONV_MIN_ROWS
     outputs = {id(v) for v in graph.outputs}
@@ -364,19 +392,21 @@ def find_inverted_residuals(graph: Graph, min_rows: int | None = None) -> dict[i
             continue
         e = dw.input(0)
         ex = e.producer
-        if ex is None or not _pointwise_nhwc(ex) or not clamp_act(ex) or ex.optional_input(3) is not None:
+        if ex is None or id(e) in outputs or e.users != [dw] or ex.input(0).data is not None:
             continue
-        if id(e) in outputs or e.users != [dw] or ex.input(0).data is not None:
+        stem = FUSE_STEM_BLOCK and _stem_conv_nhwc(ex)
+        if not stem and (not _pointwise_nhwc(ex) or not clamp_act(ex) or ex.optional_input(3) is not None):
             continue
         xt, et, dt = ex.input(0).tensor_type, e.tensor_type, d.tensor_type
-        if ops.window_geometry(ex, xt.shape[1:3], (1, 1)).strides != (1, 1):
+        if not stem and ops.window_geometry(ex, xt.shape[1:3], (1, 1)).strides != (1, 1):
             continue
         if ops.window_geometry(pw, dt.shape[1:3], (1, 1)).strides != (1, 1):
             continue
-        cin, cexp, cout = xt.shape[3], et.shape[3], pw.input(1).tensor_type.shape[3]
+        cin, cexp, cout = 32 if stem else xt.shape[3], et.shape[3], pw.input(1).tensor_type.shape[3]
         if cin not in MBCONV_CIN or cexp % 4 or cexp > MBCONV_MAX_CEXP or cout > MBCONV_MAX_COUT:
             continue
-        if dt.shape[0] * dt.shape[1] * dt.shape[2] < min_rows or _tensor_bytes(ex.input(0)) >= FUSED_OPERAND_LIMIT:
+        rows = min(min_rows, MBCONV_STEM_MIN_ROWS) if stem else min_rows
+        if dt.shape[0] * dt.shape[1] * dt.shape[2] < rows or _tensor_bytes(ex.input(0)) >= FUSED_OPERAND_LIMIT:
             continue
         found[id(pw)] = (ex, dw)
     return found
@@ -579,6 +609,18 @@ class HipEmitter:
                 if self._s2d[id(n)] is not None:
                     self._s2d_skip.add(id(n.input(0).producer))
                 self._scratch_bytes = max(self._scratch_bytes, n.input(0).tensor_type.nbytes)
+        # Stem blocks read their image in place when it reaches the stem through an NCHW -> NHWC
+        # Transpose: id(projection) -> the NCHW tensor.
+        self._stem_src: dict[int, Value] = {}
+        order = {id(n): i for i, n in enumerate(graph.nodes)}
+        for pw in graph.nodes:
+            pair = self._mb.get(id(pw))
+            if pair is None or not _stem_conv_nhwc(pair[0]):
+                continue
+            src = self._s2d_source(pair[0], order, excluded - self._mb_skip, reader=pw)
+            if src is not None:
+                self._stem_src[id(pw)] = src
+                self._s2d_skip.add(id(pair[0].input(0).producer))
         # FusedGemm -> LayerNormalization of its rows, scheduled back to back: the LayerNorm runs
         # in the GEMM's split-K reduction. id(gemm) -> (LayerNorm, partials in scratch?)
         self._gemm_ln: dict[int, tuple[Node, bool]] = {}
@@ -736,7 +778,7 @@ class HipEmitter:
             self.count("folded")
             return
         if id(node) in self._s2d_skip:
-            self.emit("/* read in NCHW by the space-to-depth copy of the convolution it feeds */")
+            self.emit("/* read in NCHW by the launch of the convolution it feeds (space-to-depth copy or stem block) */")
             self.count("folded")
             return
         if id(node) in self._shortcut_skip:
@@ -1162,10 +1204,12 @@ class HipEmitter:
                    beta: float = 1.0, act: str = "none", lo: float = 0.0, hi: float = 6.0,
                    workspace: str = "NULL", workspace_floats: int = 0,
                    layer_norm: tuple[str, str, str, str] | None = None, extra: Sequence[str] = (),
-                   depthwise: str | None = None, mbconv: str | None = None, extra_flops: int = 0) -> None:
+                   depthwise: str | None = None, mbconv: str | None = None, stem: str | None = None,
+                   extra_flops: int = 0) -> None:
         """One mgc_hip_gemm call; ``layer_norm`` = (scale, bias, eps, out) makes it an
         mgc_hip_gemm_layer_norm call whose split-K reduction also normalizes the rows; ``mbconv``
-        declares and fills an mgc_hip_mbconv_args ``mb`` and makes it an mgc_hip_mbconv call; ``extra``
+        declares and fills an mgc_hip_mbconv_args ``mb`` and makes it an mgc_hip_mbconv call (with
+        ``stem``, which declares and fills an mgc_hip_stem_args ``st``, mgc_hip_mbconv_stem); ``extra``
         are further field assignments (the concatenated-K operand); ``depthwise`` declares and
         fills an mgc_hip_dw_args ``d`` and makes it an mgc_hip_gemm_dw call."""
         if len(batch) > MAX_BATCH_RANK:
@@ -1186,6 +1230,8 @@ class HipEmitter:
             parts.append(f"mgc_hip_gemm_layer_norm(x, &g, {scale}, {lbias}, {eps}, {out});")
         elif depthwise is not None:
             parts += [depthwise, "mgc_hip_gemm_dw(x, &g, &d);"]
+        elif mbconv is not None and stem is not None:
+            parts += [mbconv, stem, "mgc_hip_mbconv_stem(x, &g, &mb, &st);"]
         elif mbconv is not None:
             parts += [mbconv, "mgc_hip_mbconv(x, &g, &mb);"]
         else:
@@ -1584,7 +1630,12 @@ class HipEmitter:
         A operand is the depthwise output of the expansion of x, both evaluated per tile; neither
         intermediate is written. When x is a caller buffer (a graph input or output) the
         generated code checks its 16-byte alignment and otherwise runs the three convolutions
-        apart."""
+        apart. A stem block (ex a 3 x 3 convolution of a 3-channel image) is one
+        mgc_hip_mbconv_stem launch reading the image through its strides (NCHW in place when
+        it reaches the stem through a Transpose); its four-byte loads need no alignment check."""
+        if _stem_conv_nhwc(ex):
+            self._stem_block(node, ex, dw)
+            return
         xv = ex.input(0)
         nb, h, wd, cin = xv.tensor_type.shape
         cexp = ex.input(1).tensor_type.shape[3]
@@ -1634,6 +1685,57 @@ class HipEmitter:
                 self._mb[id(node)] = saved
                 self._mb_skip |= skipped
             self.emit("}")
+
+    def _stem_block(self, node: Node, stem: Node, dw: Node) -> None:
+        """pw(act_d(dw(act_s(stem(img))))) as one mgc_hip_mbconv_stem launch: the stem's output
+        and the depthwise output are evaluated per 8 x 8-pixel tile and never written; the image
+        is read in place through its strides."""
+        xv = stem.input(0)
+        nb, h0, w0, c0 = xv.tensor_type.shape
+        et = dw.input(0).tensor_type
+        h, wd, cexp = et.shape[1], et.shape[2], et.shape[3]
+        sg = ops.window_geometry(stem, (h0, w0), (3, 3))
+        g = ops.window_geometry(dw, (h, wd), (3, 3))
+        oh, ow = g.out_hw
+        # stem weights [3][3][3][Cexp] -> k = (3 ty + tx) 3 + c, padded to 32 window values
+        wmat = np.zeros((32, cexp), np.float32)
+        wmat[:27] = stem.input(1).data.reshape(27, cexp)
+        we = self._packed_b(wmat, ("stem", id(stem.input(1))))[0]
+        we_ptr = we.split("g.b.p = ")[1].split(";")[0]
+        ebias_v = stem.optional_input(2)
+        ebias = self._vector_ptr(ebias_v, cexp, "Conv bias") if ebias_v is not None else "NULL"
+        wdw = np.ascontiguousarray(dw.input(1).data.reshape(9, cexp), np.float32)
+        dwoff = self.weights.add(wdw, key=("dw", id(dw.input(1))))
+        dbias_v = dw.optional_input(2)
+        dbias = self._vector_ptr(dbias_v, cexp, "Conv bias") if dbias_v is not None else "NULL"
+        eact, elo, ehi = self._act(stem)
+        dact, dlo, dhi = self._act(dw)
+        n = node.input(1).tensor_type.shape[3]
+        bspec = self._packed_b(node.input(1).data.reshape(cexp, n), ("conv", id(node.input(1)), 0))
+        bias_v, res_v = node.optional_input(2), node.optional_input(3)
+        bias = self._vector_ptr(bias_v, n, "Conv bias") if bias_v is not None else "NULL"
+        res = self.fptr(res_v) if res_v is not None else "NULL"
+        act, lo, hi = self._act(node) if node.op == "FusedConv" else ("none", 0.0, 6.0)
+        src = self._stem_src.get(id(node))
+        if src is not None:  # NCHW [n][c][y][x], read in place
+            img, strides = f"(const float *){self.ptr(src)}", (c0 * h0 * w0, h0 * w0, w0, 1)
+        else:  # NHWC [n][y][x][c]
+            img, strides = self.fptr(xv), (h0 * w0 * c0, 1, w0 * c0, c0)
+        mbs = (f"mgc_hip_mbconv_args mb; memset(&mb, 0, sizeof mb); mb.x = NULL; "
+               f"mb.we = (const float *){we_ptr}; mb.be = {ebias}; mb.wd = (const float *)(W + {dwoff}); "
+               f"mb.bd = {dbias}; mb.H = {h}; mb.W = {wd}; mb.Cin = 32; mb.Cexp = {cexp}; "
+               f"mb.SH = {g.strides[0]}; mb.SW = {g.strides[1]}; mb.PT = {g.pads[0]}; mb.PL = {g.pads[1]}; "
+               f"mb.OH = {oh}; mb.OW = {ow}; mb.act_e = {ACT_CODES[eact]}; mb.lo_e = {_f(elo)}; "
+               f"mb.hi_e = {_f(ehi)}; mb.act_d = {ACT_CODES[dact]}; mb.lo_d = {_f(dlo)}; mb.hi_d = {_f(dhi)};")
+        sts = (f"mgc_hip_stem_args st; memset(&st, 0, sizeof st); st.img = {img}; st.C = {c0}; st.H = {h0}; "
+               f"st.W = {w0}; st.sn = {strides[0]}L; st.sc = {strides[1]}L; st.sh = {strides[2]}L; "
+               f"st.sw = {strides[3]}L; st.KH = 3; st.KW = 3; st.SH = {sg.strides[0]}; st.SW = {sg.strides[1]}; "
+               f"st.PT = {sg.pads[0]}; st.PL = {sg.pads[1]};")
+        self._gemm_call(nb * oh * ow, n, cexp, [], bspec, self.fptr(node.output), n, bias=bias,
+                        bias_mode=1 if bias != "NULL" else 0, res=res, ldr=n, act=act, lo=lo, hi=hi, mbconv=mbs,
+                        stem=sts, extra_flops=ops.flops(stem) + ops.flops(dw))
+        self.count("gemm_mbconv")
+        self.count("mbconv_stem")
 
     def _expand_depthwise(self, node: Node, ex: Node) -> None:
         """act_d(dw(act_e(ex(x)))) as one mgc_hip_expand_dw launch writing the depthwise node's
@@ -1710,10 +1812,11 @@ class HipEmitter:
                     KH=-(-(kh + 2 * P - pt) // 2), KW=-(-(kw + 2 * Q - pl) // 2),
                     oh=g.out_hw[0], ow=g.out_hw[1])
 
-    def _s2d_source(self, conv: Node, order: dict[int, int], excluded: set[int]) -> Value | None:
-        """The NCHW tensor the space-to-depth copy can read directly when the convolution's
-        input is an NCHW -> NHWC Transpose used by nothing else (the Transpose then emits
-        nothing), provided nothing between the two overwrites that tensor."""
+    def _s2d_source(self, conv: Node, order: dict[int, int], excluded: set[int], reader: Node | None = None) -> Value | None:
+        """The NCHW tensor the space-to-depth copy (or, for a stem block, the launch of
+        ``reader``) can read directly when the convolution's input is an NCHW -> NHWC Transpose
+        used by nothing else (the Transpose then emits nothing), provided nothing between the
+        Transpose and the reading node overwrites that tensor."""
         x = conv.input(0)
         t = x.producer
         if t is None or t.op != "Transpose" or id(t) in excluded or id(t) in self._folds.skipped:
@@ -1721,7 +1824,7 @@ class HipEmitter:
         if x in self.graph.outputs or x.users != [conv] or ops.transpose_perm(t, 4) != [0, 2, 3, 1]:
             return None
         src = t.input(0)
-        for n in self.graph.nodes[order[id(t)] + 1 : order[id(conv)]]:
+        for n in self.graph.nodes[order[id(t)] + 1 : order[id(reader or conv)]]:
             if any(fold_overlap(self.plan, o, src) for o in n.outputs):
                 return None
             if id(n) in self.plan.workspaces:

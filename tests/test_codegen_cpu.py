@@ -110,6 +110,7 @@ def test_kernel_mix_matches_reference(name, kernels, arena, monkeypatch):
     make = builders.SAMPLES.get(name) or builders.CONFIGS[name]
     monkeypatch.setattr(hip_codegen, "FUSE_PROJECTION_SHORTCUT", False)
     monkeypatch.setattr(hip_codegen, "FUSE_DEPTHWISE_POINTWISE", False)
+    monkeypatch.setattr(hip_codegen, "FUSE_STEM_BLOCK", False)
     monkeypatch.setattr(hip_codegen, "SPACE_TO_DEPTH", False)
     gen = generate_hip(o3(make()))
     assert gen.kernels == kernels
@@ -197,10 +198,12 @@ def test_depthwise_pointwise_pairs_join_one_gemm(monkeypatch):
 def test_inverted_residual_blocks_run_as_one_launch(monkeypatch):
     """MobileNetV2 at batch 32: the five expanded blocks whose outputs have at least
     MBCONV_MIN_ROWS pixels (56 x 56 and 28 x 28, both strides, 16 / 24 / 32 input channels) each
-    run as one mgc_hip_mbconv call; the first block (no expansion) keeps the fused depthwise
-    GEMM. The block input stays alive (its arena block clear of everything placed) until the
-    call reads it, and the expansion and depthwise FLOPs are counted at the call's node. At
-    batch 1 no block has enough output pixels."""
+    run as one mgc_hip_mbconv call, and the stem with the first block (no expansion) as one
+    mgc_hip_mbconv_stem call reading the NCHW input in place (the input Transpose, the stem and
+    the depthwise convolution emit nothing; no space-to-depth copy). The block input stays
+    alive (its arena block clear of everything placed) until the call reads it, and the
+    expansion (stem) and depthwise FLOPs are counted at the call's node. At batch 1 only the
+    stem block is fused (MBCONV_STEM_MIN_ROWS)."""
     from ml_graph_compiler import ops
     from ml_graph_compiler.codegen import hip as emitter
     from ml_graph_compiler.codegen.hip import find_inverted_residuals
@@ -210,10 +213,13 @@ def test_inverted_residual_blocks_run_as_one_launch(monkeypatch):
     blocks = find_inverted_residuals(g)
     shapes = sorted((ex.input(0).tensor_type.shape[1:], dw.output.tensor_type.shape[1:]) for ex, dw in blocks.values())
     assert shapes == [((28, 28, 32), (28, 28, 192))] * 2 + [((56, 56, 24), (28, 28, 144)), ((56, 56, 24), (56, 56, 144)),
-                                                            ((112, 112, 16), (56, 56, 96))]
+                                                            ((112, 112, 16), (56, 56, 96)), ((224, 224, 3), (112, 112, 32))]
     gen = generate_hip(g, gemm_workspace=native.gemm_workspace_floats)
-    assert gen.kernels["gemm_mbconv"] == 5 and gen.kernels["gemm_depthwise"] == 1 and gen.kernels["depthwise"] == 11
+    assert gen.kernels["gemm_mbconv"] == 6 and gen.kernels["mbconv_stem"] == 1 and gen.kernels["depthwise"] == 11
+    assert "gemm_depthwise" not in gen.kernels and "space_to_depth" not in gen.kernels and "transpose" not in gen.kernels
     assert gen.source.count("mgc_hip_mbconv(x, &g, &mb);") == 5
+    assert gen.source.count("mgc_hip_mbconv_stem(x, &g, &mb, &st);") == 1
+    assert "st.sn = 150528L; st.sc = 50176L; st.sh = 224L; st.sw = 1L;" in gen.source  # NCHW [32, 3, 224, 224]
     assert sum(gen.node_flops) == sum(ops.flops(n) for n in g.nodes)
     skipped = {id(n) for pair in blocks.values() for n in pair}
     assert all(gen.node_flops[i] == 0 for i, n in enumerate(g.nodes) if id(n) in skipped)
@@ -229,6 +235,9 @@ def test_inverted_residual_blocks_run_as_one_launch(monkeypatch):
             if b is x or not (b.start <= order[id(pw)] <= b.end):
                 continue
             assert b.offset + b.size <= x.offset or x.offset + x.size <= b.offset
+    b1 = find_inverted_residuals(o3(builders.mobilenet_v2(batch=1)))
+    assert [ex.input(1).tensor_type.shape[:3] for ex, _ in b1.values()] == [(3, 3, 3)]
+    monkeypatch.setattr(emitter, "FUSE_STEM_BLOCK", False)
     assert not find_inverted_residuals(o3(builders.mobilenet_v2(batch=1)))
 
 
@@ -238,8 +247,7 @@ def test_expansion_and_depthwise_run_as_one_launch():
     convolution as one mgc_hip_expand_dw call writing the depthwise output (384-960 workgroups
     of an image and 32 channels each); the projection stays a GEMM. Only the 28 -> 14 block
     (28 x 28 input: too large a window) keeps its depthwise launch, so with the five whole-block
-    launches and the first block's fused depthwise GEMM one standalone depthwise launch is left
-    of 17. The block input stays alive (its arena block clear of everything placed) until the
+    launches and the stem block one standalone depthwise launch is left of 17. The block input stays alive (its arena block clear of everything placed) until the
     call reads it, the expansion FLOPs are counted at the call's node, and at batch 1 (12-30
     workgroups) and batch 8 the pairs stay apart."""
     from ml_graph_compiler import ops
@@ -253,7 +261,7 @@ def test_expansion_and_depthwise_run_as_one_launch():
                       + [((14, 14, 96), (7, 7, 576))] + [((14, 14, 96), (14, 14, 576))] * 2)
     gen = generate_hip(g, gemm_workspace=native.gemm_workspace_floats)
     assert gen.kernels["expand_depthwise"] == 10 and gen.kernels["depthwise"] == 1
-    assert gen.kernels["gemm_mbconv"] == 5 and gen.kernels["gemm_depthwise"] == 1 and gen.kernels["gemm"] == 21
+    assert gen.kernels["gemm_mbconv"] == 6 and "gemm_depthwise" not in gen.kernels and gen.kernels["gemm"] == 20
     assert gen.source.count("mgc_hip_expand_dw(x, &xd);") == 10
     assert sum(gen.node_flops) == sum(ops.flops(n) for n in g.nodes)
     skipped = {id(ex) for ex in pairs.values()}

@@ -147,3 +147,100 @@ def test_inverted_residual_over_caller_buffers(hip_cache, monkeypatch):
     finally:
         model.release()
     np.testing.assert_allclose(got, expected, rtol=RTOL, atol=ATOL)
+
+
+def stem_block(n: int, h: int, w: int, cexp: int, cout: int, stem_stride: int, stride: int, act: str,
+               seed: int = 0) -> tuple[Graph, dict[str, np.ndarray]]:
+    """image -> act(3x3 stem / stem_stride, 3 -> cexp) -> act(3x3 depthwise / stride) -> 1x1
+    project: MobileNetV2's stem and first block (no expansion), over an NCHW graph input."""
+    rng = np.random.default_rng(seed)
+    g = Graph("stem_block")
+    x = g.add_input("x", TensorType("float32", (n, 3, h, w)))
+    lo = g.constant(np.asarray(0.0, np.float32), "lo")
+    hi = g.constant(np.asarray(6.0, np.float32), "hi")
+
+    def activation(v, name):
+        if act == "relu":
+            return g.add_node("Relu", [v], 1, {}, name=name).output
+        return g.add_node("Clip", [v, lo, hi], 1, {}, name=name).output
+
+    y = activation(_conv(g, rng, x, 3, cexp, 3, stem_stride, "stem"), "a0")
+    y = activation(_conv(g, rng, y, cexp, cexp, 3, stride, "dw", group=cexp), "a1")
+    y = _conv(g, rng, y, cexp, cout, 1, 1, "project")
+    g.add_output(y, "y")
+    infer_shapes(g)
+    return g, {"x": rng.standard_normal((n, 3, h, w)).astype(np.float32)}
+
+
+STEM_CASES = [
+    # (n, h, w, cexp, cout, stem stride, depthwise stride, act)
+    (2, 64, 64, 32, 16, 2, 1, "clip"),   # MobileNetV2's stem and first block (scaled): 32 x 32 output
+    (1, 37, 29, 32, 16, 2, 1, "clip"),   # odd image: a 19 x 15 stem output, partial tiles
+    (2, 30, 34, 36, 5, 2, 2, "relu"),    # 36 channels (a second stage of four), stride-2 depthwise
+    (1, 20, 22, 8, 32, 1, 1, "clip"),    # a stride-1 stem, eight channels, 32 outputs
+    (3, 18, 18, 64, 24, 2, 1, "relu"),   # two full stages, three images
+]
+
+
+@pytest.mark.parametrize("case", STEM_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_stem_block_matches_oracle(case, hip_cache, monkeypatch):
+    """The stem convolution, the depthwise convolution and the projection as one
+    mgc_hip_mbconv_stem launch reading the NCHW input in place (the layout pass's input
+    Transpose emits nothing)."""
+    n, h, w, cexp, cout, s0, s1, act = case
+    print(f"[gpu] stem block {case}", flush=True)
+    g, feeds = stem_block(n, h, w, cexp, cout, s0, s1, act, seed=3 + sum(c for c in case if isinstance(c, int)))
+    expected = oracle.run_graph(g, feeds)["y"]
+    got, kernels = _run(g, feeds, hip_cache, monkeypatch)
+    assert kernels.get("mbconv_stem") == 1 and kernels.get("gemm") == 1, kernels
+    # folded: the input Transpose, the stem and the depthwise convolution; the one transpose left
+    # is the output's NHWC -> NCHW
+    assert kernels.get("folded") == 3 and kernels.get("transpose") == 1, kernels
+    assert "depthwise" not in kernels and "space_to_depth" not in kernels, kernels
+    np.testing.assert_allclose(got["y"], expected, rtol=RTOL, atol=ATOL)
+
+
+def test_stem_block_over_an_nhwc_caller_buffer(hip_cache, monkeypatch):
+    """An NHWC image that is the caller's buffer, also 4 bytes off a 16-byte boundary: the stem
+    block reads it through NHWC strides with four-byte loads, so the fused launch runs either
+    way."""
+    import torch
+
+    print("[gpu] stem block over an NHWC caller buffer", flush=True)
+    monkeypatch.setattr(hip_codegen, "MBCONV_MIN_ROWS", 0)
+    rng = np.random.default_rng(11)
+    g = Graph("nhwc_stem_block")
+    x = g.add_input("x", TensorType("float32", (2, 27, 31, 3)))
+
+    def conv(v, k, c_in, c_out, s, group, name, act):
+        wt = g.constant((rng.standard_normal((k, k, c_in // group, c_out)) / np.sqrt(k * k * c_in / group))
+                        .astype(np.float32), f"{name}_w")
+        b = g.constant((rng.standard_normal(c_out) * 0.2).astype(np.float32), f"{name}_b")
+        return g.add_node("FusedConv", [v, wt, b], 1,
+                          {"kernel_shape": [k, k], "pads": [k // 2] * 4, "strides": [s, s], "group": group,
+                           "layout": "NHWC", "activation": act, "clip_min": 0.0, "clip_max": 6.0}, name=name).output
+
+    y = conv(x, 3, 3, 32, 2, 1, "stem", "clip")
+    y = conv(y, 3, 32, 32, 1, 32, "dw", "clip")
+    y = conv(y, 1, 32, 16, 1, 1, "pw", "none")
+    g.add_output(y, "y")
+    infer_shapes(g)
+    feeds = {"x": rng.standard_normal((2, 27, 31, 3)).astype(np.float32)}
+    expected = oracle.run_graph(g, feeds)["y"]
+    model = compile_hip(g, hip_cache, "O0")
+    try:
+        assert model.report.kernels.get("mbconv_stem") == 1, model.report.kernels
+        np.testing.assert_allclose(model.run(feeds)["y"], expected, rtol=RTOL, atol=ATOL)
+        dev = torch.device("cuda:0")
+        host = torch.from_numpy(np.ascontiguousarray(feeds["x"]).reshape(-1))
+        buf = torch.zeros(host.numel() + 1, dtype=torch.float32, device=dev)
+        view = buf[1:]  # 4 bytes past the allocation's start
+        view.copy_(host)
+        assert view.data_ptr() % 16 == 4
+        out = torch.empty(expected.size, dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+        model.run_device([view.data_ptr()], [out.data_ptr()])
+        got = out.cpu().numpy().reshape(expected.shape)
+    finally:
+        model.release()
+    np.testing.assert_allclose(got, expected, rtol=RTOL, atol=ATOL)
