@@ -17,6 +17,8 @@
  *   mgc_hip_gemm_layer_norm <- mgc_gemm then mgc_layer_norm, fused (mgc_runtime.h:120-161, 199-200)
  *   mgc_hip_elementwise     <- the loop nests CEmitter.elementwise/loops emit (codegen/c.py:360-529)
  *   mgc_hip_space_to_depth  <- no counterpart (feeds the stem convolution's stride-1 form)
+ *   mgc_hip_conv_stem       <- mgc_gemm over the stem's MGC_OP_CONV_NCHW operand (codegen/c.py:1099-1226,
+ *                              mgc_kernels.c:86-133, 370-396), reading the NCHW image in place
  *   mgc_hip_copy            <- the identity-body loop nests of op_Transpose/Expand/Tile/Slice/
  *                              Concat/Split/Pad (codegen/c.py:558-660) and output copies (c.py:1283)
  *   mgc_hip_fill            <- constant loops of _write_constant/op_ConstantOfShape (c.py:690-722)
@@ -289,6 +291,35 @@ typedef struct {
 int mgc_hip_mbconv_stem_supported(int C, int KH, int KW, int Cexp, int Cout, int stride);
 void mgc_hip_mbconv_stem(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const mgc_hip_mbconv_args *mb,
                          const mgc_hip_stem_args *st);
+
+/* The ResNet stem convolution as one launch that reads the image in place (an NCHW graph input
+ * needs no NHWC or space-to-depth copy):
+ *   out[n][oh][ow][k] = act(bias[k] + sum_{c < 3, i, j < 7} img(n, c, oh SH - PT + i, ow SW - PL + j) W[k][c][i][j])
+ * with img(n, c, r, s) = st->img[n sn + c sc + r sh + s sw] (zero outside the st->H x st->W
+ * image) and out NHWC with a->ldc floats per pixel. st->C = 3, KH = KW = 7, SH = SW = 2 and 64
+ * output channels (mgc_hip_conv_stem_supported); st->img 4-byte aligned and the image below
+ * 2 GiB; a->w, a->bias and a->out 16-byte aligned, a->ldc >= 64 and a multiple of 4. a->w holds
+ * mgc_hip_conv_stem_weight_floats() floats packed as
+ *   a->w[((e 32 + l) 2 + h) 2 + b] = W[32 b + l][c][i][2 q + h]  (zero for 2 q + h >= 7)
+ * for step e = (c 7 + i) 4 + q. a->tile_rows picks the output tile (8 or 4 rows of 16 pixels;
+ * 0: the library's choice). Sets the launch error outside these limits. Replaces the stem's
+ * mgc_gemm over its MGC_OP_CONV_NCHW operand in the reference's C backend
+ * (src/ml_graph_compiler/codegen/c.py:1099-1226; runtime/mgc_kernels.c:86-133 packs the im2col
+ * panels, :370-396 multiplies). */
+typedef struct {
+    const float *w;     /* packed weights, mgc_hip_conv_stem_weight_floats() floats */
+    const float *bias;  /* [64] or NULL */
+    float *out;         /* NHWC [N][OH][OW] pixels of ldc floats (channels 0..63 written) */
+    long ldc;
+    int N, OH, OW;
+    int act;            /* MGC_ACT_* */
+    float lo, hi;
+    int tile_rows;      /* 0 (library's choice), 4 or 8 */
+} mgc_hip_conv_stem_args;
+
+int mgc_hip_conv_stem_supported(int C, int KH, int KW, int SH, int SW, int Cout);
+long mgc_hip_conv_stem_weight_floats(void);
+void mgc_hip_conv_stem(mgc_hip_exec *x, const mgc_hip_stem_args *st, const mgc_hip_conv_stem_args *a);
 
 /* The expansion and depthwise convolutions of an inverted-residual block as one launch, with
  * the expanded tensor never in memory:

@@ -93,6 +93,10 @@ _INT_OPS = frozenset({"Add", "Sub", "Mul", "Div", "Max", "Min", "Neg", "Abs", "R
 FOLD_TRANSPOSES = True
 # Run stride-2 convolutions over few channels on a space-to-depth copy of the input.
 SPACE_TO_DEPTH = True
+# Run the ResNet stem (7 x 7, stride 2, 3 -> 64 channels) as one mgc_hip_conv_stem launch that
+# reads the image in place (NCHW through its strides when it reaches the stem through a
+# Transpose) instead of the space-to-depth copy and a GEMM; tests turn it off to compare.
+CONV_STEM = True
 # Fuse recognized attention chains into mgc_hip_attention (tests turn it off to compare).
 FUSE_ATTENTION = True
 # Run a LayerNormalization that directly follows the FusedGemm producing its input inside that
@@ -600,10 +604,20 @@ class HipEmitter:
         # (scratch contents live only within one node's launches, so every use shares it).
         self._s2d: dict[int, Value | None] = {}
         self._s2d_skip: set[int] = set()
+        # ResNet stems: id(conv) -> the NCHW tensor read in place, or None for the NHWC input
+        self._cstem: dict[int, Value | None] = {}
+        if CONV_STEM:
+            order = {id(n): i for i, n in enumerate(graph.nodes)}
+            for n in graph.nodes:
+                if id(n) in excluded or not self._conv_stem_ok(n):
+                    continue
+                self._cstem[id(n)] = self._s2d_source(n, order, excluded)
+                if self._cstem[id(n)] is not None:
+                    self._s2d_skip.add(id(n.input(0).producer))
         if SPACE_TO_DEPTH:
             order = {id(n): i for i, n in enumerate(graph.nodes)}
             for n in graph.nodes:
-                if id(n) in excluded or self._s2d_geometry(n) is None:
+                if id(n) in excluded or id(n) in self._cstem or self._s2d_geometry(n) is None:
                     continue
                 self._s2d[id(n)] = self._s2d_source(n, order, excluded)
                 if self._s2d[id(n)] is not None:
@@ -626,7 +640,7 @@ class HipEmitter:
         self._gemm_ln: dict[int, tuple[Node, bool]] = {}
         self._ln_skip: dict[int, Node] = {}
         if FUSE_GEMM_LAYER_NORM and gemm_ln_workspace is not None:
-            taken = excluded | set(self._folds.skipped) | self._s2d_skip | set(self._s2d)
+            taken = excluded | set(self._folds.skipped) | self._s2d_skip | set(self._s2d) | set(self._cstem)
             for node, ln in zip(graph.nodes, graph.nodes[1:]):
                 shape = self._gemm_ln_shape(node, ln, taken)
                 if shape is None:
@@ -1488,6 +1502,9 @@ class HipEmitter:
             )
             self.count("depthwise")
             return
+        if id(node) in self._cstem:
+            self._conv_stem(node, bias, act, lo, hi)
+            return
         if id(node) in self._s2d:
             self._conv_space_to_depth(node, bias, res, act, lo, hi)
             return
@@ -1811,6 +1828,56 @@ class HipEmitter:
         return dict(nb=nb, h=h, w=wd, c=c, kh=kh, kw=kw, kout=kout, pt=pt, pl=pl, P=P, Q=Q,
                     KH=-(-(kh + 2 * P - pt) // 2), KW=-(-(kw + 2 * Q - pl) // 2),
                     oh=g.out_hw[0], ow=g.out_hw[1])
+
+    def _conv_stem_ok(self, node: Node) -> bool:
+        """A ResNet stem mgc_hip_conv_stem computes: a float32 NHWC 7 x 7 convolution of a
+        3-channel image into 64 channels at stride 2, constant weights, no residual, its output
+        in the arena (so 16-byte aligned) and the image below the launch's 2 GiB offset limit."""
+        if node.op not in ("Conv", "FusedConv") or ops.conv_layout(node) != "NHWC":
+            return False
+        if int(node.attrs.get("group", 1)) != 1 or node.input(1).data is None:
+            return False
+        if node.optional_input(3) is not None or node.output in self.graph.outputs:
+            return False
+        xt, wt = node.input(0).tensor_type, node.input(1).tensor_type
+        if xt.dtype != "float32" or xt.rank != 4 or xt.shape[3] != 3 or tuple(wt.shape) != (7, 7, 3, 64):
+            return False
+        g = ops.window_geometry(node, (xt.shape[1], xt.shape[2]), (7, 7))
+        if tuple(g.strides) != (2, 2) or tuple(g.dilations) != (1, 1) or min(g.pads) < 0:
+            return False
+        return xt.nbytes < FUSED_OPERAND_LIMIT
+
+    def _conv_stem(self, node: Node, bias: str, act: str, lo: float, hi: float) -> None:
+        """The ResNet stem as one mgc_hip_conv_stem launch: its image window per output tile is
+        read in place (NCHW through the strides when a Transpose brought it to NHWC) and the
+        weights are packed into the kernel's step order, k pair (c, i, tap columns 2 q, 2 q + 1)
+        with the seventh column padded to eight."""
+        xv = node.input(0)
+        nb, h, wd, c = xv.tensor_type.shape
+        g = ops.window_geometry(node, (h, wd), (7, 7))
+        oh, ow = g.out_hw
+        w = node.input(1).data  # [7][7][3][64]
+        wpad = np.zeros((7, 8, 3, 64), np.float32)
+        wpad[:, :7] = w
+        # [i][q][h][c][b][l] -> [c][i][q][l][h][b]: step e = (c 7 + i) 4 + q, lane (l, h), n block b
+        packed = np.ascontiguousarray(wpad.reshape(7, 4, 2, 3, 2, 32).transpose(3, 0, 1, 5, 2, 4), np.float32)
+        woff = self.weights.add(packed.reshape(-1), key=("stem7", id(node.input(1))))
+        src = self._cstem[id(node)]
+        if src is not None:  # NCHW [n][c][y][x], read in place
+            img, strides = f"(const float *){self.ptr(src)}", (c * h * wd, h * wd, wd, 1)
+        else:  # NHWC [n][y][x][c]
+            img, strides = self.fptr(xv), (h * wd * c, 1, wd * c, c)
+        self.emit(
+            f"{{ mgc_hip_stem_args st; memset(&st, 0, sizeof st); st.img = {img}; st.C = {c}; st.H = {h}; "
+            f"st.W = {wd}; st.sn = {strides[0]}L; st.sc = {strides[1]}L; st.sh = {strides[2]}L; "
+            f"st.sw = {strides[3]}L; st.KH = 7; st.KW = 7; st.SH = 2; st.SW = 2; st.PT = {g.pads[0]}; "
+            f"st.PL = {g.pads[1]}; mgc_hip_conv_stem_args cs; memset(&cs, 0, sizeof cs); "
+            f"cs.w = (const float *)(W + {woff}); cs.bias = {bias}; cs.out = {self.fptr(node.output)}; "
+            f"cs.ldc = 64; cs.N = {nb}; cs.OH = {oh}; cs.OW = {ow}; cs.act = {ACT_CODES[act]}; "
+            f"cs.lo = {_f(lo)}; cs.hi = {_f(hi)}; mgc_hip_conv_stem(x, &st, &cs); }}"
+        )
+        self.count("gemm_stem")
+        self._gemm_flops += ops.flops(node)
 
     def _s2d_source(self, conv: Node, order: dict[int, int], excluded: set[int], reader: Node | None = None) -> Value | None:
         """The NCHW tensor the space-to-depth copy (or, for a stem block, the launch of

@@ -104,7 +104,8 @@ def test_kernel_mix_matches_reference(name, kernels, arena, monkeypatch):
     """Reference kernel mixes at O3: ResNet-50 gemm 54, pool 1, reduce 1, transpose 1, view 1;
     MobileNetV2 gemm 36, depthwise 17 (benchmarks/results/ablation_cnn.json:759-830,1468-1540);
     tiny-cnn gemm 9, depthwise 1 (tests/test_codegen.py:638-647). With the space-to-depth stem
-    the input Transpose folds into the stem's copy; the planned arena is the same either way."""
+    the input Transpose folds into the stem's copy, and with ResNet-50's stem launch into that
+    launch's image reads; the planned arena is the same every way."""
     from ml_graph_compiler.codegen import hip as hip_codegen
 
     make = builders.SAMPLES.get(name) or builders.CONFIGS[name]
@@ -112,6 +113,7 @@ def test_kernel_mix_matches_reference(name, kernels, arena, monkeypatch):
     monkeypatch.setattr(hip_codegen, "FUSE_DEPTHWISE_POINTWISE", False)
     monkeypatch.setattr(hip_codegen, "FUSE_STEM_BLOCK", False)
     monkeypatch.setattr(hip_codegen, "SPACE_TO_DEPTH", False)
+    monkeypatch.setattr(hip_codegen, "CONV_STEM", False)
     gen = generate_hip(o3(make()))
     assert gen.kernels == kernels
     if arena is not None:
@@ -122,6 +124,14 @@ def test_kernel_mix_matches_reference(name, kernels, arena, monkeypatch):
     del moved["transpose"]
     assert s2d.kernels == moved
     assert s2d.plan.arena_bytes == gen.plan.arena_bytes
+    # ResNet-50's 7 x 7 stem reads the NCHW image in place as one mgc_hip_conv_stem launch
+    monkeypatch.setattr(hip_codegen, "CONV_STEM", True)
+    stem = generate_hip(o3(make()))
+    if name == "resnet50":
+        moved = dict(moved, gemm=kernels["gemm"] - 1, gemm_stem=1)
+        del moved["space_to_depth"]
+    assert stem.kernels == moved
+    assert stem.plan.arena_bytes == gen.plan.arena_bytes
     assert gen.weights.nbytes % 256 == 0 and len(gen.weights.digest()) == 24
     assert "mgc_forward" in gen.source and "int mgc_run(" in gen.source
 
@@ -135,7 +145,7 @@ def test_projection_shortcuts_join_their_block_gemm():
     pairs = find_projection_shortcuts(g)
     assert len(pairs) == 4
     gen = generate_hip(g, gemm_workspace=native.gemm_workspace_floats)
-    assert gen.kernels["gemm_shortcut"] == 4 and gen.kernels["gemm"] == 50
+    assert gen.kernels["gemm_shortcut"] == 4 and gen.kernels["gemm"] == 49 and gen.kernels["gemm_stem"] == 1
     assert gen.source.count("g.k1 = ") == 4
     # the shortcut's FLOPs are timed with the GEMM that computes them
     from ml_graph_compiler import ops
