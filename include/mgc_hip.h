@@ -297,13 +297,14 @@ void mgc_hip_mbconv_stem(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const mgc_
  *   out[n][oh][ow][k] = act(bias[k] + sum_{c < 3, i, j < 7} img(n, c, oh SH - PT + i, ow SW - PL + j) W[k][c][i][j])
  * with img(n, c, r, s) = st->img[n sn + c sc + r sh + s sw] (zero outside the st->H x st->W
  * image) and out NHWC with a->ldc floats per pixel. st->C = 3, KH = KW = 7, SH = SW = 2 and 64
- * output channels (mgc_hip_conv_stem_supported); st->img 4-byte aligned and the image below
- * 2 GiB; a->w, a->bias and a->out 16-byte aligned, a->ldc >= 64 and a multiple of 4. a->w holds
+ * output channels (mgc_hip_conv_stem_supported); st->img and a->out 4-byte aligned, the image
+ * below 2 GiB, a->w 16-byte aligned, a->ldc >= 64. a->w holds
  * mgc_hip_conv_stem_weight_floats() floats packed as
  *   a->w[((e 32 + l) 2 + h) 2 + b] = W[32 b + l][c][i][2 q + h]  (zero for 2 q + h >= 7)
- * for step e = (c 7 + i) 4 + q. a->tile_rows picks the output tile (8 or 4 rows of 16 pixels;
- * 0: the library's choice). Sets the launch error outside these limits. Replaces the stem's
- * mgc_gemm over its MGC_OP_CONV_NCHW operand in the reference's C backend
+ * for step e = (c 7 + i) 4 + q. The output is cut into tiles of 4 x 16 pixels that persistent
+ * workgroups take in turn; a->workgroups caps their number (0: the library's choice, one round
+ * over the CUs). Sets the launch error outside these limits. Replaces the stem's mgc_gemm over
+ * its MGC_OP_CONV_NCHW operand in the reference's C backend
  * (src/ml_graph_compiler/codegen/c.py:1099-1226; runtime/mgc_kernels.c:86-133 packs the im2col
  * panels, :370-396 multiplies). */
 typedef struct {
@@ -314,7 +315,7 @@ typedef struct {
     int N, OH, OW;
     int act;            /* MGC_ACT_* */
     float lo, hi;
-    int tile_rows;      /* 0 (library's choice), 4 or 8 */
+    int workgroups;     /* 0 (library's choice) or at most this many persistent workgroups */
 } mgc_hip_conv_stem_args;
 
 int mgc_hip_conv_stem_supported(int C, int KH, int KW, int SH, int SW, int Cout);

@@ -7,50 +7,52 @@
 // (src/ml_graph_compiler/codegen/c.py:1099-1226 emits mgc_gemm over an MGC_OP_CONV_NCHW
 // operand; runtime/mgc_kernels.c:86-133 packs it, :370-396 multiplies). Here the packing is an
 // LDS window per output tile:
-//  1. A workgroup of 256 threads owns TH x 16 output pixels of one image and all 64 channels.
-//     The image window those pixels read (3 channels x (2 (TH - 1) + 7) rows x 38 columns; zero
-//     outside the image, as the padding says) is loaded once, coalesced (neighbouring threads
-//     read neighbouring columns of one row), together with the packed weights, and both go to
-//     LDS.
-//  2. The contraction runs over k = (c, i, j) with the tap column j padded from 7 to 8, as 84
-//     steps of v_mfma_f32_32x32x2f32; step e = (c 7 + i) 4 + q takes j = 2 q in lane half 0 and
-//     j = 2 q + 1 in lane half 1, so every A operand is one LDS read at an address the step
-//     fixes at compile time plus the lane's own (pixel, half) offset, and every B operand one
-//     read of the packed weights (two n blocks in one 8-byte read when a wave owns all 64
-//     channels). The window's row pitch of 48 floats puts the 32 pixels (two rows of 16) a wave
-//     reads per step in 32 different bank pairs.
-//  3. The accumulators go through LDS (in the weights' space) and leave as 16-byte stores of
-//     whole pixel rows, with the bias and activation applied on the way (the folded BatchNorm
-//     and ReLU of the graph).
-// TH = 8 (128 pixels: wave w owns tile rows 2 w, 2 w + 1 and both 32-channel blocks) for large
-// batches; TH = 4 (64 pixels: wave w owns rows 2 (w / 2), 2 (w / 2) + 1 and channel block
-// w % 2) spreads a small batch over twice the workgroups.
+//  * An output tile is 4 x 16 pixels of one image times all 64 channels. Wave w of a workgroup
+//    owns tile rows 2 (w / 2) and 2 (w / 2) + 1 (32 pixels, lane li = pixel (li / 16, li % 16))
+//    and channel block w % 2 (32 channels).
+//  * The contraction runs over k = (c, i, j) with the tap column j padded from 7 to 8, as 84
+//    steps of v_mfma_f32_32x32x2f32; step e = (c 7 + i) 4 + q takes j = 2 q in lane half 0 and
+//    j = 2 q + 1 in lane half 1. A wave's B operand for every step (its 32 channels: 84 values
+//    per lane) stays in registers for the whole launch; each A operand is one LDS read of the
+//    tile's image window at an address the step fixes at compile time plus the lane's own
+//    (pixel, half) offset. The window (3 channels x 13 rows x 38 columns, zero outside the image
+//    as the padding says) has a row pitch of 48 floats, which puts the 64 lanes of a read in 64
+//    different banks.
+//  * Workgroups are persistent: each takes tiles g, g + G, ... (G workgroups; neighbouring
+//    workgroups, which run on one XCD, take neighbouring tiles of one image, whose windows
+//    overlap), and requests the next tile's window (coalesced four-byte loads: neighbouring
+//    threads read neighbouring columns of one row) before multiplying the current one, so the
+//    load latency hides behind the MFMAs; two LDS window buffers alternate.
+//  * The accumulators leave straight from registers with the bias and activation applied (the
+//    folded BatchNorm and ReLU of the graph): for each register, lanes 0-31 write 32
+//    consecutive channels (128 bytes) of one pixel and lanes 32-63 those of another.
 #include "mgc_device.h"
-
-#include <stdio.h>
 
 namespace mgc {
 
 typedef float floatx16s __attribute__((ext_vector_type(16)));
-typedef float f4s __attribute__((ext_vector_type(4)));
-typedef const __attribute__((address_space(1))) f4s gf4s;
 
 constexpr int kCsC = 3;                          // image channels
 constexpr int kCsK = 7;                          // window rows and columns
 constexpr int kCsS = 2;                          // stride
 constexpr int kCsCout = 64;                      // output channels
 constexpr int kCsSteps = kCsC * kCsK * 4;        // k pairs (c, i, q): tap columns 2 q, 2 q + 1
+constexpr int kCsTH = 4;                         // output rows per tile
 constexpr int kCsTW = 16;                        // output columns per tile
-constexpr int kCsWC = kCsS * (kCsTW - 1) + 8;    // window columns a tile reads: 38
+constexpr int kCsWR = kCsS * (kCsTH - 1) + kCsK; // window rows: 13
+constexpr int kCsWC = kCsS * (kCsTW - 1) + 8;    // window columns: 38
 constexpr int kCsPitch = 48;                     // window row pitch (floats)
+constexpr int kCsPlane = kCsWR * kCsPitch;       // one channel's window rows
+constexpr int kCsWin = kCsC * kCsPlane;          // one window buffer (floats)
 constexpr int kCsWFloats = kCsSteps * 128;       // packed weights: [step][32 lanes][2 halves][2 n blocks]
-constexpr int kCsSP = 72;                        // staging row pitch (floats) per output pixel
+constexpr int kCsCUs = 256;                      // MI355X compute units
+constexpr int kCsPerCU = 3;                      // workgroups a CU holds at once (the registers allow three)
 
 struct CsDev {
     const float *img;
     unsigned sn, sc, sh, sw;  // element strides of image, channel, row and column
     int H, W, PT, PL;
-    int OH, OW, tiles_h, tiles_w;
+    int OH, OW, tiles_h, tiles_w, tiles;
     long img_bytes;           // bytes from img to the last element the strides reach
     const float *w;           // packed weights
     const float *bias;        // [64] or null
@@ -60,127 +62,133 @@ struct CsDev {
     float lo, hi;
 };
 
-template <int TH>
-__global__ void __launch_bounds__(256) gemm_stem_kernel(const CsDev d) {
-    constexpr int WR = kCsS * (TH - 1) + kCsK;  // window rows
-    constexpr int PLANE = WR * kCsPitch;
-    constexpr int WIN_ELEMS = kCsC * WR * kCsWC;
-    constexpr int NPIX = TH * kCsTW;
-    constexpr int WQUADS = kCsWFloats / 4;
-    constexpr int WQ_PER = (WQUADS + 255) / 256;
-    constexpr int WIN_PER = (WIN_ELEMS + 255) / 256;
-    static_assert(NPIX * kCsSP <= kCsWFloats, "the staged outputs fit the weights' space");
-    __shared__ __attribute__((aligned(16))) float lds[kCsWFloats + kCsC * PLANE];
-    float *const wl = lds;
-    float *const win = lds + kCsWFloats;
+// Three waves per SIMD: 163 registers (the 84 B values among them) without spilling.
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) gemm_stem_kernel(const CsDev d) {
+    __shared__ __attribute__((aligned(16))) float win[2][kCsWin];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int li = lane & 31, lh = lane >> 5;
+    const int pb = wave >> 1, nb = wave & 1;
 
-    // neighbouring tiles of one image (whose windows overlap) run on one XCD
-    const int blk = xcd_block();
-    const int per_img = d.tiles_h * d.tiles_w;
-    const int n = blk / per_img;
-    const int rem = blk - n * per_img;
-    const int ty = rem / d.tiles_w;
-    const int oy0 = ty * TH, ox0 = (rem - ty * d.tiles_w) * kCsTW;
-    const int iy0 = oy0 * kCsS - d.PT, ix0 = ox0 * kCsS - d.PL;
-
-    // 1. every load of the tile goes out before the first is used: the packed weights (16-byte
-    // loads) and the image window (four-byte buffer loads; an element outside the image gets an
-    // offset past the resource's end and reads as zero)
-    f4s wq[WQ_PER];
+    // the wave's B operand of every step: W[32 nb + li][k = 2 e + lh]
+    float bw[kCsSteps];
+    const float *const wsrc = d.w + (li * 2 + lh) * 2 + nb;
 #pragma unroll
-    for (int u = 0; u < WQ_PER; ++u) {
-        const int e = tid + 256 * u;
-        if (e < WQUADS) wq[u] = *(gf4s *)(d.w + 4 * e);
-    }
+    for (int e = 0; e < kCsSteps; ++e) bw[e] = wsrc[e * 128];
+    const float bias = d.bias ? d.bias[32 * nb + li] : 0.0f;
+
     constexpr unsigned OOB = 0x80000000u;
     const __amdgpu_buffer_rsrc_t rimg =
         __builtin_amdgcn_make_buffer_rsrc((void *)d.img, (short)0, (int)d.img_bytes, 0x00020000);
-    const unsigned ibase = (unsigned)n * d.sn;
-    float wv[WIN_PER];
+    const int per_img = d.tiles_h * d.tiles_w;
+    // image, first output row and column of tile t
+    auto origin = [&](int t, int &n, int &oy0, int &ox0) __attribute__((always_inline)) {
+        n = t / per_img;
+        const int rem = t - n * per_img;
+        const int ty = rem / d.tiles_w;
+        oy0 = ty * kCsTH;
+        ox0 = (rem - ty * d.tiles_w) * kCsTW;
+    };
+    // The window of tile t into registers: wave w moves window rows w, w + 4, ... (row R =
+    // channel R / 13, image row R % 13 of the window), lane l column l < 38, so the row
+    // arithmetic is scalar and the column bounds are tested once per tile. An element outside
+    // the image gets an offset past the resource's end and reads as zero.
+    constexpr int WROWS = kCsC * kCsWR;              // 39 window rows over the channels
+    constexpr int RPW = (WROWS + 3) / 4;             // rows per wave
+    static_assert(kCsWC <= 64, "a window row fits a wave");
+    const bool col_ok = lane < kCsWC;
+    auto fetch_window = [&](int t, float (&v)[RPW]) __attribute__((always_inline)) {
+        int n, oy0, ox0;
+        origin(t, n, oy0, ox0);
+        const int iy0 = oy0 * kCsS - d.PT, ix0 = ox0 * kCsS - d.PL;
+        const int x = ix0 + lane;
+        const bool x_ok = col_ok && (unsigned)x < (unsigned)d.W;
+        const unsigned xoff = (unsigned)n * d.sn + (unsigned)x * d.sw;
 #pragma unroll
-    for (int u = 0; u < WIN_PER; ++u) {
-        const int e = tid + 256 * u;
-        const int c = e / (WR * kCsWC), r0 = e - c * (WR * kCsWC);
-        const int r = r0 / kCsWC, col = r0 - r * kCsWC;
-        const int y = iy0 + r, x = ix0 + col;
-        const bool in = e < WIN_ELEMS && (unsigned)y < (unsigned)d.H && (unsigned)x < (unsigned)d.W;
-        const unsigned off = in ? (ibase + (unsigned)c * d.sc + (unsigned)y * d.sh + (unsigned)x * d.sw) * 4u : OOB;
-        wv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rimg, off, 0, 0));
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int u = 0; u < WQ_PER; ++u) {
-        const int e = tid + 256 * u;
-        if (e < WQUADS) *reinterpret_cast<f4s *>(&wl[4 * e]) = wq[u];
-    }
-#pragma unroll
-    for (int u = 0; u < WIN_PER; ++u) {
-        const int e = tid + 256 * u;
-        if (e < WIN_ELEMS) {
-            const int c = e / (WR * kCsWC), r0 = e - c * (WR * kCsWC);
-            const int r = r0 / kCsWC, col = r0 - r * kCsWC;
-            win[c * PLANE + r * kCsPitch + col] = wv[u];
+        for (int j = 0; j < RPW; ++j) {
+            const int R = wave + 4 * j;
+            const int c = R / kCsWR, y = iy0 + (R - c * kCsWR);
+            const bool in = R < WROWS && x_ok && (unsigned)y < (unsigned)d.H;
+            const unsigned off = in ? (xoff + (unsigned)c * d.sc + (unsigned)y * d.sh) * 4u : OOB;
+            v[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rimg, off, 0, 0));
         }
+    };
+    auto place_window = [&](const float (&v)[RPW], float *buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < RPW; ++j) {
+            const int R = wave + 4 * j;
+            const int c = R / kCsWR;
+            if (R < WROWS && col_ok) buf[c * kCsPlane + (R - c * kCsWR) * kCsPitch + lane] = v[j];
+        }
+    };
+
+    // neighbouring workgroups (one XCD) take neighbouring tiles
+    const int G = gridDim.x;
+    int t = xcd_block();
+    float pv[RPW];
+    if (t < d.tiles) {
+        fetch_window(t, pv);
+        place_window(pv, win[0]);
     }
     __syncthreads();
+    const int aoff = (2 * pb + (li >> 4)) * kCsS * kCsPitch + kCsS * (li & 15) + lh;
+    int cur = 0;
+    for (; t < d.tiles; t += G) {
+        const int tn = t + G;
+        if (tn < d.tiles) fetch_window(tn, pv);
 
-    // 2. the contraction. TH = 8: wave w owns pixels 32 w .. 32 w + 31 and both n blocks;
-    // TH = 4: pixels 32 (w / 2) .. + 31 and n block w % 2. Lane li is pixel (row, column)
-    // (li / 16, li % 16) of the wave's two rows.
-    constexpr bool BOTH = TH == 8;
-    const int pb = BOTH ? wave : wave >> 1;
-    const int nb = BOTH ? 0 : wave & 1;
-    const float *const wa = win + (2 * pb + (li >> 4)) * kCsS * kCsPitch + kCsS * (li & 15) + lh;
-    const float *const wb = wl + (li * 2 + lh) * 2 + nb;
-    floatx16s acc0, acc1;
+        // the contraction over the current window: A operands move from LDS to registers a
+        // chunk of CH steps ahead of the multiplies that use them; the scheduling barriers keep
+        // the compiler from sinking the reads back to their uses
+        const float *const wa = win[cur] + aoff;
+        floatx16s acc;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc0[r] = acc1[r] = 0.0f;
+        for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+        constexpr int CH = 6;
+        static_assert(kCsSteps % CH == 0, "whole chunks");
+        float ra[2][CH];
+        auto fetch_a = [&](const int ch, const int buf) __attribute__((always_inline)) {
 #pragma unroll
-    for (int c = 0; c < kCsC; ++c)
-#pragma unroll
-        for (int i = 0; i < kCsK; ++i)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int e = (c * kCsK + i) * 4 + q;
-                const float a = wa[c * PLANE + i * kCsPitch + 2 * q];
-                if constexpr (BOTH) {
-                    const float2 b = *reinterpret_cast<const float2 *>(&wb[e * 128]);
-                    acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b.x, acc0, 0, 0, 0);
-                    acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b.y, acc1, 0, 0, 0);
-                } else {
-                    acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a, wb[e * 128], acc0, 0, 0, 0);
-                }
+            for (int s = 0; s < CH; ++s) {
+                const int e = ch * CH + s;
+                const int c = e / (kCsK * 4), i = (e / 4) % kCsK, q = e % 4;
+                ra[buf][s] = wa[c * kCsPlane + i * kCsPitch + 2 * q];
             }
-
-    // 3. register r of lane (li, lh) is pixel 8 (r / 4) + 4 lh + r % 4 of the wave's 32, channel
-    // li of its n block; staged as [pixel][64] (pitch 72: lane halves 32 banks apart)
-    __syncthreads();  // every wave is past its last read of the weights
-    float *const stg = lds;
+        };
+        fetch_a(0, 0);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int pix = 32 * pb + 8 * (r >> 2) + 4 * lh + (r & 3);
-        stg[pix * kCsSP + 32 * nb + li] = acc0[r];
-        if constexpr (BOTH) stg[pix * kCsSP + 32 + li] = acc1[r];
-    }
-    __syncthreads();
-    const int q4 = tid & 15;  // the channel quad this thread stores (the same for every pixel it takes)
-    const f4s zero4 = {0.f, 0.f, 0.f, 0.f};
-    const f4s b4 = d.bias ? *(gf4s *)(d.bias + 4 * q4) : zero4;
+        for (int ch = 0; ch < kCsSteps / CH; ++ch) {
+            if (ch + 1 < kCsSteps / CH) fetch_a(ch + 1, (ch + 1) & 1);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int u = 0; u < NPIX * 16 / 256; ++u) {
-        const int pix = (tid >> 4) + 16 * u;
-        const int oy = oy0 + (pix >> 4), ox = ox0 + (pix & 15);
-        if (oy < d.OH && ox < d.OW) {
-            f4s v = *reinterpret_cast<const f4s *>(&stg[pix * kCsSP + 4 * q4]) + b4;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) v[t] = apply_act(v[t], d.act, d.lo, d.hi);
-            *reinterpret_cast<f4s *>(d.out + (((long)n * d.OH + oy) * d.OW + ox) * d.ldc + 4 * q4) = v;
+            for (int s = 0; s < CH; ++s)
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(ra[ch & 1][s], bw[ch * CH + s], acc, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
         }
+
+        // the next window goes to the other buffer (its last readers finished before the
+        // previous iteration's barrier)
+        if (tn < d.tiles) place_window(pv, win[cur ^ 1]);
+
+        // register r of lane (li, lh): pixel 8 (r / 4) + 4 lh + r % 4 of the wave's 32, channel
+        // 32 nb + li; a tile wholly inside the output takes no bounds tests
+        int n, oy0, ox0;
+        origin(t, n, oy0, ox0);
+        float *const obase = d.out + (((long)n * d.OH + oy0) * d.OW + ox0) * d.ldc + 32 * nb + li;
+        const bool whole = oy0 + kCsTH <= d.OH && ox0 + kCsTW <= d.OW;
+        const long row_st = (long)d.OW * d.ldc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int pix = 32 * pb + 8 * (r >> 2) + 4 * lh + (r & 3);
+            const int py = pix >> 4, px = pix & 15;
+            float v = acc[r] + bias;
+            v = d.act == MGC_ACT_RELU ? (v > 0.0f ? v : 0.0f) : apply_act(v, d.act, d.lo, d.hi);
+            if (whole || (oy0 + py < d.OH && ox0 + px < d.OW)) obase[py * row_st + px * d.ldc] = v;
+        }
+        __syncthreads();
+        cur ^= 1;
     }
 }
 
@@ -207,14 +215,10 @@ extern "C" void mgc_hip_conv_stem(mgc_hip_exec *x, const mgc_hip_stem_args *st, 
     const long img_bytes = geo ? ((long)(a->N - 1) * st->sn + (long)(st->C - 1) * st->sc +
                                   (long)(st->H - 1) * st->sh + (long)(st->W - 1) * st->sw + 1) * 4
                                : -1;
-    const int th = a->tile_rows == 4 || a->tile_rows == 8 ? a->tile_rows : 0;
-    const int th_auto = (long)a->N * ((a->OH + 7) / 8) * ((a->OW + kCsTW - 1) / kCsTW) < 512 ? 4 : 8;
-    const int TH = th ? th : th_auto;
-    const long tiles = (long)a->N * ((a->OH + TH - 1) / TH) * ((a->OW + kCsTW - 1) / kCsTW);
+    const long tiles = (long)a->N * ((a->OH + kCsTH - 1) / kCsTH) * ((a->OW + kCsTW - 1) / kCsTW);
     const bool ok = geo && st->img && ((uintptr_t)st->img & 3) == 0 && img_bytes > 0 && img_bytes < 0x7fffffffL &&
-                    (a->tile_rows == 0 || th != 0) && a->w && ((uintptr_t)a->w & 15) == 0 &&
-                    ((uintptr_t)a->bias & 15) == 0 && a->out && ((uintptr_t)a->out & 15) == 0 &&
-                    a->ldc >= kCsCout && a->ldc % 4 == 0 && tiles < 0x7fffffffL &&
+                    a->workgroups >= 0 && a->w && ((uintptr_t)a->w & 15) == 0 && a->out &&
+                    ((uintptr_t)a->out & 3) == 0 && a->ldc >= kCsCout && tiles < 0x7fffffffL &&
                     (long)(st->H + kCsK) * (st->W + kCsK) < 0x40000000L;
     if (!ok) {
         x->launch_error = (int)hipErrorInvalidValue;
@@ -233,8 +237,9 @@ extern "C" void mgc_hip_conv_stem(mgc_hip_exec *x, const mgc_hip_stem_args *st, 
     d.PL = st->PL;
     d.OH = a->OH;
     d.OW = a->OW;
-    d.tiles_h = (a->OH + TH - 1) / TH;
+    d.tiles_h = (a->OH + kCsTH - 1) / kCsTH;
     d.tiles_w = (a->OW + kCsTW - 1) / kCsTW;
+    d.tiles = (int)tiles;
     d.img_bytes = img_bytes;
     d.w = a->w;
     d.bias = a->bias;
@@ -243,8 +248,8 @@ extern "C" void mgc_hip_conv_stem(mgc_hip_exec *x, const mgc_hip_stem_args *st, 
     d.act = a->act;
     d.lo = a->lo;
     d.hi = a->hi;
-    if (TH == 8)
-        MGC_LAUNCH(x, gemm_stem_kernel<8>, dim3((unsigned)tiles), dim3(256), 0, d);
-    else
-        MGC_LAUNCH(x, gemm_stem_kernel<4>, dim3((unsigned)tiles), dim3(256), 0, d);
+    // one round of workgroups over the CUs (three per CU), or one per tile when tiles are fewer
+    const long cap = a->workgroups > 0 ? a->workgroups : (long)kCsPerCU * kCsCUs;
+    const unsigned grid = (unsigned)(tiles < cap ? tiles : cap);
+    MGC_LAUNCH(x, gemm_stem_kernel, dim3(grid), dim3(256), 0, d);
 }

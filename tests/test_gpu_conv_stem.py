@@ -9,9 +9,10 @@ contraction on MFMA from LDS. Graph cases compile a stem at O3 and compare with 
 unoptimized graph at the CNN bound (1e-4 absolute) and with the space-to-depth path it replaces;
 shapes cover ResNet-50's 224 x 224 input, odd images whose last tiles are partial in both
 directions, asymmetric padding, no padding, and each activation the emitter fuses. The C-ABI
-cases call the entry point directly with each output tile (4 and 8 rows of 16 pixels) forced,
-over an NHWC caller image with a padded output row stride, against a float64 convolution, and
-check that shapes outside its limits are refused with MGC_ERR_ARGS.
+cases call the entry point directly with the persistent workgroups capped at one and seven (so
+one workgroup walks every tile through its prefetch loop, or tiles are dealt unevenly) and at
+the library's choice, over an NHWC caller image with a padded output row stride, against a
+float64 convolution, and check that shapes outside its limits are refused with MGC_ERR_ARGS.
 """
 
 from __future__ import annotations
@@ -142,7 +143,7 @@ class ConvStemArgs(ctypes.Structure):
 
     _fields_ = [("w", ctypes.c_void_p), ("bias", ctypes.c_void_p), ("out", ctypes.c_void_p), ("ldc", ctypes.c_long),
                 ("N", ctypes.c_int), ("OH", ctypes.c_int), ("OW", ctypes.c_int), ("act", ctypes.c_int),
-                ("lo", ctypes.c_float), ("hi", ctypes.c_float), ("tile_rows", ctypes.c_int)]
+                ("lo", ctypes.c_float), ("hi", ctypes.c_float), ("workgroups", ctypes.c_int)]
 
 
 def pack_weights(w_oihw: np.ndarray) -> np.ndarray:
@@ -177,13 +178,15 @@ def capi():
     hip.free()
 
 
-@pytest.mark.parametrize("tile_rows", [4, 8])
-def test_stem_entry_point_each_tile(capi, tile_rows):
+@pytest.mark.parametrize("workgroups", [0, 1, 7])
+def test_stem_entry_point(capi, workgroups):
     """NHWC caller image of 2 x 53 x 38, pads (3, 2), output rows of 68 floats (channels 64..67
-    must stay untouched), each activation the entry point applies."""
+    must stay untouched), each activation the entry point applies; the persistent workgroups
+    capped at one (every tile through one workgroup's prefetch loop) and at seven (tiles dealt
+    unevenly) as well as the library's choice."""
     lib, hip, x = capi
     assert lib.mgc_hip_conv_stem_weight_floats() == 84 * 128
-    rng = np.random.default_rng(20 + tile_rows)
+    rng = np.random.default_rng(20 + workgroups)
     n, h, w, pt, pl, ldc = 2, 53, 38, 3, 2, 68
     oh, ow = (h + 2 * pt - 7) // 2 + 1, (w + 2 * pl - 7) // 2 + 1
     img = rng.standard_normal((n, h, w, 3)).astype(np.float32)
@@ -200,7 +203,7 @@ def test_stem_entry_point_each_tile(capi, tile_rows):
     for act in ("none", "relu", "clip"):
         hip.put(out, np.full(n * oh * ow * ldc, np.nan, np.float32))
         a = ConvStemArgs(w=wbuf, bias=bbuf, out=out, ldc=ldc, N=n, OH=oh, OW=ow, act=ACTS.index(act), lo=-0.5,
-                         hi=0.75, tile_rows=tile_rows)
+                         hi=0.75, workgroups=workgroups)
         lib.mgc_hip_conv_stem(x, ctypes.byref(st), ctypes.byref(a))
         assert lib.mgc_hip_exec_status(x) == MGC_OK, lib.mgc_hip_last_error()
         got = hip.download(out, (n, oh, ow, ldc))
@@ -216,11 +219,11 @@ def test_stem_entry_point_refuses_unsupported(capi):
     ok = dict(C=3, H=16, W=16, sn=4 * 256, sc=256, sh=16, sw=1, KH=7, KW=7, SH=2, SW=2, PT=3, PL=3)
     for bad in (dict(C=4), dict(KH=5), dict(SW=1), dict(PT=-1)):
         st = StemArgs(img=img, **{**ok, **bad})
-        a = ConvStemArgs(w=wbuf, out=out, ldc=64, N=1, OH=8, OW=8, act=0, tile_rows=0)
+        a = ConvStemArgs(w=wbuf, out=out, ldc=64, N=1, OH=8, OW=8, act=0, workgroups=0)
         lib.mgc_hip_conv_stem(x, ctypes.byref(st), ctypes.byref(a))
         assert lib.mgc_hip_exec_status(x) == MGC_ERR_ARGS, bad
     st = StemArgs(img=img, **ok)
-    for bad in (dict(ldc=62), dict(tile_rows=5)):
-        a = ConvStemArgs(**{**dict(w=wbuf, out=out, ldc=64, N=1, OH=8, OW=8, act=0, tile_rows=0), **bad})
+    for bad in (dict(ldc=62), dict(workgroups=-1)):
+        a = ConvStemArgs(**{**dict(w=wbuf, out=out, ldc=64, N=1, OH=8, OW=8, act=0, workgroups=0), **bad})
         lib.mgc_hip_conv_stem(x, ctypes.byref(st), ctypes.byref(a))
         assert lib.mgc_hip_exec_status(x) == MGC_ERR_ARGS, bad
