@@ -775,6 +775,147 @@ __global__ void __launch_bounds__(256) depthwise3x3_nhwc_lds(const DwGeo g, int 
     }
 }
 
+// 3x3, stride 1, dilation 1, C % 4 == 0, for large launches: a workgroup streams down a strip
+// of output columns for a slice of at most 64 channel quads over a run of output rows. Thread
+// (j, q) owns channel quad q of the slice and output columns 4 j .. 4 j + 3 of the strip (so
+// the strip is 4 * floor(256 / nq) columns wide): its nine weight quads stay in registers and
+// each output row costs it 18 LDS reads for four outputs. The input rows the strip reads go
+// through an LDS ring of four rows: while output row k of the run (input rows counted from the
+// run's first) is computed from ring rows k .. k + 2, input row k + 4 is requested into
+// registers and input row k + 3, requested during output row k - 1, lands in the slot that
+// row k - 1 held, so every row's latency hides behind two output rows of work and each input
+// byte crosses HBM -> CU about once. Taps accumulate after the bias in row-major order and rows
+// or columns outside the image add zero products, as in the other depthwise kernels.
+constexpr int kDwRowsCQ = 64;     // channel quads per workgroup at most
+constexpr int kDwRowsQuads = 4 * 256 + 2 * kDwRowsCQ;  // quads of a ring row at most: (4 G + 2) nq
+__global__ void __launch_bounds__(256) depthwise3x3_nhwc_rows(const DwGeo g, int strips, int cgroups, int cq,
+                                                              int chunks, int rows_per, const float *in,
+                                                              const float *w, const float *bias, const float *res,
+                                                              float *out) {
+    __shared__ float4 ring[4][kDwRowsQuads];
+    int b = xcd_block();
+    const int cgi = b % cgroups;
+    b /= cgroups;
+    const int chunk = b % chunks;
+    b /= chunks;
+    const int strip = b % strips;
+    const int n = b / strips;
+    const int C4 = g.C >> 2;
+    const int c4base = cgi * cq;
+    const int nq = min(cq, C4 - c4base);     // quads of this slice
+    const int G = 256 / nq;                  // column groups
+    const int TW = 4 * G;                    // strip width
+    const int IWp = TW + 2;                  // input pixels per ring row
+    const int ow0 = strip * TW, iw0 = ow0 - g.PL;
+    const int oh_begin = chunk * rows_per, oh_end = min(g.OH, oh_begin + rows_per);
+    const float4 *img = reinterpret_cast<const float4 *>(in) + (long)n * g.H * g.W * C4 + c4base;
+    const float4 zero4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const int tid = threadIdx.x;
+    const int row_elems = IWp * nq;          // quads of one ring row (<= 4 * 256 + 2 * nq)
+    const int per = (row_elems + 255) / 256;
+    constexpr int PER_MAX = (kDwRowsQuads + 255) / 256;
+    const int q = tid % nq, j = tid / nq;
+    const bool worker = j < G;
+    const int c4 = c4base + q;
+
+    float4 wv[9];
+    const float4 *w4 = reinterpret_cast<const float4 *>(w);
+#pragma unroll
+    for (int t = 0; t < 9; ++t) wv[t] = worker ? w4[t * C4 + c4] : zero4;
+    const float4 bv = worker && bias ? reinterpret_cast<const float4 *>(bias)[c4] : zero4;
+
+    auto slot_of = [](int ih) { return (ih + 8) & 3; };
+    // input row ih of the strip into registers: buffer loads over the image, an element outside
+    // it (or past the slice) at an offset past the resource's end, which reads as zero
+    const __amdgpu_buffer_rsrc_t rimg = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)img, (short)0, (int)(((long)g.H * g.W * C4 - c4base) * 16), 0x00020000);
+    constexpr unsigned OOB = 0x80000000u;
+    auto fetch = [&](int ih, float4 (&v)[PER_MAX]) __attribute__((always_inline)) {
+        const bool row_in = ih >= 0 && ih < g.H;
+#pragma unroll
+        for (int k = 0; k < PER_MAX; ++k) {
+            const int e = tid + 256 * k;
+            const int px = e / nq, qq = e - px * nq;
+            const int iw = iw0 + px;
+            const bool ok = k < per && e < row_elems && row_in && iw >= 0 && iw < g.W;
+            const unsigned off = ok ? (unsigned)(((ih * g.W + iw) * C4 + qq) * 16) : OOB;
+            v[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rimg, off, 0, 0));
+        }
+    };
+    auto place = [&](int slot, const float4 (&v)[PER_MAX]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < PER_MAX; ++k) {
+            const int e = tid + 256 * k;
+            if (k < per && e < row_elems) ring[slot][e] = v[k];
+        }
+    };
+    // input rows oh_begin - PT .. oh_begin - PT + 3: the first output row's three and the next one
+    const int ih0 = oh_begin - g.PT;
+    float4 pa[PER_MAX], pb[PER_MAX];
+    fetch(ih0, pa);
+    fetch(ih0 + 1, pb);
+    place(slot_of(ih0), pa);
+    place(slot_of(ih0 + 1), pb);
+    fetch(ih0 + 2, pa);
+    fetch(ih0 + 3, pb);
+    place(slot_of(ih0 + 2), pa);
+    place(slot_of(ih0 + 3), pb);
+    __syncthreads();
+    // one output row: request input row oh - PT + 4 into rq, compute, then place input row
+    // oh - PT + 3 (requested during the previous output row, in rl) in the slot of row
+    // oh - PT - 1, which the finished output row oh - 1 read last
+    auto step = [&](const int oh, float4 (&rq)[PER_MAX], float4 (&rl)[PER_MAX]) __attribute__((always_inline)) {
+        if (oh + 2 < oh_end) fetch(oh - g.PT + 4, rq);
+        if (worker) {
+            float4 acc[4] = {bv, bv, bv, bv};
+#pragma unroll
+            for (int kh = 0; kh < 3; ++kh) {
+                const float4 *rr = ring[slot_of(oh - g.PT + kh)] + 4 * j * nq + q;
+                float4 xs[6];
+#pragma unroll
+                for (int c = 0; c < 6; ++c) xs[c] = rr[c * nq];
+#pragma unroll
+                for (int kw = 0; kw < 3; ++kw) {
+                    const float4 wt = wv[kh * 3 + kw];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        acc[u].x = fmaf(xs[u + kw].x, wt.x, acc[u].x);
+                        acc[u].y = fmaf(xs[u + kw].y, wt.y, acc[u].y);
+                        acc[u].z = fmaf(xs[u + kw].z, wt.z, acc[u].z);
+                        acc[u].w = fmaf(xs[u + kw].w, wt.w, acc[u].w);
+                    }
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int ow = ow0 + 4 * j + u;
+                if (ow >= g.OW) break;
+                const long o = ((long)(n * g.OH + oh) * g.OW + ow) * C4 + c4;
+                float4 v = acc[u];
+                if (res) {
+                    const float4 rv = reinterpret_cast<const float4 *>(res)[o];
+                    v.x += rv.x;
+                    v.y += rv.y;
+                    v.z += rv.z;
+                    v.w += rv.w;
+                }
+                v.x = apply_act(v.x, g.act, g.lo, g.hi);
+                v.y = apply_act(v.y, g.act, g.lo, g.hi);
+                v.z = apply_act(v.z, g.act, g.lo, g.hi);
+                v.w = apply_act(v.w, g.act, g.lo, g.hi);
+                reinterpret_cast<float4 *>(out)[o] = v;
+            }
+        }
+        if (oh > oh_begin && oh + 1 < oh_end) place(slot_of(oh - g.PT + 3), rl);
+        __syncthreads();
+    };
+    // the two register buffers alternate by output row; pairs keep their roles static
+    for (int oh = oh_begin; oh < oh_end; oh += 2) {
+        step(oh, pa, pb);
+        if (oh + 1 < oh_end) step(oh + 1, pb, pa);
+    }
+}
+
 __global__ void depthwise_nhwc(const DwGeo g, const float *in, const float *w, const float *bias,
                                const float *res, float *out) {
     const long total = (long)g.N * g.OH * g.OW * g.C;
@@ -984,7 +1125,7 @@ static int dw3_tile_s1(int OW) { return OW >= 28 ? 4 : 2; }
 // column kernel (MobileNetV2 at batch 1: 0.404 vs 0.428 ms per forward). On large launches it
 // measured slower (the 112 x 112 x 144 s1 layer of 32 images at 32% of HBM peak instead of 47%:
 // its 128-byte channel slices of 576-byte pixels straddle cache lines and the tile does not
-// overlap its loads with its arithmetic), so those keep the column kernel.
+// overlap its loads with its arithmetic), so those take the preloading or row-streaming kernel.
 static bool dw3_lds(int N, int OH, int OW, int C) {
     return (long)N * OH * OW * (C / 4) <= (1L << 18);
 }
@@ -1007,6 +1148,25 @@ extern "C" void mgc_hip_depthwise(mgc_hip_exec *x, int nhwc, int N, int H, int W
             auto kern = SW == 2 ? depthwise3x3_nhwc_lds<2> : depthwise3x3_nhwc_lds<1>;
             MGC_LAUNCH(x, kern, dim3((unsigned)blocks), dim3(256), 0, g, tiles_w, tiles_h, cgroups, in, w, bias,
                        res, out);
+        } else if (vec && k3 && SH == 1 && SW == 1 && PT <= 1 && PL <= 1 &&
+                   !dw3_preload_s1(OW, (long)N * H * W * C * 4)) {
+            // the row-streaming kernel where the column kernels would run (inputs over 64 MB,
+            // narrow rows): 32 x 112 x 112 x 144 in 98 us against 128 us (hipEvent timing, one
+            // box); one round of two workgroups per CU, each walking OH / 4 rows or more
+            // channel slices of at most kDwRowsCQ quads, as even as they go; strips of
+            // 4 * floor(256 / cq) columns
+            const int cgr = (C / 4 + kDwRowsCQ - 1) / kDwRowsCQ;
+            const int cq = (C / 4 + cgr - 1) / cgr;
+            const int tw = 4 * (256 / cq);
+            const int strips = (OW + tw - 1) / tw;
+            const long base = (long)N * strips * cgr;
+            long chunks = (512 + base - 1) / base;
+            if (chunks > (OH + 3) / 4) chunks = (OH + 3) / 4;
+            if (chunks < 1) chunks = 1;
+            const int rows_per = (int)((OH + chunks - 1) / chunks);
+            chunks = (OH + rows_per - 1) / rows_per;
+            MGC_LAUNCH(x, depthwise3x3_nhwc_rows, dim3((unsigned)(base * chunks)), dim3(256), 0, g, strips, cgr, cq,
+                       (int)chunks, rows_per, in, w, bias, res, out);
         } else if (vec && k3) {
             const bool pre = SW == 2 || dw3_preload_s1(OW, (long)N * H * W * C * 4);
             const int tile = pre ? 2 : dw3_tile_s1(OW);

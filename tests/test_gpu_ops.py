@@ -335,9 +335,13 @@ def test_depthwise_with_residual_and_clip(hip_cache):
         ((2, 64, 60, 60), 1),
         ((2, 64, 112, 112), 1),   # more, wide rows: the preloading kernel, two outputs per thread
         ((2, 64, 240, 240), 2),   # ... stride 2
-        ((64, 64, 20, 20), 1),    # narrow rows: the column kernel, two outputs per thread
-        ((1, 1024, 130, 130), 1), # wide rows over 64 MB of input: the column kernel, four outputs
-                                  # per thread (130 is not a multiple of four)
+        ((64, 64, 20, 20), 1),    # narrow rows: the row-streaming kernel, one 64-column strip
+                                  # (16 quads) per image, 20 of its columns used
+        ((1, 1024, 130, 130), 1), # wide rows over 64 MB of input: the row-streaming kernel, four
+                                  # slices of 64 quads, strips of 16 columns (130 = 8 x 16 + 2)
+        ((12, 272, 26, 26), 1),   # narrow rows, two slices of 34 quads, one 28-column strip
+                                  # (26 used), runs of 4 rows
+        ((48, 144, 26, 26), 1),   # 144 channels in one 36-quad slice
     ],
 )
 def test_depthwise_kernels_by_launch_size(x_shape, stride, hip_cache):
@@ -345,6 +349,32 @@ def test_depthwise_kernels_by_launch_size(x_shape, stride, hip_cache):
     attrs = {"kernel_shape": [3, 3], "pads": [1, 1, 1, 1], "group": c, "strides": [stride, stride]}
     g, feeds = op_graph("Conv", [f32(*x_shape), f32(c, 1, 3, 3) * 0.3, f32(c)], const={1, 2}, attrs=attrs)
     check_hip(g, feeds, hip_cache, opt="O3")
+
+
+@pytest.mark.parametrize("pads", [[1, 1, 1, 1], [0, 0, 0, 0], [0, 1, 1, 0]])
+def test_row_streaming_depthwise_residual_clip(pads, hip_cache):
+    """The row-streaming stride-1 kernel (narrow rows, more than 2^18 output quads) with the
+    residual Add and ReLU6 in its epilogue, at the three paddings it takes (top and left 0 or
+    1; the output rows then start at input row 0 or -1)."""
+    from ml_graph_compiler.ir import Graph, TensorType
+    from ml_graph_compiler.shape_inference import infer_shapes
+
+    n, c, hw = 40, 96, 22
+    oh = hw + pads[0] + pads[2] - 2
+    g = Graph("dw_rows")
+    x = g.add_input("x", TensorType("float32", (n, c, hw, hw)))
+    r = g.add_input("r", TensorType("float32", (n, c, oh, hw + pads[1] + pads[3] - 2)))
+    w = g.constant(f32(c, 1, 3, 3) * 0.3, "w")
+    b = g.constant(f32(c), "b")
+    y = g.add_node("Conv", [x, w, b], 1, {"kernel_shape": [3, 3], "pads": pads, "group": c}, name="dw").output
+    y = g.add_node("Add", [y, r], 1, {}, name="res").output
+    lo = g.constant(np.asarray(0.0, np.float32), "lo")
+    hi = g.constant(np.asarray(6.0, np.float32), "hi")
+    y = g.add_node("Clip", [y, lo, hi], 1, {}, name="clip").output
+    g.add_output(y, "y")
+    infer_shapes(g)
+    ow = hw + pads[1] + pads[3] - 2
+    check_hip(g, {"x": f32(n, c, hw, hw) * 3, "r": f32(n, c, oh, ow)}, hip_cache, opt="O3")
 
 
 def test_narrow_pointwise_with_residual(hip_cache):
