@@ -137,10 +137,12 @@ MBCONV_STEM_MIN_ROWS = 0
 # convolution (relu / clip) that alone reads it as one mgc_hip_expand_dw launch (a workgroup per
 # image and 32 expanded channels; the expanded tensor never goes to memory) when
 # mgc_hip_expand_dw_supported accepts the shape and the images times 32-channel slices number
-# at least EXPAND_DW_MIN_WORKGROUPS (fewer leave CUs idle: batch 1 keeps the two launches);
-# tests turn it off to compare.
+# at least EXPAND_DW_MIN_WORKGROUPS; tests turn it off to compare. Measured on MI355X with no
+# lower bound: MobileNetV2 batch 1 0.266 -> 0.256 ms (its 14 x 14 and 7 x 7 blocks then run as
+# 6 to 30 workgroups each, still ahead of two launches), batch 32 unchanged (0.5455 ms with a
+# bound of 0, 32, 96 or 256).
 FUSE_EXPAND_DEPTHWISE = True
-EXPAND_DW_MIN_WORKGROUPS = 256
+EXPAND_DW_MIN_WORKGROUPS = 0
 # The fused GEMMs address their image and weight operands through buffer resources with 32-bit
 # byte offsets, and their launchers refuse operands of this many bytes or more (the unfused
 # kernels have a generic path for them): both fusions are only taken below it.

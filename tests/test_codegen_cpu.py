@@ -112,6 +112,7 @@ def test_kernel_mix_matches_reference(name, kernels, arena, monkeypatch):
     monkeypatch.setattr(hip_codegen, "FUSE_PROJECTION_SHORTCUT", False)
     monkeypatch.setattr(hip_codegen, "FUSE_DEPTHWISE_POINTWISE", False)
     monkeypatch.setattr(hip_codegen, "FUSE_STEM_BLOCK", False)
+    monkeypatch.setattr(hip_codegen, "FUSE_EXPAND_DEPTHWISE", False)
     monkeypatch.setattr(hip_codegen, "SPACE_TO_DEPTH", False)
     monkeypatch.setattr(hip_codegen, "CONV_STEM", False)
     gen = generate_hip(o3(make()))
@@ -270,8 +271,8 @@ def test_expansion_and_depthwise_run_as_one_launch():
     of an image and 32 channels each); the projection stays a GEMM. Only the 28 -> 14 block
     (28 x 28 input: too large a window) keeps its depthwise launch, so with the five whole-block
     launches and the stem block one standalone depthwise launch is left of 17. The block input stays alive (its arena block clear of everything placed) until the
-    call reads it, the expansion FLOPs are counted at the call's node, and at batch 1 (12-30
-    workgroups) and batch 8 the pairs stay apart."""
+    call reads it, the expansion FLOPs are counted at the call's node, and batches 1 and 8 fuse
+    the same ten pairs (6-30 and 48-240 workgroups: still ahead of two launches)."""
     from ml_graph_compiler import ops
     from ml_graph_compiler.codegen.hip import expand_dw_supported, find_expand_depthwise
 
@@ -300,8 +301,9 @@ def test_expansion_and_depthwise_run_as_one_launch():
             if b is x or not (b.start <= order[id(dw)] <= b.end):
                 continue
             assert b.offset + b.size <= x.offset or x.offset + x.size <= b.offset
-    assert not find_expand_depthwise(o3(builders.mobilenet_v2(batch=1)))
-    assert not find_expand_depthwise(o3(builders.mobilenet_v2(batch=8)))
+    for batch in (1, 8):
+        small = find_expand_depthwise(o3(builders.mobilenet_v2(batch=batch)))
+        assert len(small) == 10, batch
     # the kernel's limits: window and row blocks per wave, per input width
     assert expand_dw_supported(14, 14, 96, 576, 2, 7, 7) and expand_dw_supported(16, 14, 64, 32, 2, 8, 7)
     assert not expand_dw_supported(28, 28, 32, 192, 2, 14, 14)
