@@ -137,16 +137,13 @@ def test_kernel_mix_matches_reference(name, kernels, arena, monkeypatch):
     assert "mgc_forward" in gen.source and "int mgc_run(" in gen.source
 
 
-def test_stem_launch_only_for_small_batches():
-    """ResNet-50's stem runs as one mgc_hip_conv_stem launch up to CONV_STEM_MAX_ROWS output
-    pixels (batch 1 here); a batch-32 stem keeps the space-to-depth copy and the GEMM."""
-    from ml_graph_compiler.codegen import hip as hip_codegen
-
-    assert 112 * 112 <= hip_codegen.CONV_STEM_MAX_ROWS < 32 * 112 * 112
-    small = generate_hip(o3(builders.resnet50(batch=1)))
-    assert small.kernels.get("gemm_stem") == 1 and "space_to_depth" not in small.kernels
-    large = generate_hip(o3(builders.resnet50(batch=32)))
-    assert "gemm_stem" not in large.kernels and large.kernels.get("space_to_depth") == 1
+def test_stem_launch_at_every_batch():
+    """ResNet-50's stem runs as one mgc_hip_conv_stem launch at batch 1 and at batch 32 (no
+    space-to-depth copy, the input Transpose read in place)."""
+    for batch in (1, 32):
+        gen = generate_hip(o3(builders.resnet50(batch=batch)))
+        assert gen.kernels.get("gemm_stem") == 1 and "space_to_depth" not in gen.kernels, batch
+        assert "transpose" not in gen.kernels, batch
 
 
 def test_projection_shortcuts_join_their_block_gemm():
