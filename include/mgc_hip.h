@@ -301,7 +301,7 @@ void mgc_hip_mbconv_stem(mgc_hip_exec *x, const mgc_hip_gemm_args *g, const mgc_
  * below 2 GiB, a->w 16-byte aligned, a->ldc >= 64. a->w holds
  * mgc_hip_conv_stem_weight_floats() floats packed as
  *   a->w[((e 32 + l) 2 + h) 2 + b] = W[32 b + l][c][i][2 q + h]  (zero for 2 q + h >= 7)
- * for step e = (c 7 + i) 4 + q. The output is cut into tiles of 4 x 16 pixels that persistent
+ * for step e = (c 7 + i) 4 + q. The output is cut into tiles of 8 x 16 pixels that persistent
  * workgroups take in turn; a->workgroups caps their number (0: the library's choice, one round
  * over the CUs). Sets the launch error outside these limits. Replaces the stem's mgc_gemm over
  * its MGC_OP_CONV_NCHW operand in the reference's C backend
