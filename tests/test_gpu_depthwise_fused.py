@@ -74,6 +74,7 @@ CASES = [
 
 def _run(g: Graph, feeds, cache, fuse: bool, monkeypatch) -> tuple[dict[str, np.ndarray], dict[str, int]]:
     monkeypatch.setattr(hip_codegen, "FUSE_INVERTED_RESIDUAL", False)  # the whole-block kernel: test_gpu_mbconv.py
+    monkeypatch.setattr(hip_codegen, "FUSE_EXPAND_DEPTHWISE", False)  # expansion + depthwise: test_gpu_expand_dw.py
     monkeypatch.setattr(hip_codegen, "FUSE_DEPTHWISE_POINTWISE", fuse)
     monkeypatch.setattr(hip_codegen, "DEPTHWISE_FUSE_MIN_ROWS", 0)
     model = compile_hip(g, cache, "O3")
