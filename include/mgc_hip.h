@@ -12,6 +12,8 @@
  *   mgc_hip_depthwise       <- mgc_depthwise_nhwc / mgc_depthwise_nchw (mgc_runtime.h:175-182)
  *   mgc_hip_pool            <- mgc_pool_nhwc / mgc_pool_nchw (mgc_runtime.h:185-190)
  *   mgc_hip_reduce_mid      <- mgc_reduce_mid (mgc_runtime.h:193)
+ *   mgc_hip_pool_fc         <- mgc_reduce_mid (global average pooling, codegen/c.py:1255-1270) then
+ *                              mgc_gemm for the FusedGemm that reads it (c.py:974-1003), fused
  *   mgc_hip_softmax         <- mgc_softmax (mgc_runtime.h:196)
  *   mgc_hip_layer_norm      <- mgc_layer_norm (mgc_runtime.h:199-200)
  *   mgc_hip_gemm_layer_norm <- mgc_gemm then mgc_layer_norm, fused (mgc_runtime.h:120-161, 199-200)
@@ -370,6 +372,27 @@ void mgc_hip_pool(mgc_hip_exec *x, int nhwc, int is_max, int N, int H, int W, in
 /* Mean or max over the middle axis of an [outer, n, inner] float tensor. */
 void mgc_hip_reduce_mid(mgc_hip_exec *x, int is_max, long outer, long n, long inner,
                         const float *in, float *out);
+
+/* Global average pooling of an NHWC activation followed by a fully connected layer, as one
+ * launch (for a few images: every workgroup pools its whole image):
+ *   out[i * ldo + f] = act(bias[f] + sum_c w[f * C + c] * (1 / P) sum_p x[(i * P + p) * C + c])
+ * for i < N, f < F. Replaces mgc_reduce_mid's mean (mgc_kernels.c:593-612) feeding mgc_gemm
+ * (mgc_kernels.c:370). x and w 16-byte aligned, C % 4 == 0 and C <= 4096
+ * (mgc_hip_pool_fc_supported), ldo >= F; anything else sets MGC_ERR_ARGS. N <= 0 or F <= 0:
+ * nothing to do. */
+typedef struct mgc_hip_pool_fc_args {
+    const float *x;     /* N images of P pixels x C channels (NHWC) */
+    const float *w;     /* F x C: row f holds output f's weights (a Gemm's B with transB = 1) */
+    const float *bias;  /* F floats, or NULL */
+    float *out;         /* row i at out + i * ldo */
+    long ldo;
+    int N, P, C, F;
+    int act;            /* MGC_ACT_* */
+    float lo, hi;       /* clip bounds for MGC_ACT_CLIP */
+} mgc_hip_pool_fc_args;
+
+int mgc_hip_pool_fc_supported(int N, int P, int C, int F);
+void mgc_hip_pool_fc(mgc_hip_exec *x, const mgc_hip_pool_fc_args *a);
 
 /* Generic reduction over the middle axis of [outer, n, inner]: kind 0 sum, 1 mean, 2 max,
  * 3 min, 4 prod; float sums/means/products accumulate in double like the reference. */

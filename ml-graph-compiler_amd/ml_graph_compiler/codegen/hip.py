@@ -99,6 +99,13 @@ SPACE_TO_DEPTH = True
 # Measured on MI355X in the ResNet-50 forward (graph replays, alternating on one box): batch 1
 # 0.3873 -> 0.3855 ms, batch 32 2.7678 -> 2.7654 ms.
 CONV_STEM = True
+# Run a GlobalAveragePool over an NHWC activation and the FusedGemm that alone reads it (through
+# a Reshape / Flatten view) as one mgc_hip_pool_fc launch when the batch is at most
+# POOL_FC_MAX_BATCH (every workgroup pools its whole image, so larger batches keep the pooling
+# launch and the GEMM); tests turn it off to compare. Measured on MI355X (graph replays,
+# alternating on one box): MobileNetV2 b1 0.2560 -> 0.2529 ms, ResNet-50 b1 0.3839 -> 0.3825 ms.
+FUSE_POOL_FC = True
+POOL_FC_MAX_BATCH = 4
 # Fuse recognized attention chains into mgc_hip_attention (tests turn it off to compare).
 FUSE_ATTENTION = True
 # Run a LayerNormalization that directly follows the FusedGemm producing its input inside that
@@ -475,6 +482,45 @@ def find_expand_depthwise(graph: Graph, min_workgroups: int | None = None) -> di
     return found
 
 
+def find_pool_fc(graph: Graph) -> dict[int, Node]:
+    """id(FusedGemm) -> the GlobalAveragePool it reads through one view, for the pairs that run as
+    one mgc_hip_pool_fc launch: an NHWC float pooling of at most POOL_FC_MAX_BATCH images whose
+    output (and the view's) nothing else reads and no graph output is, and a FusedGemm over the
+    pooled vectors (K = the channel count, at most 4096 and a multiple of 4) with a constant
+    right-hand side and no residual."""
+    found: dict[int, Node] = {}
+    outputs = set(map(id, graph.outputs))
+    for gap in graph.nodes:
+        if gap.op != "GlobalAveragePool" or ops.conv_layout(gap) != "NHWC":
+            continue
+        xt = gap.input(0).tensor_type
+        if xt.dtype != "float32" or xt.rank != 4 or not 1 <= xt.shape[0] <= POOL_FC_MAX_BATCH:
+            continue
+        n, c = xt.shape[0], xt.shape[3]
+        if c % 4 or not 4 <= c <= 4096 or xt.shape[1] * xt.shape[2] < 1:
+            continue
+        pooled = gap.output
+        if id(pooled) in outputs or len(pooled.users) != 1:
+            continue
+        view = pooled.users[0]
+        if view.op not in ("Reshape", "Flatten", "Squeeze") or view.input(0) is not pooled:
+            continue
+        if id(view.output) in outputs or len(view.output.users) != 1:
+            continue
+        fc = view.output.users[0]
+        if fc.op != "FusedGemm" or fc.input(0) is not view.output or fc.optional_input(3) is not None:
+            continue
+        b = fc.input(1)
+        bt = b.tensor_type
+        if b.data is None or bt.rank != 2 or fc.output.tensor_type.dtype != "float32":
+            continue
+        k = bt.shape[1] if int(fc.attrs.get("trans_b", 0)) else bt.shape[0]
+        if k != c or view.output.tensor_type.size != n * c:
+            continue
+        found[id(fc)] = gap
+    return found
+
+
 def pack_b_nk(b: np.ndarray) -> np.ndarray:
     """A constant K x N right-hand side stored as its transpose [N][K] (k contiguous), the
     layout the MFMA GEMM reads with 16-byte k-quad loads."""
@@ -556,9 +602,15 @@ class HipEmitter:
         for dw_id in [i for i, ex in self._xd.items() if i in taken or id(ex) in taken]:
             del self._xd[dw_id]
         self._xd_skip = {id(ex) for ex in self._xd.values()}
+        # id(FusedGemm) -> the global average pooling computed in its launch (mgc_hip_pool_fc);
+        # the pooling's input is then read at the GEMM's step.
+        self._pool_fc: dict[int, Node] = find_pool_fc(graph) if FUSE_POOL_FC else {}
+        self._pool_fc_skip = {id(gap) for gap in self._pool_fc.values()}
         order = {id(n): i for i, n in enumerate(graph.nodes)}
         keep = {id(ds.input(0)): order[id(c3)] for c3 in graph.nodes
                 if (ds := self._shortcut.get(id(c3))) is not None}
+        for fc_id, gap in self._pool_fc.items():
+            keep[id(gap.input(0))] = max(keep.get(id(gap.input(0)), 0), order[fc_id])
         for pw in graph.nodes:
             if (dw := self._dwpw.get(id(pw))) is not None:
                 keep[id(dw.input(0))] = max(keep.get(id(dw.input(0)), 0), order[id(pw)])
@@ -598,7 +650,7 @@ class HipEmitter:
                     qkv_bytes = max(qkv_bytes, 3 * m.out.tensor_type.nbytes)
         excluded = (set(self._attn_skip) | set(self._attn_emit) | set(self._shortcut) | self._shortcut_skip
                     | set(self._dwpw) | self._dwpw_skip | set(self._mb) | self._mb_skip | set(self._xd)
-                    | self._xd_skip)
+                    | self._xd_skip | set(self._pool_fc) | self._pool_fc_skip)
         self._folds = plan_folds(graph, self.plan, self._workspace_bytes, excluded) if FOLD_TRANSPOSES else FoldPlan()
         self._scratch_qkv_off = self._scratch_off
         self._scratch_out_off = self._scratch_off + (qkv_bytes + ALIGN - 1) // ALIGN * ALIGN
@@ -817,6 +869,10 @@ class HipEmitter:
             return
         if id(node) in self._ln_skip:
             self.emit(f"/* computed in the split-K reduction of {comment_text(self._ln_skip[id(node)].name)} */")
+            return
+        if id(node) in self._pool_fc_skip:
+            self.emit("/* global average pooling: computed in the launch of the fully connected layer that reads it */")
+            self.count("folded")
             return
         if node.op in ALIAS_OPS:
             if node.op == "Dropout" and len(node.outputs) > 1:
@@ -1281,6 +1337,9 @@ class HipEmitter:
         return ptr, self._workspace_bytes(node) // 4
 
     def op_FusedGemm(self, node: Node) -> None:
+        if id(node) in self._pool_fc:
+            self._pool_fc_call(node, self._pool_fc[id(node)])
+            return
         a, b = node.input(0), node.input(1)
         at, bt = a.tensor_type, b.tensor_type
         self._require_f32(node, at)
@@ -1312,6 +1371,28 @@ class HipEmitter:
             res=self.fptr(res_v) if res_v is not None else "NULL", ldr=n, act=act, lo=lo, hi=hi,
             workspace=ws, workspace_floats=ws_floats, layer_norm=layer_norm,
         )
+
+    def _pool_fc_call(self, node: Node, gap: Node) -> None:
+        """GlobalAveragePool (NHWC) -> view -> FusedGemm as one mgc_hip_pool_fc launch: the
+        reference's mgc_reduce_mid mean (codegen/c.py:1255-1270) and the GEMM over the pooled
+        vectors (c.py:974-1003)."""
+        xt = gap.input(0).tensor_type
+        nb, h, w, c = xt.shape
+        b = node.input(1)
+        trans = int(node.attrs.get("trans_b", 0))
+        matrix = b.data.T if trans else b.data  # K x N
+        f = matrix.shape[1]
+        woff = self.weights.add(pack_b_nk(matrix), key=("packed", id(b), trans))
+        bias_v = node.optional_input(2)
+        act, lo, hi = self._act(node)
+        bias = self._vector_ptr(bias_v, f, "FusedGemm bias") if bias_v is not None else "NULL"
+        self.emit(
+            f"{{ mgc_hip_pool_fc_args pf; pf.x = {self.fptr(gap.input(0))}; pf.w = (const float *)(W + {woff}); "
+            f"pf.bias = {bias}; pf.out = {self.fptr(node.output)}; pf.ldo = {f}L; pf.N = {nb}; pf.P = {h * w}; "
+            f"pf.C = {c}; pf.F = {f}; pf.act = {ACT_CODES[act]}; pf.lo = {_f(lo)}; pf.hi = {_f(hi)}; "
+            f"mgc_hip_pool_fc(x, &pf); }}"
+        )
+        self.count("pool_fc")
 
     def op_Gemm(self, node: Node) -> None:
         a, b, c = node.input(0), node.input(1), node.optional_input(2)
@@ -2082,7 +2163,8 @@ class HipEmitter:
     def _node_flops(self) -> list[int]:
         """FLOPs per node, with the nodes a fused attention call absorbs (among them a QKV
         projection GEMM) counted at the node that emits the call, and a projection shortcut or a
-        depthwise convolution at the convolution whose GEMM computes it: the launches of that
+        depthwise convolution at the convolution whose GEMM computes it, and a global average
+        pooling at the fully connected layer whose launch computes it: the launches of that
         node do the work."""
         index = {id(n): i for i, n in enumerate(self.graph.nodes)}
         flops = [ops.flops(n) for n in self.graph.nodes]
@@ -2103,6 +2185,10 @@ class HipEmitter:
                 i = index[id(n)]
                 flops[index[pw_id]] += flops[i]
                 flops[i] = 0
+        for fc_id, gap in self._pool_fc.items():
+            i = index[id(gap)]
+            flops[index[fc_id]] += flops[i]
+            flops[i] = 0
         for dw_id, ex in self._xd.items():
             i = index[id(ex)]
             flops[index[dw_id]] += flops[i]

@@ -115,6 +115,7 @@ def test_kernel_mix_matches_reference(name, kernels, arena, monkeypatch):
     monkeypatch.setattr(hip_codegen, "FUSE_EXPAND_DEPTHWISE", False)
     monkeypatch.setattr(hip_codegen, "SPACE_TO_DEPTH", False)
     monkeypatch.setattr(hip_codegen, "CONV_STEM", False)
+    monkeypatch.setattr(hip_codegen, "FUSE_POOL_FC", False)
     gen = generate_hip(o3(make()))
     assert gen.kernels == kernels
     if arena is not None:
@@ -133,6 +134,13 @@ def test_kernel_mix_matches_reference(name, kernels, arena, monkeypatch):
         del moved["space_to_depth"]
     assert stem.kernels == moved
     assert stem.plan.arena_bytes == gen.plan.arena_bytes
+    # at batch 1 the global average pooling runs in the launch of the classifier that reads it
+    # (all three networks end GlobalAveragePool -> Flatten -> Gemm)
+    monkeypatch.setattr(hip_codegen, "FUSE_POOL_FC", True)
+    head = generate_hip(o3(make()))
+    moved = dict(moved, gemm=moved["gemm"] - 1, folded=moved.get("folded", 0) + 1, pool_fc=1)
+    del moved["reduce"]
+    assert head.kernels == moved
     assert gen.weights.nbytes % 256 == 0 and len(gen.weights.digest()) == 24
     assert "mgc_forward" in gen.source and "int mgc_run(" in gen.source
 
@@ -155,7 +163,10 @@ def test_projection_shortcuts_join_their_block_gemm():
     pairs = find_projection_shortcuts(g)
     assert len(pairs) == 4
     gen = generate_hip(g, gemm_workspace=native.gemm_workspace_floats)
-    assert gen.kernels["gemm_shortcut"] == 4 and gen.kernels["gemm"] == 49 and gen.kernels["gemm_stem"] == 1
+    # 53 convolutions and the classifier: the stem launch, four shortcut GEMMs in their blocks'
+    # GEMMs, and at batch 1 the classifier in the pooling launch (pool_fc)
+    assert gen.kernels["gemm_shortcut"] == 4 and gen.kernels["gemm"] == 48 and gen.kernels["gemm_stem"] == 1
+    assert gen.kernels["pool_fc"] == 1
     assert gen.source.count("g.k1 = ") == 4
     # the shortcut's FLOPs are timed with the GEMM that computes them
     from ml_graph_compiler import ops
@@ -448,12 +459,20 @@ def test_gemm_family_flops_are_the_algorithmic_work():
     """The emitter's count of the GEMM-family launches' algorithmic FLOPs (what the profiles'
     TFLOP/s divide): ResNet-50 is 8,178,368,512 per image (the 53 convolutions and the FC, with
     the space-to-depth stem counted as the original 7 x 7 convolution and the projection
-    shortcuts at the launches that compute them); BERT-base is everything but the attention
-    products (4 B H S^2 D per layer, which the attention kernel computes)."""
+    shortcuts at the launches that compute them), less the FC's 2 x 2048 x 1000 per image at the
+    batches where the classifier runs in the pooling launch (mgc_hip_pool_fc, not an MFMA kernel);
+    BERT-base is everything but the attention products (4 B H S^2 D per layer, which the attention
+    kernel computes)."""
     from ml_graph_compiler import ops
+    from ml_graph_compiler.codegen import hip as hip_codegen
 
     gen = generate_hip(o3(builders.resnet50(batch=2)), gemm_workspace=native.gemm_workspace_floats)
-    assert gen.gemm_flops == 2 * 8_178_368_512
+    assert gen.kernels.get("pool_fc") == 1
+    assert gen.gemm_flops == 2 * (8_178_368_512 - 2 * 2048 * 1000)
+    batch = hip_codegen.POOL_FC_MAX_BATCH + 1
+    gen = generate_hip(o3(builders.resnet50(batch=batch)), gemm_workspace=native.gemm_workspace_floats)
+    assert "pool_fc" not in gen.kernels
+    assert gen.gemm_flops == batch * 8_178_368_512
     g = o3(builders.bert_base(batch=1, layers=2))
     gen = generate_hip(g, gemm_workspace=native.gemm_workspace_floats,
                        gemm_ln_workspace=native.gemm_layer_norm_workspace_floats)

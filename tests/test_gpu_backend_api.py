@@ -68,7 +68,9 @@ def test_save_load_and_profile(hip_cache, tmp_path):
     prof = compiled.profile()
     assert len(prof) == len(graph.nodes) and all(t >= 0 for _, _, t in prof)
     assert [(op, name) for op, name, _ in prof] == [(n.op, n.name) for n in graph.nodes]
-    assert compiled.report is not None and compiled.report.kernels["gemm"] == 9
+    # the tiny CNN's nine GEMMs, its classifier computed in the global pooling's launch
+    assert compiled.report is not None and compiled.report.kernels["gemm"] == 8
+    assert compiled.report.kernels["pool_fc"] == 1
     compiled.save(tmp_path / "saved")
     compiled.release()
     loaded = HipCompiledModel.load(tmp_path / "saved")
