@@ -12,6 +12,8 @@
  *   mgc_hip_depthwise       <- mgc_depthwise_nhwc / mgc_depthwise_nchw (mgc_runtime.h:175-182)
  *   mgc_hip_pool            <- mgc_pool_nhwc / mgc_pool_nchw (mgc_runtime.h:185-190)
  *   mgc_hip_reduce_mid      <- mgc_reduce_mid (mgc_runtime.h:193)
+ *   mgc_hip_gather_layer_norm <- op_Gather (codegen/c.py:662-688), the Add after it (c.py:360-529)
+ *                              and mgc_layer_norm (mgc_runtime.h:199-200), fused
  *   mgc_hip_pool_fc         <- mgc_reduce_mid (global average pooling, codegen/c.py:1255-1270) then
  *                              mgc_gemm for the FusedGemm that reads it (c.py:974-1003), fused
  *   mgc_hip_softmax         <- mgc_softmax (mgc_runtime.h:196)
@@ -392,6 +394,30 @@ typedef struct mgc_hip_pool_fc_args {
 } mgc_hip_pool_fc_args;
 
 int mgc_hip_pool_fc_supported(int N, int P, int C, int F);
+
+/* Embedding lookup, addend and LayerNorm as one launch (a transformer encoder's input):
+ *   y = table[idx[r]] + addend[r % add_rows];  out[r] = (y - mean(y)) / sqrt(var(y) + eps) * scale + bias
+ * for each of the rows rows of cols floats. Replaces op_Gather (codegen/c.py:662-688), the Add
+ * that reads it (c.py:360-529) and mgc_layer_norm (mgc_runtime.h:199-200); rounds as the Add and
+ * mgc_hip_layer_norm do apart. cols % 4 == 0 and cols <= 1024, table, addend, scale, bias and out
+ * 16-byte aligned (anything else sets MGC_ERR_ARGS); an index outside [-dim, dim) sets
+ * MGC_ERR_GATHER_INDEX and leaves its row unwritten, as mgc_hip_gather does. */
+typedef struct mgc_hip_gather_ln_args {
+    const float *table;  /* dim rows of cols floats */
+    long dim;
+    const void *idx;     /* rows indices */
+    int idx_dtype;       /* MGC_I64 or MGC_I32 */
+    const float *addend; /* add_rows rows of cols floats, row r % add_rows added to row r; or NULL */
+    long add_rows;
+    const float *scale;  /* cols floats, or NULL */
+    const float *bias;   /* cols floats, or NULL */
+    float eps;
+    float *out;          /* rows rows of cols floats */
+    long rows;
+    int cols;
+} mgc_hip_gather_ln_args;
+
+void mgc_hip_gather_layer_norm(mgc_hip_exec *x, const mgc_hip_gather_ln_args *a);
 void mgc_hip_pool_fc(mgc_hip_exec *x, const mgc_hip_pool_fc_args *a);
 
 /* Generic reduction over the middle axis of [outer, n, inner]: kind 0 sum, 1 mean, 2 max,

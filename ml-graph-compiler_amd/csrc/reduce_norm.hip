@@ -315,6 +315,49 @@ __global__ void __launch_bounds__(256) layer_norm_rows_vec4(int rows, int cols4,
     layer_norm_row_vec4(v, lane, cols4, aff, eps, out + (long)r * cols4);
 }
 
+// Embedding lookup, the addend and the LayerNorm in one pass (a transformer encoder's input:
+// Gather of the token table, codegen/c.py:662-688, the Add of the position / segment embeddings,
+// c.py:360-529, and mgc_layer_norm, mgc_runtime.h:199-200): one wavefront per output row r takes
+// row ids[r] of the table and row r % add_rows of the addend (a full-shape addend or one that
+// repeats over the leading dimensions), adds them and normalizes the sum from registers with
+// layer_norm_row_vec4, so it rounds as the Add and the LayerNorm kernel do apart. An index out of
+// range sets the flag and leaves its row unwritten, as gather_rows16_kernel does.
+__global__ void __launch_bounds__(256) gather_add_layer_norm_rows(long rows, int cols4, const float4 *table, long dim,
+                                                                  const void *idx, int idx_dtype,
+                                                                  const float4 *addend, long add_rows,
+                                                                  const float4 *scale, const float4 *bias,
+                                                                  float eps, float4 *out, int *flag) {
+    const int lane = threadIdx.x & 63;
+    const long r = ((long)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    if (r >= rows) return;
+    long k = idx_dtype == MGC_I64 ? static_cast<const long long *>(idx)[r] : (long)static_cast<const int *>(idx)[r];
+    if (k < 0) k += dim;
+    if (k < 0 || k >= dim) {
+        if (lane == 0) *flag = 1;
+        return;
+    }
+    const float4 *src = table + k * cols4;
+    const float4 *add = addend ? addend + (r % add_rows) * cols4 : nullptr;
+    const LnAffine aff = ln_affine_load(lane, cols4, scale, bias);
+    float4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int q = lane + 64 * j;
+        v[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (q < cols4) {
+            v[j] = src[q];
+            if (add) {
+                const float4 a = add[q];
+                v[j].x += a.x;
+                v[j].y += a.y;
+                v[j].z += a.z;
+                v[j].w += a.w;
+            }
+        }
+    }
+    layer_norm_row_vec4(v, lane, cols4, aff, eps, out + r * cols4);
+}
+
 // ---- pooling -----------------------------------------------------------------------------------
 struct PoolGeo {
     int N, H, W, C, KH, KW, SH, SW, DH, DW, PT, PL, PB, PR, OH, OW, include_pad, is_max;
@@ -1068,6 +1111,26 @@ __global__ void __launch_bounds__(kPfThreads) pool_fc_kernel(const float *x, con
 }  // namespace mgc
 
 using namespace mgc;
+
+extern "C" void mgc_hip_gather_layer_norm(mgc_hip_exec *x, const mgc_hip_gather_ln_args *a) {
+    if (a && a->rows <= 0) return;
+    const bool ok = a && a->table && a->idx && a->out && a->dim > 0 && a->cols >= 4 && a->cols % 4 == 0 &&
+                    a->cols <= 1024 && (a->idx_dtype == MGC_I64 || a->idx_dtype == MGC_I32) &&
+                    (!a->addend || a->add_rows >= 1) &&
+                    ((uintptr_t)a->table & 15) == 0 && ((uintptr_t)a->out & 15) == 0 &&
+                    ((uintptr_t)a->addend & 15) == 0 && ((uintptr_t)a->scale & 15) == 0 &&
+                    ((uintptr_t)a->bias & 15) == 0 && a->rows < (1L << 32);
+    if (!ok) {
+        x->launch_error = (int)hipErrorInvalidValue;
+        set_error("mgc_hip_gather_layer_norm: shape, index type or alignment outside its limits",
+                  hipErrorInvalidValue);
+        return;
+    }
+    const long blocks = (a->rows + 3) / 4;  // four rows (one per wave) per workgroup
+    MGC_LAUNCH(x, gather_add_layer_norm_rows, dim3((unsigned)blocks), dim3(256), 0, a->rows, a->cols / 4,
+               (const float4 *)a->table, a->dim, a->idx, a->idx_dtype, (const float4 *)a->addend, a->add_rows,
+               (const float4 *)a->scale, (const float4 *)a->bias, a->eps, (float4 *)a->out, x->flag);
+}
 
 extern "C" int mgc_hip_pool_fc_supported(int N, int P, int C, int F) {
     return N >= 1 && N <= 65535 && P >= 1 && F >= 1 && C >= 4 && C % 4 == 0 && C / 4 <= kPfMaxC4 &&

@@ -106,6 +106,12 @@ CONV_STEM = True
 # alternating on one box): MobileNetV2 b1 0.2560 -> 0.2529 ms, ResNet-50 b1 0.3839 -> 0.3825 ms.
 FUSE_POOL_FC = True
 POOL_FC_MAX_BATCH = 4
+# Run an embedding lookup (Gather of a constant table), the Add of a same-shape or leading-
+# broadcast addend that alone reads it and the LayerNormalization over its rows that alone reads
+# the sum as one mgc_hip_gather_layer_norm launch; tests turn it off to compare. Measured on
+# MI355X (graph replays, alternating on one box): BERT-base b1 0.7702 -> 0.7626 ms, b16 3.440 ->
+# 3.426 ms.
+FUSE_GATHER_LAYER_NORM = True
 # Fuse recognized attention chains into mgc_hip_attention (tests turn it off to compare).
 FUSE_ATTENTION = True
 # Run a LayerNormalization that directly follows the FusedGemm producing its input inside that
@@ -482,6 +488,64 @@ def find_expand_depthwise(graph: Graph, min_workgroups: int | None = None) -> di
     return found
 
 
+def find_gather_layer_norm(graph: Graph) -> dict[int, tuple[Node, Node, Value, int]]:
+    """id(LayerNormalization) -> (Gather, Add, addend, addend rows) for every embedding lookup
+    that runs as one mgc_hip_gather_layer_norm launch: a Gather along axis 0 of a constant float
+    table (rows of cols floats, cols a multiple of 4 and at most 1024) with int64 / int32 indices,
+    whose output only an Add reads; the Add's other operand a float tensor that is the output's
+    shape or repeats over its leading dimensions; and a LayerNormalization over the last axis
+    that alone reads the sum (no Mean / InvStdDev wanted). None of the three outputs but the
+    LayerNorm's may be a graph output."""
+    found: dict[int, tuple[Node, Node, Value, int]] = {}
+    outputs = set(map(id, graph.outputs))
+    for gather in graph.nodes:
+        if gather.op != "Gather" or len(gather.inputs) != 2:
+            continue
+        table, ids = gather.input(0), gather.input(1)
+        tt = table.tensor_type
+        if table.data is None or tt.dtype != "float32" or tt.rank != 2:
+            continue
+        axis = int(gather.attrs.get("axis", 0))
+        if (axis + tt.rank if axis < 0 else axis) != 0 or ids.tensor_type.dtype not in ("int64", "int32"):
+            continue
+        cols = tt.shape[1]
+        if cols % 4 or not 4 <= cols <= 1024:
+            continue
+        g_out = gather.output
+        if id(g_out) in outputs or len(g_out.users) != 1 or g_out.users[0].op != "Add":
+            continue
+        add = g_out.users[0]
+        if len(add.inputs) != 2 or add.input(0) is add.input(1):
+            continue
+        other = add.input(1) if add.input(0) is g_out else add.input(0)
+        ot, yt = other.tensor_type, add.output.tensor_type
+        if ot.dtype != "float32" or yt.shape != g_out.tensor_type.shape or ot.rank > yt.rank:
+            continue
+        dims = (1,) * (yt.rank - ot.rank) + tuple(ot.shape)
+        if dims[-1] != cols:
+            continue
+        lead = 0
+        while lead < yt.rank - 1 and dims[lead] == 1:
+            lead += 1
+        if tuple(dims[lead:-1]) != tuple(yt.shape[lead:-1]):
+            continue
+        add_rows = int(np.prod(dims[lead:-1])) if lead < yt.rank - 1 else 1
+        if id(add.output) in outputs or len(add.output.users) != 1:
+            continue
+        ln = add.output.users[0]
+        if ln.op != "LayerNormalization" or ln.input(0) is not add.output:
+            continue
+        ln_axis = int(ln.attrs.get("axis", -1))
+        if (ln_axis + yt.rank if ln_axis < 0 else ln_axis) != yt.rank - 1:
+            continue
+        if any(o.users or id(o) in outputs for o in ln.outputs[1:]):
+            continue
+        if ln.output.tensor_type.dtype != "float32":
+            continue
+        found[id(ln)] = (gather, add, other, add_rows)
+    return found
+
+
 def find_pool_fc(graph: Graph) -> dict[int, Node]:
     """id(FusedGemm) -> the GlobalAveragePool it reads through one view, for the pairs that run as
     one mgc_hip_pool_fc launch: an NHWC float pooling of at most POOL_FC_MAX_BATCH images whose
@@ -606,11 +670,19 @@ class HipEmitter:
         # the pooling's input is then read at the GEMM's step.
         self._pool_fc: dict[int, Node] = find_pool_fc(graph) if FUSE_POOL_FC else {}
         self._pool_fc_skip = {id(gap) for gap in self._pool_fc.values()}
+        # id(LayerNormalization) -> (Gather, Add, addend, addend rows) run as one launch; the
+        # indices and the addend are then read at the LayerNorm's step.
+        self._gln: dict[int, tuple[Node, Node, Value, int]] = (
+            find_gather_layer_norm(graph) if FUSE_GATHER_LAYER_NORM else {})
+        self._gln_skip = {id(n) for g, a, _, _ in self._gln.values() for n in (g, a)}
         order = {id(n): i for i, n in enumerate(graph.nodes)}
         keep = {id(ds.input(0)): order[id(c3)] for c3 in graph.nodes
                 if (ds := self._shortcut.get(id(c3))) is not None}
         for fc_id, gap in self._pool_fc.items():
             keep[id(gap.input(0))] = max(keep.get(id(gap.input(0)), 0), order[fc_id])
+        for ln_id, (gather, _, other, _) in self._gln.items():
+            for v in (gather.input(1), other):
+                keep[id(v)] = max(keep.get(id(v), 0), order[ln_id])
         for pw in graph.nodes:
             if (dw := self._dwpw.get(id(pw))) is not None:
                 keep[id(dw.input(0))] = max(keep.get(id(dw.input(0)), 0), order[id(pw)])
@@ -650,7 +722,7 @@ class HipEmitter:
                     qkv_bytes = max(qkv_bytes, 3 * m.out.tensor_type.nbytes)
         excluded = (set(self._attn_skip) | set(self._attn_emit) | set(self._shortcut) | self._shortcut_skip
                     | set(self._dwpw) | self._dwpw_skip | set(self._mb) | self._mb_skip | set(self._xd)
-                    | self._xd_skip | set(self._pool_fc) | self._pool_fc_skip)
+                    | self._xd_skip | set(self._pool_fc) | self._pool_fc_skip | set(self._gln) | self._gln_skip)
         self._folds = plan_folds(graph, self.plan, self._workspace_bytes, excluded) if FOLD_TRANSPOSES else FoldPlan()
         self._scratch_qkv_off = self._scratch_off
         self._scratch_out_off = self._scratch_off + (qkv_bytes + ALIGN - 1) // ALIGN * ALIGN
@@ -869,6 +941,10 @@ class HipEmitter:
             return
         if id(node) in self._ln_skip:
             self.emit(f"/* computed in the split-K reduction of {comment_text(self._ln_skip[id(node)].name)} */")
+            return
+        if id(node) in self._gln_skip:
+            self.emit("/* computed in the launch of the LayerNormalization that reads it (gather + add + LayerNorm) */")
+            self.count("folded")
             return
         if id(node) in self._pool_fc_skip:
             self.emit("/* global average pooling: computed in the launch of the fully connected layer that reads it */")
@@ -1239,6 +1315,9 @@ class HipEmitter:
         return self.fptr(value)
 
     def op_LayerNormalization(self, node: Node) -> None:
+        if id(node) in self._gln:
+            self._gather_layer_norm(node, *self._gln[id(node)])
+            return
         xv = node.input(0)
         xt = xv.tensor_type
         self._require_f32(node, xt)
@@ -1251,6 +1330,25 @@ class HipEmitter:
         eps = _f(float(node.attrs.get("epsilon", 1e-5)))
         self.emit(f"mgc_hip_layer_norm(x, {rows}L, {cols}L, {self.fptr(xv)}, {scale}, {bias}, {eps}, {self.fptr(node.output)});")
         self.count("layer_norm")
+
+    def _gather_layer_norm(self, ln: Node, gather: Node, add: Node, other: Value, add_rows: int) -> None:
+        """Gather -> Add -> LayerNormalization as one mgc_hip_gather_layer_norm launch (the
+        reference's op_Gather, codegen/c.py:662-688, the Add's loop nest, c.py:360-529, and
+        mgc_layer_norm)."""
+        table, ids = gather.input(0), gather.input(1)
+        dim, cols = table.tensor_type.shape
+        rows = ids.tensor_type.size
+        scale = self._vector_ptr(ln.optional_input(1), cols, "LayerNormalization scale")
+        bias = self._vector_ptr(ln.optional_input(2), cols, "LayerNormalization bias")
+        eps = _f(float(ln.attrs.get("epsilon", 1e-5)))
+        self.emit(
+            f"{{ mgc_hip_gather_ln_args gl; gl.table = {self.fptr(table)}; gl.dim = {dim}L; "
+            f"gl.idx = {self.ptr(ids)}; gl.idx_dtype = {DTYPE_CODES[ids.tensor_type.dtype]}; "
+            f"gl.addend = {self.fptr(other)}; gl.add_rows = {add_rows}L; gl.scale = {scale}; gl.bias = {bias}; "
+            f"gl.eps = {eps}; gl.out = {self.fptr(ln.output)}; gl.rows = {rows}L; gl.cols = {cols}; "
+            f"mgc_hip_gather_layer_norm(x, &gl); }}"
+        )
+        self.count("gather_layer_norm")
 
     def op_BatchNormalization(self, node: Node) -> None:
         xv = node.input(0)

@@ -154,6 +154,23 @@ def test_stem_launch_at_every_batch():
         assert "transpose" not in gen.kernels, batch
 
 
+def test_bert_embedding_runs_as_one_launch():
+    """BERT-base's token lookup, the position embeddings added to it and the first LayerNorm run
+    as one mgc_hip_gather_layer_norm launch at batch 1 and 16 (the (1, 128, 768) position addend
+    repeats over the batch); the token ids stay alive until that launch reads them."""
+    from ml_graph_compiler.codegen import hip as hip_codegen
+
+    for batch in (1, 16):
+        g = o3(builders.bert_base(batch=batch, layers=1))
+        fused = hip_codegen.find_gather_layer_norm(g)
+        assert len(fused) == 1
+        (gather, add, other, add_rows), = fused.values()
+        assert add_rows == 128 and other.tensor_type.shape == (1, 128, 768)
+        gen = generate_hip(g)
+        assert gen.kernels.get("gather_layer_norm") == 1 and "gather" not in gen.kernels, gen.kernels
+        assert "gl.rows = %dL; gl.cols = 768;" % (128 * batch) in gen.source
+
+
 def test_projection_shortcuts_join_their_block_gemm():
     """ResNet-50's four downsample blocks each lose their shortcut GEMM; the shortcut input
     stays alive (its arena block clear of everything placed) until the fused GEMM reads it."""
