@@ -394,14 +394,16 @@ typedef struct mgc_hip_pool_fc_args {
 } mgc_hip_pool_fc_args;
 
 int mgc_hip_pool_fc_supported(int N, int P, int C, int F);
+void mgc_hip_pool_fc(mgc_hip_exec *x, const mgc_hip_pool_fc_args *a);
 
 /* Embedding lookup, addend and LayerNorm as one launch (a transformer encoder's input):
  *   y = table[idx[r]] + addend[r % add_rows];  out[r] = (y - mean(y)) / sqrt(var(y) + eps) * scale + bias
- * for each of the rows rows of cols floats. Replaces op_Gather (codegen/c.py:662-688), the Add
- * that reads it (c.py:360-529) and mgc_layer_norm (mgc_runtime.h:199-200); rounds as the Add and
- * mgc_hip_layer_norm do apart. cols % 4 == 0 and cols <= 1024, table, addend, scale, bias and out
- * 16-byte aligned (anything else sets MGC_ERR_ARGS); an index outside [-dim, dim) sets
- * MGC_ERR_GATHER_INDEX and leaves its row unwritten, as mgc_hip_gather does. */
+ * for each of the rows rows of cols floats, y itself also stored to sum when that is not NULL.
+ * Replaces op_Gather (codegen/c.py:662-688), the Add that reads it (c.py:360-529) and
+ * mgc_layer_norm (mgc_runtime.h:199-200); rounds as the Add and mgc_hip_layer_norm do apart.
+ * cols % 4 == 0 and cols <= 1024; table, addend, scale, bias, out and sum 16-byte aligned
+ * (anything else sets MGC_ERR_ARGS); an index outside [-dim, dim) sets MGC_ERR_GATHER_INDEX and
+ * leaves its row unwritten, as mgc_hip_gather does. */
 typedef struct mgc_hip_gather_ln_args {
     const float *table;  /* dim rows of cols floats */
     long dim;
@@ -415,10 +417,10 @@ typedef struct mgc_hip_gather_ln_args {
     float *out;          /* rows rows of cols floats */
     long rows;
     int cols;
+    float *sum;          /* rows rows of cols floats: the sum before the LayerNorm, or NULL */
 } mgc_hip_gather_ln_args;
 
 void mgc_hip_gather_layer_norm(mgc_hip_exec *x, const mgc_hip_gather_ln_args *a);
-void mgc_hip_pool_fc(mgc_hip_exec *x, const mgc_hip_pool_fc_args *a);
 
 /* Generic reduction over the middle axis of [outer, n, inner]: kind 0 sum, 1 mean, 2 max,
  * 3 min, 4 prod; float sums/means/products accumulate in double like the reference. */

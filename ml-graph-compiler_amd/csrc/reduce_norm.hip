@@ -320,13 +320,15 @@ __global__ void __launch_bounds__(256) layer_norm_rows_vec4(int rows, int cols4,
 // c.py:360-529, and mgc_layer_norm, mgc_runtime.h:199-200): one wavefront per output row r takes
 // row ids[r] of the table and row r % add_rows of the addend (a full-shape addend or one that
 // repeats over the leading dimensions), adds them and normalizes the sum from registers with
-// layer_norm_row_vec4, so it rounds as the Add and the LayerNorm kernel do apart. An index out of
+// layer_norm_row_vec4, so it rounds as the Add and the LayerNorm kernel do apart; when the sum
+// is read elsewhere too (GPT-2's first residual) it is also stored (sum_out). An index out of
 // range sets the flag and leaves its row unwritten, as gather_rows16_kernel does.
 __global__ void __launch_bounds__(256) gather_add_layer_norm_rows(long rows, int cols4, const float4 *table, long dim,
                                                                   const void *idx, int idx_dtype,
                                                                   const float4 *addend, long add_rows,
                                                                   const float4 *scale, const float4 *bias,
-                                                                  float eps, float4 *out, int *flag) {
+                                                                  float eps, float4 *out, float4 *sum_out,
+                                                                  int *flag) {
     const int lane = threadIdx.x & 63;
     const long r = ((long)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     if (r >= rows) return;
@@ -354,6 +356,11 @@ __global__ void __launch_bounds__(256) gather_add_layer_norm_rows(long rows, int
                 v[j].w += a.w;
             }
         }
+    }
+    if (sum_out) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (lane + 64 * j < cols4) sum_out[r * cols4 + lane + 64 * j] = v[j];
     }
     layer_norm_row_vec4(v, lane, cols4, aff, eps, out + r * cols4);
 }
@@ -1119,7 +1126,7 @@ extern "C" void mgc_hip_gather_layer_norm(mgc_hip_exec *x, const mgc_hip_gather_
                     (!a->addend || a->add_rows >= 1) &&
                     ((uintptr_t)a->table & 15) == 0 && ((uintptr_t)a->out & 15) == 0 &&
                     ((uintptr_t)a->addend & 15) == 0 && ((uintptr_t)a->scale & 15) == 0 &&
-                    ((uintptr_t)a->bias & 15) == 0 && a->rows < (1L << 32);
+                    ((uintptr_t)a->bias & 15) == 0 && ((uintptr_t)a->sum & 15) == 0 && a->rows < (1L << 32);
     if (!ok) {
         x->launch_error = (int)hipErrorInvalidValue;
         set_error("mgc_hip_gather_layer_norm: shape, index type or alignment outside its limits",
@@ -1129,7 +1136,8 @@ extern "C" void mgc_hip_gather_layer_norm(mgc_hip_exec *x, const mgc_hip_gather_
     const long blocks = (a->rows + 3) / 4;  // four rows (one per wave) per workgroup
     MGC_LAUNCH(x, gather_add_layer_norm_rows, dim3((unsigned)blocks), dim3(256), 0, a->rows, a->cols / 4,
                (const float4 *)a->table, a->dim, a->idx, a->idx_dtype, (const float4 *)a->addend, a->add_rows,
-               (const float4 *)a->scale, (const float4 *)a->bias, a->eps, (float4 *)a->out, x->flag);
+               (const float4 *)a->scale, (const float4 *)a->bias, a->eps, (float4 *)a->out, (float4 *)a->sum,
+               x->flag);
 }
 
 extern "C" int mgc_hip_pool_fc_supported(int N, int P, int C, int F) {

@@ -107,10 +107,11 @@ CONV_STEM = True
 FUSE_POOL_FC = True
 POOL_FC_MAX_BATCH = 4
 # Run an embedding lookup (Gather of a constant table), the Add of a same-shape or leading-
-# broadcast addend that alone reads it and the LayerNormalization over its rows that alone reads
-# the sum as one mgc_hip_gather_layer_norm launch; tests turn it off to compare. Measured on
-# MI355X (graph replays, alternating on one box): BERT-base b1 0.7702 -> 0.7626 ms, b16 3.440 ->
-# 3.426 ms.
+# broadcast addend that alone reads it and the LayerNormalization over the sum's rows as one
+# mgc_hip_gather_layer_norm launch (which also stores the sum when later nodes read it); tests
+# turn it off to compare. Measured on MI355X (graph replays, alternating on one box): BERT-base
+# b1 0.7702 -> 0.7626 ms, b16 3.440 -> 3.426 ms; GPT-2 b1 0.8800 -> 0.8721 ms, b8 2.7305 ->
+# 2.7212 ms.
 FUSE_GATHER_LAYER_NORM = True
 # Fuse recognized attention chains into mgc_hip_attention (tests turn it off to compare).
 FUSE_ATTENTION = True
@@ -488,16 +489,19 @@ def find_expand_depthwise(graph: Graph, min_workgroups: int | None = None) -> di
     return found
 
 
-def find_gather_layer_norm(graph: Graph) -> dict[int, tuple[Node, Node, Value, int]]:
-    """id(LayerNormalization) -> (Gather, Add, addend, addend rows) for every embedding lookup
+def find_gather_layer_norm(graph: Graph) -> dict[int, tuple[Node, Node, Value, int, bool]]:
+    """id(LayerNormalization) -> (Gather, Add, addend, addend rows, store the sum?) for every
+    embedding lookup
     that runs as one mgc_hip_gather_layer_norm launch: a Gather along axis 0 of a constant float
     table (rows of cols floats, cols a multiple of 4 and at most 1024) with int64 / int32 indices,
     whose output only an Add reads; the Add's other operand a float tensor that is the output's
     shape or repeats over its leading dimensions; and a LayerNormalization over the last axis
-    that alone reads the sum (no Mean / InvStdDev wanted). None of the three outputs but the
-    LayerNorm's may be a graph output."""
-    found: dict[int, tuple[Node, Node, Value, int]] = {}
+    that reads the sum (no Mean / InvStdDev wanted). Other readers of the sum (GPT-2's first
+    residual) must come after the LayerNorm in schedule order; the launch then also stores the
+    sum. None of the three outputs but the LayerNorm's may be a graph output."""
+    found: dict[int, tuple[Node, Node, Value, int, bool]] = {}
     outputs = set(map(id, graph.outputs))
+    order = {id(n): i for i, n in enumerate(graph.nodes)}
     for gather in graph.nodes:
         if gather.op != "Gather" or len(gather.inputs) != 2:
             continue
@@ -530,10 +534,14 @@ def find_gather_layer_norm(graph: Graph) -> dict[int, tuple[Node, Node, Value, i
         if tuple(dims[lead:-1]) != tuple(yt.shape[lead:-1]):
             continue
         add_rows = int(np.prod(dims[lead:-1])) if lead < yt.rank - 1 else 1
-        if id(add.output) in outputs or len(add.output.users) != 1:
+        if id(add.output) in outputs:
             continue
-        ln = add.output.users[0]
-        if ln.op != "LayerNormalization" or ln.input(0) is not add.output:
+        lns = [u for u in add.output.users if u.op == "LayerNormalization" and u.input(0) is add.output]
+        if not lns:
+            continue
+        ln = min(lns, key=lambda u: order[id(u)])
+        others = [u for u in add.output.users if u is not ln]
+        if any(order[id(u)] <= order[id(ln)] for u in others):
             continue
         ln_axis = int(ln.attrs.get("axis", -1))
         if (ln_axis + yt.rank if ln_axis < 0 else ln_axis) != yt.rank - 1:
@@ -542,7 +550,7 @@ def find_gather_layer_norm(graph: Graph) -> dict[int, tuple[Node, Node, Value, i
             continue
         if ln.output.tensor_type.dtype != "float32":
             continue
-        found[id(ln)] = (gather, add, other, add_rows)
+        found[id(ln)] = (gather, add, other, add_rows, bool(others))
     return found
 
 
@@ -670,17 +678,17 @@ class HipEmitter:
         # the pooling's input is then read at the GEMM's step.
         self._pool_fc: dict[int, Node] = find_pool_fc(graph) if FUSE_POOL_FC else {}
         self._pool_fc_skip = {id(gap) for gap in self._pool_fc.values()}
-        # id(LayerNormalization) -> (Gather, Add, addend, addend rows) run as one launch; the
-        # indices and the addend are then read at the LayerNorm's step.
-        self._gln: dict[int, tuple[Node, Node, Value, int]] = (
+        # id(LayerNormalization) -> (Gather, Add, addend, addend rows, store the sum?) run as
+        # one launch; the indices and the addend are then read at the LayerNorm's step.
+        self._gln: dict[int, tuple[Node, Node, Value, int, bool]] = (
             find_gather_layer_norm(graph) if FUSE_GATHER_LAYER_NORM else {})
-        self._gln_skip = {id(n) for g, a, _, _ in self._gln.values() for n in (g, a)}
+        self._gln_skip = {id(n) for g, a, *_ in self._gln.values() for n in (g, a)}
         order = {id(n): i for i, n in enumerate(graph.nodes)}
         keep = {id(ds.input(0)): order[id(c3)] for c3 in graph.nodes
                 if (ds := self._shortcut.get(id(c3))) is not None}
         for fc_id, gap in self._pool_fc.items():
             keep[id(gap.input(0))] = max(keep.get(id(gap.input(0)), 0), order[fc_id])
-        for ln_id, (gather, _, other, _) in self._gln.items():
+        for ln_id, (gather, _, other, *_) in self._gln.items():
             for v in (gather.input(1), other):
                 keep[id(v)] = max(keep.get(id(v), 0), order[ln_id])
         for pw in graph.nodes:
@@ -1331,10 +1339,11 @@ class HipEmitter:
         self.emit(f"mgc_hip_layer_norm(x, {rows}L, {cols}L, {self.fptr(xv)}, {scale}, {bias}, {eps}, {self.fptr(node.output)});")
         self.count("layer_norm")
 
-    def _gather_layer_norm(self, ln: Node, gather: Node, add: Node, other: Value, add_rows: int) -> None:
+    def _gather_layer_norm(self, ln: Node, gather: Node, add: Node, other: Value, add_rows: int,
+                           store_sum: bool) -> None:
         """Gather -> Add -> LayerNormalization as one mgc_hip_gather_layer_norm launch (the
         reference's op_Gather, codegen/c.py:662-688, the Add's loop nest, c.py:360-529, and
-        mgc_layer_norm)."""
+        mgc_layer_norm); the sum is stored too when later nodes read it."""
         table, ids = gather.input(0), gather.input(1)
         dim, cols = table.tensor_type.shape
         rows = ids.tensor_type.size
@@ -1346,7 +1355,7 @@ class HipEmitter:
             f"gl.idx = {self.ptr(ids)}; gl.idx_dtype = {DTYPE_CODES[ids.tensor_type.dtype]}; "
             f"gl.addend = {self.fptr(other)}; gl.add_rows = {add_rows}L; gl.scale = {scale}; gl.bias = {bias}; "
             f"gl.eps = {eps}; gl.out = {self.fptr(ln.output)}; gl.rows = {rows}L; gl.cols = {cols}; "
-            f"mgc_hip_gather_layer_norm(x, &gl); }}"
+            f"gl.sum = {self.fptr(add.output) if store_sum else 'NULL'}; mgc_hip_gather_layer_norm(x, &gl); }}"
         )
         self.count("gather_layer_norm")
 

@@ -164,11 +164,25 @@ def test_bert_embedding_runs_as_one_launch():
         g = o3(builders.bert_base(batch=batch, layers=1))
         fused = hip_codegen.find_gather_layer_norm(g)
         assert len(fused) == 1
-        (gather, add, other, add_rows), = fused.values()
-        assert add_rows == 128 and other.tensor_type.shape == (1, 128, 768)
+        (gather, add, other, add_rows, store_sum), = fused.values()
+        assert add_rows == 128 and other.tensor_type.shape == (1, 128, 768) and not store_sum
         gen = generate_hip(g)
         assert gen.kernels.get("gather_layer_norm") == 1 and "gather" not in gen.kernels, gen.kernels
         assert "gl.rows = %dL; gl.cols = 768;" % (128 * batch) in gen.source
+
+
+def test_gpt2_embedding_runs_as_one_launch_that_stores_the_sum():
+    """GPT-2's token lookup plus position embeddings is both the first LayerNorm's input and the
+    first residual: the one launch also stores the sum, which the residual reads later."""
+    from ml_graph_compiler.codegen import hip as hip_codegen
+
+    g = o3(builders.gpt2(batch=1, layers=1))
+    fused = hip_codegen.find_gather_layer_norm(g)
+    (gather, add, other, add_rows, store_sum), = fused.values()
+    assert store_sum and add_rows == 128
+    gen = generate_hip(g)
+    assert gen.kernels.get("gather_layer_norm") == 1 and "gather" not in gen.kernels, gen.kernels
+    assert "gl.sum = NULL" not in gen.source and "gl.sum = ((float *)" in gen.source
 
 
 def test_projection_shortcuts_join_their_block_gemm():

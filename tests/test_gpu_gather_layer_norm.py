@@ -8,8 +8,8 @@ wavefront per token row. Graph cases compile such a chain at O3, assert the fuse
 with the oracle on the unoptimized graph and bit for bit with the three launches it replaces
 (the same single add and the same row LayerNorm code). Cases cover BERT's form (a (1, S, D)
 constant addend repeated over the batch), a full-shape addend that is a graph input, a
-(D,)-vector addend, int32 and negative indices, the 1024-column limit and a LayerNorm without a
-bias. An index out of range raises the Gather error as the unfused gather does; the C-ABI cases
+(D,)-vector addend, int32 and negative indices, the 1024-column limit, a LayerNorm without a
+bias, and GPT-2's form, whose sum is also read later as a residual (the launch then stores it). An index out of range raises the Gather error as the unfused gather does; the C-ABI cases
 check that shapes, index types and alignments outside the entry point's limits are refused.
 """
 
@@ -36,8 +36,9 @@ RTOL = 1e-5
 
 
 def embed_graph(b: int, s: int, vocab: int, d: int, addend: str, idx_dtype: str, ln_bias: bool,
-                seed: int) -> tuple[Graph, dict[str, np.ndarray]]:
-    """ids -> Gather(table) -> Add(addend) -> LayerNormalization(gamma[, beta])."""
+                residual: bool, seed: int) -> tuple[Graph, dict[str, np.ndarray]]:
+    """ids -> Gather(table) -> Add(addend) -> LayerNormalization(gamma[, beta]) [+ the sum, as
+    GPT-2's first residual]."""
     rng = np.random.default_rng(seed)
     g = Graph("embed")
     ids = g.add_input("ids", TensorType(idx_dtype, (b, s)))
@@ -51,12 +52,14 @@ def embed_graph(b: int, s: int, vocab: int, d: int, addend: str, idx_dtype: str,
         feeds["extra"] = rng.standard_normal((b, s, d)).astype(np.float32)
     else:
         other = g.constant(rng.standard_normal(d).astype(np.float32), "vec")
-    y = g.add_node("Add", [y, other], 1, {}, name="add").output
+    total = y = g.add_node("Add", [y, other], 1, {}, name="add").output
     gamma = g.constant(rng.uniform(0.5, 1.5, d).astype(np.float32), "gamma")
     inputs = [y, gamma]
     if ln_bias:
         inputs.append(g.constant(rng.normal(0, 0.1, d).astype(np.float32), "beta"))
     y = g.add_node("LayerNormalization", inputs, 1, {"axis": -1, "epsilon": 1e-12}, name="ln").output
+    if residual:
+        y = g.add_node("Add", [y, total], 1, {}, name="residual").output
     g.add_output(y, "y")
     infer_shapes(g)
     ids_v = rng.integers(-vocab, vocab, (b, s)).astype(np.dtype(idx_dtype))
@@ -65,10 +68,11 @@ def embed_graph(b: int, s: int, vocab: int, d: int, addend: str, idx_dtype: str,
 
 
 CASES = [
-    # (b, s, vocab, d, addend, idx dtype, ln bias)
-    (3, 128, 1000, 768, "position", "int64", True),   # BERT's form, negative indices too
-    (2, 17, 50, 1024, "input", "int32", True),        # the column limit, a full-shape graph-input addend
-    (1, 9, 7, 12, "vector", "int64", False),          # three quads per row, no LayerNorm bias
+    # (b, s, vocab, d, addend, idx dtype, ln bias, sum read later)
+    (3, 128, 1000, 768, "position", "int64", True, False),  # BERT's form, negative indices too
+    (2, 17, 50, 1024, "input", "int32", True, False),       # the column limit, a full-shape graph-input addend
+    (1, 9, 7, 12, "vector", "int64", False, False),         # three quads per row, no LayerNorm bias
+    (2, 64, 300, 768, "position", "int64", True, True),     # GPT-2's form: the sum is also the first residual
 ]
 
 
@@ -97,7 +101,7 @@ def test_gather_layer_norm_matches_oracle(case, hip_cache, monkeypatch):
 
 def test_gather_layer_norm_index_out_of_range(hip_cache, monkeypatch):
     print("[gpu] gather + add + layer norm with an index out of range", flush=True)
-    g, feeds = embed_graph(2, 8, 16, 64, "position", "int64", True, seed=5)
+    g, feeds = embed_graph(2, 8, 16, 64, "position", "int64", True, False, seed=5)
     monkeypatch.setattr(hip_codegen, "FUSE_GATHER_LAYER_NORM", True)
     model = compile_hip(g, hip_cache, "O3")
     try:
@@ -118,7 +122,7 @@ class GatherLnArgs(ctypes.Structure):
         ("table", ctypes.c_void_p), ("dim", ctypes.c_long), ("idx", ctypes.c_void_p), ("idx_dtype", ctypes.c_int),
         ("addend", ctypes.c_void_p), ("add_rows", ctypes.c_long), ("scale", ctypes.c_void_p),
         ("bias", ctypes.c_void_p), ("eps", ctypes.c_float), ("out", ctypes.c_void_p), ("rows", ctypes.c_long),
-        ("cols", ctypes.c_int),
+        ("cols", ctypes.c_int), ("sum", ctypes.c_void_p),
     ]
 
 
@@ -135,7 +139,7 @@ def test_gather_layer_norm_entry_point_refuses_unsupported():
         ok = dict(table=table, dim=8, idx=idx, idx_dtype=2, addend=None, add_rows=0, scale=None, bias=None,
                   eps=1e-5, out=out, rows=4, cols=64)
         for bad in (dict(cols=66), dict(cols=1028), dict(out=out + 4), dict(idx_dtype=0), dict(dim=0),
-                    dict(addend=table, add_rows=0)):
+                    dict(addend=table, add_rows=0), dict(sum=out + 8)):
             a = GatherLnArgs(**{**ok, **bad})
             lib.mgc_hip_gather_layer_norm(x, ctypes.byref(a))
             assert lib.mgc_hip_exec_status(x) == MGC_ERR_ARGS, bad
