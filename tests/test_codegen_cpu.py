@@ -54,13 +54,18 @@ def test_kernel_library_exports_every_declared_symbol():
 
 
 def test_ctypes_views_match_the_header_layout(tmp_path):
-    """The ctypes structures the GPU tests pass to the C ABI (tests/capi.py) have the size and
-    field offsets a C compiler gives the header's structs."""
+    """The ctypes structures the GPU tests pass to the C ABI (tests/capi.py and the entry-point
+    tests' own mirrors) have the size and field offsets a C compiler gives the header's structs."""
     import ctypes
 
     import capi
+    from test_gpu_conv_stem import ConvStemArgs, StemArgs
+    from test_gpu_gather_layer_norm import GatherLnArgs
+    from test_gpu_pool_fc import PoolFcArgs
 
-    checks = [("mgc_hip_gemm_args", capi.GemmArgs), ("mgc_hip_operand", capi.Operand)]
+    checks = [("mgc_hip_gemm_args", capi.GemmArgs), ("mgc_hip_operand", capi.Operand),
+              ("mgc_hip_stem_args", StemArgs), ("mgc_hip_conv_stem_args", ConvStemArgs),
+              ("mgc_hip_pool_fc_args", PoolFcArgs), ("mgc_hip_gather_ln_args", GatherLnArgs)]
     lines = ["#include <stddef.h>", "#include <stdio.h>", '#include "mgc_hip.h"', "int main(void) {"]
     for cname, cls in checks:
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
